@@ -1,0 +1,222 @@
+// C ABI: argument validation, error reporting and kernel launches.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+
+#include "attn_kernels.h"
+#include "fwn_attn.h"
+#include "fwn_internal.h"
+
+namespace fwn {
+namespace {
+thread_local char g_error[512] = "";
+}
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_error, sizeof(g_error), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+void clear_error() { g_error[0] = '\0'; }
+
+int check_tile_list(int32_t n_blocks, int32_t n_tiles, int32_t n_cols, const int32_t* ptr,
+                    const int32_t* col) {
+  if (ptr[0] != 0) return fail(FWN_ERR_TILES, "tile list: ptr[0] = %d, expected 0", ptr[0]);
+  const int32_t n_kb = (n_cols + FWN_BLOCK - 1) / FWN_BLOCK;
+  for (int32_t b = 0; b < n_blocks; ++b) {
+    if (ptr[b + 1] < ptr[b]) return fail(FWN_ERR_TILES, "tile list: ptr decreases at block %d", b);
+    for (int32_t t = ptr[b]; t < ptr[b + 1] && t < n_tiles; ++t) {
+      if (col[t] < 0 || col[t] >= n_kb)
+        return fail(FWN_ERR_TILES, "tile list: tile %d column block %d outside [0, %d)", t, col[t], n_kb);
+      if (t > ptr[b] && col[t] <= col[t - 1])
+        return fail(FWN_ERR_TILES, "tile list: column blocks of block %d not strictly increasing", b);
+    }
+  }
+  if (ptr[n_blocks] != n_tiles)
+    return fail(FWN_ERR_TILES, "tile list: ptr[n_blocks] = %d, expected n_tiles = %d", ptr[n_blocks], n_tiles);
+  return FWN_OK;
+}
+
+namespace {
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+int check_desc(const fwn_attn_desc* d) {
+  if (!d) return fail(FWN_ERR_INVALID_ARG, "null descriptor");
+  if (d->batch <= 0 || d->n <= 0 || d->heads <= 0)
+    return fail(FWN_ERR_INVALID_ARG, "batch, n and heads must be positive (got %d, %d, %d)", d->batch, d->n,
+                d->heads);
+  if (d->head_dim != 32 && d->head_dim != 64 && d->head_dim != 128)
+    return fail(FWN_ERR_UNSUPPORTED, "head_dim %d not built (32, 64, 128)", d->head_dim);
+  if (d->dtype != FWN_F32 && d->dtype != FWN_BF16)
+    return fail(FWN_ERR_UNSUPPORTED, "dtype %d not supported (0 = f32, 1 = bf16)", d->dtype);
+  if (!(d->scale > 0.f) || !std::isfinite(d->scale))
+    return fail(FWN_ERR_INVALID_ARG, "scale must be positive and finite");
+  const int64_t vec = d->dtype == FWN_BF16 ? 8 : 4;  // elements per 16 bytes
+  if (d->stride_b < 0 || d->stride_n <= 0 || d->stride_h < 0 || d->stride_b % vec || d->stride_n % vec ||
+      d->stride_h % vec)
+    return fail(FWN_ERR_INVALID_ARG, "strides must be non-negative multiples of 16 bytes");
+  if (d->stride_n < d->head_dim || (d->heads > 1 && d->stride_h < d->head_dim))
+    return fail(FWN_ERR_INVALID_ARG, "strides overlap rows or heads");
+  const int64_t n_blocks = (d->n + FWN_BLOCK - 1) / FWN_BLOCK;
+  if (n_blocks * d->batch * d->heads > INT32_MAX)
+    return fail(FWN_ERR_INVALID_ARG, "grid too large");
+  // Buffer offsets are 32-bit: every row of a (batch, head) slice, padding rows of the last block
+  // included, must be addressable below 2 GiB.
+  const int64_t elem = d->dtype == FWN_BF16 ? 2 : 4;
+  if ((n_blocks * FWN_BLOCK + 1) * d->stride_n * elem >= ((int64_t)1 << 31))
+    return fail(FWN_ERR_INVALID_ARG, "a (batch, head) slice spans 2 GiB or more");
+  return FWN_OK;
+}
+
+int check_tensor(const void* p, const char* name) {
+  if (!p) return fail(FWN_ERR_INVALID_ARG, "%s is null", name);
+  if (!aligned16(p)) return fail(FWN_ERR_INVALID_ARG, "%s is not 16-byte aligned", name);
+  return FWN_OK;
+}
+
+int check_tiles(const fwn_attn_desc* d, const fwn_tiles* t, const char* name) {
+  if (!t) return fail(FWN_ERR_INVALID_ARG, "%s is null", name);
+  const int32_t n_blocks = (d->n + FWN_BLOCK - 1) / FWN_BLOCK;
+  if (t->n_blocks != n_blocks)
+    return fail(FWN_ERR_TILES, "%s has %d row blocks, expected %d for n = %d", name, t->n_blocks, n_blocks, d->n);
+  if (t->n_tiles < 0 || !t->ptr || (t->n_tiles > 0 && (!t->col || !t->lanes || !t->full)))
+    return fail(FWN_ERR_TILES, "%s: missing device arrays", name);
+  return FWN_OK;
+}
+
+KArgs base_args(const fwn_attn_desc* d) {
+  KArgs a = {};
+  a.n = d->n;
+  a.heads = d->heads;
+  a.batch = d->batch;
+  a.n_blocks = (d->n + FWN_BLOCK - 1) / FWN_BLOCK;
+  a.sb = d->stride_b;
+  a.sn = d->stride_n;
+  a.sh = d->stride_h;
+  a.slice_bytes = (uint32_t)(((int64_t)(d->n - 1) * d->stride_n + d->head_dim) * (d->dtype == FWN_BF16 ? 2 : 4));
+  a.scale = d->scale;
+  a.c2 = (float)((double)d->scale * 1.4426950408889634);
+  return a;
+}
+
+void set_tiles(KArgs& a, const fwn_tiles* t) {
+  a.ptr = t->ptr;
+  a.col = t->col;
+  a.lanes = t->lanes;
+  a.full = t->full;
+  a.order = t->order;
+  a.n_tiles = t->n_tiles;
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) return FWN_OK;
+  return fail(FWN_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+}  // namespace
+}  // namespace fwn
+
+using namespace fwn;
+
+extern "C" {
+
+const char* fwn_last_error(void) { return fwn::g_error; }
+
+int fwn_attn_fwd_launch(const fwn_attn_desc* desc, const void* q, const void* k, const void* v,
+                        const fwn_tiles* tiles, void* o, float* lse, void* stream) {
+  clear_error();
+  if (int rc = check_desc(desc)) return rc;
+  if (int rc = check_tensor(q, "q")) return rc;
+  if (int rc = check_tensor(k, "k")) return rc;
+  if (int rc = check_tensor(v, "v")) return rc;
+  if (int rc = check_tensor(o, "o")) return rc;
+  if (int rc = check_tiles(desc, tiles, "tiles")) return rc;
+  KArgs a = base_args(desc);
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.out0 = o;
+  a.lse_out = lse;
+  set_tiles(a, tiles);
+  return hip_status(launch(Kind::kFwd, desc->dtype, desc->head_dim, a, (hipStream_t)stream), "forward launch");
+}
+
+int fwn_attn_bwd_delta_launch(const fwn_attn_desc* desc, const void* o, const void* dout, float* delta,
+                              void* stream) {
+  clear_error();
+  if (int rc = check_desc(desc)) return rc;
+  if (int rc = check_tensor(o, "o")) return rc;
+  if (int rc = check_tensor(dout, "dout")) return rc;
+  if (!delta) return fail(FWN_ERR_INVALID_ARG, "delta is null");
+  KArgs a = base_args(desc);
+  a.o = o;
+  a.dout = dout;
+  a.lse_out = delta;
+  return hip_status(launch(Kind::kDelta, desc->dtype, desc->head_dim, a, (hipStream_t)stream), "delta launch");
+}
+
+int fwn_attn_bwd_dq_launch(const fwn_attn_desc* desc, const void* q, const void* k, const void* v,
+                           const void* dout, const float* lse, const float* delta, const fwn_tiles* tiles,
+                           void* dq, void* stream) {
+  clear_error();
+  if (int rc = check_desc(desc)) return rc;
+  if (int rc = check_tensor(q, "q")) return rc;
+  if (int rc = check_tensor(k, "k")) return rc;
+  if (int rc = check_tensor(v, "v")) return rc;
+  if (int rc = check_tensor(dout, "dout")) return rc;
+  if (int rc = check_tensor(dq, "dq")) return rc;
+  if (!lse || !delta) return fail(FWN_ERR_INVALID_ARG, "lse and delta are required");
+  if (int rc = check_tiles(desc, tiles, "tiles")) return rc;
+  KArgs a = base_args(desc);
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.dout = dout;
+  a.lse = lse;
+  a.delta = delta;
+  a.out0 = dq;
+  set_tiles(a, tiles);
+  return hip_status(launch(Kind::kDq, desc->dtype, desc->head_dim, a, (hipStream_t)stream), "dq launch");
+}
+
+int fwn_attn_bwd_dkv_launch(const fwn_attn_desc* desc, const void* q, const void* k, const void* v,
+                            const void* dout, const float* lse, const float* delta, const fwn_tiles* tiles_t,
+                            void* dk, void* dv, void* stream) {
+  clear_error();
+  if (int rc = check_desc(desc)) return rc;
+  if (int rc = check_tensor(q, "q")) return rc;
+  if (int rc = check_tensor(k, "k")) return rc;
+  if (int rc = check_tensor(v, "v")) return rc;
+  if (int rc = check_tensor(dout, "dout")) return rc;
+  if (int rc = check_tensor(dk, "dk")) return rc;
+  if (int rc = check_tensor(dv, "dv")) return rc;
+  if (!lse || !delta) return fail(FWN_ERR_INVALID_ARG, "lse and delta are required");
+  if (int rc = check_tiles(desc, tiles_t, "tiles_t")) return rc;
+  KArgs a = base_args(desc);
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.dout = dout;
+  a.lse = lse;
+  a.delta = delta;
+  a.out0 = dk;
+  a.out1 = dv;
+  set_tiles(a, tiles_t);
+  return hip_status(launch(Kind::kDkv, desc->dtype, desc->head_dim, a, (hipStream_t)stream), "dkv launch");
+}
+
+int fwn_attn_bwd_launch(const fwn_attn_desc* desc, const void* q, const void* k, const void* v, const void* o,
+                        const void* dout, const float* lse, float* delta, const fwn_tiles* tiles,
+                        const fwn_tiles* tiles_t, void* dq, void* dk, void* dv, void* stream) {
+  if (int rc = fwn_attn_bwd_delta_launch(desc, o, dout, delta, stream)) return rc;
+  if (int rc = fwn_attn_bwd_dq_launch(desc, q, k, v, dout, lse, delta, tiles, dq, stream)) return rc;
+  return fwn_attn_bwd_dkv_launch(desc, q, k, v, dout, lse, delta, tiles_t ? tiles_t : tiles, dk, dv, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,356 @@
+// Host mask pipeline: k-hop neighbourhoods, Hilbert order, CSR live-tile lists.
+//
+// The reference does this at trace time in numpy/scipy (patch.py:208-219): `adj ** k` as a
+// sparse matrix power (35 s for the 32-hop r6 mask, docs/results/attn_bwd/...:3), hilbert_order
+// (pallas_attn.py:71-82) and build_tile_mask (pallas_attn.py:85-109). Here each stage is a
+// multi-threaded pass over CSR rows: a bounded breadth-first search per node for the k-hop
+// mask, and a per-row-block merge for the tile list.
+#include <algorithm>
+#include <atomic>
+#include <cmath>
+#include <cstring>
+#include <thread>
+#include <vector>
+
+#include "fwn_attn.h"
+#include "fwn_internal.h"
+
+namespace {
+
+int worker_count() {
+  unsigned hw = std::thread::hardware_concurrency();
+  if (hw == 0) hw = 4;
+  return (int)std::min<unsigned>(hw, 16);
+}
+
+// Runs fn(begin, end) over [0, n) split into chunks handed out dynamically to the workers.
+template <typename Fn>
+void parallel_for(int64_t n, int64_t grain, Fn fn) {
+  int workers = worker_count();
+  if (n <= grain || workers <= 1) {
+    fn((int64_t)0, n);
+    return;
+  }
+  std::atomic<int64_t> next(0);
+  std::vector<std::thread> pool;
+  for (int w = 0; w < workers; ++w) {
+    pool.emplace_back([&]() {
+      for (;;) {
+        int64_t b = next.fetch_add(grain);
+        if (b >= n) break;
+        fn(b, std::min(n, b + grain));
+      }
+    });
+  }
+  for (auto& t : pool) t.join();
+}
+
+// Breadth-first ball of radius k around src; `stamp` marks visited nodes with `mark`.
+void bfs_ball(int32_t src, int32_t k, const int64_t* adj_ptr, const int32_t* adj_idx,
+              std::vector<int32_t>& stamp, int32_t mark, std::vector<int32_t>& ball) {
+  ball.clear();
+  ball.push_back(src);
+  stamp[src] = mark;
+  size_t lo = 0;
+  for (int32_t hop = 0; hop < k; ++hop) {
+    size_t hi = ball.size();
+    if (lo == hi) break;
+    for (size_t f = lo; f < hi; ++f) {
+      int32_t u = ball[f];
+      for (int64_t e = adj_ptr[u]; e < adj_ptr[u + 1]; ++e) {
+        int32_t w = adj_idx[e];
+        if (stamp[w] != mark) {
+          stamp[w] = mark;
+          ball.push_back(w);
+        }
+      }
+    }
+    lo = hi;
+  }
+}
+
+bool check_adjacency(int32_t n, const int64_t* adj_ptr, const int32_t* adj_idx) {
+  if (n <= 0 || !adj_ptr || (adj_ptr[n] > 0 && !adj_idx)) return false;
+  if (adj_ptr[0] != 0) return false;
+  for (int32_t i = 0; i < n; ++i)
+    if (adj_ptr[i + 1] < adj_ptr[i]) return false;
+  for (int64_t e = 0; e < adj_ptr[n]; ++e)
+    if (adj_idx[e] < 0 || adj_idx[e] >= n) return false;
+  return true;
+}
+
+// Skilling's transpose algorithm for the 3-D Hilbert index ("Programming the Hilbert curve",
+// AIP Conf. Proc. 707, 2004), interleaved most-significant bit first with axis 0 leading each
+// triple, as pallas_attn._hilbert3 (pallas_attn.py:41-68).
+int64_t hilbert3(int64_t x0, int64_t x1, int64_t x2, int bits) {
+  int64_t x[3] = {x0, x1, x2};
+  const int64_t top = (int64_t)1 << (bits - 1);
+  for (int64_t q = top; q > 1; q >>= 1) {
+    const int64_t low = q - 1;
+    for (int i = 0; i < 3; ++i) {
+      if (x[i] & q) {
+        x[0] ^= low;
+      } else {
+        int64_t t = (x[0] ^ x[i]) & low;
+        x[0] ^= t;
+        x[i] ^= t;
+      }
+    }
+  }
+  x[1] ^= x[0];
+  x[2] ^= x[1];
+  int64_t flip = 0;
+  for (int64_t q = top; q > 1; q >>= 1)
+    if (x[2] & q) flip ^= q - 1;
+  for (int i = 0; i < 3; ++i) x[i] ^= flip;
+  int64_t code = 0;
+  for (int b = bits - 1; b >= 0; --b)
+    for (int i = 0; i < 3; ++i) code = (code << 1) | ((x[i] >> b) & 1);
+  return code;
+}
+
+struct Csr {
+  int32_t n_rows, n_cols;
+  const int64_t* row_ptr;
+  const int32_t* idx;
+  const int64_t* perm;      // permuted row i is original row perm[i]
+  std::vector<int32_t> inv;  // original column c is permuted column inv[c]
+
+  int64_t orig_row(int32_t r) const { return perm ? perm[r] : r; }
+  int32_t col(int32_t c) const { return perm ? inv[c] : c; }
+};
+
+int make_csr(Csr& m, int32_t n_rows, int32_t n_cols, const int64_t* row_ptr, const int32_t* idx,
+             const int64_t* perm) {
+  if (n_rows <= 0 || n_cols <= 0 || !row_ptr) return fwn::fail(FWN_ERR_INVALID_ARG, "empty or null mask");
+  if (row_ptr[0] != 0) return fwn::fail(FWN_ERR_INVALID_ARG, "row_ptr[0] != 0");
+  for (int32_t i = 0; i < n_rows; ++i)
+    if (row_ptr[i + 1] < row_ptr[i]) return fwn::fail(FWN_ERR_INVALID_ARG, "row_ptr not monotone");
+  if (row_ptr[n_rows] > 0 && !idx) return fwn::fail(FWN_ERR_INVALID_ARG, "null column indices");
+  for (int64_t e = 0; e < row_ptr[n_rows]; ++e)
+    if (idx[e] < 0 || idx[e] >= n_cols) return fwn::fail(FWN_ERR_INVALID_ARG, "column index out of range");
+  m.n_rows = n_rows;
+  m.n_cols = n_cols;
+  m.row_ptr = row_ptr;
+  m.idx = idx;
+  m.perm = perm;
+  if (perm) {
+    if (n_rows != n_cols) return fwn::fail(FWN_ERR_INVALID_ARG, "perm needs a square mask");
+    m.inv.assign(n_cols, -1);
+    for (int32_t i = 0; i < n_rows; ++i) {
+      if (perm[i] < 0 || perm[i] >= n_rows || m.inv[perm[i]] != -1)
+        return fwn::fail(FWN_ERR_INVALID_ARG, "perm is not a permutation");
+      m.inv[perm[i]] = i;
+    }
+  }
+  return FWN_OK;
+}
+
+// Sorted distinct column blocks of row block qb.
+void block_columns(const Csr& m, int32_t qb, std::vector<int32_t>& seen, std::vector<int32_t>& out) {
+  out.clear();
+  int32_t r0 = qb * FWN_BLOCK, r1 = std::min(m.n_rows, r0 + FWN_BLOCK);
+  for (int32_t r = r0; r < r1; ++r) {
+    int64_t o = m.orig_row(r);
+    for (int64_t e = m.row_ptr[o]; e < m.row_ptr[o + 1]; ++e) {
+      int32_t kb = m.col(m.idx[e]) / FWN_BLOCK;
+      if (seen[kb] != qb) {
+        seen[kb] = qb;
+        out.push_back(kb);
+      }
+    }
+  }
+  std::sort(out.begin(), out.end());
+}
+
+}  // namespace
+
+extern "C" {
+
+int fwn_khop_count(int32_t n, const int64_t* adj_ptr, const int32_t* adj_idx, int32_t k,
+                   int64_t* row_ptr) {
+  fwn::clear_error();
+  if (k < 0 || !row_ptr || !check_adjacency(n, adj_ptr, adj_idx))
+    return fwn::fail(FWN_ERR_INVALID_ARG, "fwn_khop_count: invalid adjacency, k or output");
+  std::vector<int64_t> size(n);
+  parallel_for(n, 256, [&](int64_t b, int64_t e) {
+    std::vector<int32_t> stamp(n, -1), ball;
+    for (int64_t s = b; s < e; ++s) {
+      bfs_ball((int32_t)s, k, adj_ptr, adj_idx, stamp, (int32_t)s, ball);
+      size[s] = (int64_t)ball.size();
+    }
+  });
+  row_ptr[0] = 0;
+  for (int32_t i = 0; i < n; ++i) row_ptr[i + 1] = row_ptr[i] + size[i];
+  return FWN_OK;
+}
+
+int fwn_khop_fill(int32_t n, const int64_t* adj_ptr, const int32_t* adj_idx, int32_t k,
+                  const int64_t* row_ptr, int32_t* idx) {
+  fwn::clear_error();
+  if (k < 0 || !row_ptr || !idx || !check_adjacency(n, adj_ptr, adj_idx))
+    return fwn::fail(FWN_ERR_INVALID_ARG, "fwn_khop_fill: invalid adjacency, k or output");
+  std::atomic<bool> bad(false);
+  parallel_for(n, 256, [&](int64_t b, int64_t e) {
+    std::vector<int32_t> stamp(n, -1), ball;
+    for (int64_t s = b; s < e; ++s) {
+      bfs_ball((int32_t)s, k, adj_ptr, adj_idx, stamp, (int32_t)s, ball);
+      if ((int64_t)ball.size() != row_ptr[s + 1] - row_ptr[s]) {
+        bad = true;
+        return;
+      }
+      std::sort(ball.begin(), ball.end());
+      std::memcpy(idx + row_ptr[s], ball.data(), ball.size() * sizeof(int32_t));
+    }
+  });
+  if (bad) return fwn::fail(FWN_ERR_INVALID_ARG, "fwn_khop_fill: row_ptr does not match the k-hop counts");
+  return FWN_OK;
+}
+
+int fwn_hilbert_order(int64_t n, const double* lat_deg, const double* lon_deg, int32_t bits,
+                      int64_t* perm) {
+  fwn::clear_error();
+  if (n <= 0 || !lat_deg || !lon_deg || !perm || bits < 1 || bits > 20)
+    return fwn::fail(FWN_ERR_INVALID_ARG, "fwn_hilbert_order: invalid arguments");
+  const double deg = M_PI / 180.0;
+  const double top = (double)((1 << bits) - 1);
+  std::vector<int64_t> code(n);
+  parallel_for(n, 4096, [&](int64_t b, int64_t e) {
+    for (int64_t i = b; i < e; ++i) {
+      double la = lat_deg[i] * deg, lo = lon_deg[i] * deg;
+      double xyz[3] = {std::cos(la) * std::cos(lo), std::cos(la) * std::sin(lo), std::sin(la)};
+      bool finite = std::isfinite(xyz[0]) && std::isfinite(xyz[1]) && std::isfinite(xyz[2]);
+      if (!finite) {
+        code[i] = INT64_MAX;
+        continue;
+      }
+      int64_t q[3];
+      for (int a = 0; a < 3; ++a) {
+        double v = std::nearbyint((xyz[a] + 1.0) / 2.0 * top);  // round half to even, as numpy
+        q[a] = (int64_t)std::min(std::max(v, 0.0), top);
+      }
+      code[i] = hilbert3(q[0], q[1], q[2], bits);
+    }
+  });
+  for (int64_t i = 0; i < n; ++i) perm[i] = i;
+  std::stable_sort(perm, perm + n, [&](int64_t a, int64_t b) { return code[a] < code[b]; });
+  return FWN_OK;
+}
+
+int fwn_tiles_count(int32_t n_rows, int32_t n_cols, const int64_t* row_ptr, const int32_t* idx,
+                    const int64_t* perm, int32_t* tile_ptr) {
+  fwn::clear_error();
+  Csr m;
+  if (int rc = make_csr(m, n_rows, n_cols, row_ptr, idx, perm)) return rc;
+  if (!tile_ptr) return fwn::fail(FWN_ERR_INVALID_ARG, "fwn_tiles_count: null tile_ptr");
+  const int32_t n_qb = (n_rows + FWN_BLOCK - 1) / FWN_BLOCK;
+  const int32_t n_kb = (n_cols + FWN_BLOCK - 1) / FWN_BLOCK;
+  std::vector<int64_t> count(n_qb);
+  parallel_for(n_qb, 4, [&](int64_t b, int64_t e) {
+    std::vector<int32_t> seen(n_kb, -1), cols;
+    for (int64_t qb = b; qb < e; ++qb) {
+      block_columns(m, (int32_t)qb, seen, cols);
+      count[qb] = (int64_t)cols.size();
+    }
+  });
+  int64_t total = 0;
+  tile_ptr[0] = 0;
+  for (int32_t qb = 0; qb < n_qb; ++qb) {
+    total += count[qb];
+    if (total > INT32_MAX) return fwn::fail(FWN_ERR_INVALID_ARG, "fwn_tiles_count: too many tiles");
+    tile_ptr[qb + 1] = (int32_t)total;
+  }
+  return FWN_OK;
+}
+
+int fwn_tiles_fill(int32_t n_rows, int32_t n_cols, const int64_t* row_ptr, const int32_t* idx,
+                   const int64_t* perm, const int32_t* tile_ptr, int32_t* tile_col,
+                   uint32_t* tile_bits) {
+  fwn::clear_error();
+  Csr m;
+  if (int rc = make_csr(m, n_rows, n_cols, row_ptr, idx, perm)) return rc;
+  if (!tile_ptr || !tile_col || !tile_bits)
+    return fwn::fail(FWN_ERR_INVALID_ARG, "fwn_tiles_fill: null output");
+  const int32_t n_qb = (n_rows + FWN_BLOCK - 1) / FWN_BLOCK;
+  const int32_t n_kb = (n_cols + FWN_BLOCK - 1) / FWN_BLOCK;
+  const int64_t words = FWN_BLOCK * (FWN_BLOCK / 32);
+  std::atomic<bool> bad(false);
+  parallel_for(n_qb, 4, [&](int64_t b, int64_t e) {
+    std::vector<int32_t> seen(n_kb, -1), local(n_kb, -1), cols;
+    for (int64_t qb = b; qb < e; ++qb) {
+      block_columns(m, (int32_t)qb, seen, cols);
+      const int64_t t0 = tile_ptr[qb];
+      if ((int64_t)cols.size() != tile_ptr[qb + 1] - t0) {
+        bad = true;
+        return;
+      }
+      for (size_t c = 0; c < cols.size(); ++c) {
+        tile_col[t0 + c] = cols[c];
+        local[cols[c]] = (int32_t)c;
+      }
+      std::memset(tile_bits + t0 * words, 0, cols.size() * words * sizeof(uint32_t));
+      int32_t r0 = (int32_t)qb * FWN_BLOCK, r1 = std::min(n_rows, r0 + FWN_BLOCK);
+      for (int32_t r = r0; r < r1; ++r) {
+        int64_t o = m.orig_row(r);
+        for (int64_t en = m.row_ptr[o]; en < m.row_ptr[o + 1]; ++en) {
+          int32_t j = m.col(m.idx[en]);
+          int64_t t = t0 + local[j / FWN_BLOCK];
+          int32_t within = j % FWN_BLOCK;
+          tile_bits[t * words + (r - r0) * (FWN_BLOCK / 32) + within / 32] |= 1u << (within % 32);
+        }
+      }
+    }
+  });
+  if (bad) return fwn::fail(FWN_ERR_INVALID_ARG, "fwn_tiles_fill: tile_ptr does not match the mask");
+  return FWN_OK;
+}
+
+int fwn_tiles_prepare(int32_t n_blocks, int32_t n_tiles, int32_t n_cols, const int32_t* tile_ptr,
+                      const int32_t* tile_col, const uint32_t* tile_bits, uint64_t* lanes,
+                      uint32_t* full, int32_t* order) {
+  fwn::clear_error();
+  if (n_blocks <= 0 || n_tiles < 0 || n_cols <= 0 || !tile_ptr || (n_tiles > 0 && (!tile_col || !tile_bits)) ||
+      (n_tiles > 0 && (!lanes || !full)) || !order)
+    return fwn::fail(FWN_ERR_INVALID_ARG, "fwn_tiles_prepare: null or empty argument");
+  if (int rc = fwn::check_tile_list(n_blocks, n_tiles, n_cols, tile_ptr, tile_col)) return rc;
+  const int32_t words = FWN_BLOCK / 32;
+  const int32_t tail = n_cols % FWN_BLOCK;  // valid columns in the last column block (0 = all)
+  const int32_t last_kb = (n_cols - 1) / FWN_BLOCK;
+  std::atomic<bool> bad(false);
+  parallel_for(n_tiles, 64, [&](int64_t b, int64_t e) {
+    for (int64_t t = b; t < e; ++t) {
+      const uint32_t* bits = tile_bits + t * (int64_t)FWN_BLOCK * words;
+      if (tile_col[t] == last_kb && tail) {
+        for (int32_t r = 0; r < FWN_BLOCK; ++r)
+          for (int32_t j = tail; j < FWN_BLOCK; ++j)
+            if ((bits[r * words + j / 32] >> (j % 32)) & 1u) bad = true;
+      }
+      uint32_t f = 0;
+      for (int32_t w = 0; w < FWN_WAVES; ++w) {
+        bool all = true;
+        for (int32_t r = 32 * w; r < 32 * w + 32 && all; ++r)
+          for (int32_t x = 0; x < words; ++x) all = all && bits[r * words + x] == 0xffffffffu;
+        if (all) f |= 1u << w;
+        for (int32_t el = 0; el < 64; ++el) {
+          const int32_t sb = el >> 4, reg = el & 15;
+          uint64_t word = 0;
+          for (int32_t lane = 0; lane < 64; ++lane) {
+            const int32_t row = 32 * w + (lane & 31);
+            const int32_t key = fwn::element_col(sb, reg, lane >> 5);
+            word |= (uint64_t)((bits[row * words + key / 32] >> (key % 32)) & 1u) << lane;
+          }
+          lanes[t * FWN_LANE_WORDS + w * 64 + el] = word;
+        }
+      }
+      full[t] = f;
+    }
+  });
+  if (bad) return fwn::fail(FWN_ERR_TILES, "fwn_tiles_prepare: a tile has bits set beyond n_cols");
+  for (int32_t i = 0; i < n_blocks; ++i) order[i] = i;
+  std::stable_sort(order, order + n_blocks, [&](int32_t a, int32_t b) {
+    return tile_ptr[a + 1] - tile_ptr[a] > tile_ptr[b + 1] - tile_ptr[b];
+  });
+  return FWN_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,45 @@
+"""MI355X-native block-sparse masked mesh attention for WeatherNext 2.
+
+    import faster_weathernext_amd as fwn
+    fwn.enable()                                    # options as the reference's enable()
+    tiles = fwn.TileList.from_mask(mask)            # k-hop mask -> 128x128 live tiles (once)
+    out = fwn.tiled_flash_attention(q, k, v, tiles, scale=q.shape[-1] ** -0.5)
+
+Drop-in for the attention hot path of Raymondlol/Faster-WeatherNext (``pallas_attn.py``): the same
+op contract, computed by hand-written gfx950 HIP kernels behind a C ABI (include/fwn_attn.h).
+"""
+
+from . import patch
+from .hip_attn import BLOCK_K, BLOCK_Q, TileList, attention_backward, attention_forward, tiled_flash_attention
+from .mesh import adjacency, build_tile_mask, hilbert_order, icosahedral_mesh, khop_mask, mesh_mask
+
+__version__ = "0.1.0"
+
+
+def enable(force: bool = False, **options):
+  """Selects the HIP attention path; keyword options update ``patch.Options``.
+
+  Mirrors ``faster_weathernext.enable`` (``__init__.py:14-30``): unknown options raise TypeError.
+  Unless ``force``, the native library must load (RuntimeError otherwise). Returns the Options.
+  """
+  for key in options:
+    if not hasattr(patch.OPTIONS, key):
+      raise TypeError(f"unknown option {key!r}; see faster_weathernext_amd.patch.Options")
+  if not force:
+    from . import _native
+    _native.lib()
+  for key, value in options.items():
+    setattr(patch.OPTIONS, key, value)
+  patch.attention_impl()
+  patch.install()
+  return patch.OPTIONS
+
+
+def disable():
+  """Restores the default options."""
+  patch.uninstall()
+  patch.OPTIONS = patch.Options()
+
+
+def options():
+  return patch.OPTIONS

@@ -1,0 +1,181 @@
+"""Block-sparse masked flash attention on MI355X: the public op and its tile lists.
+
+Mirrors the reference's ``faster_weathernext.pallas_attn`` (``pallas_attn.py:317-354``):
+
+    out = tiled_flash_attention(q, k, v, tile_ptr, tile_kb, tile_bits, scale=D**-0.5, tiles_t=None)
+
+with q, k, v [batch, n, heads, head_dim] (torch tensors on the GPU, float32 or bfloat16), the tile
+list from ``build_tile_mask`` (128 x 128 tiles here, 64 x 32 in the reference) and the same
+gradient contract: differentiable with respect to q, k, v; the dK/dV kernel walks ``tiles_t``, the
+transposed mask's tile list, which defaults to the forward list (right for symmetric masks such as
+k-hop neighbourhoods). The reference's Pallas knobs (block_q, block_k, num_warps, num_stages,
+bwd_num_warps, bwd_split, interpret) have no counterpart: tile shape and wave count are fixed by
+the gfx950 kernels, and there is no interpreter or CPU path.
+
+All compute runs in the HIP kernels of libfwn_attn.so through its C ABI; torch only provides
+device memory and the stream. Tensors must be on a ROCm device: there is no CPU fallback.
+"""
+import threading
+
+import numpy as np
+import torch
+
+from . import _native as nat
+from .mesh import build_tile_mask, hilbert_order  # noqa: F401  (re-exported, as in the reference module)
+
+BLOCK_Q = nat.BLOCK
+BLOCK_K = nat.BLOCK
+
+_DTYPES = {torch.float32: nat.F32, torch.bfloat16: nat.BF16}
+
+
+class TileList:
+  """A tile list prepared for the kernels and resident on one device.
+
+  Built from the canonical arrays of ``build_tile_mask`` (validated on the host, converted to the
+  kernels' per-lane mask layout by ``fwn_tiles_prepare`` and copied once), then shared by every
+  call, as the reference shares one device copy of the mask across layers (``patch.py:263-266``).
+  """
+
+  def __init__(self, tile_ptr, tile_kb, tile_bits, n_cols, device="cuda"):
+    tile_ptr = nat.as_c(tile_ptr, np.int32)
+    tile_kb = nat.as_c(tile_kb, np.int32)
+    tile_bits = nat.as_c(tile_bits, np.uint32).reshape(len(tile_kb), nat.BLOCK, nat.BLOCK // 32)
+    self.n_blocks = len(tile_ptr) - 1
+    self.n_tiles = len(tile_kb)
+    self.n_cols = int(n_cols)
+    lanes = np.zeros((self.n_tiles, nat.LANE_WORDS), np.uint64)
+    full = np.zeros(self.n_tiles, np.uint32)
+    order = np.zeros(self.n_blocks, np.int32)
+    nat.check(nat.lib().fwn_tiles_prepare(self.n_blocks, self.n_tiles, self.n_cols, nat.ptr(tile_ptr),
+                                          nat.ptr(tile_kb), nat.ptr(tile_bits), nat.ptr(lanes), nat.ptr(full),
+                                          nat.ptr(order)))
+    self.device = torch.device(device)
+    put = lambda a: torch.from_numpy(a).to(self.device)
+    self.ptr = put(tile_ptr)
+    self.col = put(tile_kb)
+    self.lanes = put(lanes.view(np.int64))
+    self.full = put(full.view(np.int32))
+    self.order = put(order)
+    self.counts = np.diff(tile_ptr)
+    self.nnz = int(np.unpackbits(tile_bits.view(np.uint8)).sum()) if self.n_tiles else 0
+    addr = lambda t: t.data_ptr() if t.numel() else None
+    self.struct = nat.Tiles(self.n_blocks, self.n_tiles, addr(self.ptr), addr(self.col), addr(self.lanes),
+                            addr(self.full), addr(self.order))
+
+  @classmethod
+  def from_mask(cls, mask, perm=None, device="cuda"):
+    """Tile list of a boolean scipy/numpy [n, n] mask (optionally permuted as mask[perm][:, perm])."""
+    tp, kb, bits = build_tile_mask(mask, perm)
+    return cls(tp, kb, bits, mask.shape[1], device)
+
+  @property
+  def density(self):
+    """Fraction of valid entries in the live tiles."""
+    return self.nnz / max(1, self.n_tiles * nat.BLOCK * nat.BLOCK)
+
+
+_cache_lock = threading.Lock()
+_cache = {}
+
+
+def _as_tiles(tiles, n, device):
+  """A TileList from a TileList or a (tile_ptr, tile_kb, tile_bits) tuple (prepared once, cached)."""
+  if isinstance(tiles, TileList):
+    return tiles
+  tp, kb, bits = tiles
+  key = (id(tp), id(kb), id(bits), n, str(device))
+  with _cache_lock:
+    hit = _cache.get(key)
+    if hit is None or hit[0] is not tp or hit[1] is not kb or hit[2] is not bits:
+      hit = (tp, kb, bits, TileList(np.asarray(tp), np.asarray(kb), np.asarray(bits), n, device))
+      _cache[key] = hit
+    return hit[3]
+
+
+def _desc(q, scale):
+  if q.dtype not in _DTYPES:
+    raise TypeError(f"unsupported dtype {q.dtype}: float32 or bfloat16")
+  if q.device.type != "cuda":
+    raise ValueError("tiled_flash_attention runs on the GPU only (tensors are on %s)" % q.device)
+  if q.dim() != 4 or q.stride(-1) != 1:
+    raise ValueError("expected [batch, n, heads, head_dim] with head_dim contiguous")
+  b, n, h, d = q.shape
+  sb, sn, sh, _ = q.stride()
+  return nat.AttnDesc(b, n, h, d, _DTYPES[q.dtype], float(scale), sb, sn, sh)
+
+
+def _same_layout(x, ref, name):
+  if x.shape != ref.shape or x.dtype != ref.dtype or x.device != ref.device:
+    raise ValueError(f"{name} must match q in shape, dtype and device")
+  return x if x.stride() == ref.stride() else x.contiguous().as_strided(ref.shape, ref.stride())
+
+
+def _stream(device):
+  return torch.cuda.current_stream(device).cuda_stream
+
+
+def attention_forward(q, k, v, tiles, scale, with_lse=True):
+  """Forward kernel: returns (out, lse) with lse float32 [batch, heads, n] (None if not requested)."""
+  q = q.contiguous()
+  k = _same_layout(k, q, "k")
+  v = _same_layout(v, q, "v")
+  desc = _desc(q, scale)
+  tl = _as_tiles(tiles, q.shape[1], q.device)
+  out = torch.empty_like(q)
+  lse = torch.empty((q.shape[0], q.shape[2], q.shape[1]), dtype=torch.float32, device=q.device) if with_lse else None
+  nat.check(nat.lib().fwn_attn_fwd_launch(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), tl.struct, out.data_ptr(),
+                                          lse.data_ptr() if with_lse else None, _stream(q.device)))
+  return out, lse
+
+
+def attention_backward(q, k, v, out, lse, dout, tiles, tiles_t, scale):
+  """Backward kernels (delta pre-pass, dQ, dK/dV): returns (dq, dk, dv)."""
+  q = q.contiguous()
+  k = _same_layout(k, q, "k")
+  v = _same_layout(v, q, "v")
+  out = _same_layout(out, q, "out")
+  dout = _same_layout(dout, q, "dout")
+  desc = _desc(q, scale)
+  n = q.shape[1]
+  tl = _as_tiles(tiles, n, q.device)
+  tlt = tl if tiles_t is None else _as_tiles(tiles_t, n, q.device)
+  delta = torch.empty_like(lse)
+  dq, dk, dv = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
+  nat.check(nat.lib().fwn_attn_bwd_launch(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                                          dout.data_ptr(), lse.data_ptr(), delta.data_ptr(), tl.struct, tlt.struct,
+                                          dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), _stream(q.device)))
+  return dq, dk, dv
+
+
+class _TiledAttention(torch.autograd.Function):
+  """custom VJP of the attention (``pallas_attn.py:260-311``): the forward saves q, k, v, out and
+  the per-row log-sum-exp; the backward recomputes P tile by tile."""
+
+  @staticmethod
+  def forward(ctx, q, k, v, tiles, tiles_t, scale):
+    need = any(ctx.needs_input_grad[:3])
+    out, lse = attention_forward(q, k, v, tiles, scale, with_lse=need)
+    if need:
+      ctx.save_for_backward(q, k, v, out, lse)
+      ctx.tiles, ctx.tiles_t, ctx.scale = tiles, tiles_t, scale
+    return out
+
+  @staticmethod
+  def backward(ctx, dout):
+    q, k, v, out, lse = ctx.saved_tensors
+    dq, dk, dv = attention_backward(q, k, v, out, lse, dout, ctx.tiles, ctx.tiles_t, ctx.scale)
+    return dq, dk, dv, None, None, None
+
+
+def tiled_flash_attention(q, k, v, tile_ptr, tile_kb=None, tile_bits=None, *, scale, tiles_t=None):
+  """q, k, v: [batch, n, heads, head_dim] float32/bfloat16 on the GPU -> [batch, n, heads, head_dim].
+
+  ``tile_ptr`` may be a prepared TileList (then tile_kb and tile_bits are omitted) or the first of
+  the three arrays of ``build_tile_mask``. ``tiles_t`` (TileList or array triple) is the
+  transposed mask's list for the dK/dV kernel; it defaults to the forward's (symmetric masks).
+  """
+  tiles = tile_ptr if isinstance(tile_ptr, TileList) else (tile_ptr, tile_kb, tile_bits)
+  if tiles_t is not None and not isinstance(tiles_t, TileList):
+    tiles_t = tuple(tiles_t)
+  return _TiledAttention.apply(q, k, v, tiles, tiles_t, float(scale))

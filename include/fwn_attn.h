@@ -1,0 +1,153 @@
+/* fwn_attn.h - C ABI of the MI355X (gfx950) block-sparse masked mesh attention library.
+ *
+ * Drop-in replacement for the attention hot path of Raymondlol/Faster-WeatherNext v0.2.0
+ * (src/faster_weathernext/pallas_attn.py). Plain C types only: device pointers are `void*`
+ * (HIP device memory), the stream is a `hipStream_t` passed as `void*` (NULL = default stream).
+ *
+ * Conventions shared by every entry point:
+ *   - Return 0 (FWN_OK) on success, a nonzero fwn_status on failure; fwn_last_error() then holds
+ *     a thread-local message. Invalid shapes, dtypes, strides, alignments and malformed tile
+ *     lists are rejected on the host before anything is launched.
+ *   - Launchers enqueue work on `stream` and return without synchronising. They allocate
+ *     nothing, keep no pointer after returning and hold no mutable global state, so they are
+ *     re-entrant and safe under stream capture.
+ *   - Tensors q, k, v, o, dout, dq, dk, dv are [batch, n, heads, head_dim] in the element strides
+ *     of fwn_attn_desc (head_dim contiguous): node-major by default, read and written in place
+ *     (the reference transposes to head-major and pads, pallas_attn.py:334-335; here no copy is made).
+ *   - lse and delta are float32 [batch, heads, n], contiguous.
+ *   - Rows are processed in blocks of FWN_BLOCK = 128 and key tiles are 128 wide
+ *     (the reference uses 64 x 32, pallas_attn.py:30-31).
+ */
+#ifndef FWN_ATTN_H_
+#define FWN_ATTN_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FWN_BLOCK 128
+#define FWN_WAVES 4                       /* waves per workgroup; each owns 32 rows of a block */
+#define FWN_LANE_WORDS (FWN_WAVES * 64)   /* uint64 lane-mask words per tile */
+
+typedef enum fwn_status {
+  FWN_OK = 0,
+  FWN_ERR_INVALID_ARG = 1,  /* null pointer, bad shape, stride or alignment */
+  FWN_ERR_UNSUPPORTED = 2,  /* head_dim or dtype not built */
+  FWN_ERR_TILES = 3,        /* malformed tile list */
+  FWN_ERR_HIP = 4,          /* a HIP runtime call failed (message has hipGetErrorString) */
+} fwn_status;
+
+typedef enum fwn_dtype { FWN_F32 = 0, FWN_BF16 = 1 } fwn_dtype;
+
+/* Shape of one attention call. scale multiplies q.k (the reference passes key_size**-0.5,
+ * patch.py:174). Strides are in elements, shared by every [batch, n, heads, head_dim] tensor. */
+typedef struct fwn_attn_desc {
+  int32_t batch;
+  int32_t n;          /* nodes (queries = keys) */
+  int32_t heads;
+  int32_t head_dim;   /* 32, 64 or 128 */
+  int32_t dtype;      /* fwn_dtype of q, k, v, o, dout, dq, dk, dv */
+  float scale;
+  int64_t stride_b;
+  int64_t stride_n;
+  int64_t stride_h;
+} fwn_attn_desc;
+
+/* Device view of a prepared tile list (see fwn_tiles_prepare). `ptr`/`col` are the CSR tile list
+ * of pallas_attn.build_tile_mask (pallas_attn.py:85-109) at 128 x 128; `lanes` and `full` hold
+ * its bitmasks in the kernels' register layout. For the dK/dV launcher the list must be the
+ * transposed mask's (rows = keys, columns = queries), as the reference's tiles_t
+ * (pallas_attn.py:297-310; equal to the forward list for symmetric masks). */
+typedef struct fwn_tiles {
+  int32_t n_blocks;         /* row blocks: ceil(n / 128) */
+  int32_t n_tiles;          /* live tiles */
+  const int32_t* ptr;       /* [n_blocks + 1] */
+  const int32_t* col;       /* [n_tiles] column block of each tile */
+  const uint64_t* lanes;    /* [n_tiles * FWN_LANE_WORDS] */
+  const uint32_t* full;     /* [n_tiles] bit w: rows 32w..32w+31 of the tile are all valid */
+  const int32_t* order;     /* [n_blocks] block processing order (most tiles first), or NULL */
+} fwn_tiles;
+
+/* Thread-local message of the last failure on this thread ("" if none). */
+const char* fwn_last_error(void);
+
+/* ---------------------------------------------------------------------------------------------
+ * Host mask pipeline (CPU, synchronous). Replaces the trace-time numpy/scipy work of
+ * patch.py:208-219: the k-hop mask (adj ** k), the Hilbert order and build_tile_mask.
+ * ------------------------------------------------------------------------------------------- */
+
+/* Number of nodes within k hops of each node (itself included) of a symmetric adjacency in CSR
+ * (adj_ptr[n + 1], adj_idx; self edges optional). Writes row_ptr[n + 1] of the k-hop mask
+ * (exclusive prefix sums). Replaces `adj ** k` (patch.py:209, scripts/attn_bench.py:32). */
+int fwn_khop_count(int32_t n, const int64_t* adj_ptr, const int32_t* adj_idx, int32_t k,
+                   int64_t* row_ptr);
+
+/* Fills the sorted column indices idx[row_ptr[n]] of the k-hop mask counted above. */
+int fwn_khop_fill(int32_t n, const int64_t* adj_ptr, const int32_t* adj_idx, int32_t k,
+                  const int64_t* row_ptr, int32_t* idx);
+
+/* Permutation sorting points on the sphere along a 3-D Hilbert curve (Skilling's transpose
+ * algorithm, `bits` bits per axis, bits <= 20), non-finite points last, ties in input order.
+ * Replaces pallas_attn.hilbert_order (pallas_attn.py:41-82). */
+int fwn_hilbert_order(int64_t n, const double* lat_deg, const double* lon_deg, int32_t bits,
+                      int64_t* perm);
+
+/* CSR live-tile list of a boolean mask given in CSR (row_ptr[n_rows + 1], idx), optionally
+ * permuted as mask[perm][:, perm] (perm of length n_rows == n_cols, or NULL). Two passes:
+ * fwn_tiles_count writes tile_ptr[ceil(n_rows / 128) + 1]; fwn_tiles_fill writes
+ * tile_col[tile_ptr[last]] and tile_bits[tile_ptr[last] * 128 * 4] (bit j of word w of row r:
+ * key col*128 + 32w + j). Replaces pallas_attn.build_tile_mask (pallas_attn.py:85-109). */
+int fwn_tiles_count(int32_t n_rows, int32_t n_cols, const int64_t* row_ptr, const int32_t* idx,
+                    const int64_t* perm, int32_t* tile_ptr);
+int fwn_tiles_fill(int32_t n_rows, int32_t n_cols, const int64_t* row_ptr, const int32_t* idx,
+                   const int64_t* perm, const int32_t* tile_ptr, int32_t* tile_col,
+                   uint32_t* tile_bits);
+
+/* Validates a canonical tile list (tile_ptr, tile_col, tile_bits as above, n_cols columns) and
+ * converts it into the kernels' layout: lanes[n_tiles * FWN_LANE_WORDS], full[n_tiles] and
+ * order[n_blocks] (host buffers; the caller copies them to the device). */
+int fwn_tiles_prepare(int32_t n_blocks, int32_t n_tiles, int32_t n_cols, const int32_t* tile_ptr,
+                      const int32_t* tile_col, const uint32_t* tile_bits, uint64_t* lanes,
+                      uint32_t* full, int32_t* order);
+
+/* ---------------------------------------------------------------------------------------------
+ * Device launchers (enqueue on `stream`).
+ * ------------------------------------------------------------------------------------------- */
+
+/* Forward: o = softmax(mask(q k^T * scale)) v, walking only live tiles with an online softmax.
+ * lse (natural log-sum-exp of the scaled logits per row) is written when non-NULL.
+ * Replaces pallas_attn._forward/_kernel (pallas_attn.py:112-141, 235-257). */
+int fwn_attn_fwd_launch(const fwn_attn_desc* desc, const void* q, const void* k, const void* v,
+                        const fwn_tiles* tiles, void* o, float* lse, void* stream);
+
+/* delta = rowsum(o * dout) in float32 [batch, heads, n] (pallas_attn.py:278). */
+int fwn_attn_bwd_delta_launch(const fwn_attn_desc* desc, const void* o, const void* dout,
+                              float* delta, void* stream);
+
+/* dq per query block over the forward tile list, P recomputed from lse
+ * (pallas_attn.py:161-184, 286-295). */
+int fwn_attn_bwd_dq_launch(const fwn_attn_desc* desc, const void* q, const void* k,
+                           const void* v, const void* dout, const float* lse,
+                           const float* delta, const fwn_tiles* tiles, void* dq, void* stream);
+
+/* dk, dv per key block over the transposed tile list; every workgroup owns its rows of dk/dv,
+ * so no atomics (pallas_attn.py:187-215, 297-310). */
+int fwn_attn_bwd_dkv_launch(const fwn_attn_desc* desc, const void* q, const void* k,
+                            const void* v, const void* dout, const float* lse,
+                            const float* delta, const fwn_tiles* tiles_t, void* dk, void* dv,
+                            void* stream);
+
+/* Whole backward: delta, dq, then dk/dv, in stream order (pallas_attn._attention_bwd,
+ * pallas_attn.py:274-311). delta is caller-provided scratch of [batch, heads, n] floats. */
+int fwn_attn_bwd_launch(const fwn_attn_desc* desc, const void* q, const void* k, const void* v,
+                        const void* o, const void* dout, const float* lse, float* delta,
+                        const fwn_tiles* tiles, const fwn_tiles* tiles_t, void* dq, void* dk,
+                        void* dv, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FWN_ATTN_H_ */
