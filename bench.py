@@ -1,0 +1,204 @@
+#!/usr/bin/env python3
+"""Benchmark of the block-sparse masked mesh attention on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c3|c2|c4|c5] [--no-cpu]
+
+A step is one pass of the hot path over one batch of synthetic input: for the default workload
+(configuration 3 of BASELINE.json) the forward kernel plus the backward (delta pre-pass, dQ,
+dK/dV) on the refinement-6 mesh (40,962 nodes) with the 16-hop mask, 4 heads x 128, bf16 inputs,
+fp32 accumulation. Inputs are resident in HBM before the timed region. The metric is effective
+TFLOP/s over live 128x128 tiles (14 * D * 128^2 per live tile, batch and head for fwd + bwd;
+4 * D * 128^2 for forward-only workloads). The mask build is timed separately.
+
+Prints one JSON line (rank 0). Also reports a roofline entry for the dominant kernel (its
+algorithmic FLOPs per launch over its mean HIP-event duration in the timed region) and a CPU
+baseline: the restated reference XLA chunked path (oracle/attention.py) on a bounded sample of
+query chunks of the same workload, on this host's cores.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path[:0] = [ROOT, os.path.join(ROOT, "faster-weathernext_amd")]
+
+METRIC = "effective attn TFLOP/s (live tiles, fwd+bwd) + sec per 0.25° 6-h step, 1 GPU"
+PEAK = {"bf16": 2500.0, "f32": 157.3}  # MI355X dense MFMA TFLOP/s (vendor figures)
+
+WORKLOADS = {
+    "c2": dict(k_hop=8, heads=4, head_dim=128, batch=1, dtype="f32", backward=False, reorder=False, sigma=128 ** -0.5,
+               desc="config 2: r6 mesh, 8-hop, 4x128, fp32 MFMA, forward"),
+    "c3": dict(k_hop=16, heads=4, head_dim=128, batch=1, dtype="bf16", backward=True, reorder=False, sigma=1.0,
+               desc="config 3: r6 mesh, 16-hop, 4x128, bf16 (fp32 accumulate), forward + backward"),
+    "c4": dict(k_hop=8, heads=4, head_dim=128, batch=8, dtype="bf16", backward=True, reorder=False, sigma=1.0,
+               desc="config 4: r6 mesh, 8-hop, 8 members x 4x128, bf16, forward + backward"),
+    "c5": dict(k_hop=32, heads=6, head_dim=128, batch=1, dtype="bf16", backward=False, reorder=True, sigma=1.0,
+               desc="WN2 mesh-transformer attention shape: r6 mesh, 32-hop, Hilbert order, 6x128, bf16, "
+                    "forward (one of 24 layers)"),
+}
+
+
+def parse():
+  p = argparse.ArgumentParser()
+  p.add_argument("--gpus", type=int, default=1)
+  p.add_argument("--steps", type=int, default=20)
+  p.add_argument("--warmup", type=int, default=3)
+  p.add_argument("--workload", default="c3", choices=sorted(WORKLOADS))
+  p.add_argument("--cpu-seconds", type=float, default=12.0, help="bounded CPU-baseline sample length")
+  p.add_argument("--no-cpu", action="store_true")
+  return p.parse_args()
+
+
+def cpu_baseline(cfg, q, k, v, do, mask, tiles, scale, budget_s):
+  """Times the restated reference XLA chunked path on whole query chunks until `budget_s` elapses."""
+  import numpy as np
+  from threadpoolctl import threadpool_info
+
+  from oracle import attention as A
+  chunk = 512
+  starts, bits, window, n_kv = A.build_chunked_mask(mask, chunk)
+  D, B, H = cfg["head_dim"], cfg["batch"], cfg["heads"]
+  done, t0 = 0, time.perf_counter()
+  while True:
+    A.chunked_attention(q, k, v, starts, bits, window, n_kv, chunk, scale, chunks=[done])
+    if cfg["backward"]:
+      A.chunked_attention_grads(q, k, v, do, starts, bits, window, n_kv, chunk, scale, chunks=[done])
+    done += 1
+    if time.perf_counter() - t0 >= budget_s or done == len(starts):
+      break
+  elapsed = time.perf_counter() - t0
+  qb_per_chunk = chunk // 128
+  ptr = tiles.ptr.cpu().numpy()
+  live = int(ptr[min(done * qb_per_chunk, len(ptr) - 1)] - ptr[0])
+  flops = (14 if cfg["backward"] else 4) * D * 128 * 128 * live * B * H
+  threads = max([t.get("num_threads", 1) for t in threadpool_info()] or [1])
+  return {"value": flops / elapsed / 1e12, "unit": "TFLOP/s", "cores": int(threads), "kind": "port",
+          "sample": f"{done} of {len(starts)} query chunks of {chunk} (window {window} keys), "
+                    f"{'fwd+bwd' if cfg['backward'] else 'fwd'} float32 numpy/BLAS, {elapsed:.1f} s",
+          "seconds": round(elapsed, 2)}
+
+
+def main():
+  args = parse()
+  world = int(os.environ.get("WORLD_SIZE", "1"))
+  if args.gpus != 1 or world != 1:
+    print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}); the attention "
+          "path has no multi-GPU implementation in this build.", file=sys.stderr)
+    return 2
+  import numpy as np
+  import torch
+
+  import faster_weathernext_amd as fwn
+  from faster_weathernext_amd import _native as nat
+
+  cfg = WORKLOADS[args.workload]
+  D, H, B = cfg["head_dim"], cfg["heads"], cfg["batch"]
+  dtype = torch.bfloat16 if cfg["dtype"] == "bf16" else torch.float32
+  dev = torch.device("cuda:0")
+  torch.cuda.set_device(dev)
+
+  t0 = time.perf_counter()
+  mask, lat, lon, perm = fwn.mesh_mask(6, cfg["k_hop"], reorder=cfg["reorder"])
+  t_mask = time.perf_counter() - t0
+  t0 = time.perf_counter()
+  tiles = fwn.TileList.from_mask(mask, perm, device=dev)
+  t_tiles = time.perf_counter() - t0
+  n = mask.shape[0]
+  if perm is not None:
+    mask = mask[perm][:, perm]
+  T = tiles.n_tiles
+
+  rng = np.random.default_rng(0)
+  host = [(cfg["sigma"] * rng.standard_normal((B, n, H, D))).astype(np.float32) for _ in range(3)]
+  host.append(rng.standard_normal((B, n, H, D)).astype(np.float32))
+  q, k, v, do = (torch.from_numpy(x).to(dev).to(dtype) for x in host)
+  scale = D ** -0.5
+  desc = nat.AttnDesc(B, n, H, D, nat.BF16 if dtype == torch.bfloat16 else nat.F32, scale, *q.stride()[:3])
+  out = torch.empty_like(q)
+  lse = torch.empty((B, H, n), device=dev, dtype=torch.float32)
+  delta = torch.empty_like(lse)
+  dq, dk, dv = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
+  L = nat.lib()
+  stream = torch.cuda.current_stream(dev)
+  sp = stream.cuda_stream
+  ts = tiles.struct
+
+  def fwd():
+    nat.check(L.fwn_attn_fwd_launch(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), ts, out.data_ptr(),
+                                    lse.data_ptr(), sp))
+
+  def bwd_delta():
+    nat.check(L.fwn_attn_bwd_delta_launch(desc, out.data_ptr(), do.data_ptr(), delta.data_ptr(), sp))
+
+  def bwd_dq():
+    nat.check(L.fwn_attn_bwd_dq_launch(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(),
+                                       lse.data_ptr(), delta.data_ptr(), ts, dq.data_ptr(), sp))
+
+  def bwd_dkv():
+    nat.check(L.fwn_attn_bwd_dkv_launch(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(),
+                                        lse.data_ptr(), delta.data_ptr(), ts, dk.data_ptr(), dv.data_ptr(), sp))
+
+  kernels = [("fwd", fwd)] + ([("delta", bwd_delta), ("dq", bwd_dq), ("dkv", bwd_dkv)] if cfg["backward"] else [])
+  for _ in range(args.warmup):
+    for _, fn in kernels:
+      fn()
+  torch.cuda.synchronize()
+
+  # Timed region: K steps; an event pair brackets every kernel (same stream as the launches).
+  events = [[torch.cuda.Event(enable_timing=True) for _ in range(len(kernels) + 1)] for _ in range(args.steps)]
+  start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+  torch.cuda.synchronize()
+  start.record(stream)
+  for s in range(args.steps):
+    events[s][0].record(stream)
+    for i, (_, fn) in enumerate(kernels):
+      fn()
+      events[s][i + 1].record(stream)
+  stop.record(stream)
+  torch.cuda.synchronize()
+  ms_step = start.elapsed_time(stop) / args.steps
+  per_kernel = {name: float(np.mean([events[s][i].elapsed_time(events[s][i + 1]) for s in range(args.steps)]))
+                for i, (name, _) in enumerate(kernels)}
+
+  unit_flops = D * 128 * 128 * T * B * H  # one live tile x D, all batch members and heads
+  total_flops = (14 if cfg["backward"] else 4) * unit_flops
+  value = total_flops / (ms_step * 1e-3) / 1e12
+  # Algorithmic FLOPs per launch: forward 4*D per live entry; the backward's 10*D (FA2 count, S
+  # recomputed once) split as dQ kernel 4*D (dQ + half of the S/dP recompute) and dK/dV kernel 6*D.
+  algo = {"fwd": 4 * unit_flops, "dq": 4 * unit_flops, "dkv": 6 * unit_flops, "delta": 0}
+  dominant = max((k_ for k_ in per_kernel if algo.get(k_)), key=lambda k_: per_kernel[k_])
+  achieved = algo[dominant] / (per_kernel[dominant] * 1e-3) / 1e12
+  peak = PEAK[cfg["dtype"]]
+
+  result = {
+      "metric": METRIC, "value": round(value, 3), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+      "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak",
+      "vs_baseline": None, "dtype": cfg["dtype"],
+      "data": "synthetic: seeded N(0, sigma) q/k/v and N(0,1) dO (numpy PCG64 seed 0) on a generated "
+              "icosahedral mesh; no weights or datasets",
+      "config": {"workload": cfg["desc"], "mesh_refinement": 6, "n": n, "k_hop": cfg["k_hop"], "batch": B,
+                 "heads": H, "head_dim": D, "order": "hilbert" if cfg["reorder"] else "subdivision",
+                 "sigma": cfg["sigma"], "live_tiles": T, "tile_density": round(tiles.density, 4),
+                 "valid_entries": int(mask.nnz)},
+      "roofline": {"bound": "mfma", "kernel": dominant, "achieved": round(achieved, 3), "peak": peak,
+                   "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": None},
+      "kernels_ms": {k_: round(v_, 4) for k_, v_ in per_kernel.items()},
+      "valid_entry_tflops": round(value * mask.nnz / (T * 128 * 128), 3),
+      "mask_build_s": round(t_mask, 3), "tile_prepare_s": round(t_tiles, 3),
+      "step_s": None,
+      "step_note": "the full WN2 0.25-deg step needs jax, haiku and weathernext, which this image lacks; "
+                   "run --workload c5 for the attention share of a step (24 layers x forward)",
+  }
+  if args.workload == "c5":
+    result["attn_s_per_step"] = round(24 * ms_step * 1e-3, 4)
+  if not args.no_cpu:
+    host_np = [x.astype(np.float32) for x in host]
+    result["cpu_baseline"] = cpu_baseline(cfg, *host_np, mask, tiles, scale, args.cpu_seconds)
+  print(json.dumps(result), flush=True)
+  return 0
+
+
+if __name__ == "__main__":
+  sys.exit(main())

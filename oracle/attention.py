@@ -99,16 +99,21 @@ def _chunk_views(q, k, v, starts, window, n_kv, chunk):
 def _chunk_probs(qc, kc, packed, window, scale):
   """Softmax weights [B, H, chunk, window] of one chunk, masked logits = -1e30.
 
-  The softmax runs in at least float32, as the reference's upcast wrapper does
-  (``patch.py:151``); float64 inputs stay float64.
+  qc [B, H, chunk, D] and kc [B, H, window, D] are head-major. The softmax runs in at least
+  float32, as the reference's upcast wrapper does (``patch.py:151``); float64 stays float64.
   """
-  logits = np.einsum("bqhd,bkhd->bhqk", qc, kc) * qc.dtype.type(scale)
+  logits = np.matmul(qc, kc.transpose(0, 1, 3, 2)) * qc.dtype.type(scale)
   valid = np.unpackbits(packed, axis=-1, count=window, bitorder="little").astype(bool)
   soft = np.promote_types(logits.dtype, np.float32)
-  logits = np.where(valid[None, None], logits, logits.dtype.type(MASK_VALUE)).astype(soft)
-  m = logits.max(-1, keepdims=True)
-  p = np.exp(logits - m)
-  return (p / p.sum(-1, keepdims=True)).astype(qc.dtype), valid
+  logits = np.where(valid[None, None], logits, logits.dtype.type(MASK_VALUE)).astype(soft, copy=False)
+  logits -= logits.max(-1, keepdims=True)
+  np.exp(logits, out=logits)
+  logits /= logits.sum(-1, keepdims=True)
+  return logits.astype(qc.dtype, copy=False)
+
+
+def _head_major(x):
+  return np.ascontiguousarray(x.transpose(0, 2, 1, 3))
 
 
 def chunked_attention(q, k, v, starts, bits, window, n_kv, chunk, scale, chunks=None):
@@ -117,40 +122,37 @@ def chunked_attention(q, k, v, starts, bits, window, n_kv, chunk, scale, chunks=
   ``chunks`` (optional iterable of chunk indices) restricts the work to those query chunks; rows
   of other chunks are left at zero (used for bounded CPU-baseline samples).
   """
-  batch, n, heads, dim = q.shape
-  qp, kp, vp = _chunk_views(q, k, v, starts, window, n_kv, chunk)
+  n = q.shape[1]
+  qp, kp, vp = (_head_major(x) for x in _chunk_views(q, k, v, starts, window, n_kv, chunk))
   out = np.zeros_like(qp)
   for c in (range(len(starts)) if chunks is None else chunks):
     s0 = int(starts[c])
-    qc = qp[:, c * chunk:(c + 1) * chunk]
-    kc, vc = kp[:, s0:s0 + window], vp[:, s0:s0 + window]
-    w, _ = _chunk_probs(qc, kc, bits[c], window, scale)
-    out[:, c * chunk:(c + 1) * chunk] = np.einsum("bhqk,bkhd->bqhd", w, vc)
-  return out[:, :n]
+    rows = slice(c * chunk, (c + 1) * chunk)
+    w = _chunk_probs(qp[:, :, rows], kp[:, :, s0:s0 + window], bits[c], window, scale)
+    out[:, :, rows] = np.matmul(w, vp[:, :, s0:s0 + window])
+  return out.transpose(0, 2, 1, 3)[:, :n]
 
 
 def chunked_attention_grads(q, k, v, do, starts, bits, window, n_kv, chunk, scale, chunks=None):
   """Reference XLA chunked path, backward (autodiff of the chunked forward): (dq, dk, dv)."""
-  batch, n, heads, dim = q.shape
-  qp, kp, vp = _chunk_views(q, k, v, starts, window, n_kv, chunk)
-  dop = np.zeros_like(qp)
-  dop[:, :n] = do
-  dq = np.zeros_like(qp)
-  dk = np.zeros_like(kp)
-  dv = np.zeros_like(vp)
+  n = q.shape[1]
+  qp, kp, vp = (_head_major(x) for x in _chunk_views(q, k, v, starts, window, n_kv, chunk))
+  dop = np.zeros(qp.shape, do.dtype)
+  dop[:, :, :n] = do.transpose(0, 2, 1, 3)
+  dq, dk, dv = np.zeros_like(qp), np.zeros_like(kp), np.zeros_like(vp)
   sc = q.dtype.type(scale)
   for c in (range(len(starts)) if chunks is None else chunks):
     s0 = int(starts[c])
-    rows = slice(c * chunk, (c + 1) * chunk)
-    qc, doc = qp[:, rows], dop[:, rows]
-    kc, vc = kp[:, s0:s0 + window], vp[:, s0:s0 + window]
-    p, _ = _chunk_probs(qc, kc, bits[c], window, scale)
-    dp = np.einsum("bqhd,bkhd->bhqk", doc, vc)
-    ds = p * (dp - (dp * p).sum(-1, keepdims=True))
-    dq[:, rows] = np.einsum("bhqk,bkhd->bqhd", ds, kc) * sc
-    dk[:, s0:s0 + window] += np.einsum("bhqk,bqhd->bkhd", ds, qc) * sc
-    dv[:, s0:s0 + window] += np.einsum("bhqk,bqhd->bkhd", p, doc)
-  return dq[:, :n], dk[:, :n], dv[:, :n]
+    rows, keys = slice(c * chunk, (c + 1) * chunk), slice(s0, s0 + window)
+    qc, doc, kc, vc = qp[:, :, rows], dop[:, :, rows], kp[:, :, keys], vp[:, :, keys]
+    p = _chunk_probs(qc, kc, bits[c], window, scale)
+    dp = np.matmul(doc, vc.transpose(0, 1, 3, 2))
+    dp -= (dp * p).sum(-1, keepdims=True)
+    dp *= p                                                     # dS
+    dq[:, :, rows] = np.matmul(dp, kc) * sc
+    dk[:, :, keys] += np.matmul(dp.transpose(0, 1, 3, 2), qc) * sc
+    dv[:, :, keys] += np.matmul(p.transpose(0, 1, 3, 2), doc)
+  return tuple(x.transpose(0, 2, 1, 3)[:, :n] for x in (dq, dk, dv))
 
 
 def rel_rms(got, ref):
@@ -165,3 +167,53 @@ def max_rel_err(got, ref):
   got = np.asarray(got, np.float64)
   ref = np.asarray(ref, np.float64)
   return float(np.abs(got - ref).max() / np.abs(ref).max())
+
+
+def sampled_attention(q, k, v, do, mask, scale, rows, keys=()):
+  """Exact float64 results at a sample of rows and keys, for masks too large for the dense oracle.
+
+  Same closed form as ``dense_attention`` / ``dense_grads``, evaluated only where needed: out, lse
+  and dq at query ``rows`` (each needs its own key set), dk and dv at ``keys`` (each needs every
+  query that attends to it, and those queries' normalisers). Returns a dict of arrays
+  out/dq [B, len(rows), H, D], lse [B, H, len(rows)], dk/dv [B, len(keys), H, D].
+  """
+  mask = sparse.csr_matrix(mask).astype(bool)
+  mask_t = mask.T.tocsr()
+  q, k, v, do = (np.asarray(x, np.float64) for x in (q, k, v, do))
+  cache = {}
+
+  def row(i):
+    if i not in cache:
+      cols = mask.indices[mask.indptr[i]:mask.indptr[i + 1]]
+      s = np.einsum("bhd,bmhd->bhm", q[:, i], k[:, cols]) * scale
+      mx = s.max(-1, keepdims=True)
+      e = np.exp(s - mx)
+      tot = e.sum(-1, keepdims=True)
+      p = e / tot
+      dp = np.einsum("bhd,bmhd->bhm", do[:, i], v[:, cols])
+      ds = p * (dp - (p * dp).sum(-1, keepdims=True))
+      cache[i] = dict(cols=cols, p=p, ds=ds, lse=(mx + np.log(tot))[..., 0])
+    return cache[i]
+
+  res = {"out": [], "lse": [], "dq": [], "dk": [], "dv": []}
+  for i in rows:
+    r = row(int(i))
+    res["out"].append(np.einsum("bhm,bmhd->bhd", r["p"], v[:, r["cols"]]))
+    res["dq"].append(np.einsum("bhm,bmhd->bhd", r["ds"], k[:, r["cols"]]) * scale)
+    res["lse"].append(r["lse"])
+  for j in keys:
+    j = int(j)
+    dk = np.zeros(q.shape[:1] + q.shape[2:])
+    dv = np.zeros_like(dk)
+    for i in mask_t.indices[mask_t.indptr[j]:mask_t.indptr[j + 1]]:
+      r = row(int(i))
+      pos = np.searchsorted(r["cols"], j)
+      dv += r["p"][..., pos, None] * do[:, i]
+      dk += r["ds"][..., pos, None] * q[:, i] * scale
+    res["dk"].append(dk)
+    res["dv"].append(dv)
+  out = {}
+  for name in ("out", "dq", "dk", "dv"):
+    out[name] = np.stack(res[name], 1) if res[name] else np.zeros(q.shape[:1] + (0,) + q.shape[2:])
+  out["lse"] = np.stack(res["lse"], -1) if res["lse"] else np.zeros(q.shape[:1] + q.shape[2:3] + (0,))
+  return out

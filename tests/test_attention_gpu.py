@@ -1,0 +1,360 @@
+"""GPU parity tests: the HIP kernels (through the C ABI) against the CPU oracle.
+
+Bars: rel RMS <= 1e-5 at float32 and <= 5e-3 at bfloat16 per output tensor, plus
+the reference's own unit-test metric max|got - ref| / max|ref| (tests/test_pallas_kernel.py:54,
+98: 1e-5 at full precision). bfloat16 cases compare against the float64 oracle evaluated on the
+bf16-rounded inputs. Small cases use the dense oracle; model-scale cases (refinement-6 mesh) use the
+exact sampled oracle on a seeded subset of rows and keys plus size-independent identities.
+"""
+
+import numpy as np
+import pytest
+import torch
+from scipy import sparse
+
+import faster_weathernext_amd as fwn
+from faster_weathernext_amd import _native as nat
+from oracle import attention as A
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+TOL = {torch.float32: 1e-5, torch.bfloat16: 5e-3}
+MAXTOL = {torch.float32: 1e-5, torch.bfloat16: 3e-2}
+
+
+def _random_mask(n, density, seed, symmetric=False, identity=True):
+  m = sparse.random(n, n, density=density, random_state=seed, format="csr").astype(bool)
+  if symmetric:
+    m = m + m.T
+  if identity:
+    m = m + sparse.identity(n, dtype=bool, format="csr")
+  return m.tocsr().astype(bool)
+
+
+def _rounded(x, dtype):
+  """Inputs as the kernel sees them (bf16 rounding, round to nearest even), back in float32."""
+  return torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(dtype).float().numpy()
+
+
+def _dev(x, dtype, grad=False):
+  t = torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(DEV).to(dtype)
+  return t.requires_grad_(grad)
+
+
+def _np(t):
+  return t.detach().float().cpu().numpy()
+
+
+def _run(q, k, v, do, tiles, scale, dtype, tiles_t=None):
+  qt, kt, vt = (_dev(x, dtype, do is not None) for x in (q, k, v))
+  out = fwn.tiled_flash_attention(qt, kt, vt, tiles, scale=scale, tiles_t=tiles_t)
+  res = {"out": _np(out)}
+  if do is not None:
+    out.backward(_dev(do, dtype))
+    res.update(dq=_np(qt.grad), dk=_np(kt.grad), dv=_np(vt.grad))
+  torch.cuda.synchronize()
+  return res
+
+
+def _check(got, ref, dtype, what):
+  rr, mr = A.rel_rms(got, ref), A.max_rel_err(got, ref)
+  assert rr <= TOL[dtype], (what, rr, mr)
+  assert mr <= MAXTOL[dtype], (what, rr, mr)
+
+
+# ---------------------------------------------------------------------------------------------
+# configuration 1 (golden vectors)
+
+
+def test_c1_golden_fp32():
+  g = np.load(__file__.replace("test_attention_gpu.py", "golden/c1_r3_2hop.npz"))
+  n = g["q"].shape[1]
+  mask = sparse.csr_matrix((np.ones(len(g["indices"]), bool), g["indices"], g["indptr"]), shape=(n, n))
+  tiles = fwn.TileList.from_mask(mask)
+  scale = float(g["scale"])
+  res = _run(g["q"], g["k"], g["v"], g["do"], tiles, scale, torch.float32)
+  for name in ("out", "dq", "dk", "dv"):
+    _check(res[name], g[name], torch.float32, name)
+  out, lse = fwn.attention_forward(_dev(g["q"], torch.float32), _dev(g["k"], torch.float32),
+                                   _dev(g["v"], torch.float32), tiles, scale)
+  np.testing.assert_allclose(_np(lse), g["lse"], rtol=0, atol=2e-5)
+
+
+def test_c1_matches_reference_chunked_path():
+  """Against the restated reference XLA chunked path (patch.py:106-162) at float32."""
+  g = np.load(__file__.replace("test_attention_gpu.py", "golden/c1_r3_2hop.npz"))
+  n = g["q"].shape[1]
+  mask = sparse.csr_matrix((np.ones(len(g["indices"]), bool), g["indices"], g["indptr"]), shape=(n, n))
+  scale = float(g["scale"])
+  starts, bits, window, n_kv = A.build_chunked_mask(mask, 512)
+  ref = A.chunked_attention(g["q"], g["k"], g["v"], starts, bits, window, n_kv, 512, scale)
+  refg = A.chunked_attention_grads(g["q"], g["k"], g["v"], g["do"], starts, bits, window, n_kv, 512, scale)
+  res = _run(g["q"], g["k"], g["v"], g["do"], fwn.TileList.from_mask(mask), scale, torch.float32)
+  assert A.rel_rms(res["out"], ref) <= 1e-5
+  for name, r in zip(("dq", "dk", "dv"), refg):
+    assert A.rel_rms(res[name], r) <= 1e-5, name
+
+
+def test_c1_bf16():
+  g = np.load(__file__.replace("test_attention_gpu.py", "golden/c1_r3_2hop.npz"))
+  n = g["q"].shape[1]
+  mask = sparse.csr_matrix((np.ones(len(g["indices"]), bool), g["indices"], g["indptr"]), shape=(n, n))
+  q, k, v, do = (_rounded(g[x], torch.bfloat16) for x in ("q", "k", "v", "do"))
+  scale = float(g["scale"])
+  res = _run(q, k, v, do, fwn.TileList.from_mask(mask), scale, torch.bfloat16)
+  dense = mask.toarray()
+  _check(res["out"], A.dense_attention(q, k, v, dense, scale), torch.bfloat16, "out")
+  for name, r in zip(("dq", "dk", "dv"), A.dense_grads(q, k, v, do, dense, scale)):
+    _check(res[name], r, torch.bfloat16, name)
+
+
+# ---------------------------------------------------------------------------------------------
+# the reference's kernel tests (tests/test_pallas_kernel.py), same generators and seeds
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("batch", [1, 2])
+def test_matches_dense_reference(batch, dtype):
+  rng = np.random.default_rng(0)
+  n, h, d = 300, 2, 64
+  q, k, v = (_rounded(rng.standard_normal((batch, n, h, d)), dtype) for _ in range(3))
+  m = _random_mask(n, 0.1, 1)
+  res = _run(q, k, v, None, fwn.TileList.from_mask(m), d ** -0.5, dtype)
+  ref = A.dense_attention(q, k, v, m.toarray(), d ** -0.5)
+  for b in range(batch):
+    _check(res["out"][b], ref[b], dtype, ("out", b))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("symmetric", [True, False])
+@pytest.mark.parametrize("batch", [1, 2])
+def test_grads_match_dense_reference(batch, symmetric, dtype):
+  rng = np.random.default_rng(2)
+  n, h, d = 300, 2, 64
+  q, k, v, do = (_rounded(rng.standard_normal((batch, n, h, d)), dtype) for _ in range(4))
+  m = _random_mask(n, 0.08, 3, symmetric=symmetric)
+  tiles = fwn.TileList.from_mask(m)
+  tiles_t = None if symmetric else fwn.TileList.from_mask(m.T.tocsr())
+  res = _run(q, k, v, do, tiles, d ** -0.5, dtype, tiles_t)
+  refs = A.dense_grads(q, k, v, do, m.toarray(), d ** -0.5)
+  for b in range(batch):
+    for name, r in zip(("dq", "dk", "dv"), refs):
+      _check(res[name][b], r[b], dtype, (name, b))
+
+
+def test_nonsymmetric_mask_needs_transposed_tiles():
+  rng = np.random.default_rng(4)
+  n, h, d = 130, 1, 32
+  q, k, v, do = (rng.standard_normal((1, n, h, d)).astype(np.float32) for _ in range(4))
+  m = _random_mask(n, 0.1, 5)
+  tiles = fwn.TileList.from_mask(m)
+  ref = A.dense_grads(q, k, v, do, m.toarray(), d ** -0.5)[1]
+  wrong = _run(q, k, v, do, tiles, d ** -0.5, torch.float32)["dk"]
+  assert A.max_rel_err(wrong, ref) > 1e-2
+  right = _run(q, k, v, do, tiles, d ** -0.5, torch.float32, fwn.TileList.from_mask(m.T.tocsr()))["dk"]
+  assert A.max_rel_err(right, ref) < 1e-5
+
+
+# ---------------------------------------------------------------------------------------------
+# shapes and edge cases
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("d", [32, 64, 128])
+@pytest.mark.parametrize("n", [100, 257, 512])
+def test_head_dims_and_ragged_sizes(n, d, dtype):
+  rng = np.random.default_rng(n + d)
+  h = 3
+  q, k, v, do = (_rounded(rng.standard_normal((1, n, h, d)), dtype) for _ in range(4))
+  m = _random_mask(n, 0.05, 6, symmetric=True)
+  res = _run(q, k, v, do, fwn.TileList.from_mask(m), d ** -0.5, dtype)
+  dense = m.toarray()
+  _check(res["out"], A.dense_attention(q, k, v, dense, d ** -0.5), dtype, "out")
+  for name, r in zip(("dq", "dk", "dv"), A.dense_grads(q, k, v, do, dense, d ** -0.5)):
+    _check(res[name], r, dtype, name)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_fully_valid_tiles(dtype):
+  """A dense mask: every tile takes the no-mask path."""
+  rng = np.random.default_rng(7)
+  n, h, d = 256, 2, 64
+  q, k, v, do = (_rounded(rng.standard_normal((1, n, h, d)), dtype) for _ in range(4))
+  m = sparse.csr_matrix(np.ones((n, n), bool))
+  tiles = fwn.TileList.from_mask(m)
+  assert tiles.n_tiles == 4
+  res = _run(q, k, v, do, tiles, d ** -0.5, dtype)
+  dense = m.toarray()
+  _check(res["out"], A.dense_attention(q, k, v, dense, d ** -0.5), dtype, "out")
+  for name, r in zip(("dq", "dk", "dv"), A.dense_grads(q, k, v, do, dense, d ** -0.5)):
+    _check(res[name], r, dtype, name)
+
+
+def test_rows_without_keys_are_zero_and_finite():
+  """Rows with no valid key produce 0 (the reference leaves such rows undefined; none occur in a
+  k-hop mask, where every row attends to itself). Other rows are unaffected."""
+  rng = np.random.default_rng(8)
+  n, h, d = 200, 2, 32
+  q, k, v, do = (rng.standard_normal((1, n, h, d)).astype(np.float32) for _ in range(4))
+  m = _random_mask(n, 0.05, 9, symmetric=True).tolil()
+  empty = [3, 64, 130, 199]
+  for r in empty:
+    m[r, :] = False
+    m[:, r] = False
+  m = m.tocsr()
+  m.eliminate_zeros()
+  res = _run(q, k, v, do, fwn.TileList.from_mask(m), d ** -0.5, torch.float32)
+  for name in res:
+    assert np.isfinite(res[name]).all(), name
+  np.testing.assert_array_equal(res["out"][:, empty], 0.0)
+  keep = np.setdiff1d(np.arange(n), empty)
+  dense = m.toarray()
+  sub = dense[np.ix_(keep, keep)]
+  ref = A.dense_attention(q[:, keep], k[:, keep], v[:, keep], sub, d ** -0.5)
+  _check(res["out"][:, keep], ref, torch.float32, "out")
+  refs = A.dense_grads(q[:, keep], k[:, keep], v[:, keep], do[:, keep], sub, d ** -0.5)
+  for name, r in zip(("dq", "dk", "dv"), refs):
+    _check(res[name][:, keep], r, torch.float32, name)
+    np.testing.assert_array_equal(res[name][:, empty], 0.0)
+
+
+def test_packed_qkv_strides_through_c_abi():
+  """q, k, v as strided views of one [B, n, 3, H, D] buffer, read in place by the kernels."""
+  rng = np.random.default_rng(10)
+  b, n, h, d = 2, 300, 2, 64
+  qkv = rng.standard_normal((b, n, 3, h, d)).astype(np.float32)
+  m = _random_mask(n, 0.05, 11, symmetric=True)
+  tiles = fwn.TileList.from_mask(m)
+  buf = torch.from_numpy(qkv).to(DEV)
+  out = torch.zeros((b, n, 3, h, d), device=DEV)  # o written in place of the q slot
+  desc = nat.AttnDesc(b, n, h, d, nat.F32, d ** -0.5, n * 3 * h * d, 3 * h * d, d)
+  lse = torch.empty((b, h, n), device=DEV)
+  base = buf.data_ptr()
+  step = h * d * 4
+  nat.check(nat.lib().fwn_attn_fwd_launch(desc, base, base + step, base + 2 * step, tiles.struct,
+                                          out.data_ptr(), lse.data_ptr(), torch.cuda.current_stream().cuda_stream))
+  torch.cuda.synchronize()
+  got = _np(out[:, :, 0])
+  ref = A.dense_attention(qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2], m.toarray(), d ** -0.5)
+  _check(got, ref, torch.float32, "out")
+  assert (_np(out[:, :, 1:]) == 0).all()  # nothing written outside the o slot
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_deterministic_and_batch_independent(dtype):
+  """No atomics: bitwise identical reruns, and each batch element equals its batch-1 run."""
+  rng = np.random.default_rng(12)
+  b, n, h, d = 3, 400, 2, 128
+  q, k, v, do = (rng.standard_normal((b, n, h, d)).astype(np.float32) for _ in range(4))
+  tiles = fwn.TileList.from_mask(_random_mask(n, 0.04, 13, symmetric=True))
+  r1 = _run(q, k, v, do, tiles, d ** -0.5, dtype)
+  r2 = _run(q, k, v, do, tiles, d ** -0.5, dtype)
+  for name in r1:
+    np.testing.assert_array_equal(r1[name], r2[name])
+  one = _run(q[1:2], k[1:2], v[1:2], do[1:2], tiles, d ** -0.5, dtype)
+  for name in r1:
+    np.testing.assert_array_equal(r1[name][1:2], one[name])
+
+
+def test_exp2_based_softmax_accuracy():
+  """The softmax uses V_EXP_F32 (2^x) with log2(e) folded into the scale: rows must sum to one and
+  the log-sum-exp must match float64 to single-precision accuracy."""
+  rng = np.random.default_rng(14)
+  n, h, d = 384, 2, 64
+  q, k = (3.0 * rng.standard_normal((1, n, h, d)).astype(np.float32) for _ in range(2))
+  m = _random_mask(n, 0.2, 15, symmetric=True)
+  tiles = fwn.TileList.from_mask(m)
+  ones = np.ones((1, n, h, d), np.float32)
+  out, lse = fwn.attention_forward(_dev(q, torch.float32), _dev(k, torch.float32), _dev(ones, torch.float32),
+                                   tiles, d ** -0.5)
+  np.testing.assert_allclose(_np(out), 1.0, rtol=0, atol=4e-6)
+  ref = A.dense_lse(q, k, m.toarray(), d ** -0.5)
+  np.testing.assert_allclose(_np(lse), ref, rtol=2e-6, atol=2e-6)
+
+
+# ---------------------------------------------------------------------------------------------
+# model scale (refinement-6 mesh, 40,962 nodes)
+
+
+@pytest.fixture(scope="module")
+def r6_masks():
+  masks = {}
+  for k in (8, 16):
+    mask, lat, lon, perm = fwn.mesh_mask(6, k, reorder=True)
+    masks[k] = (mask, perm)
+  return masks
+
+
+def _sample(n, count, seed):
+  return np.sort(np.random.default_rng(seed).choice(n, count, replace=False))
+
+
+@pytest.mark.parametrize("sigma", [128 ** -0.5, 1.0])
+def test_c2_fp32_forward_model_scale(r6_masks, sigma):
+  """Configuration 2: 8-hop mask, 4 heads x 128, float32 MFMA, forward."""
+  mask, _ = r6_masks[8]
+  n = mask.shape[0]
+  rng = np.random.default_rng(0)
+  q, k, v = (sigma * rng.standard_normal((1, n, 4, 128)).astype(np.float32) for _ in range(3))
+  tiles = fwn.TileList.from_mask(mask)
+  out, lse = fwn.attention_forward(*(_dev(x, torch.float32) for x in (q, k, v)), tiles, 128 ** -0.5)
+  rows = _sample(n, 512, 1)
+  ref = A.sampled_attention(q, k, v, np.zeros_like(q), mask, 128 ** -0.5, rows)
+  _check(_np(out)[:, rows], ref["out"], torch.float32, "out")
+  np.testing.assert_allclose(_np(lse)[:, :, rows], ref["lse"], rtol=0, atol=1e-5)
+
+
+def test_c3_bf16_forward_backward_model_scale(r6_masks):
+  """Configuration 3: 16-hop mask, 4 heads x 128, bf16 with fp32 accumulation, fwd + bwd."""
+  mask, _ = r6_masks[16]
+  n = mask.shape[0]
+  rng = np.random.default_rng(0)
+  q, k, v, do = (_rounded(rng.standard_normal((1, n, 4, 128)), torch.bfloat16) for _ in range(4))
+  tiles = fwn.TileList.from_mask(mask)
+  res = _run(q, k, v, do, tiles, 128 ** -0.5, torch.bfloat16)
+  rows, keys = _sample(n, 128, 2), _sample(n, 6, 3)
+  ref = A.sampled_attention(q, k, v, do, mask, 128 ** -0.5, rows, keys)
+  _check(res["out"][:, rows], ref["out"], torch.bfloat16, "out")
+  _check(res["dq"][:, rows], ref["dq"], torch.bfloat16, "dq")
+  _check(res["dk"][:, keys], ref["dk"], torch.bfloat16, "dk")
+  _check(res["dv"][:, keys], ref["dv"], torch.bfloat16, "dv")
+  # Size-independent identities over all 40,962 nodes: rows of P sum to one, so sum_j dV_j equals
+  # sum_i dO_i; rows of dS sum to zero, so sum_j dK_j = 0.
+  scale_dv = np.abs(do).sum(1)
+  np.testing.assert_allclose(res["dv"].astype(np.float64).sum(1), do.astype(np.float64).sum(1),
+                             rtol=0, atol=float(5e-3 * scale_dv.max()))
+  assert np.abs(res["dk"].astype(np.float64).sum(1)).max() <= 5e-3 * np.abs(res["dk"]).sum(1).max()
+
+
+def test_c4_bf16_ensemble_batch(r6_masks):
+  """Configuration 4: 8 members sharing one 8-hop tile list, bf16; member m drawn from seed m."""
+  mask, _ = r6_masks[8]
+  n = mask.shape[0]
+  members = [np.random.default_rng(m) for m in range(8)]
+  q, k, v = (np.concatenate([_rounded(r.standard_normal((1, n, 4, 128)), torch.bfloat16) for r in members])
+             for _ in range(3))
+  tiles = fwn.TileList.from_mask(mask)
+  res = _run(q, k, v, None, tiles, 128 ** -0.5, torch.bfloat16)
+  rows = _sample(n, 64, 4)
+  for m in (0, 5, 7):
+    ref = A.sampled_attention(q[m:m + 1], k[m:m + 1], v[m:m + 1], np.zeros_like(q[:1]), mask, 128 ** -0.5, rows)
+    _check(res["out"][m:m + 1, rows], ref["out"], torch.bfloat16, ("out", m))
+  one = _run(q[5:6], k[5:6], v[5:6], None, tiles, 128 ** -0.5, torch.bfloat16)
+  np.testing.assert_array_equal(res["out"][5:6], one["out"])
+
+
+def test_hilbert_reordering_is_exact_up_to_rounding(r6_masks):
+  """Attention on Hilbert-permuted nodes with the permuted mask, un-permuted, equals attention in
+  subdivision order (patch.py:275-292 relies on this)."""
+  mask, perm = r6_masks[8]
+  n = mask.shape[0]
+  rng = np.random.default_rng(5)
+  q, k, v = (rng.standard_normal((1, n, 2, 64)).astype(np.float32) for _ in range(3))
+  plain = fwn.TileList.from_mask(mask)
+  hil = fwn.TileList.from_mask(mask, perm)
+  assert hil.n_tiles < plain.n_tiles
+  a, _ = fwn.attention_forward(*(_dev(x, torch.float32) for x in (q, k, v)), plain, 64 ** -0.5, with_lse=False)
+  b, _ = fwn.attention_forward(*(_dev(x[:, perm], torch.float32) for x in (q, k, v)), hil, 64 ** -0.5,
+                               with_lse=False)
+  inv = np.argsort(perm)
+  assert A.rel_rms(_np(b)[:, inv], _np(a)) <= 1e-6

@@ -239,3 +239,21 @@ def test_tile_mask_roundtrip(n, bq, bk):
     seg = kb[ptr[qb]:ptr[qb + 1]]
     assert len(np.unique(seg)) == len(seg) and (np.diff(seg) > 0).all()
     assert bits[ptr[qb]:ptr[qb + 1]].reshape(len(seg), -1).any(axis=1).all()
+
+
+def test_sampled_attention_equals_dense():
+  rng = np.random.default_rng(16)
+  b, n, h, d = 2, 150, 3, 8
+  q, k, v, do = (rng.standard_normal((b, n, h, d)) for _ in range(4))
+  m = _random_mask(n, 0.06, 9)  # non-symmetric: dk/dv need the transposed neighbourhoods
+  rows = np.array([0, 7, 149, 77])
+  keys = np.array([3, 149, 0])
+  got = A.sampled_attention(q, k, v, do, m, 0.3, rows, keys)
+  out = A.dense_attention(q, k, v, m.toarray(), 0.3)
+  lse = A.dense_lse(q, k, m.toarray(), 0.3)
+  dq, dk, dv = A.dense_grads(q, k, v, do, m.toarray(), 0.3)
+  np.testing.assert_allclose(got["out"], out[:, rows], atol=1e-12)
+  np.testing.assert_allclose(got["lse"], lse[:, :, rows], atol=1e-12)
+  np.testing.assert_allclose(got["dq"], dq[:, rows], atol=1e-12)
+  np.testing.assert_allclose(got["dk"], dk[:, keys], atol=1e-12)
+  np.testing.assert_allclose(got["dv"], dv[:, keys], atol=1e-12)
