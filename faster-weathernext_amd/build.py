@@ -44,8 +44,11 @@ def build(jobs=4, verbose=False):
   objs = []
   for src in DEVICE_SOURCES:
     obj = os.path.join(objdir, src + ".o")
+    # MFMA results in VGPRs (VGPR form): the accumulators stay where the softmax VALU code reads
+    # them instead of being copied between AGPRs and VGPRs every tile.
     cmds.append([HIPCC, f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-I", INCLUDE,
                  "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+                 "-mllvm", "-amdgpu-mfma-vgpr-form=1",
                  "-c", os.path.join(CSRC, src), "-o", obj])
     objs.append(obj)
   for src in HOST_SOURCES:

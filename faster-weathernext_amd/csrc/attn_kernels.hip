@@ -106,11 +106,12 @@ __device__ __forceinline__ f32x16 zero16() {
   return z;
 }
 
-// sel ? x : y per lane, with the lane-mask `sel` held in an SGPR pair.
+// Bit `lane` of the wave-uniform mask `sel` ? x : y. inverse_ballot turns the 64-bit SGPR mask
+// into the per-lane condition, so this is one v_cndmask with the SGPR pair as its selector, and
+// (unlike inline assembly) the compiler sees the operands and inserts the wait states an MFMA
+// result needs before a VALU read.
 __device__ __forceinline__ float select_lane(uint64_t sel, float x, float y) {
-  float r;
-  asm("v_cndmask_b32_e64 %0, %1, %2, %3" : "=v"(r) : "v"(y), "v"(x), "s"(sel));
-  return r;
+  return __builtin_amdgcn_inverse_ballot_w64(sel) ? x : y;
 }
 
 // 2^x on the hardware transcendental unit (V_EXP_F32); callers fold log2(e) into their scales.
@@ -205,21 +206,28 @@ struct Bf16Stage {
     for (int e = 0; e < 8; ++e) x[e] = bload16(r, voff + (uint32_t)(row0 + e) * snb);
   }
 
+  // The store addresses are recomputed at every call (the empty asm hides that dc and kblk are
+  // loop-invariant): keeping 16 hoisted addresses alive across the tile loop costs more VGPRs than
+  // the few VALU ops it saves.
   __device__ __forceinline__ void store_rows(char* lds) const {
+    int dcv = dc, kb = kblk;
+    asm volatile("" : "+v"(dcv), "+v"(kb));
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const int row = 8 * kblk + e;
-      *(u32x4*)(lds + row * (D * 2) + ((dc ^ swz_row<C>(row)) << 4)) = x[e];
+      const int row = 8 * kb + e;
+      *(u32x4*)(lds + row * (D * 2) + ((dcv ^ swz_row<C>(row)) << 4)) = x[e];
     }
   }
 
   __device__ __forceinline__ void store_transposed(char* lds) const {
+    int dcv = dc, kb = kblk;
+    asm volatile("" : "+v"(dcv), "+v"(kb));
     u32x4 y[8];
     transpose8x8(x, y);
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
-      const int d = 8 * dc + c;
-      *(u32x4*)(lds + d * 256 + ((kblk ^ swz_t(d)) << 4)) = y[c];
+      const int d = 8 * dcv + c;
+      *(u32x4*)(lds + d * 256 + ((kb ^ swz_t(d)) << 4)) = y[c];
     }
   }
 };
@@ -346,15 +354,8 @@ struct SoftmaxState {
   float l;  // running sum of exp2(s*c2 - m) over this lane's half of the keys
 };
 
-__device__ __forceinline__ float softmax_tile(f32x16 (&s)[4], SoftmaxState& st, float c2, bool masked,
-                                              cu64_ptr mk) {
+__device__ __forceinline__ float softmax_tile(f32x16 (&s)[4], SoftmaxState& st, float c2) {
   const float ninf = -__builtin_inff();
-  if (masked) {
-#pragma unroll
-    for (int sb = 0; sb < 4; ++sb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) s[sb][r] = select_lane(mk[sb * 16 + r], s[sb][r], ninf);
-  }
   float mx = s[0][0];
 #pragma unroll
   for (int sb = 0; sb < 4; ++sb)
@@ -377,6 +378,17 @@ __device__ __forceinline__ float softmax_tile(f32x16 (&s)[4], SoftmaxState& st, 
   st.m = m_new;
   return corr;
 }
+
+// The 16 lane masks of sub-block sb of a tile (scalar loads, issued ahead of the sub-block's MFMAs).
+// Fully valid tiles hold all-ones words, so masks are applied unconditionally: one v_cndmask per
+// element and no branch.
+struct SubMask {
+  uint64_t w[16];
+  __device__ __forceinline__ void load(cu64_ptr mk, int sb) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) w[r] = mk[sb * 16 + r];
+  }
+};
 
 // Natural log-sum-exp of the scaled logits: (m + log2 l) * ln 2 (pallas_attn.py:140-141).
 __device__ __forceinline__ void write_lse(const KArgs& a, const Job& j, int row, const SoftmaxState& st, float ltot) {
@@ -419,29 +431,34 @@ __global__ void __launch_bounds__(NT, 2) fwd_bf16_kernel(KArgs a) {
   const bool stager = Bf16Stage<D>::active(w);
   ks.init(w, lane, snb);
   vs.init(w, lane, snb);
-  // K of the next tile is prefetched into registers during this tile's compute; V is loaded at
-  // the top of its own iteration (keeps the kernel within 256 VGPRs for two workgroups per CU).
-  if (t0 < t1 && stager) ks.load(rK, ((ci32_ptr)a.col)[t0] * BLK, snb);
+  // K and V are loaded after the barrier that ends the previous tile's LDS reads, so the loaded
+  // registers live only until their LDS store and the kernel stays within 256 VGPRs; with two
+  // workgroups per CU the other workgroup computes while this one waits for memory.
   for (int tt = t0; tt < t1; ++tt) {
     const int t = __builtin_amdgcn_readfirstlane(tt);  // uniform: keeps tile metadata in SGPRs
-    if (stager) vs.load(rV, ((ci32_ptr)a.col)[t] * BLK, snb);
     __syncthreads();
     if (stager) {
+      const int kb = ((ci32_ptr)a.col)[t];
+      ks.load(rK, kb * BLK, snb);
+      vs.load(rV, kb * BLK, snb);
       ks.store_rows(ldsK);
       vs.store_transposed(ldsVt);
     }
     __syncthreads();
-    if (t + 1 < t1 && stager) ks.load(rK, ((ci32_ptr)a.col)[t + 1] * BLK, snb);
+    const cu64_ptr mk = (cu64_ptr)a.lanes + ((int64_t)t * 4 + w) * 64;
     f32x16 s[4];
 #pragma unroll
     for (int sb = 0; sb < 4; ++sb) {
+      SubMask m;
+      m.load(mk, sb);
       s[sb] = zero16();
 #pragma unroll
       for (int step = 0; step < D / 16; ++step)
         s[sb] = mfma_bf16(lds16(ldsK + off.row[step] + sb * 32 * (D * 2)), qf[step], s[sb]);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[sb][r] = select_lane(m.w[r], s[sb][r], -__builtin_inff());
     }
-    const bool masked = !((((cu32_ptr)a.full)[t] >> w) & 1u);
-    const float corr = softmax_tile(s, st, a.c2, masked, (cu64_ptr)a.lanes + ((int64_t)t * 4 + w) * 64);
+    const float corr = softmax_tile(s, st, a.c2);
 #pragma unroll
     for (int db = 0; db < D / 32; ++db) o[db] *= corr;
 #pragma unroll
@@ -496,9 +513,12 @@ __global__ void __launch_bounds__(NT, 1) fwd_f32_kernel(KArgs a) {
     stage_rows_f32<D>(ldsK, rK, kb * BLK, snb, tid, true);
     stage_rows_f32<D>(ldsV, rV, kb * BLK, snb, tid, false);
     __syncthreads();
+    const cu64_ptr mk = (cu64_ptr)a.lanes + ((int64_t)t * 4 + w) * 64;
     f32x16 s[4];
 #pragma unroll
     for (int sb = 0; sb < 4; ++sb) {
+      SubMask m;
+      m.load(mk, sb);
       s[sb] = zero16();
 #pragma unroll
       for (int u = 0; u < D / 8; ++u) {
@@ -506,9 +526,10 @@ __global__ void __launch_bounds__(NT, 1) fwd_f32_kernel(KArgs a) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) s[sb] = mfma_f32(kx[e], qf[u][e], s[sb]);
       }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[sb][r] = select_lane(m.w[r], s[sb][r], -__builtin_inff());
     }
-    const bool masked = !((((cu32_ptr)a.full)[t] >> w) & 1u);
-    const float corr = softmax_tile(s, st, a.c2, masked, (cu64_ptr)a.lanes + ((int64_t)t * 4 + w) * 64);
+    const float corr = softmax_tile(s, st, a.c2);
 #pragma unroll
     for (int db = 0; db < D / 32; ++db) o[db] *= corr;
 #pragma unroll
@@ -584,10 +605,11 @@ __global__ void __launch_bounds__(NT, 1) dq_bf16_kernel(KArgs a) {
       ks.load(rK, kb * BLK, snb);
       vs.load(rV, kb * BLK, snb);
     }
-    const bool masked = !((((cu32_ptr)a.full)[t] >> w) & 1u);
     const cu64_ptr mk = (cu64_ptr)a.lanes + ((int64_t)t * 4 + w) * 64;
 #pragma unroll
     for (int sb = 0; sb < 4; ++sb) {
+      SubMask m;
+      m.load(mk, sb);
       f32x16 s = zero16(), dp = zero16();
 #pragma unroll
       for (int step = 0; step < D / 16; ++step) {
@@ -597,7 +619,7 @@ __global__ void __launch_bounds__(NT, 1) dq_bf16_kernel(KArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         float p = fast_exp2(fmaf(s[r], a.c2, -lse_t));
-        if (masked) p = select_lane(mk[sb * 16 + r], p, 0.f);
+        p = select_lane(m.w[r], p, 0.f);
         dp[r] = p * (dp[r] - delta);
       }
       const bf16x8 d0 = pack_bf16(dp, 0), d1 = pack_bf16(dp, 1);
@@ -650,10 +672,11 @@ __global__ void __launch_bounds__(NT, 1) dq_f32_kernel(KArgs a) {
     stage_rows_f32<D>(ldsK, rK, kb * BLK, snb, tid, true);
     stage_rows_f32<D>(ldsV, rV, kb * BLK, snb, tid, true);
     __syncthreads();
-    const bool masked = !((((cu32_ptr)a.full)[t] >> w) & 1u);
     const cu64_ptr mk = (cu64_ptr)a.lanes + ((int64_t)t * 4 + w) * 64;
 #pragma unroll
     for (int sb = 0; sb < 4; ++sb) {
+      SubMask m;
+      m.load(mk, sb);
       f32x16 s = zero16(), dp = zero16();
 #pragma unroll
       for (int u = 0; u < D / 8; ++u) {
@@ -668,7 +691,7 @@ __global__ void __launch_bounds__(NT, 1) dq_f32_kernel(KArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         float p = fast_exp2(fmaf(s[r], a.c2, -lse_t));
-        if (masked) p = select_lane(mk[sb * 16 + r], p, 0.f);
+        p = select_lane(m.w[r], p, 0.f);
         dp[r] = p * (dp[r] - delta);
       }
 #pragma unroll
@@ -748,10 +771,11 @@ __global__ void __launch_bounds__(NT, 1) dkv_bf16_kernel(KArgs a) {
     (tid < BLK ? ldsL : ldsDl)[tid & (BLK - 1)] = stat;
     __syncthreads();
     if (t + 1 < t1) load_tile(t + 1);
-    const bool masked = !((((cu32_ptr)a.full)[t] >> w) & 1u);
     const cu64_ptr mk = (cu64_ptr)a.lanes + ((int64_t)t * 4 + w) * 64;
 #pragma unroll
     for (int sb = 0; sb < 4; ++sb) {
+      SubMask m;
+      m.load(mk, sb);
       f32x16 s = zero16(), dp = zero16();
 #pragma unroll
       for (int step = 0; step < D / 16; ++step) {
@@ -776,7 +800,7 @@ __global__ void __launch_bounds__(NT, 1) dkv_bf16_kernel(KArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         float p = fast_exp2(fmaf(s[r], a.c2, -Lr[r]));
-        if (masked) p = select_lane(mk[sb * 16 + r], p, 0.f);
+        p = select_lane(m.w[r], p, 0.f);
         s[r] = p;
         dp[r] = p * (dp[r] - Dr[r]);
       }
@@ -842,10 +866,11 @@ __global__ void __launch_bounds__(NT, 1) dkv_f32_kernel(KArgs a) {
       (tid < BLK ? ldsL : ldsDl)[tid & (BLK - 1)] = stat;
     }
     __syncthreads();
-    const bool masked = !((((cu32_ptr)a.full)[t] >> w) & 1u);
     const cu64_ptr mk = (cu64_ptr)a.lanes + ((int64_t)t * 4 + w) * 64;
 #pragma unroll
     for (int sb = 0; sb < 4; ++sb) {
+      SubMask m;
+      m.load(mk, sb);
       f32x16 s = zero16(), dp = zero16();
 #pragma unroll
       for (int u = 0; u < D / 8; ++u) {
@@ -861,7 +886,7 @@ __global__ void __launch_bounds__(NT, 1) dkv_f32_kernel(KArgs a) {
       for (int r = 0; r < 16; ++r) {
         const int qq = element_col(sb, r, g);
         float p = fast_exp2(fmaf(s[r], a.c2, -ldsL[qq]));
-        if (masked) p = select_lane(mk[sb * 16 + r], p, 0.f);
+        p = select_lane(m.w[r], p, 0.f);
         s[r] = p;
         dp[r] = p * (dp[r] - ldsDl[qq]);
       }

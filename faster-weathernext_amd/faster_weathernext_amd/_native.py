@@ -9,7 +9,8 @@ import threading
 
 import numpy as np
 
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libfwn_attn.so")
+# FWN_LIB overrides the location (e.g. to compare two builds of the library).
+LIB_PATH = os.environ.get("FWN_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libfwn_attn.so")
 
 BLOCK = 128
 WAVES = 4
