@@ -1,0 +1,469 @@
+// bfloat16 attention kernels for gfx950: forward, dQ, dK/dV (V_MFMA_F32_32X32X16_BF16, fp32
+// accumulation, fp32 softmax statistics).
+//
+// Tiles live in LDS only row-major ([128 rows][D], 16-byte chunks XOR-swizzled) and are copied
+// there by the buffer unit (buffer_load ... lds: each wave-wide instruction writes 1 KB, lane l at
+// M0 + 16*l, from any per-lane global address), double-buffered: tile t+1 streams in while tile
+// t is computed, with no staging registers. Both contractions read their A operands from the
+// same copy:
+//   - row reads (ds_read_b128) of the sigma-ordered rows for the first contraction;
+//   - transpose reads (ds_read_b64_tr_b16) for the second: within each 16-lane group, lane 4e+q
+//     addresses 4 consecutive columns d0+4q.. of row k0+e, and lane j receives column d0+j of rows
+//     k0..k0+3, i.e. four consecutive keys of its own column, which is the key-contiguous operand
+//     the MFMA needs. Two such reads form the 8-element operand.
+// The swizzle keeps the row reads (8 lanes of distinct rows per 128 bytes) and the transpose
+// reads (4 consecutive rows x 32 bytes per 16 lanes) free of bank conflicts.
+//
+// Reference: pallas_attn.py:112-141 (forward), 161-215 (dQ, dK/dV), 274-311 (VJP driver).
+#include "attn_device.h"
+
+namespace fwn {
+namespace {
+
+using namespace dev;
+
+// XOR swizzle of the 16-byte chunk index of a bf16 row-major tile with C chunks per row; depends
+// on the row's low 4 bits only.
+template <int C>
+__device__ __forceinline__ int swz(int row) {
+  if constexpr (C >= 16) {
+    return ((row & 3) << 1) | ((row >> 3) & 1) | (((row >> 2) & 1) << 3);
+  } else if constexpr (C == 8) {
+    return ((row & 3) << 1) | ((row >> 3) & 1);
+  } else {
+    return (((row >> 1) & 1) << 1) | ((row >> 3) & 1);
+  }
+}
+
+template <int D>
+struct Tile {
+  static constexpr int C = D / 8;                     // 16-byte chunks per row
+  static constexpr int BYTES = BLK * D * 2;           // one 128 x D tile
+  static constexpr int ROWS_PER_OP = 64 / C;          // rows one wave-wide DMA instruction fills
+  static constexpr int OPS_PER_WAVE = BLK / ROWS_PER_OP / 4;
+};
+
+// Global -> LDS copy of one 128 x D tile by the 4 waves (buffer_load_dwordx4 ... lds).
+// Instruction (op, w) fills physical chunks [(4*op + w) * 64, +64): lane l the chunk at row
+// (4*op + w) * ROWS_PER_OP + l / C, physical column l % C, which holds logical column
+// (l % C) ^ swz(row). The swizzle depends on row % 16, which is the same for every op.
+template <int D>
+struct TileDma {
+  static constexpr int C = Tile<D>::C;
+  static constexpr int RPO = Tile<D>::ROWS_PER_OP;
+  uint32_t voff;
+
+  __device__ __forceinline__ void init(int w, int lane, uint32_t snb) {
+    const int row = w * RPO + lane / C;
+    voff = (uint32_t)row * snb + (uint32_t)((((lane % C) ^ swz<C>(row))) << 4);
+  }
+
+  __device__ __forceinline__ void issue(rsrc_t r, lds_char* tile, int w, int row0, uint32_t snb) const {
+#pragma unroll
+    for (int op = 0; op < Tile<D>::OPS_PER_WAVE; ++op) {
+      const uint32_t vo = voff + (uint32_t)(row0 + op * 4 * RPO) * snb;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(tile + (op * 4 + w) * 1024),
+                                               16, (int)vo, 0, 0, 0);
+    }
+  }
+};
+
+// Per-lane LDS byte offsets of the MFMA A operands.
+//   row[s]:     sigma-ordered row of this lane, columns 16*s + 8*g.. (+ sb * 32 * 2D).
+//   tr[db][h]:  transpose read for columns 32*db.. and keys 8*g + 4*h.. of a 16-key chunk
+//               (+ (32*sb + 16*c) * 2D).
+template <int D>
+struct Off {
+  static constexpr int C = Tile<D>::C;
+  uint32_t row[D / 16];
+  uint32_t tr[D / 32][2];
+
+  __device__ __forceinline__ void init(int lane) {
+    const int i = lane & 31, g = lane >> 5;
+    const int rho = sigma(i);
+#pragma unroll
+    for (int s = 0; s < D / 16; ++s) row[s] = rho * (2 * D) + (((2 * s + g) ^ swz<C>(rho)) << 4);
+    const int G = lane >> 4, t = lane & 15, e = t >> 2, q = t & 3, gg = G >> 1;
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int r = 8 * gg + 4 * h + e;
+        const int chunk = 4 * db + 2 * (G & 1) + (q >> 1);
+        tr[db][h] = r * (2 * D) + ((chunk ^ swz<C>(r)) << 4) + (q & 1) * 8;
+      }
+  }
+};
+
+__device__ __forceinline__ u32x4 row_read(const lds_char* tile, uint32_t off) {
+  return *(const __attribute__((address_space(3))) u32x4*)(tile + off);
+}
+
+__device__ __forceinline__ u32x2 tr_read(const lds_char* tile, uint32_t off) {
+  const i16x4 v =
+      __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(tile + off));
+  return __builtin_bit_cast(u32x2, v);
+}
+
+// A operand of the second contraction for columns 32*db.. and keys 32*sb + 16*c .. +15.
+template <int D>
+__device__ __forceinline__ u32x4 tr_operand(const lds_char* tile, const Off<D>& off, int db, int sb, int c) {
+  const uint32_t base = (uint32_t)(32 * sb + 16 * c) * (2 * D);
+  const u32x2 lo = tr_read(tile, off.tr[db][0] + base), hi = tr_read(tile, off.tr[db][1] + base);
+  return u32x4{lo[0], lo[1], hi[0], hi[1]};
+}
+
+// This lane's row fragment (B operand of the first contraction): columns 16*s + 8*g .. +7.
+template <int D>
+__device__ __forceinline__ void load_frag(u32x4 (&f)[D / 16], rsrc_t r, int row, uint32_t snb, int g) {
+#pragma unroll
+  for (int s = 0; s < D / 16; ++s) f[s] = bload16(r, (uint32_t)row * snb + (uint32_t)(32 * s + 16 * g));
+}
+
+template <int D>
+constexpr int min_blocks() {
+  return D <= 64 ? 2 : 1;
+}
+
+// ------------------------------------------------------------------------------------------
+// Forward: per query block, O^T += V^T P^T over live tiles with an online softmax.
+
+template <int D>
+__global__ void __launch_bounds__(NT, min_blocks<D>()) fwd_kernel(KArgs a) {
+  constexpr int TB = Tile<D>::BYTES;
+  __shared__ __attribute__((aligned(1024))) char lds0[2 * TB];  // K | V of even iterations
+  __shared__ __attribute__((aligned(1024))) char lds1[2 * TB];  // K | V of odd iterations
+  lds_char* bufs[2] = {(lds_char*)lds0, (lds_char*)lds1};
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int i = lane & 31, g = lane >> 5;
+  const Job j = decode_job(a);
+  const uint32_t snb = (uint32_t)a.sn * 2;
+  const rsrc_t rK = make_rsrc((const uint16_t*)a.k + j.base, a.slice_bytes);
+  const rsrc_t rV = make_rsrc((const uint16_t*)a.v + j.base, a.slice_bytes);
+
+  const int qrow = j.blk * BLK + 32 * w + i;
+  u32x4 qf[D / 16];
+  load_frag<D>(qf, make_rsrc((const uint16_t*)a.q + j.base, a.slice_bytes), qrow, snb, g);
+  Off<D> off;
+  off.init(lane);
+  TileDma<D> dma;
+  dma.init(w, lane, snb);
+  f32x16 o[D / 32];
+#pragma unroll
+  for (int db = 0; db < D / 32; ++db) o[db] = zero16();
+  SoftmaxState st{-__builtin_inff(), 0.f};
+
+  int t0, t1;
+  tile_range(a, j.blk, t0, t1);
+  if (t0 < t1) {
+    const int kb = ((ci32_ptr)a.col)[t0];
+    dma.issue(rK, bufs[0], w, kb * BLK, snb);
+    dma.issue(rV, bufs[0] + TB, w, kb * BLK, snb);
+  }
+  auto step = [&](int tt, lds_char* cur, lds_char* nxt) {
+    const int t = __builtin_amdgcn_readfirstlane(tt);
+    wait_vmem();      // this wave's copy of tile t (and the Q fragment) has landed
+    __syncthreads();  // every wave's copy has; every wave is done with the previous tile
+    if (t + 1 < t1) {
+      const int kb = ((ci32_ptr)a.col)[t + 1];
+      dma.issue(rK, nxt, w, kb * BLK, snb);
+      dma.issue(rV, nxt + TB, w, kb * BLK, snb);
+    }
+    const lds_char* K = cur;
+    const lds_char* V = cur + TB;
+    const cu64_ptr mk = tile_masks(a, t, w);
+    f32x16 s[4];
+#pragma unroll
+    for (int sb = 0; sb < 4; ++sb) {
+      u32x4 ka[D / 16];
+#pragma unroll
+      for (int k = 0; k < D / 16; ++k) ka[k] = row_read(K, off.row[k] + sb * 32 * (2 * D));
+      SubMask m;
+      m.load(mk, sb);
+      __builtin_amdgcn_sched_barrier(0);  // keep the operand reads ahead of the MFMAs
+      s[sb] = zero16();
+#pragma unroll
+      for (int k = 0; k < D / 16; ++k) s[sb] = mfma_bf16(ka[k], qf[k], s[sb]);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[sb][r] = select_lane(m.w[r], s[sb][r], -__builtin_inff());
+    }
+    const float corr = softmax_tile(s, st, a.c2);
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db) o[db] *= corr;
+#pragma unroll
+    for (int sb = 0; sb < 4; ++sb) {
+      u32x4 va[D / 32][2];
+#pragma unroll
+      for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) va[db][c] = tr_operand<D>(V, off, db, sb, c);
+      const bf16x8 p0 = pack_bf16(s[sb], 0), p1 = pack_bf16(s[sb], 1);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int db = 0; db < D / 32; ++db) {
+        o[db] = mfma_bf16(va[db][0], p0, o[db]);
+        o[db] = mfma_bf16(va[db][1], p1, o[db]);
+      }
+    }
+  };
+  for (int tt = t0; tt < t1; tt += 2) {
+    step(tt, bufs[0], bufs[1]);
+    if (tt + 1 < t1) step(tt + 1, bufs[1], bufs[0]);
+  }
+  const float ltot = st.l + __shfl_xor(st.l, 32);
+  const float inv = ltot > 0.f ? 1.f / ltot : 0.f;
+  store_acc_bf16<D>(make_rsrc((uint16_t*)a.out0 + j.base, a.slice_bytes), qrow, snb, o, inv, g);
+  if (g == 0) write_lse(a, j, qrow, st, ltot);
+}
+
+// ------------------------------------------------------------------------------------------
+// dQ: per query block over the forward tile list (pallas_attn.py:161-184).
+// P = where(valid, exp(s*scale - lse), 0); dS = P * (dP - delta); dQ = scale * dS K.
+
+template <int D>
+__global__ void __launch_bounds__(NT, min_blocks<D>()) dq_kernel(KArgs a) {
+  constexpr int TB = Tile<D>::BYTES;
+  __shared__ __attribute__((aligned(1024))) char lds0[2 * TB];  // K | V
+  __shared__ __attribute__((aligned(1024))) char lds1[2 * TB];
+  lds_char* bufs[2] = {(lds_char*)lds0, (lds_char*)lds1};
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int i = lane & 31, g = lane >> 5;
+  const Job j = decode_job(a);
+  const uint32_t snb = (uint32_t)a.sn * 2;
+  const rsrc_t rK = make_rsrc((const uint16_t*)a.k + j.base, a.slice_bytes);
+  const rsrc_t rV = make_rsrc((const uint16_t*)a.v + j.base, a.slice_bytes);
+
+  const int qrow = j.blk * BLK + 32 * w + i;
+  u32x4 qf[D / 16], df[D / 16];
+  load_frag<D>(qf, make_rsrc((const uint16_t*)a.q + j.base, a.slice_bytes), qrow, snb, g);
+  load_frag<D>(df, make_rsrc((const uint16_t*)a.dout + j.base, a.slice_bytes), qrow, snb, g);
+  float lse_t = 0.f, delta = 0.f;
+  if (qrow < a.n) {
+    lse_t = a.lse[stat_index(a, j, qrow)] * LOG2E;
+    delta = a.delta[stat_index(a, j, qrow)];
+  }
+  Off<D> off;
+  off.init(lane);
+  TileDma<D> dma;
+  dma.init(w, lane, snb);
+  f32x16 acc[D / 32];
+#pragma unroll
+  for (int db = 0; db < D / 32; ++db) acc[db] = zero16();
+
+  int t0, t1;
+  tile_range(a, j.blk, t0, t1);
+  if (t0 < t1) {
+    const int kb = ((ci32_ptr)a.col)[t0];
+    dma.issue(rK, bufs[0], w, kb * BLK, snb);
+    dma.issue(rV, bufs[0] + TB, w, kb * BLK, snb);
+  }
+  auto step = [&](int tt, lds_char* cur, lds_char* nxt) {
+    const int t = __builtin_amdgcn_readfirstlane(tt);
+    wait_vmem();
+    __syncthreads();
+    if (t + 1 < t1) {
+      const int kb = ((ci32_ptr)a.col)[t + 1];
+      dma.issue(rK, nxt, w, kb * BLK, snb);
+      dma.issue(rV, nxt + TB, w, kb * BLK, snb);
+    }
+    const lds_char* K = cur;
+    const lds_char* V = cur + TB;
+    const cu64_ptr mk = tile_masks(a, t, w);
+#pragma unroll
+    for (int sb = 0; sb < 4; ++sb) {
+      u32x4 ka[D / 16], va[D / 16];
+#pragma unroll
+      for (int k = 0; k < D / 16; ++k) {
+        ka[k] = row_read(K, off.row[k] + sb * 32 * (2 * D));
+        va[k] = row_read(V, off.row[k] + sb * 32 * (2 * D));
+      }
+      SubMask m;
+      m.load(mk, sb);
+      __builtin_amdgcn_sched_barrier(0);
+      f32x16 s = zero16(), dp = zero16();
+#pragma unroll
+      for (int k = 0; k < D / 16; ++k) {
+        s = mfma_bf16(ka[k], qf[k], s);
+        dp = mfma_bf16(va[k], df[k], dp);
+      }
+      u32x4 kt[D / 32][2];
+#pragma unroll
+      for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) kt[db][c] = tr_operand<D>(K, off, db, sb, c);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = select_lane(m.w[r], fast_exp2(fmaf(s[r], a.c2, -lse_t)), 0.f);
+        dp[r] = p * (dp[r] - delta);
+      }
+      const bf16x8 d0 = pack_bf16(dp, 0), d1 = pack_bf16(dp, 1);
+#pragma unroll
+      for (int db = 0; db < D / 32; ++db) {
+        acc[db] = mfma_bf16(kt[db][0], d0, acc[db]);
+        acc[db] = mfma_bf16(kt[db][1], d1, acc[db]);
+      }
+    }
+  };
+  for (int tt = t0; tt < t1; tt += 2) {
+    step(tt, bufs[0], bufs[1]);
+    if (tt + 1 < t1) step(tt + 1, bufs[1], bufs[0]);
+  }
+  store_acc_bf16<D>(make_rsrc((uint16_t*)a.out0 + j.base, a.slice_bytes), qrow, snb, acc, a.scale, g);
+}
+
+// ------------------------------------------------------------------------------------------
+// dK/dV: per key block over the transposed tile list; each workgroup owns its dK/dV rows, so
+// there are no atomics (pallas_attn.py:187-215). The tile's 128 log-sum-exps and deltas are
+// copied next to its Q and dO tiles.
+
+template <int D>
+__global__ void __launch_bounds__(NT, min_blocks<D>()) dkv_kernel(KArgs a) {
+  constexpr int TB = Tile<D>::BYTES;
+  constexpr int BUF = 2 * TB + 1536;
+  __shared__ __attribute__((aligned(1024))) char lds0[BUF];  // Q | dO | lse[128] | gap | delta[128]
+  __shared__ __attribute__((aligned(1024))) char lds1[BUF];
+  lds_char* bufs[2] = {(lds_char*)lds0, (lds_char*)lds1};
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int i = lane & 31, g = lane >> 5;
+  const Job j = decode_job(a);
+  const uint32_t snb = (uint32_t)a.sn * 2;
+  const rsrc_t rQ = make_rsrc((const uint16_t*)a.q + j.base, a.slice_bytes);
+  const rsrc_t rO = make_rsrc((const uint16_t*)a.dout + j.base, a.slice_bytes);
+  const rsrc_t rL = make_rsrc(a.lse + stat_index(a, j, 0), (uint32_t)a.n * 4);
+  const rsrc_t rD = make_rsrc(a.delta + stat_index(a, j, 0), (uint32_t)a.n * 4);
+
+  const int krow = j.blk * BLK + 32 * w + i;  // this lane's key
+  u32x4 kf[D / 16], vf[D / 16];
+  load_frag<D>(kf, make_rsrc((const uint16_t*)a.k + j.base, a.slice_bytes), krow, snb, g);
+  load_frag<D>(vf, make_rsrc((const uint16_t*)a.v + j.base, a.slice_bytes), krow, snb, g);
+  Off<D> off;
+  off.init(lane);
+  TileDma<D> dma;
+  dma.init(w, lane, snb);
+  f32x16 dk[D / 32], dv[D / 32];
+#pragma unroll
+  for (int db = 0; db < D / 32; ++db) {
+    dk[db] = zero16();
+    dv[db] = zero16();
+  }
+
+  int t0, t1;
+  tile_range(a, j.blk, t0, t1);
+  // Wave 0 also copies the tile's statistics with two full-wave copies and no branch: the first
+  // (log-sum-exps) lands at stats + 16 * lane, the second (deltas) at stats + 512 + 16 * lane.
+  // Lanes 0-31 of the first and 32-63 of the second carry the data; the other halves address
+  // past the end of their buffer, read zeros and land in the 512-byte gap.
+  constexpr uint32_t kPastEnd = 0x7FFFFFF0u;
+  auto issue = [&](int t, lds_char* buf) {
+    const int qb = ((ci32_ptr)a.col)[t];
+    dma.issue(rQ, buf, w, qb * BLK, snb);
+    dma.issue(rO, buf + TB, w, qb * BLK, snb);
+    if (w == 0) {
+      const uint32_t vo = (uint32_t)(qb * BLK + 4 * (lane & 31)) * 4;
+      lds_char* stats = buf + 2 * TB;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rL, (__attribute__((address_space(3))) void*)stats, 16,
+                                               (int)(lane < 32 ? vo : kPastEnd), 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rD, (__attribute__((address_space(3))) void*)(stats + 512), 16,
+                                               (int)(lane < 32 ? kPastEnd : vo), 0, 0, 0);
+    }
+  };
+  if (t0 < t1) issue(t0, bufs[0]);
+  auto step = [&](int tt, lds_char* cur, lds_char* nxt) {
+    const int t = __builtin_amdgcn_readfirstlane(tt);
+    wait_vmem();
+    __syncthreads();
+    if (t + 1 < t1) issue(t + 1, nxt);
+    const lds_char* Q = cur;
+    const lds_char* O = cur + TB;
+    const __attribute__((address_space(3))) float* L = (const __attribute__((address_space(3))) float*)(cur + 2 * TB);
+    const __attribute__((address_space(3))) float* Dl = L + 2 * BLK;
+    const cu64_ptr mk = tile_masks(a, t, w);
+#pragma unroll
+    for (int sb = 0; sb < 4; ++sb) {
+      u32x4 qa[D / 16], oa[D / 16];
+#pragma unroll
+      for (int k = 0; k < D / 16; ++k) {
+        qa[k] = row_read(Q, off.row[k] + sb * 32 * (2 * D));
+        oa[k] = row_read(O, off.row[k] + sb * 32 * (2 * D));
+      }
+      SubMask m;
+      m.load(mk, sb);
+      // Statistics of the 16 queries in this lane's accumulator rows: 32*sb + 16*c + 8*g + 0..7.
+      f32x4 lr[4], dr[4];
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          const int q0 = 32 * sb + 16 * c + 8 * g + 4 * hh;
+          lr[2 * c + hh] = *(const __attribute__((address_space(3))) f32x4*)(L + q0);
+          dr[2 * c + hh] = *(const __attribute__((address_space(3))) f32x4*)(Dl + q0);
+        }
+      f32x16 s = zero16(), dp = zero16();
+#pragma unroll
+      for (int k = 0; k < D / 16; ++k) {
+        s = mfma_bf16(qa[k], kf[k], s);
+        dp = mfma_bf16(oa[k], vf[k], dp);
+      }
+      u32x4 qt[D / 32][2], ot[D / 32][2];
+#pragma unroll
+      for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          qt[db][c] = tr_operand<D>(Q, off, db, sb, c);
+          ot[db][c] = tr_operand<D>(O, off, db, sb, c);
+        }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float lse_t = lr[r >> 2][r & 3] * LOG2E;
+        const float p = select_lane(m.w[r], fast_exp2(fmaf(s[r], a.c2, -lse_t)), 0.f);
+        s[r] = p;
+        dp[r] = p * (dp[r] - dr[r >> 2][r & 3]);
+      }
+      const bf16x8 p0 = pack_bf16(s, 0), p1 = pack_bf16(s, 1);
+      const bf16x8 d0 = pack_bf16(dp, 0), d1 = pack_bf16(dp, 1);
+#pragma unroll
+      for (int db = 0; db < D / 32; ++db) {
+        dv[db] = mfma_bf16(ot[db][0], p0, dv[db]);
+        dv[db] = mfma_bf16(ot[db][1], p1, dv[db]);
+        dk[db] = mfma_bf16(qt[db][0], d0, dk[db]);
+        dk[db] = mfma_bf16(qt[db][1], d1, dk[db]);
+      }
+    }
+  };
+  for (int tt = t0; tt < t1; tt += 2) {
+    step(tt, bufs[0], bufs[1]);
+    if (tt + 1 < t1) step(tt + 1, bufs[1], bufs[0]);
+  }
+  store_acc_bf16<D>(make_rsrc((uint16_t*)a.out0 + j.base, a.slice_bytes), krow, snb, dk, a.scale, g);
+  store_acc_bf16<D>(make_rsrc((uint16_t*)a.out1 + j.base, a.slice_bytes), krow, snb, dv, 1.f, g);
+}
+
+template <int D>
+hipError_t launch_d(Kind kind, const KArgs& a, hipStream_t stream) {
+  const dim3 grid((unsigned)a.n_blocks * (unsigned)(a.batch * a.heads)), block(NT);
+  switch (kind) {
+    case Kind::kFwd: hipLaunchKernelGGL(fwd_kernel<D>, grid, block, 0, stream, a); break;
+    case Kind::kDq: hipLaunchKernelGGL(dq_kernel<D>, grid, block, 0, stream, a); break;
+    case Kind::kDkv: hipLaunchKernelGGL(dkv_kernel<D>, grid, block, 0, stream, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_bf16(Kind kind, int head_dim, const KArgs& a, hipStream_t stream) {
+  switch (head_dim) {
+    case 32: return launch_d<32>(kind, a, stream);
+    case 64: return launch_d<64>(kind, a, stream);
+    case 128: return launch_d<128>(kind, a, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace fwn

@@ -1,0 +1,231 @@
+// Device-side building blocks shared by the bf16 and fp32 attention kernels (gfx950 only).
+//
+// Conventions used by every kernel:
+//   - One workgroup = 4 waves = one 128-row block of queries (forward, dQ) or keys (dK/dV) for one
+//     (batch, head); wave w owns rows 32w..32w+31 of the block; lane l has i = l % 32, g = l / 32.
+//   - The first contraction is computed transposed, X^T[col][row] (S^T = K Q^T in the forward),
+//     so the 32x32 MFMA accumulator column (lane % 32) is the wave's own row and softmax
+//     statistics are per lane. Its A-operand rows are loaded in the order sigma(i), which makes
+//     accumulator register r of lane group g hold column element_col(sb, r, g): 8 consecutive
+//     columns per lane group and 16-column chunk, i.e. the B-operand layout of the second
+//     contraction. P and dS therefore go from accumulator to MFMA operand in registers.
+//   - Global memory is read through raw buffer resources, one per (batch, head) slice; the
+//     hardware range check returns zeros for rows >= n and drops their stores.
+//   - Tile masks are one 64-bit lane mask per accumulator element (fwn_tiles_prepare), loaded
+//     with scalar loads through the constant address space and applied with one v_cndmask.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "attn_kernels.h"
+
+namespace fwn {
+namespace dev {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+typedef const __attribute__((address_space(4))) uint64_t* cu64_ptr;
+typedef const __attribute__((address_space(4))) uint32_t* cu32_ptr;
+typedef const __attribute__((address_space(4))) int32_t* ci32_ptr;
+typedef __attribute__((address_space(3))) char lds_char;
+
+constexpr int BLK = 128;
+constexpr int NT = 256;
+constexpr int RSRC_DW3 = 0x00020000;  // raw buffer, 32-bit dword format (gfx9 family)
+constexpr float LOG2E = 1.4426950408889634f;
+constexpr float LN2 = 0.6931471805599453f;
+
+// Operand row that MFMA row i of a 32-row sub-block loads.
+__device__ __forceinline__ int sigma(int i) {
+  return ((i >> 4) << 4) | (((i >> 2) & 1) << 3) | (((i >> 3) & 1) << 2) | (i & 3);
+}
+
+// Column (key or query) within a 128-wide tile held by accumulator register r of sub-block sb.
+__device__ __forceinline__ int element_col(int sb, int r, int g) { return 32 * sb + 16 * (r >> 3) + 8 * g + (r & 7); }
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, RSRC_DW3);
+}
+
+__device__ __forceinline__ u32x4 bload16(rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+}
+
+__device__ __forceinline__ u32x4 lds16(const char* p) { return *(const u32x4*)p; }
+
+__device__ __forceinline__ f32x16 zero16() {
+  f32x16 z;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) z[r] = 0.f;
+  return z;
+}
+
+// Bit `lane` of the wave-uniform mask `sel` ? x : y. inverse_ballot turns the 64-bit SGPR mask
+// into the per-lane condition, so this is one v_cndmask with the SGPR pair as its selector, and
+// (unlike inline assembly) the compiler sees the operands and inserts the wait states an MFMA
+// result needs before a VALU read.
+__device__ __forceinline__ float select_lane(uint64_t sel, float x, float y) {
+  return __builtin_amdgcn_inverse_ballot_w64(sel) ? x : y;
+}
+
+// Waits for every outstanding vector-memory operation (s_waitcnt vmcnt(0); expcnt and lgkmcnt
+// left free).
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// 2^x on the hardware transcendental unit (V_EXP_F32); callers fold log2(e) into their scales.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ bf16x8 pack_bf16(const f32x16& v, int half) {
+  bf16x8 r;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) r[e] = (__bf16)v[8 * half + e];
+  return r;
+}
+
+__device__ __forceinline__ f32x16 mfma_bf16(const u32x4& a, const bf16x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x16 mfma_bf16(const u32x4& a, const u32x4& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
+                                                 c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x16 mfma_f32(float a, float b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+struct Job {
+  int blk;
+  int b, h;
+  int64_t base;  // element offset of (b, h)
+};
+
+// Blocks are visited in `order` (most tiles first); the (batch, head) index varies fastest, so
+// the heads of one block run side by side and share its mask words in L2.
+__device__ __forceinline__ Job decode_job(const KArgs& a) {
+  Job j;
+  const int bh_count = a.batch * a.heads;
+  const int slot = blockIdx.x / bh_count;
+  const int bh = blockIdx.x - slot * bh_count;
+  j.blk = a.order ? ((ci32_ptr)a.order)[slot] : slot;
+  j.b = bh / a.heads;
+  j.h = bh - j.b * a.heads;
+  j.base = (int64_t)j.b * a.sb + (int64_t)j.h * a.sh;
+  return j;
+}
+
+__device__ __forceinline__ void tile_range(const KArgs& a, int blk, int& t0, int& t1) {
+  t0 = ((ci32_ptr)a.ptr)[blk];
+  t1 = ((ci32_ptr)a.ptr)[blk + 1];
+  t0 = t0 < 0 ? 0 : t0;
+  t1 = t1 > a.n_tiles ? a.n_tiles : t1;
+}
+
+__device__ __forceinline__ int64_t stat_index(const KArgs& a, const Job& j, int row) {
+  return ((int64_t)j.b * a.heads + j.h) * a.n + row;
+}
+
+// The 16 lane masks of sub-block sb of a tile (scalar loads). Fully valid tiles hold all-ones
+// words, so masks are applied unconditionally: one v_cndmask per element and no branch.
+struct SubMask {
+  uint64_t w[16];
+  __device__ __forceinline__ void load(cu64_ptr mk, int sb) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) w[r] = mk[sb * 16 + r];
+  }
+};
+
+__device__ __forceinline__ cu64_ptr tile_masks(const KArgs& a, int t, int w) {
+  return (cu64_ptr)a.lanes + ((int64_t)t * 4 + w) * 64;
+}
+
+// Online softmax of the forward kernels. s[sb][r] holds this lane's masked logits (raw q.k, -inf
+// where masked); on return it holds exp2(s*c2 - m). Returns the rescale factor of the running
+// sums.
+struct SoftmaxState {
+  float m;  // running max of s*c2 (log2 domain), -inf before the first valid key
+  float l;  // running sum of exp2(s*c2 - m) over this lane's half of the keys
+};
+
+__device__ __forceinline__ float softmax_tile(f32x16 (&s)[4], SoftmaxState& st, float c2) {
+  const float ninf = -__builtin_inff();
+  float mx = s[0][0];
+#pragma unroll
+  for (int sb = 0; sb < 4; ++sb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[sb][r]);
+  mx = fmaxf(mx, __shfl_xor(mx, 32));
+  const float m_new = fmaxf(st.m, mx * c2);
+  const float base = m_new == ninf ? 0.f : m_new;
+  const float corr = fast_exp2(st.m - base);
+  float sum = 0.f;
+#pragma unroll
+  for (int sb = 0; sb < 4; ++sb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float p = fast_exp2(fmaf(s[sb][r], c2, -base));
+      s[sb][r] = p;
+      sum += p;
+    }
+  st.l = st.l * corr + sum;
+  st.m = m_new;
+  return corr;
+}
+
+// Natural log-sum-exp of the scaled logits: (m + log2 l) * ln 2 (pallas_attn.py:140-141).
+__device__ __forceinline__ void write_lse(const KArgs& a, const Job& j, int row, const SoftmaxState& st, float ltot) {
+  if (a.lse_out && row < a.n) {
+    const float lse = (st.m + __builtin_amdgcn_logf(fmaxf(ltot, 1e-30f))) * LN2;
+    a.lse_out[stat_index(a, j, row)] = lse;
+  }
+}
+
+// Stores a transposed accumulator (rows d, column = this lane's row) as bf16, times `mul`.
+template <int D>
+__device__ __forceinline__ void store_acc_bf16(rsrc_t r, int row, uint32_t snb, const f32x16 (&acc)[D / 32],
+                                               float mul, int g) {
+#pragma unroll
+  for (int db = 0; db < D / 32; ++db) {
+#pragma unroll
+    for (int k4 = 0; k4 < 4; ++k4) {
+      const int d = 32 * db + 8 * k4 + 4 * g;
+      u32x2 w;
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2) {
+        const __bf16 lo = (__bf16)(acc[db][4 * k4 + 2 * h2] * mul);
+        const __bf16 hi = (__bf16)(acc[db][4 * k4 + 2 * h2 + 1] * mul);
+        w[h2] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+      }
+      __builtin_amdgcn_raw_buffer_store_b64(w, r, (int)((uint32_t)row * snb + (uint32_t)(2 * d)), 0, 0);
+    }
+  }
+}
+
+// Stores a transposed accumulator as float32, times `mul`.
+template <int D>
+__device__ __forceinline__ void store_acc_f32(rsrc_t r, int row, uint32_t snb, const f32x16 (&acc)[D / 32], float mul,
+                                              int g) {
+#pragma unroll
+  for (int db = 0; db < D / 32; ++db) {
+#pragma unroll
+    for (int k4 = 0; k4 < 4; ++k4) {
+      const int d = 32 * db + 8 * k4 + 4 * g;
+      f32x4 w;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) w[e] = acc[db][4 * k4 + e] * mul;
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, w), r,
+                                             (int)((uint32_t)row * snb + (uint32_t)(4 * d)), 0, 0);
+    }
+  }
+}
+
+}  // namespace dev
+}  // namespace fwn

@@ -1,0 +1,382 @@
+// float32 attention kernels for gfx950: forward, dQ, dK/dV (V_MFMA_F32_32X32X2_F32, full fp32
+// products and accumulation), and the delta pre-pass for both dtypes.
+//
+// fp32 MFMA operands are one element per lane, so the second contraction's A operand (V^T, K^T,
+// Q^T, dO^T) is read element-wise straight from the row-major LDS tile; no transposed copy is
+// needed. Tiles are staged through registers (256 threads, coalesced 16-byte loads).
+//
+// Reference: pallas_attn.py:112-141 (forward), 161-215 (dQ, dK/dV), 274-311 (VJP driver).
+#include "attn_device.h"
+
+namespace fwn {
+namespace {
+
+using namespace dev;
+
+// 3-bit variant for fp32 tiles: keeps 32-column blocks of a row inside one aligned 128 bytes.
+__device__ __forceinline__ int swz_row3(int row) { return (row & 3) | (((row >> 3) & 1) << 2); }
+
+// ------------------------------------------------------------------------------------------
+// fp32 staging: linear chunk mapping (coalesced), row-major tiles in LDS, optionally swizzled.
+
+template <int D>
+__device__ __forceinline__ void stage_rows_f32(char* lds, rsrc_t r, int row0, uint32_t snb, int tid, bool swizzle) {
+  constexpr int C = D / 4;
+  constexpr int PER = BLK * C / NT;
+#pragma unroll
+  for (int it = 0; it < PER; ++it) {
+    const int id = tid + it * NT;
+    const int row = id / C, ch = id % C;
+    const u32x4 x = bload16(r, (uint32_t)(row0 + row) * snb + (uint32_t)(16 * ch));
+    const int pc = swizzle ? (ch ^ swz_row3(row)) : ch;
+    *(u32x4*)(lds + row * (D * 4) + (pc << 4)) = x;
+  }
+}
+
+// Per-lane LDS offsets of the fp32 MFMA A operands.
+//   row[u & 3]: sigma row of this lane, chunk 2*u + g of a swizzled tile;
+//               + 128 * (u / 4) + sb * 32 * 4D.
+//   el[r & 3]:  element (row element_col(sb, r, g), column 32*db + i) of a swizzled tile;
+//               + (32*sb + 16*(r/8) + r%8) * 4D + 128 * db.
+//   el_plain:   the same element of an unswizzled tile.
+template <int D>
+struct F32Offsets {
+  uint32_t row[4];
+  uint32_t el[4];
+  uint32_t el_plain;
+
+  __device__ __forceinline__ void init(int i, int g) {
+    const int rho = sigma(i);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      row[k] = rho * (D * 4) + ((((2 * k + g) & 7) ^ swz_row3(rho)) << 4);
+      el[k] = 8 * g * (D * 4) + ((((i >> 2) ^ (k | (g << 2)))) << 4) + ((i & 3) << 2);
+    }
+    el_plain = 8 * g * (D * 4) + 4 * i;
+  }
+  __device__ __forceinline__ static uint32_t row_imm(int sb, int u) { return sb * 32 * (D * 4) + 128 * (u >> 2); }
+  __device__ __forceinline__ static uint32_t el_imm(int sb, int r, int db) {
+    return (32 * sb + 16 * (r >> 3) + (r & 7)) * (D * 4) + 128 * db;
+  }
+};
+
+// fp32 fragment: f[u] = columns 8*u + 4*g .. +3 of `row` (MFMA step 4*u + e uses f[u][e]).
+template <int D>
+__device__ __forceinline__ void load_frag_f32(f32x4 (&f)[D / 8], rsrc_t r, int row, uint32_t snb, int g) {
+#pragma unroll
+  for (int u = 0; u < D / 8; ++u)
+    f[u] = __builtin_bit_cast(f32x4, bload16(r, (uint32_t)row * snb + (uint32_t)(32 * u + 16 * g)));
+}
+
+// ------------------------------------------------------------------------------------------
+// Forward, fp32. 128 KB of LDS: one workgroup per CU.
+
+template <int D>
+__global__ void __launch_bounds__(NT, 1) fwd_f32_kernel(KArgs a) {
+  __shared__ __attribute__((aligned(16))) char smem[2 * BLK * D * 4];
+  char* ldsK = smem;                // [128][D] swizzled
+  char* ldsV = smem + BLK * D * 4;  // [128][D] plain
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int i = lane & 31, g = lane >> 5;
+  const Job j = decode_job(a);
+  const uint32_t snb = (uint32_t)a.sn * 4;
+  const rsrc_t rQ = make_rsrc((const float*)a.q + j.base, a.slice_bytes);
+  const rsrc_t rK = make_rsrc((const float*)a.k + j.base, a.slice_bytes);
+  const rsrc_t rV = make_rsrc((const float*)a.v + j.base, a.slice_bytes);
+
+  const int qrow = j.blk * BLK + 32 * w + i;
+  f32x4 qf[D / 8];
+  load_frag_f32<D>(qf, rQ, qrow, snb, g);
+  wait_vmem();
+  F32Offsets<D> off;
+  off.init(i, g);
+  f32x16 o[D / 32];
+#pragma unroll
+  for (int db = 0; db < D / 32; ++db) o[db] = zero16();
+  SoftmaxState st{-__builtin_inff(), 0.f};
+
+  int t0, t1;
+  tile_range(a, j.blk, t0, t1);
+  for (int tt = t0; tt < t1; ++tt) {
+    const int t = __builtin_amdgcn_readfirstlane(tt);
+    const int kb = ((ci32_ptr)a.col)[t];
+    __syncthreads();
+    stage_rows_f32<D>(ldsK, rK, kb * BLK, snb, tid, true);
+    stage_rows_f32<D>(ldsV, rV, kb * BLK, snb, tid, false);
+    __syncthreads();
+    const cu64_ptr mk = (cu64_ptr)a.lanes + ((int64_t)t * 4 + w) * 64;
+    f32x16 s[4];
+#pragma unroll
+    for (int sb = 0; sb < 4; ++sb) {
+      SubMask m;
+      m.load(mk, sb);
+      s[sb] = zero16();
+#pragma unroll
+      for (int u = 0; u < D / 8; ++u) {
+        const f32x4 kx = *(const f32x4*)(ldsK + off.row[u & 3] + off.row_imm(sb, u));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) s[sb] = mfma_f32(kx[e], qf[u][e], s[sb]);
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[sb][r] = select_lane(m.w[r], s[sb][r], -__builtin_inff());
+    }
+    const float corr = softmax_tile(s, st, a.c2);
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db) o[db] *= corr;
+#pragma unroll
+    for (int sb = 0; sb < 4; ++sb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+#pragma unroll
+        for (int db = 0; db < D / 32; ++db)
+          o[db] = mfma_f32(*(const float*)(ldsV + off.el_plain + off.el_imm(sb, r, db)), s[sb][r], o[db]);
+      }
+  }
+  const float ltot = st.l + __shfl_xor(st.l, 32);
+  const float inv = ltot > 0.f ? 1.f / ltot : 0.f;
+  store_acc_f32<D>(make_rsrc((float*)a.out0 + j.base, a.slice_bytes), qrow, snb, o, inv, g);
+  if (g == 0) write_lse(a, j, qrow, st, ltot);
+}
+
+// dQ, fp32.
+
+template <int D>
+__global__ void __launch_bounds__(NT, 1) dq_f32_kernel(KArgs a) {
+  __shared__ __attribute__((aligned(16))) char smem[2 * BLK * D * 4];
+  char* ldsK = smem;
+  char* ldsV = smem + BLK * D * 4;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int i = lane & 31, g = lane >> 5;
+  const Job j = decode_job(a);
+  const uint32_t snb = (uint32_t)a.sn * 4;
+  const rsrc_t rK = make_rsrc((const float*)a.k + j.base, a.slice_bytes);
+  const rsrc_t rV = make_rsrc((const float*)a.v + j.base, a.slice_bytes);
+
+  const int qrow = j.blk * BLK + 32 * w + i;
+  f32x4 qf[D / 8], df[D / 8];
+  load_frag_f32<D>(qf, make_rsrc((const float*)a.q + j.base, a.slice_bytes), qrow, snb, g);
+  load_frag_f32<D>(df, make_rsrc((const float*)a.dout + j.base, a.slice_bytes), qrow, snb, g);
+  float lse_t = 0.f, delta = 0.f;
+  if (qrow < a.n) {
+    lse_t = a.lse[stat_index(a, j, qrow)] * LOG2E;
+    delta = a.delta[stat_index(a, j, qrow)];
+  }
+  wait_vmem();
+  F32Offsets<D> off;
+  off.init(i, g);
+  f32x16 acc[D / 32];
+#pragma unroll
+  for (int db = 0; db < D / 32; ++db) acc[db] = zero16();
+
+  int t0, t1;
+  tile_range(a, j.blk, t0, t1);
+  for (int tt = t0; tt < t1; ++tt) {
+    const int t = __builtin_amdgcn_readfirstlane(tt);
+    const int kb = ((ci32_ptr)a.col)[t];
+    __syncthreads();
+    stage_rows_f32<D>(ldsK, rK, kb * BLK, snb, tid, true);
+    stage_rows_f32<D>(ldsV, rV, kb * BLK, snb, tid, true);
+    __syncthreads();
+    const cu64_ptr mk = (cu64_ptr)a.lanes + ((int64_t)t * 4 + w) * 64;
+#pragma unroll
+    for (int sb = 0; sb < 4; ++sb) {
+      SubMask m;
+      m.load(mk, sb);
+      f32x16 s = zero16(), dp = zero16();
+#pragma unroll
+      for (int u = 0; u < D / 8; ++u) {
+        const f32x4 kx = *(const f32x4*)(ldsK + off.row[u & 3] + off.row_imm(sb, u));
+        const f32x4 vx = *(const f32x4*)(ldsV + off.row[u & 3] + off.row_imm(sb, u));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          s = mfma_f32(kx[e], qf[u][e], s);
+          dp = mfma_f32(vx[e], df[u][e], dp);
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float p = fast_exp2(fmaf(s[r], a.c2, -lse_t));
+        p = select_lane(m.w[r], p, 0.f);
+        dp[r] = p * (dp[r] - delta);
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+#pragma unroll
+        for (int db = 0; db < D / 32; ++db)
+          acc[db] = mfma_f32(*(const float*)(ldsK + off.el[r & 3] + off.el_imm(sb, r, db)), dp[r], acc[db]);
+      }
+    }
+  }
+  store_acc_f32<D>(make_rsrc((float*)a.out0 + j.base, a.slice_bytes), qrow, snb, acc, a.scale, g);
+}
+
+// dK/dV, fp32.
+
+template <int D>
+__global__ void __launch_bounds__(NT, 1) dkv_f32_kernel(KArgs a) {
+  __shared__ __attribute__((aligned(16))) char smem[2 * BLK * D * 4 + 2 * BLK * 4];
+  char* ldsQ = smem;                // [128][D] swizzled
+  char* ldsO = smem + BLK * D * 4;  // dO [128][D] swizzled
+  float* ldsL = (float*)(smem + 2 * BLK * D * 4);
+  float* ldsDl = ldsL + BLK;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int i = lane & 31, g = lane >> 5;
+  const Job j = decode_job(a);
+  const uint32_t snb = (uint32_t)a.sn * 4;
+  const rsrc_t rQ = make_rsrc((const float*)a.q + j.base, a.slice_bytes);
+  const rsrc_t rO = make_rsrc((const float*)a.dout + j.base, a.slice_bytes);
+  const float* lse = a.lse + stat_index(a, j, 0);
+  const float* dl = a.delta + stat_index(a, j, 0);
+
+  const int krow = j.blk * BLK + 32 * w + i;
+  f32x4 kf[D / 8], vf[D / 8];
+  load_frag_f32<D>(kf, make_rsrc((const float*)a.k + j.base, a.slice_bytes), krow, snb, g);
+  load_frag_f32<D>(vf, make_rsrc((const float*)a.v + j.base, a.slice_bytes), krow, snb, g);
+  wait_vmem();
+  F32Offsets<D> off;
+  off.init(i, g);
+  f32x16 dk[D / 32], dv[D / 32];
+#pragma unroll
+  for (int db = 0; db < D / 32; ++db) {
+    dk[db] = zero16();
+    dv[db] = zero16();
+  }
+
+  int t0, t1;
+  tile_range(a, j.blk, t0, t1);
+  for (int tt = t0; tt < t1; ++tt) {
+    const int t = __builtin_amdgcn_readfirstlane(tt);
+    const int qb = ((ci32_ptr)a.col)[t];
+    __syncthreads();
+    stage_rows_f32<D>(ldsQ, rQ, qb * BLK, snb, tid, true);
+    stage_rows_f32<D>(ldsO, rO, qb * BLK, snb, tid, true);
+    {
+      const int row = qb * BLK + (tid & (BLK - 1));
+      float stat = 0.f;
+      if (row < a.n) stat = tid < BLK ? lse[row] * LOG2E : dl[row];
+      (tid < BLK ? ldsL : ldsDl)[tid & (BLK - 1)] = stat;
+    }
+    __syncthreads();
+    const cu64_ptr mk = (cu64_ptr)a.lanes + ((int64_t)t * 4 + w) * 64;
+#pragma unroll
+    for (int sb = 0; sb < 4; ++sb) {
+      SubMask m;
+      m.load(mk, sb);
+      f32x16 s = zero16(), dp = zero16();
+#pragma unroll
+      for (int u = 0; u < D / 8; ++u) {
+        const f32x4 qx = *(const f32x4*)(ldsQ + off.row[u & 3] + off.row_imm(sb, u));
+        const f32x4 ox = *(const f32x4*)(ldsO + off.row[u & 3] + off.row_imm(sb, u));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          s = mfma_f32(qx[e], kf[u][e], s);
+          dp = mfma_f32(ox[e], vf[u][e], dp);
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int qq = element_col(sb, r, g);
+        float p = fast_exp2(fmaf(s[r], a.c2, -ldsL[qq]));
+        p = select_lane(m.w[r], p, 0.f);
+        s[r] = p;
+        dp[r] = p * (dp[r] - ldsDl[qq]);
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+#pragma unroll
+        for (int db = 0; db < D / 32; ++db) {
+          dv[db] = mfma_f32(*(const float*)(ldsO + off.el[r & 3] + off.el_imm(sb, r, db)), s[r], dv[db]);
+          dk[db] = mfma_f32(*(const float*)(ldsQ + off.el[r & 3] + off.el_imm(sb, r, db)), dp[r], dk[db]);
+        }
+      }
+    }
+  }
+  store_acc_f32<D>(make_rsrc((float*)a.out0 + j.base, a.slice_bytes), krow, snb, dk, a.scale, g);
+  store_acc_f32<D>(make_rsrc((float*)a.out1 + j.base, a.slice_bytes), krow, snb, dv, 1.f, g);
+}
+
+// ------------------------------------------------------------------------------------------
+// delta = rowsum(o * dout) (pallas_attn.py:278): L lanes per (batch, head, row), 16 B per lane.
+
+template <typename T, int D>
+__global__ void __launch_bounds__(NT) delta_kernel(KArgs a) {
+  constexpr int EPC = 16 / (int)sizeof(T);
+  constexpr int L = D / EPC;
+  const int64_t gid = (int64_t)blockIdx.x * NT + threadIdx.x;
+  const int64_t item = gid / L;
+  const int part = (int)(gid % L);
+  const int64_t total = (int64_t)a.batch * a.heads * a.n;
+  float sum = 0.f;
+  if (item < total) {
+    const int row = (int)(item % a.n);
+    const int64_t bh = item / a.n;
+    const int h = (int)(bh % a.heads), b = (int)(bh / a.heads);
+    const int64_t off = (int64_t)b * a.sb + (int64_t)h * a.sh + (int64_t)row * a.sn + part * EPC;
+    const u32x4 x = *(const u32x4*)((const T*)a.o + off);
+    const u32x4 y = *(const u32x4*)((const T*)a.dout + off);
+    if constexpr (sizeof(T) == 4) {
+      const f32x4 fx = __builtin_bit_cast(f32x4, x), fy = __builtin_bit_cast(f32x4, y);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sum += fx[e] * fy[e];
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        sum += __uint_as_float(x[e] << 16) * __uint_as_float(y[e] << 16);
+        sum += __uint_as_float(x[e] & 0xffff0000u) * __uint_as_float(y[e] & 0xffff0000u);
+      }
+    }
+  }
+#pragma unroll
+  for (int o = L / 2; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
+  if (item < total && part == 0) a.lse_out[item] = sum;
+}
+
+template <int D>
+hipError_t launch_d(Kind kind, const KArgs& a, hipStream_t stream) {
+  const dim3 block(NT);
+  if (kind == Kind::kDelta) {
+    const int64_t lanes = (int64_t)a.batch * a.heads * a.n * (D / 4);
+    hipLaunchKernelGGL((delta_kernel<float, D>), dim3((unsigned)((lanes + NT - 1) / NT)), block, 0, stream, a);
+    return hipGetLastError();
+  }
+  const dim3 grid((unsigned)a.n_blocks * (unsigned)(a.batch * a.heads));
+  switch (kind) {
+    case Kind::kFwd: hipLaunchKernelGGL(fwd_f32_kernel<D>, grid, block, 0, stream, a); break;
+    case Kind::kDq: hipLaunchKernelGGL(dq_f32_kernel<D>, grid, block, 0, stream, a); break;
+    case Kind::kDkv: hipLaunchKernelGGL(dkv_f32_kernel<D>, grid, block, 0, stream, a); break;
+    default: break;
+  }
+  return hipGetLastError();
+}
+
+template <int D>
+hipError_t launch_delta_bf16_d(const KArgs& a, hipStream_t stream) {
+  const int64_t lanes = (int64_t)a.batch * a.heads * a.n * (D / 8);
+  hipLaunchKernelGGL((delta_kernel<uint16_t, D>), dim3((unsigned)((lanes + NT - 1) / NT)), dim3(NT), 0, stream, a);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_f32(Kind kind, int head_dim, const KArgs& a, hipStream_t stream) {
+  switch (head_dim) {
+    case 32: return launch_d<32>(kind, a, stream);
+    case 64: return launch_d<64>(kind, a, stream);
+    case 128: return launch_d<128>(kind, a, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_delta_bf16(int head_dim, const KArgs& a, hipStream_t stream) {
+  switch (head_dim) {
+    case 32: return launch_delta_bf16_d<32>(a, stream);
+    case 64: return launch_delta_bf16_d<64>(a, stream);
+    case 128: return launch_delta_bf16_d<128>(a, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace fwn

@@ -31,7 +31,16 @@ struct KArgs {
 
 enum class Kind { kFwd, kDq, kDkv, kDelta };
 
-// Enqueues one kernel; returns hipSuccess or the launch error. dtype: 0 f32, 1 bf16.
-hipError_t launch(Kind kind, int dtype, int head_dim, const KArgs& a, hipStream_t stream);
+// Kernel launchers (each enqueues one kernel and returns hipSuccess or the launch error).
+hipError_t launch_bf16(Kind kind, int head_dim, const KArgs& a, hipStream_t stream);  // attn_bf16.hip
+hipError_t launch_f32(Kind kind, int head_dim, const KArgs& a, hipStream_t stream);   // attn_f32.hip
+hipError_t launch_delta_bf16(int head_dim, const KArgs& a, hipStream_t stream);      // attn_f32.hip
+
+// Dispatch on dtype (0 f32, 1 bf16).
+inline hipError_t launch(Kind kind, int dtype, int head_dim, const KArgs& a, hipStream_t stream) {
+  if (dtype == 0) return launch_f32(kind, head_dim, a, stream);
+  if (kind == Kind::kDelta) return launch_delta_bf16(head_dim, a, stream);
+  return launch_bf16(kind, head_dim, a, stream);
+}
 
 }  // namespace fwn
