@@ -48,7 +48,53 @@ def parse():
   p.add_argument("--workload", default="c3", choices=sorted(WORKLOADS))
   p.add_argument("--cpu-seconds", type=float, default=12.0, help="bounded CPU-baseline sample length")
   p.add_argument("--no-cpu", action="store_true")
+  p.add_argument("--copy-mib", type=int, default=0,
+                 help="instead of the attention step, time a plain device-to-device copy of this many MiB "
+                      "(the known-size kernel that scales the FETCH_SIZE / WRITE_SIZE counters)")
   return p.parse_args()
+
+
+TRAFFIC_DIR = os.path.join(ROOT, "profiles")
+
+
+def measured_traffic(workload, kernel):
+  """HBM bytes per launch of `kernel` on `workload` from the committed PMC summary, if there is one.
+
+  The summary (profiles/hbm_traffic_<kernel>_<workload>.txt) holds a line
+  `traffic_bytes_per_launch <N>`: FETCH_SIZE + WRITE_SIZE per dispatch, each scaled by what the same
+  counter reads for a copy of known size.
+  """
+  path = os.path.join(TRAFFIC_DIR, f"hbm_traffic_{kernel}_{workload}.txt")
+  if not os.path.exists(path):
+    return None, None
+  with open(path) as f:
+    for line in f:
+      parts = line.split()
+      if len(parts) == 2 and parts[0] == "traffic_bytes_per_launch":
+        return int(float(parts[1])), os.path.relpath(path, ROOT)
+  return None, None
+
+
+def copy_calibration(mib, steps, warmup):
+  """Times `steps` device-to-device copies of `mib` MiB (one blit kernel each) and prints one JSON line."""
+  import torch
+  dev = torch.device("cuda:0")
+  nbytes = mib << 20
+  src = torch.ones(nbytes // 4, dtype=torch.float32, device=dev)
+  dst = torch.empty_like(src)
+  for _ in range(warmup):
+    dst.copy_(src)
+  torch.cuda.synchronize()
+  start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+  start.record()
+  for _ in range(steps):
+    dst.copy_(src)
+  stop.record()
+  torch.cuda.synchronize()
+  ms = start.elapsed_time(stop) / steps
+  print(json.dumps({"copy_bytes_read": nbytes, "copy_bytes_written": nbytes, "steps": steps, "ms_per_copy": round(ms, 4),
+                    "GB_per_s": round(2 * nbytes / (ms * 1e-3) / 1e9, 1)}), flush=True)
+  return 0
 
 
 def cpu_baseline(cfg, q, k, v, do, mask, tiles, scale, budget_s):
@@ -87,6 +133,8 @@ def main():
     print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}); the attention "
           "path has no multi-GPU implementation in this build.", file=sys.stderr)
     return 2
+  if args.copy_mib:
+    return copy_calibration(args.copy_mib, args.steps, args.warmup)
   import numpy as np
   import torch
 
@@ -110,9 +158,13 @@ def main():
     mask = mask[perm][:, perm]
   T = tiles.n_tiles
 
-  rng = np.random.default_rng(0)
-  host = [(cfg["sigma"] * rng.standard_normal((B, n, H, D))).astype(np.float32) for _ in range(3)]
-  host.append(rng.standard_normal((B, n, H, D)).astype(np.float32))
+  # Member m draws q, k, v (N(0, sigma)) then dO (N(0, 1)) from PCG64 seed m.
+  members = []
+  for m in range(B):
+    rng = np.random.default_rng(m)
+    xs = [(cfg["sigma"] * rng.standard_normal((n, H, D))).astype(np.float32) for _ in range(3)]
+    members.append(xs + [rng.standard_normal((n, H, D)).astype(np.float32)])
+  host = [np.stack([mem[i] for mem in members]) for i in range(4)]
   q, k, v, do = (torch.from_numpy(x).to(dev).to(dtype) for x in host)
   scale = D ** -0.5
   desc = nat.AttnDesc(B, n, H, D, nat.BF16 if dtype == torch.bfloat16 else nat.F32, scale, *q.stride()[:3])
@@ -171,19 +223,21 @@ def main():
   dominant = max((k_ for k_ in per_kernel if algo.get(k_)), key=lambda k_: per_kernel[k_])
   achieved = algo[dominant] / (per_kernel[dominant] * 1e-3) / 1e12
   peak = PEAK[cfg["dtype"]]
+  traffic, traffic_src = measured_traffic(args.workload, dominant)
 
   result = {
       "metric": METRIC, "value": round(value, 3), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
       "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak",
       "vs_baseline": None, "dtype": cfg["dtype"],
-      "data": "synthetic: seeded N(0, sigma) q/k/v and N(0,1) dO (numpy PCG64 seed 0) on a generated "
+      "data": "synthetic: N(0, sigma) q/k/v and N(0,1) dO, member m from numpy PCG64 seed m, on a generated "
               "icosahedral mesh; no weights or datasets",
       "config": {"workload": cfg["desc"], "mesh_refinement": 6, "n": n, "k_hop": cfg["k_hop"], "batch": B,
                  "heads": H, "head_dim": D, "order": "hilbert" if cfg["reorder"] else "subdivision",
                  "sigma": cfg["sigma"], "live_tiles": T, "tile_density": round(tiles.density, 4),
                  "valid_entries": int(mask.nnz)},
       "roofline": {"bound": "mfma", "kernel": dominant, "achieved": round(achieved, 3), "peak": peak,
-                   "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": None},
+                   "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": traffic,
+                   "traffic_source": traffic_src},
       "kernels_ms": {k_: round(v_, 4) for k_, v_ in per_kernel.items()},
       "valid_entry_tflops": round(value * mask.nnz / (T * 128 * 128), 3),
       "mask_build_s": round(t_mask, 3), "tile_prepare_s": round(t_tiles, 3),

@@ -11,8 +11,10 @@
 //     addresses 4 consecutive columns d0+4q.. of row k0+e, and lane j receives column d0+j of rows
 //     k0..k0+3, i.e. four consecutive keys of its own column, which is the key-contiguous operand
 //     the MFMA needs. Two such reads form the 8-element operand.
-// The swizzle keeps the row reads (8 lanes of distinct rows per 128 bytes) and the transpose
-// reads (4 consecutive rows x 32 bytes per 16 lanes) free of bank conflicts.
+// gfx950's LDS has 64 banks of 4 bytes, so a b128 read is served 16 lanes (256 bytes) and a b64
+// read 32 lanes (256 bytes) at a time. The swizzle keeps both access patterns conflict-free: the 16
+// lanes of a row read hit 16 distinct rows at one logical chunk, and the 32 lanes of a transpose
+// read hit 4 consecutive rows x 4 consecutive chunks.
 //
 // Reference: pallas_attn.py:112-141 (forward), 161-215 (dQ, dK/dV), 274-311 (VJP driver).
 #include "attn_device.h"
@@ -23,15 +25,17 @@ namespace {
 using namespace dev;
 
 // XOR swizzle of the 16-byte chunk index of a bf16 row-major tile with C chunks per row; depends
-// on the row's low 4 bits only.
+// on the row's low 4 bits only. Over the 16 rows of a row read it is a bijection within each set of
+// rows that share a 256-byte bank line (row reads), and it sends the aligned 4-chunk group of each
+// of 4 consecutive rows to a distinct part of the bank line (transpose reads).
 template <int C>
 __device__ __forceinline__ int swz(int row) {
   if constexpr (C >= 16) {
-    return ((row & 3) << 1) | ((row >> 3) & 1) | (((row >> 2) & 1) << 3);
+    return ((row & 3) << 2) | ((row >> 2) & 3);
   } else if constexpr (C == 8) {
-    return ((row & 3) << 1) | ((row >> 3) & 1);
+    return (((row >> 1) & 1) << 2) | ((row >> 2) & 3);
   } else {
-    return (((row >> 1) & 1) << 1) | ((row >> 3) & 1);
+    return (row >> 2) & 3;
   }
 }
 
