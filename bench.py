@@ -176,21 +176,24 @@ def main():
   stream = torch.cuda.current_stream(dev)
   sp = stream.cuda_stream
   ts = tiles.struct
+  ws = fwn.hip_attn.workspace(desc, dev, tiles)
+  wsp, wsn = (ws.data_ptr(), ws.numel()) if ws is not None else (None, 0)
 
   def fwd():
     nat.check(L.fwn_attn_fwd_launch(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), ts, out.data_ptr(),
-                                    lse.data_ptr(), sp))
+                                    lse.data_ptr(), wsp, wsn, sp))
 
   def bwd_delta():
     nat.check(L.fwn_attn_bwd_delta_launch(desc, out.data_ptr(), do.data_ptr(), delta.data_ptr(), sp))
 
   def bwd_dq():
     nat.check(L.fwn_attn_bwd_dq_launch(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(),
-                                       lse.data_ptr(), delta.data_ptr(), ts, dq.data_ptr(), sp))
+                                       lse.data_ptr(), delta.data_ptr(), ts, dq.data_ptr(), wsp, wsn, sp))
 
   def bwd_dkv():
     nat.check(L.fwn_attn_bwd_dkv_launch(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(),
-                                        lse.data_ptr(), delta.data_ptr(), ts, dk.data_ptr(), dv.data_ptr(), sp))
+                                        lse.data_ptr(), delta.data_ptr(), ts, dk.data_ptr(), dv.data_ptr(), wsp,
+                                        wsn, sp))
 
   kernels = [("fwd", fwd)] + ([("delta", bwd_delta), ("dq", bwd_dq), ("dkv", bwd_dkv)] if cfg["backward"] else [])
   for _ in range(args.warmup):

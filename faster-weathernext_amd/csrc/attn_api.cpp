@@ -87,6 +87,29 @@ int check_tiles(const fwn_attn_desc* d, const fwn_tiles* t, const char* name) {
     return fail(FWN_ERR_TILES, "%s has %d row blocks, expected %d for n = %d", name, t->n_blocks, n_blocks, d->n);
   if (t->n_tiles < 0 || !t->ptr || (t->n_tiles > 0 && (!t->col || !t->lanes || !t->full)))
     return fail(FWN_ERR_TILES, "%s: missing device arrays", name);
+  if (t->n_items < n_blocks || !t->items)
+    return fail(FWN_ERR_TILES, "%s: %d work items for %d blocks (every block needs at least one)", name, t->n_items,
+                n_blocks);
+  if (t->n_parts < 0 || t->n_split < 0 || (t->n_split > 0 && !t->split) || (t->n_split > 0) != (t->n_parts > 0))
+    return fail(FWN_ERR_TILES, "%s: inconsistent split schedule (%d parts, %d split blocks)", name, t->n_parts,
+                t->n_split);
+  if ((int64_t)t->n_items * d->batch * d->heads > INT32_MAX || (int64_t)t->n_split * d->batch * d->heads > INT32_MAX)
+    return fail(FWN_ERR_INVALID_ARG, "%s: grid too large", name);
+  return FWN_OK;
+}
+
+uint64_t workspace_bytes_for(const fwn_attn_desc* d, const fwn_tiles* t) {
+  return (uint64_t)t->n_parts * (uint64_t)d->batch * (uint64_t)d->heads * (uint64_t)slot_words(d->head_dim) * 4u;
+}
+
+int check_workspace(const fwn_attn_desc* d, const fwn_tiles* t, const void* ws, uint64_t ws_bytes) {
+  const uint64_t need = workspace_bytes_for(d, t);
+  if (need == 0) return FWN_OK;
+  if (!ws) return fail(FWN_ERR_INVALID_ARG, "workspace is null but %llu bytes are needed", (unsigned long long)need);
+  if (((uintptr_t)ws & 255u) != 0) return fail(FWN_ERR_INVALID_ARG, "workspace is not 256-byte aligned");
+  if (ws_bytes < need)
+    return fail(FWN_ERR_INVALID_ARG, "workspace holds %llu bytes, %llu needed", (unsigned long long)ws_bytes,
+                (unsigned long long)need);
   return FWN_OK;
 }
 
@@ -105,13 +128,30 @@ KArgs base_args(const fwn_attn_desc* d) {
   return a;
 }
 
-void set_tiles(KArgs& a, const fwn_tiles* t) {
+void set_tiles(KArgs& a, const fwn_tiles* t, void* ws) {
   a.ptr = t->ptr;
   a.col = t->col;
   a.lanes = t->lanes;
   a.full = t->full;
-  a.order = t->order;
+  a.items = (const int32_t*)t->items;
+  a.split = t->split;
   a.n_tiles = t->n_tiles;
+  a.n_items = t->n_items;
+  a.n_parts = t->n_parts;
+  a.n_split = t->n_split;
+  a.work = (float*)ws;
+}
+
+// The main kernel, then (when the list has split blocks) the combine pass, in stream order.
+int launch_with_combine(Kind kind, Kind combine, const fwn_attn_desc* d, const KArgs& a, hipStream_t stream,
+                        const char* what) {
+  if (hipError_t e = launch(kind, d->dtype, d->head_dim, a, stream); e != hipSuccess)
+    return fail(FWN_ERR_HIP, "%s launch: %s", what, hipGetErrorString(e));
+  if (a.n_split > 0) {
+    if (hipError_t e = launch(combine, d->dtype, d->head_dim, a, stream); e != hipSuccess)
+      return fail(FWN_ERR_HIP, "%s combine launch: %s", what, hipGetErrorString(e));
+  }
+  return FWN_OK;
 }
 
 int hip_status(hipError_t e, const char* what) {
@@ -128,8 +168,18 @@ extern "C" {
 
 const char* fwn_last_error(void) { return fwn::g_error; }
 
+int fwn_attn_workspace_size(const fwn_attn_desc* desc, const fwn_tiles* tiles, uint64_t* bytes) {
+  clear_error();
+  if (int rc = check_desc(desc)) return rc;
+  if (int rc = check_tiles(desc, tiles, "tiles")) return rc;
+  if (!bytes) return fail(FWN_ERR_INVALID_ARG, "bytes is null");
+  *bytes = workspace_bytes_for(desc, tiles);
+  return FWN_OK;
+}
+
 int fwn_attn_fwd_launch(const fwn_attn_desc* desc, const void* q, const void* k, const void* v,
-                        const fwn_tiles* tiles, void* o, float* lse, void* stream) {
+                        const fwn_tiles* tiles, void* o, float* lse, void* workspace, uint64_t workspace_bytes,
+                        void* stream) {
   clear_error();
   if (int rc = check_desc(desc)) return rc;
   if (int rc = check_tensor(q, "q")) return rc;
@@ -137,14 +187,15 @@ int fwn_attn_fwd_launch(const fwn_attn_desc* desc, const void* q, const void* k,
   if (int rc = check_tensor(v, "v")) return rc;
   if (int rc = check_tensor(o, "o")) return rc;
   if (int rc = check_tiles(desc, tiles, "tiles")) return rc;
+  if (int rc = check_workspace(desc, tiles, workspace, workspace_bytes)) return rc;
   KArgs a = base_args(desc);
   a.q = q;
   a.k = k;
   a.v = v;
   a.out0 = o;
   a.lse_out = lse;
-  set_tiles(a, tiles);
-  return hip_status(launch(Kind::kFwd, desc->dtype, desc->head_dim, a, (hipStream_t)stream), "forward launch");
+  set_tiles(a, tiles, workspace);
+  return launch_with_combine(Kind::kFwd, Kind::kFwdCombine, desc, a, (hipStream_t)stream, "forward");
 }
 
 int fwn_attn_bwd_delta_launch(const fwn_attn_desc* desc, const void* o, const void* dout, float* delta,
@@ -163,7 +214,7 @@ int fwn_attn_bwd_delta_launch(const fwn_attn_desc* desc, const void* o, const vo
 
 int fwn_attn_bwd_dq_launch(const fwn_attn_desc* desc, const void* q, const void* k, const void* v,
                            const void* dout, const float* lse, const float* delta, const fwn_tiles* tiles,
-                           void* dq, void* stream) {
+                           void* dq, void* workspace, uint64_t workspace_bytes, void* stream) {
   clear_error();
   if (int rc = check_desc(desc)) return rc;
   if (int rc = check_tensor(q, "q")) return rc;
@@ -173,6 +224,7 @@ int fwn_attn_bwd_dq_launch(const fwn_attn_desc* desc, const void* q, const void*
   if (int rc = check_tensor(dq, "dq")) return rc;
   if (!lse || !delta) return fail(FWN_ERR_INVALID_ARG, "lse and delta are required");
   if (int rc = check_tiles(desc, tiles, "tiles")) return rc;
+  if (int rc = check_workspace(desc, tiles, workspace, workspace_bytes)) return rc;
   KArgs a = base_args(desc);
   a.q = q;
   a.k = k;
@@ -181,13 +233,13 @@ int fwn_attn_bwd_dq_launch(const fwn_attn_desc* desc, const void* q, const void*
   a.lse = lse;
   a.delta = delta;
   a.out0 = dq;
-  set_tiles(a, tiles);
-  return hip_status(launch(Kind::kDq, desc->dtype, desc->head_dim, a, (hipStream_t)stream), "dq launch");
+  set_tiles(a, tiles, workspace);
+  return launch_with_combine(Kind::kDq, Kind::kDqCombine, desc, a, (hipStream_t)stream, "dq");
 }
 
 int fwn_attn_bwd_dkv_launch(const fwn_attn_desc* desc, const void* q, const void* k, const void* v,
                             const void* dout, const float* lse, const float* delta, const fwn_tiles* tiles_t,
-                            void* dk, void* dv, void* stream) {
+                            void* dk, void* dv, void* workspace, uint64_t workspace_bytes, void* stream) {
   clear_error();
   if (int rc = check_desc(desc)) return rc;
   if (int rc = check_tensor(q, "q")) return rc;
@@ -198,6 +250,7 @@ int fwn_attn_bwd_dkv_launch(const fwn_attn_desc* desc, const void* q, const void
   if (int rc = check_tensor(dv, "dv")) return rc;
   if (!lse || !delta) return fail(FWN_ERR_INVALID_ARG, "lse and delta are required");
   if (int rc = check_tiles(desc, tiles_t, "tiles_t")) return rc;
+  if (int rc = check_workspace(desc, tiles_t, workspace, workspace_bytes)) return rc;
   KArgs a = base_args(desc);
   a.q = q;
   a.k = k;
@@ -207,16 +260,19 @@ int fwn_attn_bwd_dkv_launch(const fwn_attn_desc* desc, const void* q, const void
   a.delta = delta;
   a.out0 = dk;
   a.out1 = dv;
-  set_tiles(a, tiles_t);
-  return hip_status(launch(Kind::kDkv, desc->dtype, desc->head_dim, a, (hipStream_t)stream), "dkv launch");
+  set_tiles(a, tiles_t, workspace);
+  return launch_with_combine(Kind::kDkv, Kind::kDkvCombine, desc, a, (hipStream_t)stream, "dkv");
 }
 
 int fwn_attn_bwd_launch(const fwn_attn_desc* desc, const void* q, const void* k, const void* v, const void* o,
                         const void* dout, const float* lse, float* delta, const fwn_tiles* tiles,
-                        const fwn_tiles* tiles_t, void* dq, void* dk, void* dv, void* stream) {
+                        const fwn_tiles* tiles_t, void* dq, void* dk, void* dv, void* workspace,
+                        uint64_t workspace_bytes, void* stream) {
   if (int rc = fwn_attn_bwd_delta_launch(desc, o, dout, delta, stream)) return rc;
-  if (int rc = fwn_attn_bwd_dq_launch(desc, q, k, v, dout, lse, delta, tiles, dq, stream)) return rc;
-  return fwn_attn_bwd_dkv_launch(desc, q, k, v, dout, lse, delta, tiles_t ? tiles_t : tiles, dk, dv, stream);
+  if (int rc = fwn_attn_bwd_dq_launch(desc, q, k, v, dout, lse, delta, tiles, dq, workspace, workspace_bytes, stream))
+    return rc;
+  return fwn_attn_bwd_dkv_launch(desc, q, k, v, dout, lse, delta, tiles_t ? tiles_t : tiles, dk, dv, workspace,
+                                 workspace_bytes, stream);
 }
 
 }  // extern "C"

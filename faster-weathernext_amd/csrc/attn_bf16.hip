@@ -3,9 +3,9 @@
 //
 // Tiles live in LDS only row-major ([128 rows][D], 16-byte chunks XOR-swizzled) and are copied
 // there by the buffer unit (buffer_load ... lds: each wave-wide instruction writes 1 KB, lane l at
-// M0 + 16*l, from any per-lane global address), double-buffered: tile t+1 streams in while tile
-// t is computed, with no staging registers. Both contractions read their A operands from the
-// same copy:
+// M0 + 16*l, from any per-lane global address), with no staging registers; the next tile streams
+// in while the current one is computed (the forward per operand, the backward kernels into a
+// second buffer). Both contractions read their A operands from the same copy:
 //   - row reads (ds_read_b128) of the sigma-ordered rows for the first contraction;
 //   - transpose reads (ds_read_b64_tr_b16) for the second: within each 16-lane group, lane 4e+q
 //     addresses 4 consecutive columns d0+4q.. of row k0+e, and lane j receives column d0+j of rows
@@ -130,14 +130,19 @@ constexpr int min_blocks() {
 }
 
 // ------------------------------------------------------------------------------------------
-// Forward: per query block, O^T += V^T P^T over live tiles with an online softmax.
-
+// Forward: per work item (a run of a query block's live tiles), O^T += V^T P^T with an online
+// softmax (pallas_attn.py:112-141).
+//
+// Two workgroups per CU: one K buffer and one V buffer (64 KB at D = 128) and at most 256 VGPRs
+// per wave, so the two resident workgroups overlap one's softmax (VALU) with the other's MFMAs.
+// K(t+1) streams in during softmax(t) and PV(t), V(t+1) during S(t+1).
 template <int D>
-__global__ void __launch_bounds__(NT, min_blocks<D>()) fwd_kernel(KArgs a) {
+__global__ void __launch_bounds__(NT, 2) fwd_kernel(KArgs a) {
   constexpr int TB = Tile<D>::BYTES;
-  __shared__ __attribute__((aligned(1024))) char lds0[2 * TB];  // K | V of even iterations
-  __shared__ __attribute__((aligned(1024))) char lds1[2 * TB];  // K | V of odd iterations
-  lds_char* bufs[2] = {(lds_char*)lds0, (lds_char*)lds1};
+  __shared__ __attribute__((aligned(1024))) char lk[TB];
+  __shared__ __attribute__((aligned(1024))) char lv[TB];
+  lds_char* K = (lds_char*)lk;
+  lds_char* V = (lds_char*)lv;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int i = lane & 31, g = lane >> 5;
@@ -159,23 +164,17 @@ __global__ void __launch_bounds__(NT, min_blocks<D>()) fwd_kernel(KArgs a) {
   SoftmaxState st{-__builtin_inff(), 0.f};
 
   int t0, t1;
-  tile_range(a, j.blk, t0, t1);
+  tile_range(a, j, t0, t1);
   if (t0 < t1) {
     const int kb = ((ci32_ptr)a.col)[t0];
-    dma.issue(rK, bufs[0], w, kb * BLK, snb);
-    dma.issue(rV, bufs[0] + TB, w, kb * BLK, snb);
+    dma.issue(rK, K, w, kb * BLK, snb);
+    wait_vmem();  // K(t0) and the Q fragment
+    dma.issue(rV, V, w, kb * BLK, snb);
   }
-  auto step = [&](int tt, lds_char* cur, lds_char* nxt) {
+  __syncthreads();
+  for (int tt = t0; tt < t1; ++tt) {
     const int t = __builtin_amdgcn_readfirstlane(tt);
-    wait_vmem();      // this wave's copy of tile t (and the Q fragment) has landed
-    __syncthreads();  // every wave's copy has; every wave is done with the previous tile
-    if (t + 1 < t1) {
-      const int kb = ((ci32_ptr)a.col)[t + 1];
-      dma.issue(rK, nxt, w, kb * BLK, snb);
-      dma.issue(rV, nxt + TB, w, kb * BLK, snb);
-    }
-    const lds_char* K = cur;
-    const lds_char* V = cur + TB;
+    // K(t) is in LDS for every wave here; V(t) may still be in flight.
     const cu64_ptr mk = tile_masks(a, t, w);
     f32x16 s[4];
 #pragma unroll
@@ -185,13 +184,15 @@ __global__ void __launch_bounds__(NT, min_blocks<D>()) fwd_kernel(KArgs a) {
       for (int k = 0; k < D / 16; ++k) ka[k] = row_read(K, off.row[k] + sb * 32 * (2 * D));
       SubMask m;
       m.load(mk, sb);
-      __builtin_amdgcn_sched_barrier(0);  // keep the operand reads ahead of the MFMAs
       s[sb] = zero16();
 #pragma unroll
       for (int k = 0; k < D / 16; ++k) s[sb] = mfma_bf16(ka[k], qf[k], s[sb]);
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[sb][r] = select_lane(m.w[r], s[sb][r], -__builtin_inff());
     }
+    wait_vmem();      // this wave's part of V(t)
+    __syncthreads();  // all of V(t) landed; every wave is done reading K(t)
+    if (t + 1 < t1) dma.issue(rK, K, w, ((ci32_ptr)a.col)[t + 1] * BLK, snb);
     const float corr = softmax_tile(s, st, a.c2);
 #pragma unroll
     for (int db = 0; db < D / 32; ++db) o[db] *= corr;
@@ -203,19 +204,21 @@ __global__ void __launch_bounds__(NT, min_blocks<D>()) fwd_kernel(KArgs a) {
 #pragma unroll
         for (int c = 0; c < 2; ++c) va[db][c] = tr_operand<D>(V, off, db, sb, c);
       const bf16x8 p0 = pack_bf16(s[sb], 0), p1 = pack_bf16(s[sb], 1);
-      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int db = 0; db < D / 32; ++db) {
         o[db] = mfma_bf16(va[db][0], p0, o[db]);
         o[db] = mfma_bf16(va[db][1], p1, o[db]);
       }
     }
-  };
-  for (int tt = t0; tt < t1; tt += 2) {
-    step(tt, bufs[0], bufs[1]);
-    if (tt + 1 < t1) step(tt + 1, bufs[1], bufs[0]);
+    wait_vmem();      // this wave's part of K(t+1)
+    __syncthreads();  // all of K(t+1) landed; every wave is done reading V(t)
+    if (t + 1 < t1) dma.issue(rV, V, w, ((ci32_ptr)a.col)[t + 1] * BLK, snb);
   }
   const float ltot = st.l + __shfl_xor(st.l, 32);
+  if (j.part >= 0) {
+    store_fwd_partial<D>(a, j, 32 * w + i, o, st.m, ltot, g);
+    return;
+  }
   const float inv = ltot > 0.f ? 1.f / ltot : 0.f;
   store_acc_bf16<D>(make_rsrc((uint16_t*)a.out0 + j.base, a.slice_bytes), qrow, snb, o, inv, g);
   if (g == 0) write_lse(a, j, qrow, st, ltot);
@@ -257,7 +260,7 @@ __global__ void __launch_bounds__(NT, min_blocks<D>()) dq_kernel(KArgs a) {
   for (int db = 0; db < D / 32; ++db) acc[db] = zero16();
 
   int t0, t1;
-  tile_range(a, j.blk, t0, t1);
+  tile_range(a, j, t0, t1);
   if (t0 < t1) {
     const int kb = ((ci32_ptr)a.col)[t0];
     dma.issue(rK, bufs[0], w, kb * BLK, snb);
@@ -315,6 +318,10 @@ __global__ void __launch_bounds__(NT, min_blocks<D>()) dq_kernel(KArgs a) {
     step(tt, bufs[0], bufs[1]);
     if (tt + 1 < t1) step(tt + 1, bufs[1], bufs[0]);
   }
+  if (j.part >= 0) {
+    store_bwd_partial<D>(a, j, 32 * w + i, acc, 0, g);
+    return;
+  }
   store_acc_bf16<D>(make_rsrc((uint16_t*)a.out0 + j.base, a.slice_bytes), qrow, snb, acc, a.scale, g);
 }
 
@@ -356,7 +363,7 @@ __global__ void __launch_bounds__(NT, min_blocks<D>()) dkv_kernel(KArgs a) {
   }
 
   int t0, t1;
-  tile_range(a, j.blk, t0, t1);
+  tile_range(a, j, t0, t1);
   // Wave 0 also copies the tile's statistics with two full-wave copies and no branch: the first
   // (log-sum-exps) lands at stats + 16 * lane, the second (deltas) at stats + 512 + 16 * lane.
   // Lanes 0-31 of the first and 32-63 of the second carry the data; the other halves address
@@ -443,13 +450,18 @@ __global__ void __launch_bounds__(NT, min_blocks<D>()) dkv_kernel(KArgs a) {
     step(tt, bufs[0], bufs[1]);
     if (tt + 1 < t1) step(tt + 1, bufs[1], bufs[0]);
   }
+  if (j.part >= 0) {
+    store_bwd_partial<D>(a, j, 32 * w + i, dk, 0, g);
+    store_bwd_partial<D>(a, j, 32 * w + i, dv, 1, g);
+    return;
+  }
   store_acc_bf16<D>(make_rsrc((uint16_t*)a.out0 + j.base, a.slice_bytes), krow, snb, dk, a.scale, g);
   store_acc_bf16<D>(make_rsrc((uint16_t*)a.out1 + j.base, a.slice_bytes), krow, snb, dv, 1.f, g);
 }
 
 template <int D>
 hipError_t launch_d(Kind kind, const KArgs& a, hipStream_t stream) {
-  const dim3 grid((unsigned)a.n_blocks * (unsigned)(a.batch * a.heads)), block(NT);
+  const dim3 grid((unsigned)a.n_items * (unsigned)(a.batch * a.heads)), block(NT);
   switch (kind) {
     case Kind::kFwd: hipLaunchKernelGGL(fwd_kernel<D>, grid, block, 0, stream, a); break;
     case Kind::kDq: hipLaunchKernelGGL(dq_kernel<D>, grid, block, 0, stream, a); break;

@@ -104,30 +104,52 @@ __device__ __forceinline__ f32x16 mfma_f32(float a, float b, const f32x16& c) {
 
 struct Job {
   int blk;
-  int b, h;
+  int b, h, bh;
+  int t0, t1;    // tile range of this work item, clamped to [0, n_tiles)
+  int part;      // partial slot, or -1 when the item covers its whole block
   int64_t base;  // element offset of (b, h)
 };
 
-// Blocks are visited in `order` (most tiles first); the (batch, head) index varies fastest, so
-// the heads of one block run side by side and share its mask words in L2.
+// Work items are visited longest first; the (batch, head) index varies fastest, so the heads of
+// one item run side by side and share its mask words in L2.
 __device__ __forceinline__ Job decode_job(const KArgs& a) {
   Job j;
   const int bh_count = a.batch * a.heads;
   const int slot = blockIdx.x / bh_count;
-  const int bh = blockIdx.x - slot * bh_count;
-  j.blk = a.order ? ((ci32_ptr)a.order)[slot] : slot;
-  j.b = bh / a.heads;
-  j.h = bh - j.b * a.heads;
+  j.bh = blockIdx.x - slot * bh_count;
+  const ci32_ptr item = (ci32_ptr)a.items + 4 * slot;
+  j.blk = item[0];
+  j.t0 = item[1] < 0 ? 0 : item[1];
+  j.t1 = item[2] > a.n_tiles ? a.n_tiles : item[2];
+  j.part = item[3];
+  // A malformed item cannot write outside the outputs or the workspace: an out-of-range block
+  // gets no tiles (its rows are >= n, so the range-checked stores drop), an out-of-range slot
+  // writes the outputs directly.
+  if ((unsigned)j.blk >= (unsigned)a.n_blocks) j.t1 = j.t0;
+  if (j.part >= a.n_parts) j.part = -1;
+  j.b = j.bh / a.heads;
+  j.h = j.bh - j.b * a.heads;
   j.base = (int64_t)j.b * a.sb + (int64_t)j.h * a.sh;
   return j;
 }
 
-__device__ __forceinline__ void tile_range(const KArgs& a, int blk, int& t0, int& t1) {
-  t0 = ((ci32_ptr)a.ptr)[blk];
-  t1 = ((ci32_ptr)a.ptr)[blk + 1];
-  t0 = t0 < 0 ? 0 : t0;
-  t1 = t1 > a.n_tiles ? a.n_tiles : t1;
+__device__ __forceinline__ void tile_range(const KArgs&, const Job& j, int& t0, int& t1) {
+  t0 = j.t0;
+  t1 = j.t1;
 }
+
+// Buffer resource of this item's partial slot for its (batch, head): [128][D] float32 rows
+// (O, dQ or dK), then [128][D] (dV) or the forward's row max [128] and row sum [128].
+template <int D>
+__device__ __forceinline__ rsrc_t part_slot(const KArgs& a, const Job& j) {
+  constexpr int64_t words = 128 * (2 * D + 2);
+  return make_rsrc(a.work + ((int64_t)j.part * a.batch * a.heads + j.bh) * words, (uint32_t)(words * 4));
+}
+
+__device__ __forceinline__ void store_f32(rsrc_t r, uint32_t byte_off, float x) {
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, x), r, (int)byte_off, 0, 0);
+}
+
 
 __device__ __forceinline__ int64_t stat_index(const KArgs& a, const Job& j, int row) {
   return ((int64_t)j.b * a.heads + j.h) * a.n + row;
@@ -225,6 +247,27 @@ __device__ __forceinline__ void store_acc_f32(rsrc_t r, int row, uint32_t snb, c
                                              (int)((uint32_t)row * snb + (uint32_t)(4 * d)), 0, 0);
     }
   }
+}
+
+// Forward partial epilogue: unnormalised O^T rows, the row max (log2 domain) and the row sum.
+// `row` is the row within the block.
+template <int D>
+__device__ __forceinline__ void store_fwd_partial(const KArgs& a, const Job& j, int row, const f32x16 (&o)[D / 32],
+                                                  float m, float ltot, int g) {
+  const rsrc_t r = part_slot<D>(a, j);
+  store_acc_f32<D>(r, row, D * 4, o, 1.f, g);
+  if (g == 0) {
+    store_f32(r, (uint32_t)(128 * D + row) * 4, m);
+    store_f32(r, (uint32_t)(128 * D + 128 + row) * 4, ltot);
+  }
+}
+
+// Backward partial epilogue: unscaled accumulator rows into the first (which = 0: dQ, dK) or
+// second (which = 1: dV) half of the slot.
+template <int D>
+__device__ __forceinline__ void store_bwd_partial(const KArgs& a, const Job& j, int row, const f32x16 (&acc)[D / 32],
+                                                  int which, int g) {
+  store_acc_f32<D>(part_slot<D>(a, j), row + 128 * which, D * 4, acc, 1.f, g);
 }
 
 }  // namespace dev

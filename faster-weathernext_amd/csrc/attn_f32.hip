@@ -97,7 +97,7 @@ __global__ void __launch_bounds__(NT, 1) fwd_f32_kernel(KArgs a) {
   SoftmaxState st{-__builtin_inff(), 0.f};
 
   int t0, t1;
-  tile_range(a, j.blk, t0, t1);
+  tile_range(a, j, t0, t1);
   for (int tt = t0; tt < t1; ++tt) {
     const int t = __builtin_amdgcn_readfirstlane(tt);
     const int kb = ((ci32_ptr)a.col)[t];
@@ -134,6 +134,10 @@ __global__ void __launch_bounds__(NT, 1) fwd_f32_kernel(KArgs a) {
       }
   }
   const float ltot = st.l + __shfl_xor(st.l, 32);
+  if (j.part >= 0) {
+    store_fwd_partial<D>(a, j, 32 * w + i, o, st.m, ltot, g);
+    return;
+  }
   const float inv = ltot > 0.f ? 1.f / ltot : 0.f;
   store_acc_f32<D>(make_rsrc((float*)a.out0 + j.base, a.slice_bytes), qrow, snb, o, inv, g);
   if (g == 0) write_lse(a, j, qrow, st, ltot);
@@ -171,7 +175,7 @@ __global__ void __launch_bounds__(NT, 1) dq_f32_kernel(KArgs a) {
   for (int db = 0; db < D / 32; ++db) acc[db] = zero16();
 
   int t0, t1;
-  tile_range(a, j.blk, t0, t1);
+  tile_range(a, j, t0, t1);
   for (int tt = t0; tt < t1; ++tt) {
     const int t = __builtin_amdgcn_readfirstlane(tt);
     const int kb = ((ci32_ptr)a.col)[t];
@@ -208,6 +212,10 @@ __global__ void __launch_bounds__(NT, 1) dq_f32_kernel(KArgs a) {
           acc[db] = mfma_f32(*(const float*)(ldsK + off.el[r & 3] + off.el_imm(sb, r, db)), dp[r], acc[db]);
       }
     }
+  }
+  if (j.part >= 0) {
+    store_bwd_partial<D>(a, j, 32 * w + i, acc, 0, g);
+    return;
   }
   store_acc_f32<D>(make_rsrc((float*)a.out0 + j.base, a.slice_bytes), qrow, snb, acc, a.scale, g);
 }
@@ -246,7 +254,7 @@ __global__ void __launch_bounds__(NT, 1) dkv_f32_kernel(KArgs a) {
   }
 
   int t0, t1;
-  tile_range(a, j.blk, t0, t1);
+  tile_range(a, j, t0, t1);
   for (int tt = t0; tt < t1; ++tt) {
     const int t = __builtin_amdgcn_readfirstlane(tt);
     const int qb = ((ci32_ptr)a.col)[t];
@@ -293,6 +301,11 @@ __global__ void __launch_bounds__(NT, 1) dkv_f32_kernel(KArgs a) {
         }
       }
     }
+  }
+  if (j.part >= 0) {
+    store_bwd_partial<D>(a, j, 32 * w + i, dk, 0, g);
+    store_bwd_partial<D>(a, j, 32 * w + i, dv, 1, g);
+    return;
   }
   store_acc_f32<D>(make_rsrc((float*)a.out0 + j.base, a.slice_bytes), krow, snb, dk, a.scale, g);
   store_acc_f32<D>(make_rsrc((float*)a.out1 + j.base, a.slice_bytes), krow, snb, dv, 1.f, g);
@@ -342,7 +355,7 @@ hipError_t launch_d(Kind kind, const KArgs& a, hipStream_t stream) {
     hipLaunchKernelGGL((delta_kernel<float, D>), dim3((unsigned)((lanes + NT - 1) / NT)), block, 0, stream, a);
     return hipGetLastError();
   }
-  const dim3 grid((unsigned)a.n_blocks * (unsigned)(a.batch * a.heads));
+  const dim3 grid((unsigned)a.n_items * (unsigned)(a.batch * a.heads));
   switch (kind) {
     case Kind::kFwd: hipLaunchKernelGGL(fwd_f32_kernel<D>, grid, block, 0, stream, a); break;
     case Kind::kDq: hipLaunchKernelGGL(dq_f32_kernel<D>, grid, block, 0, stream, a); break;

@@ -21,26 +21,36 @@ struct KArgs {
   const int32_t* col;
   const uint64_t* lanes;
   const uint32_t* full;
-  const int32_t* order;
-  int32_t n, heads, batch, n_blocks, n_tiles;
+  const int32_t* items;   // fwn_item[n_items] as int32 quadruples (block, t0, t1, part)
+  const int32_t* split;   // [n_split * 3] block, first partial slot, slot count (combine pass)
+  float* work;            // partial slots: [n_parts][batch * heads][128][2 * head_dim + 2] float32
+  int32_t n, heads, batch, n_blocks, n_tiles, n_items, n_parts, n_split;
   int64_t sb, sn, sh;
   uint32_t slice_bytes;   // bytes of one (batch, head) slice: ((n - 1) * sn + head_dim) * elem
   float scale;            // softmax scale
   float c2;               // scale * log2(e)
 };
 
-enum class Kind { kFwd, kDq, kDkv, kDelta };
+enum class Kind { kFwd, kDq, kDkv, kDelta, kFwdCombine, kDqCombine, kDkvCombine };
 
 // Kernel launchers (each enqueues one kernel and returns hipSuccess or the launch error).
 hipError_t launch_bf16(Kind kind, int head_dim, const KArgs& a, hipStream_t stream);  // attn_bf16.hip
 hipError_t launch_f32(Kind kind, int head_dim, const KArgs& a, hipStream_t stream);   // attn_f32.hip
 hipError_t launch_delta_bf16(int head_dim, const KArgs& a, hipStream_t stream);      // attn_f32.hip
+hipError_t launch_combine(Kind kind, int dtype, int head_dim, const KArgs& a,
+                          hipStream_t stream);                                     // attn_combine.hip
 
 // Dispatch on dtype (0 f32, 1 bf16).
 inline hipError_t launch(Kind kind, int dtype, int head_dim, const KArgs& a, hipStream_t stream) {
+  if (kind == Kind::kFwdCombine || kind == Kind::kDqCombine || kind == Kind::kDkvCombine)
+    return launch_combine(kind, dtype, head_dim, a, stream);
   if (dtype == 0) return launch_f32(kind, head_dim, a, stream);
   if (kind == Kind::kDelta) return launch_delta_bf16(head_dim, a, stream);
   return launch_bf16(kind, head_dim, a, stream);
 }
+
+// Float32 words of one partial slot of one (batch, head): O or dQ or dK rows [128][D], then dV
+// rows [128][D] (dK/dV) or the forward's row max [128] and row sum [128].
+inline int64_t slot_words(int head_dim) { return 128 * (2 * (int64_t)head_dim + 2); }
 
 }  // namespace fwn

@@ -307,10 +307,10 @@ int fwn_tiles_fill(int32_t n_rows, int32_t n_cols, const int64_t* row_ptr, const
 
 int fwn_tiles_prepare(int32_t n_blocks, int32_t n_tiles, int32_t n_cols, const int32_t* tile_ptr,
                       const int32_t* tile_col, const uint32_t* tile_bits, uint64_t* lanes,
-                      uint32_t* full, int32_t* order) {
+                      uint32_t* full) {
   fwn::clear_error();
   if (n_blocks <= 0 || n_tiles < 0 || n_cols <= 0 || !tile_ptr || (n_tiles > 0 && (!tile_col || !tile_bits)) ||
-      (n_tiles > 0 && (!lanes || !full)) || !order)
+      (n_tiles > 0 && (!lanes || !full)))
     return fwn::fail(FWN_ERR_INVALID_ARG, "fwn_tiles_prepare: null or empty argument");
   if (int rc = fwn::check_tile_list(n_blocks, n_tiles, n_cols, tile_ptr, tile_col)) return rc;
   const int32_t words = FWN_BLOCK / 32;
@@ -346,10 +346,64 @@ int fwn_tiles_prepare(int32_t n_blocks, int32_t n_tiles, int32_t n_cols, const i
     }
   });
   if (bad) return fwn::fail(FWN_ERR_TILES, "fwn_tiles_prepare: a tile has bits set beyond n_cols");
-  for (int32_t i = 0; i < n_blocks; ++i) order[i] = i;
-  std::stable_sort(order, order + n_blocks, [&](int32_t a, int32_t b) {
-    return tile_ptr[a + 1] - tile_ptr[a] > tile_ptr[b + 1] - tile_ptr[b];
-  });
+  return FWN_OK;
+}
+
+int fwn_tiles_schedule_count(int32_t n_blocks, const int32_t* tile_ptr, int32_t max_item_tiles,
+                             int32_t* n_items, int32_t* n_parts, int32_t* n_split) {
+  fwn::clear_error();
+  if (n_blocks <= 0 || !tile_ptr || !n_items || !n_parts || !n_split)
+    return fwn::fail(FWN_ERR_INVALID_ARG, "fwn_tiles_schedule_count: null or empty argument");
+  const int64_t chunk = max_item_tiles > 0 ? max_item_tiles : FWN_ITEM_TILES;
+  int64_t items = 0, parts = 0, split = 0;
+  for (int32_t b = 0; b < n_blocks; ++b) {
+    const int64_t count = (int64_t)tile_ptr[b + 1] - tile_ptr[b];
+    if (count < 0) return fwn::fail(FWN_ERR_TILES, "fwn_tiles_schedule_count: tile_ptr decreases at block %d", b);
+    const int64_t p = count > chunk ? (count + chunk - 1) / chunk : 1;
+    items += p;
+    if (p > 1) {
+      parts += p;
+      ++split;
+    }
+  }
+  if (items > INT32_MAX) return fwn::fail(FWN_ERR_INVALID_ARG, "fwn_tiles_schedule_count: too many items");
+  *n_items = (int32_t)items;
+  *n_parts = (int32_t)parts;
+  *n_split = (int32_t)split;
+  return FWN_OK;
+}
+
+int fwn_tiles_schedule_fill(int32_t n_blocks, const int32_t* tile_ptr, int32_t max_item_tiles,
+                            fwn_item* items, int32_t* split) {
+  fwn::clear_error();
+  int32_t n_items = 0, n_parts = 0, n_split = 0;
+  if (int rc = fwn_tiles_schedule_count(n_blocks, tile_ptr, max_item_tiles, &n_items, &n_parts, &n_split))
+    return rc;
+  if (!items || (n_split > 0 && !split))
+    return fwn::fail(FWN_ERR_INVALID_ARG, "fwn_tiles_schedule_fill: null output");
+  const int64_t chunk = max_item_tiles > 0 ? max_item_tiles : FWN_ITEM_TILES;
+  int32_t it = 0, part = 0, sp = 0;
+  for (int32_t b = 0; b < n_blocks; ++b) {
+    const int32_t t0 = tile_ptr[b], count = tile_ptr[b + 1] - t0;
+    const int32_t p = count > chunk ? (int32_t)((count + chunk - 1) / chunk) : 1;
+    if (p == 1) {
+      items[it++] = fwn_item{b, t0, t0 + count, -1};
+      continue;
+    }
+    split[3 * sp] = b;
+    split[3 * sp + 1] = part;
+    split[3 * sp + 2] = p;
+    ++sp;
+    // Near-equal runs: the first count % p runs get one tile more.
+    int32_t t = t0;
+    for (int32_t c = 0; c < p; ++c) {
+      const int32_t len = count / p + (c < count % p ? 1 : 0);
+      items[it++] = fwn_item{b, t, t + len, part++};
+      t += len;
+    }
+  }
+  std::stable_sort(items, items + n_items,
+                   [](const fwn_item& x, const fwn_item& y) { return x.t1 - x.t0 > y.t1 - y.t0; });
   return FWN_OK;
 }
 

@@ -43,11 +43,15 @@ class AttnDesc(ctypes.Structure):
 class Tiles(ctypes.Structure):
   _fields_ = [("n_blocks", ctypes.c_int32), ("n_tiles", ctypes.c_int32), ("ptr", ctypes.c_void_p),
               ("col", ctypes.c_void_p), ("lanes", ctypes.c_void_p), ("full", ctypes.c_void_p),
-              ("order", ctypes.c_void_p)]
+              ("n_items", ctypes.c_int32), ("n_parts", ctypes.c_int32), ("n_split", ctypes.c_int32),
+              ("reserved", ctypes.c_int32), ("items", ctypes.c_void_p), ("split", ctypes.c_void_p)]
+
+
+ITEM_TILES = 64  # FWN_ITEM_TILES: default longest run of tiles per work item
 
 
 _P = ctypes.c_void_p
-_I32, _I64, _F = ctypes.c_int32, ctypes.c_int64, ctypes.c_float
+_I32, _I64, _U64, _F = ctypes.c_int32, ctypes.c_int64, ctypes.c_uint64, ctypes.c_float
 _DESC = ctypes.POINTER(AttnDesc)
 _TILES = ctypes.POINTER(Tiles)
 
@@ -59,12 +63,15 @@ SIGNATURES = {
     "fwn_hilbert_order": [_I64, _P, _P, _I32, _P],
     "fwn_tiles_count": [_I32, _I32, _P, _P, _P, _P],
     "fwn_tiles_fill": [_I32, _I32, _P, _P, _P, _P, _P, _P],
-    "fwn_tiles_prepare": [_I32, _I32, _I32, _P, _P, _P, _P, _P, _P],
-    "fwn_attn_fwd_launch": [_DESC, _P, _P, _P, _TILES, _P, _P, _P],
+    "fwn_tiles_prepare": [_I32, _I32, _I32, _P, _P, _P, _P, _P],
+    "fwn_tiles_schedule_count": [_I32, _P, _I32, _P, _P, _P],
+    "fwn_tiles_schedule_fill": [_I32, _P, _I32, _P, _P],
+    "fwn_attn_workspace_size": [_DESC, _TILES, _P],
+    "fwn_attn_fwd_launch": [_DESC, _P, _P, _P, _TILES, _P, _P, _P, _U64, _P],
     "fwn_attn_bwd_delta_launch": [_DESC, _P, _P, _P, _P],
-    "fwn_attn_bwd_dq_launch": [_DESC, _P, _P, _P, _P, _P, _P, _TILES, _P, _P],
-    "fwn_attn_bwd_dkv_launch": [_DESC, _P, _P, _P, _P, _P, _P, _TILES, _P, _P, _P],
-    "fwn_attn_bwd_launch": [_DESC, _P, _P, _P, _P, _P, _P, _P, _TILES, _TILES, _P, _P, _P, _P],
+    "fwn_attn_bwd_dq_launch": [_DESC, _P, _P, _P, _P, _P, _P, _TILES, _P, _P, _U64, _P],
+    "fwn_attn_bwd_dkv_launch": [_DESC, _P, _P, _P, _P, _P, _P, _TILES, _P, _P, _P, _U64, _P],
+    "fwn_attn_bwd_launch": [_DESC, _P, _P, _P, _P, _P, _P, _P, _TILES, _TILES, _P, _P, _P, _P, _U64, _P],
 }
 
 _lock = threading.Lock()

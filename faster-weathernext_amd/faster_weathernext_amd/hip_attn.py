@@ -15,6 +15,7 @@ the gfx950 kernels, and there is no interpreter or CPU path.
 All compute runs in the HIP kernels of libfwn_attn.so through its C ABI; torch only provides
 device memory and the stream. Tensors must be on a ROCm device: there is no CPU fallback.
 """
+import ctypes
 import threading
 
 import numpy as np
@@ -37,37 +38,55 @@ class TileList:
   call, as the reference shares one device copy of the mask across layers (``patch.py:263-266``).
   """
 
-  def __init__(self, tile_ptr, tile_kb, tile_bits, n_cols, device="cuda"):
+  def __init__(self, tile_ptr, tile_kb, tile_bits, n_cols, device="cuda", max_item_tiles=nat.ITEM_TILES):
     tile_ptr = nat.as_c(tile_ptr, np.int32)
     tile_kb = nat.as_c(tile_kb, np.int32)
     tile_bits = nat.as_c(tile_bits, np.uint32).reshape(len(tile_kb), nat.BLOCK, nat.BLOCK // 32)
     self.n_blocks = len(tile_ptr) - 1
     self.n_tiles = len(tile_kb)
     self.n_cols = int(n_cols)
+    L = nat.lib()
     lanes = np.zeros((self.n_tiles, nat.LANE_WORDS), np.uint64)
     full = np.zeros(self.n_tiles, np.uint32)
-    order = np.zeros(self.n_blocks, np.int32)
-    nat.check(nat.lib().fwn_tiles_prepare(self.n_blocks, self.n_tiles, self.n_cols, nat.ptr(tile_ptr),
-                                          nat.ptr(tile_kb), nat.ptr(tile_bits), nat.ptr(lanes), nat.ptr(full),
-                                          nat.ptr(order)))
+    nat.check(L.fwn_tiles_prepare(self.n_blocks, self.n_tiles, self.n_cols, nat.ptr(tile_ptr), nat.ptr(tile_kb),
+                                  nat.ptr(tile_bits), nat.ptr(lanes), nat.ptr(full)))
+    # Work items: each block's run of tiles cut into pieces of at most max_item_tiles (split-K).
+    counts = np.zeros(3, np.int32)
+    nat.check(L.fwn_tiles_schedule_count(self.n_blocks, nat.ptr(tile_ptr), int(max_item_tiles), nat.ptr(counts[0:]),
+                                         nat.ptr(counts[1:]), nat.ptr(counts[2:])))
+    self.n_items, self.n_parts, self.n_split = (int(c) for c in counts)
+    items = np.zeros((self.n_items, 4), np.int32)
+    split = np.zeros((max(self.n_split, 1), 3), np.int32)
+    nat.check(L.fwn_tiles_schedule_fill(self.n_blocks, nat.ptr(tile_ptr), int(max_item_tiles), nat.ptr(items),
+                                        nat.ptr(split)))
+    self.items_host = items
+    self.split_host = split[:self.n_split]
     self.device = torch.device(device)
     put = lambda a: torch.from_numpy(a).to(self.device)
     self.ptr = put(tile_ptr)
     self.col = put(tile_kb)
     self.lanes = put(lanes.view(np.int64))
     self.full = put(full.view(np.int32))
-    self.order = put(order)
+    self.items = put(items)
+    self.split = put(split)
     self.counts = np.diff(tile_ptr)
     self.nnz = int(np.unpackbits(tile_bits.view(np.uint8)).sum()) if self.n_tiles else 0
     addr = lambda t: t.data_ptr() if t.numel() else None
     self.struct = nat.Tiles(self.n_blocks, self.n_tiles, addr(self.ptr), addr(self.col), addr(self.lanes),
-                            addr(self.full), addr(self.order))
+                            addr(self.full), self.n_items, self.n_parts, self.n_split, 0, addr(self.items),
+                            addr(self.split) if self.n_split else None)
+
+  def workspace_bytes(self, desc):
+    """Workspace the launchers need for this list and the call shape `desc` (0 if nothing is split)."""
+    n = ctypes.c_uint64(0)
+    nat.check(nat.lib().fwn_attn_workspace_size(desc, self.struct, ctypes.byref(n)))
+    return int(n.value)
 
   @classmethod
-  def from_mask(cls, mask, perm=None, device="cuda"):
+  def from_mask(cls, mask, perm=None, device="cuda", max_item_tiles=nat.ITEM_TILES):
     """Tile list of a boolean scipy/numpy [n, n] mask (optionally permuted as mask[perm][:, perm])."""
     tp, kb, bits = build_tile_mask(mask, perm)
-    return cls(tp, kb, bits, mask.shape[1], device)
+    return cls(tp, kb, bits, mask.shape[1], device, max_item_tiles)
 
   @property
   def density(self):
@@ -115,6 +134,16 @@ def _stream(device):
   return torch.cuda.current_stream(device).cuda_stream
 
 
+def workspace(desc, device, *lists):
+  """A device workspace large enough for every tile list in `lists` (None if none needs one)."""
+  size = max(tl.workspace_bytes(desc) for tl in lists)
+  return torch.empty(size, dtype=torch.uint8, device=device) if size else None
+
+
+def _ws_args(ws):
+  return (ws.data_ptr(), ws.numel()) if ws is not None else (None, 0)
+
+
 def attention_forward(q, k, v, tiles, scale, with_lse=True):
   """Forward kernel: returns (out, lse) with lse float32 [batch, heads, n] (None if not requested)."""
   q = q.contiguous()
@@ -124,8 +153,9 @@ def attention_forward(q, k, v, tiles, scale, with_lse=True):
   tl = _as_tiles(tiles, q.shape[1], q.device)
   out = torch.empty_like(q)
   lse = torch.empty((q.shape[0], q.shape[2], q.shape[1]), dtype=torch.float32, device=q.device) if with_lse else None
+  ws = workspace(desc, q.device, tl)
   nat.check(nat.lib().fwn_attn_fwd_launch(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), tl.struct, out.data_ptr(),
-                                          lse.data_ptr() if with_lse else None, _stream(q.device)))
+                                          lse.data_ptr() if with_lse else None, *_ws_args(ws), _stream(q.device)))
   return out, lse
 
 
@@ -142,9 +172,11 @@ def attention_backward(q, k, v, out, lse, dout, tiles, tiles_t, scale):
   tlt = tl if tiles_t is None else _as_tiles(tiles_t, n, q.device)
   delta = torch.empty_like(lse)
   dq, dk, dv = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
+  ws = workspace(desc, q.device, tl, tlt)
   nat.check(nat.lib().fwn_attn_bwd_launch(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
                                           dout.data_ptr(), lse.data_ptr(), delta.data_ptr(), tl.struct, tlt.struct,
-                                          dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), _stream(q.device)))
+                                          dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), *_ws_args(ws),
+                                          _stream(q.device)))
   return dq, dk, dv
 
 

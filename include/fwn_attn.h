@@ -9,8 +9,9 @@
  *     a thread-local message. Invalid shapes, dtypes, strides, alignments and malformed tile
  *     lists are rejected on the host before anything is launched.
  *   - Launchers enqueue work on `stream` and return without synchronising. They allocate
- *     nothing, keep no pointer after returning and hold no mutable global state, so they are
- *     re-entrant and safe under stream capture.
+ *     nothing (temporary results go to a caller-provided workspace, see
+ *     fwn_attn_workspace_size), keep no pointer after returning and hold no mutable global
+ *     state, so they are re-entrant and safe under stream capture.
  *   - Tensors q, k, v, o, dout, dq, dk, dv are [batch, n, heads, head_dim] in the element strides
  *     of fwn_attn_desc (head_dim contiguous): node-major by default, read and written in place
  *     (the reference transposes to head-major and pads, pallas_attn.py:334-335; here no copy is made).
@@ -55,11 +56,22 @@ typedef struct fwn_attn_desc {
   int64_t stride_h;
 } fwn_attn_desc;
 
-/* Device view of a prepared tile list (see fwn_tiles_prepare). `ptr`/`col` are the CSR tile list
- * of pallas_attn.build_tile_mask (pallas_attn.py:85-109) at 128 x 128; `lanes` and `full` hold
- * its bitmasks in the kernels' register layout. For the dK/dV launcher the list must be the
- * transposed mask's (rows = keys, columns = queries), as the reference's tiles_t
- * (pallas_attn.py:297-310; equal to the forward list for symmetric masks). */
+/* One work item of a tile list: tiles [t0, t1) of row block `block`. With part < 0 the item
+ * covers its whole block and writes the outputs directly; with part >= 0 it writes float32
+ * partial results into partial slot `part` of the workspace, and a combine pass over the
+ * block's slots writes the outputs (split-K: no block's tile run bounds the launch). */
+typedef struct fwn_item {
+  int32_t block;
+  int32_t t0;
+  int32_t t1;
+  int32_t part;
+} fwn_item;
+
+/* Device view of a prepared tile list (see fwn_tiles_prepare, fwn_tiles_schedule_fill).
+ * `ptr`/`col` are the CSR tile list of pallas_attn.build_tile_mask (pallas_attn.py:85-109) at
+ * 128 x 128; `lanes` and `full` hold its bitmasks in the kernels' register layout. For the dK/dV
+ * launcher the list must be the transposed mask's (rows = keys, columns = queries), as the
+ * reference's tiles_t (pallas_attn.py:297-310; equal to the forward list for symmetric masks). */
 typedef struct fwn_tiles {
   int32_t n_blocks;         /* row blocks: ceil(n / 128) */
   int32_t n_tiles;          /* live tiles */
@@ -67,7 +79,12 @@ typedef struct fwn_tiles {
   const int32_t* col;       /* [n_tiles] column block of each tile */
   const uint64_t* lanes;    /* [n_tiles * FWN_LANE_WORDS] */
   const uint32_t* full;     /* [n_tiles] bit w: rows 32w..32w+31 of the tile are all valid */
-  const int32_t* order;     /* [n_blocks] block processing order (most tiles first), or NULL */
+  int32_t n_items;          /* work items: every block appears, empty blocks included */
+  int32_t n_parts;          /* partial slots (items with part >= 0) */
+  int32_t n_split;          /* blocks cut into more than one item */
+  int32_t reserved;         /* 0 */
+  const fwn_item* items;    /* [n_items], longest first */
+  const int32_t* split;     /* [n_split * 3]: block, first partial slot, slot count */
 } fwn_tiles;
 
 /* Thread-local message of the last failure on this thread ("" if none). */
@@ -106,21 +123,44 @@ int fwn_tiles_fill(int32_t n_rows, int32_t n_cols, const int64_t* row_ptr, const
                    uint32_t* tile_bits);
 
 /* Validates a canonical tile list (tile_ptr, tile_col, tile_bits as above, n_cols columns) and
- * converts it into the kernels' layout: lanes[n_tiles * FWN_LANE_WORDS], full[n_tiles] and
- * order[n_blocks] (host buffers; the caller copies them to the device). */
+ * converts it into the kernels' layout: lanes[n_tiles * FWN_LANE_WORDS] and full[n_tiles]
+ * (host buffers; the caller copies them to the device). */
 int fwn_tiles_prepare(int32_t n_blocks, int32_t n_tiles, int32_t n_cols, const int32_t* tile_ptr,
                       const int32_t* tile_col, const uint32_t* tile_bits, uint64_t* lanes,
-                      uint32_t* full, int32_t* order);
+                      uint32_t* full);
+
+/* Work items of a tile list: the tiles of each block are cut into ceil(count / max_item_tiles)
+ * runs of near-equal length (max_item_tiles <= 0 selects FWN_ITEM_TILES). The reference runs one
+ * program per block (pallas_attn.py:244-247), so its launch lasts as long as its longest block;
+ * splitting bounds every item. Two passes: fwn_tiles_schedule_count gives the sizes,
+ * fwn_tiles_schedule_fill writes items[n_items] (longest first, ties by block) and
+ * split[n_split * 3] (host buffers). */
+#define FWN_ITEM_TILES 64
+int fwn_tiles_schedule_count(int32_t n_blocks, const int32_t* tile_ptr, int32_t max_item_tiles,
+                             int32_t* n_items, int32_t* n_parts, int32_t* n_split);
+int fwn_tiles_schedule_fill(int32_t n_blocks, const int32_t* tile_ptr, int32_t max_item_tiles,
+                            fwn_item* items, int32_t* split);
 
 /* ---------------------------------------------------------------------------------------------
  * Device launchers (enqueue on `stream`).
+ *
+ * `workspace` is device memory of at least fwn_attn_workspace_size bytes, 256-byte aligned,
+ * owned by the caller and used only between a launch and the completion of its stream work (so
+ * launches on one stream may share it; launches that can overlap need their own). It may be NULL
+ * when the size is 0 (no block of the tile list is split).
  * ------------------------------------------------------------------------------------------- */
+
+/* Workspace bytes the forward, dq and dk/dv launchers need for `tiles`:
+ * tiles->n_parts * batch * heads * 128 * (2 * head_dim + 2) * 4 (float32 partial outputs plus
+ * the forward's per-row max and sum). */
+int fwn_attn_workspace_size(const fwn_attn_desc* desc, const fwn_tiles* tiles, uint64_t* bytes);
 
 /* Forward: o = softmax(mask(q k^T * scale)) v, walking only live tiles with an online softmax.
  * lse (natural log-sum-exp of the scaled logits per row) is written when non-NULL.
  * Replaces pallas_attn._forward/_kernel (pallas_attn.py:112-141, 235-257). */
 int fwn_attn_fwd_launch(const fwn_attn_desc* desc, const void* q, const void* k, const void* v,
-                        const fwn_tiles* tiles, void* o, float* lse, void* stream);
+                        const fwn_tiles* tiles, void* o, float* lse, void* workspace,
+                        uint64_t workspace_bytes, void* stream);
 
 /* delta = rowsum(o * dout) in float32 [batch, heads, n] (pallas_attn.py:278). */
 int fwn_attn_bwd_delta_launch(const fwn_attn_desc* desc, const void* o, const void* dout,
@@ -130,21 +170,24 @@ int fwn_attn_bwd_delta_launch(const fwn_attn_desc* desc, const void* o, const vo
  * (pallas_attn.py:161-184, 286-295). */
 int fwn_attn_bwd_dq_launch(const fwn_attn_desc* desc, const void* q, const void* k,
                            const void* v, const void* dout, const float* lse,
-                           const float* delta, const fwn_tiles* tiles, void* dq, void* stream);
+                           const float* delta, const fwn_tiles* tiles, void* dq, void* workspace,
+                           uint64_t workspace_bytes, void* stream);
 
 /* dk, dv per key block over the transposed tile list; every workgroup owns its rows of dk/dv,
  * so no atomics (pallas_attn.py:187-215, 297-310). */
 int fwn_attn_bwd_dkv_launch(const fwn_attn_desc* desc, const void* q, const void* k,
                             const void* v, const void* dout, const float* lse,
                             const float* delta, const fwn_tiles* tiles_t, void* dk, void* dv,
-                            void* stream);
+                            void* workspace, uint64_t workspace_bytes, void* stream);
 
 /* Whole backward: delta, dq, then dk/dv, in stream order (pallas_attn._attention_bwd,
- * pallas_attn.py:274-311). delta is caller-provided scratch of [batch, heads, n] floats. */
+ * pallas_attn.py:274-311). delta is caller-provided scratch of [batch, heads, n] floats; the
+ * workspace must hold the larger of the two lists' sizes (dq and dk/dv run one after the other
+ * on `stream` and share it). */
 int fwn_attn_bwd_launch(const fwn_attn_desc* desc, const void* q, const void* k, const void* v,
                         const void* o, const void* dout, const float* lse, float* delta,
                         const fwn_tiles* tiles, const fwn_tiles* tiles_t, void* dq, void* dk,
-                        void* dv, void* stream);
+                        void* dv, void* workspace, uint64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

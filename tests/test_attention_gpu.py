@@ -232,7 +232,8 @@ def test_packed_qkv_strides_through_c_abi():
   base = buf.data_ptr()
   step = h * d * 4
   nat.check(nat.lib().fwn_attn_fwd_launch(desc, base, base + step, base + 2 * step, tiles.struct,
-                                          out.data_ptr(), lse.data_ptr(), torch.cuda.current_stream().cuda_stream))
+                                          out.data_ptr(), lse.data_ptr(), None, 0,
+                                          torch.cuda.current_stream().cuda_stream))
   torch.cuda.synchronize()
   got = _np(out[:, :, 0])
   ref = A.dense_attention(qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2], m.toarray(), d ** -0.5)
@@ -254,6 +255,74 @@ def test_deterministic_and_batch_independent(dtype):
   one = _run(q[1:2], k[1:2], v[1:2], do[1:2], tiles, d ** -0.5, dtype)
   for name in r1:
     np.testing.assert_array_equal(r1[name][1:2], one[name])
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("d", [32, 128])
+@pytest.mark.parametrize("max_item_tiles", [1, 3])
+def test_split_items_match_dense_reference(max_item_tiles, d, dtype):
+  """Blocks cut into several work items (split-K) give the same outputs and gradients: forward
+  partials merge by the online-softmax rule, dQ/dK/dV partials by summation. Rows without keys
+  inside a split block stay zero."""
+  rng = np.random.default_rng(30 + d)
+  b, n, h = 2, 900, 2
+  q, k, v, do = (_rounded(rng.standard_normal((b, n, h, d)), dtype) for _ in range(4))
+  m = _random_mask(n, 0.03, 31, symmetric=True).tolil()
+  empty = [5, 300, 777]
+  for r in empty:
+    m[r, :] = False
+    m[:, r] = False
+  m = m.tocsr()
+  m.eliminate_zeros()
+  tp, kb, bits = fwn.build_tile_mask(m)
+  tiles = fwn.TileList(tp, kb, bits, n, DEV, max_item_tiles)
+  assert tiles.n_split >= len(tp) - 2 and tiles.n_parts > tiles.n_split
+  res = _run(q, k, v, do, tiles, d ** -0.5, dtype)
+  for name in res:
+    assert np.isfinite(res[name]).all(), name
+    np.testing.assert_array_equal(res[name][:, empty], 0.0)
+  keep = np.setdiff1d(np.arange(n), empty)
+  sub = m.toarray()[np.ix_(keep, keep)]
+  ref = A.dense_attention(q[:, keep], k[:, keep], v[:, keep], sub, d ** -0.5)
+  refs = A.dense_grads(q[:, keep], k[:, keep], v[:, keep], do[:, keep], sub, d ** -0.5)
+  for bb in range(b):
+    _check(res["out"][bb, keep], ref[bb], dtype, ("out", bb))
+    for name, r in zip(("dq", "dk", "dv"), refs):
+      _check(res[name][bb, keep], r[bb], dtype, (name, bb))
+  # Same log-sum-exp as the unsplit schedule (up to fp32 rounding of the merge).
+  whole = fwn.TileList(tp, kb, bits, n, DEV, 10 ** 6)
+  assert whole.n_split == 0
+  args = [_dev(x, dtype) for x in (q, k, v)]
+  _, lse_split = fwn.attention_forward(*args, tiles, d ** -0.5)
+  _, lse_whole = fwn.attention_forward(*args, whole, d ** -0.5)
+  ls, lw = _np(lse_split), _np(lse_whole)
+  assert np.array_equal(np.isinf(ls), np.isinf(lw))
+  fin = np.isfinite(lw)
+  np.testing.assert_allclose(ls[fin], lw[fin], rtol=0, atol=1e-5)
+
+
+def test_split_workspace_is_reused_across_calls():
+  """One workspace serves consecutive launches on a stream: a second, smaller call with the
+  same buffer gives the same result as a fresh one."""
+  rng = np.random.default_rng(40)
+  n, h, d = 700, 2, 64
+  m = _random_mask(n, 0.05, 41, symmetric=True)
+  tp, kb, bits = fwn.build_tile_mask(m)
+  tiles = fwn.TileList(tp, kb, bits, n, DEV, 2)
+  stream = torch.cuda.current_stream().cuda_stream
+  outs = []
+  for batch in (3, 1):
+    q, k, v = (_dev(rng.standard_normal((batch, n, h, d)), torch.float32) for _ in range(3))
+    desc = nat.AttnDesc(batch, n, h, d, nat.F32, d ** -0.5, *q.stride()[:3])
+    ws = torch.full((tiles.workspace_bytes(nat.AttnDesc(3, n, h, d, nat.F32, d ** -0.5, n * h * d, h * d, d)),),
+                    255, dtype=torch.uint8, device=DEV) if not outs else ws
+    out = torch.empty_like(q)
+    nat.check(nat.lib().fwn_attn_fwd_launch(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), tiles.struct,
+                                            out.data_ptr(), None, ws.data_ptr(), ws.numel(), stream))
+    ref, _ = fwn.attention_forward(q, k, v, tiles, d ** -0.5)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(_np(out), _np(ref))
+    outs.append(out)
 
 
 def test_exp2_based_softmax_accuracy():

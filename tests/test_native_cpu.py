@@ -109,7 +109,7 @@ def _decode_lanes(lanes, n_tiles):
   return bits
 
 
-def test_prepare_layout_roundtrip_and_order():
+def test_prepare_layout_roundtrip():
   n = 700
   m = _random_mask(n, 0.03, 11)
   m = m.tolil()
@@ -119,9 +119,8 @@ def test_prepare_layout_roundtrip_and_order():
   T, nb = len(kb), len(tp) - 1
   lanes = np.zeros((T, nat.LANE_WORDS), np.uint64)
   full = np.zeros(T, np.uint32)
-  order = np.zeros(nb, np.int32)
   nat.check(nat.lib().fwn_tiles_prepare(nb, T, n, nat.ptr(tp), nat.ptr(kb), nat.ptr(bits), nat.ptr(lanes),
-                                        nat.ptr(full), nat.ptr(order)))
+                                        nat.ptr(full)))
   dense = ((bits[:, :, :, None] >> np.arange(32, dtype=np.uint32)) & 1).astype(bool).reshape(T, 128, 128)
   np.testing.assert_array_equal(_decode_lanes(lanes, T), dense)
   expect_full = np.zeros(T, np.uint32)
@@ -129,9 +128,54 @@ def test_prepare_layout_roundtrip_and_order():
     expect_full |= dense[:, 32 * w:32 * w + 32].reshape(T, -1).all(1).astype(np.uint32) << w
   np.testing.assert_array_equal(full, expect_full)
   assert full.max() == 15
-  counts = np.diff(tp)
-  assert sorted(order.tolist()) == list(range(nb))
-  assert (np.diff(counts[order]) <= 0).all()
+
+
+def _schedule(tp, max_item_tiles):
+  L = nat.lib()
+  nb = len(tp) - 1
+  counts = np.zeros(3, np.int32)
+  nat.check(L.fwn_tiles_schedule_count(nb, nat.ptr(tp), max_item_tiles, nat.ptr(counts[0:]), nat.ptr(counts[1:]),
+                                       nat.ptr(counts[2:])))
+  n_items, n_parts, n_split = (int(c) for c in counts)
+  items = np.zeros((n_items, 4), np.int32)
+  split = np.zeros((max(n_split, 1), 3), np.int32)
+  nat.check(L.fwn_tiles_schedule_fill(nb, nat.ptr(tp), max_item_tiles, nat.ptr(items), nat.ptr(split)))
+  return items, split[:n_split], n_parts
+
+
+@pytest.mark.parametrize("max_item_tiles", [1, 2, 3, 7, 64, 0, -5])
+def test_schedule_covers_every_tile_once(max_item_tiles):
+  """Work items partition each block's tile run into near-equal pieces of at most max_item_tiles
+  (default FWN_ITEM_TILES = 64 for max_item_tiles <= 0), longest first; split blocks own a
+  contiguous range of partial slots."""
+  rng = np.random.default_rng(3)
+  counts = rng.integers(0, 200, 40)
+  counts[[0, 5]] = 0  # empty blocks still get one item (they write zero rows)
+  counts[7] = 320
+  tp = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+  items, split, n_parts = _schedule(tp, max_item_tiles)
+  cap = max_item_tiles if max_item_tiles > 0 else nat.ITEM_TILES
+  lengths = items[:, 2] - items[:, 1]
+  assert (np.diff(lengths) <= 0).all()
+  assert lengths.max() <= max(cap, 0) or (lengths.max() == 0)
+  covered = np.zeros(tp[-1], np.int32)
+  for blk, t0, t1, part in items:
+    assert tp[blk] <= t0 <= t1 <= tp[blk + 1]
+    covered[t0:t1] += 1
+  assert (covered == 1).all()
+  per_block = np.bincount(items[:, 0], minlength=len(counts))
+  assert (per_block == np.maximum(1, -(-counts // cap))).all()
+  # Slots: whole blocks have part -1; split blocks' items use slots [first, first + count).
+  whole = items[items[:, 3] < 0]
+  assert (per_block[whole[:, 0]] == 1).all()
+  assert sorted(items[items[:, 3] >= 0, 3].tolist()) == list(range(n_parts))
+  for blk, first, cnt in split:
+    mine = items[items[:, 0] == blk]
+    assert sorted(mine[:, 3].tolist()) == list(range(first, first + cnt))
+    ln = mine[:, 2] - mine[:, 1]
+    assert ln.max() - ln.min() <= 1
+  assert len(split) == int((per_block > 1).sum())
+  assert n_parts == int(per_block[per_block > 1].sum())
 
 
 @pytest.mark.parametrize("case", ["ptr0", "decreasing", "col_range", "col_order", "total", "tail_bits"])
@@ -155,9 +199,8 @@ def test_prepare_rejects_malformed_lists(case):
   T, nb = len(kb), len(tp) - 1
   lanes = np.zeros((T, nat.LANE_WORDS), np.uint64)
   full = np.zeros(T, np.uint32)
-  order = np.zeros(nb, np.int32)
   status = nat.lib().fwn_tiles_prepare(nb, T, n, nat.ptr(tp), nat.ptr(kb), nat.ptr(bits), nat.ptr(lanes),
-                                       nat.ptr(full), nat.ptr(order))
+                                       nat.ptr(full))
   assert status == nat.ERR_TILES
   assert nat.lib().fwn_last_error()
 
@@ -169,6 +212,13 @@ def _desc(**kw):
   return nat.AttnDesc(**d)
 
 
+FAKE = 1 << 20  # a device address the launchers never dereference: validation fails first
+
+
+def _tiles(n_blocks=3, n_tiles=0, n_items=3, n_parts=0, n_split=0, ptr=FAKE, items=FAKE, split=None):
+  return nat.Tiles(n_blocks, n_tiles, ptr, None, None, None, n_items, n_parts, n_split, 0, items, split)
+
+
 @pytest.mark.parametrize("kw,code", [
     (dict(head_dim=48), nat.ERR_UNSUPPORTED), (dict(dtype=7), nat.ERR_UNSUPPORTED),
     (dict(n=0), nat.ERR_INVALID_ARG), (dict(scale=0.0), nat.ERR_INVALID_ARG),
@@ -176,28 +226,53 @@ def _desc(**kw):
     (dict(stride_n=32), nat.ERR_INVALID_ARG), (dict(n=40962, stride_n=1 << 16), nat.ERR_INVALID_ARG)])
 def test_launchers_validate_before_launching(kw, code):
   # Every launcher checks its arguments on the host and returns before any HIP call.
-  tiles = nat.Tiles(3, 0, None, None, None, None, None)
+  tiles = _tiles(ptr=None, items=None)
   desc = _desc(**kw)
-  fake = 1 << 20  # never dereferenced: validation fails first
+  fake = FAKE
   L = nat.lib()
-  assert L.fwn_attn_fwd_launch(desc, fake, fake, fake, tiles, fake, None, None) == code
+  assert L.fwn_attn_fwd_launch(desc, fake, fake, fake, tiles, fake, None, None, 0, None) == code
   assert L.fwn_attn_bwd_delta_launch(desc, fake, fake, fake, None) == code
-  assert L.fwn_attn_bwd_dq_launch(desc, fake, fake, fake, fake, fake, fake, tiles, fake, None) == code
-  assert L.fwn_attn_bwd_dkv_launch(desc, fake, fake, fake, fake, fake, fake, tiles, fake, fake, None) == code
+  assert L.fwn_attn_bwd_dq_launch(desc, fake, fake, fake, fake, fake, fake, tiles, fake, None, 0, None) == code
+  assert L.fwn_attn_bwd_dkv_launch(desc, fake, fake, fake, fake, fake, fake, tiles, fake, fake, None, 0, None) == code
 
 
 def test_launchers_reject_bad_pointers_and_tiles():
   L = nat.lib()
   desc = _desc()
-  good_tiles = nat.Tiles(3, 0, 1 << 20, None, None, None, None)
-  assert L.fwn_attn_fwd_launch(desc, None, 1 << 20, 1 << 20, good_tiles, 1 << 20, None, None) == nat.ERR_INVALID_ARG
-  assert L.fwn_attn_fwd_launch(desc, (1 << 20) + 4, 1 << 20, 1 << 20, good_tiles, 1 << 20, None,
-                               None) == nat.ERR_INVALID_ARG
-  wrong_blocks = nat.Tiles(5, 0, 1 << 20, None, None, None, None)
-  assert L.fwn_attn_fwd_launch(desc, 1 << 20, 1 << 20, 1 << 20, wrong_blocks, 1 << 20, None, None) == nat.ERR_TILES
-  missing = nat.Tiles(3, 10, 1 << 20, None, None, None, None)
-  assert L.fwn_attn_fwd_launch(desc, 1 << 20, 1 << 20, 1 << 20, missing, 1 << 20, None, None) == nat.ERR_TILES
+  F = FAKE
+  good = _tiles()
+  assert L.fwn_attn_fwd_launch(desc, None, F, F, good, F, None, None, 0, None) == nat.ERR_INVALID_ARG
+  assert L.fwn_attn_fwd_launch(desc, F + 4, F, F, good, F, None, None, 0, None) == nat.ERR_INVALID_ARG
+  assert L.fwn_attn_fwd_launch(desc, F, F, F, _tiles(n_blocks=5), F, None, None, 0, None) == nat.ERR_TILES
+  assert L.fwn_attn_fwd_launch(desc, F, F, F, _tiles(n_tiles=10), F, None, None, 0, None) == nat.ERR_TILES
   assert "tiles" in L.fwn_last_error().decode()
+  # every block needs a work item; split schedules need their slot table
+  assert L.fwn_attn_fwd_launch(desc, F, F, F, _tiles(n_items=2), F, None, None, 0, None) == nat.ERR_TILES
+  assert L.fwn_attn_fwd_launch(desc, F, F, F, _tiles(items=None), F, None, None, 0, None) == nat.ERR_TILES
+  assert L.fwn_attn_fwd_launch(desc, F, F, F, _tiles(n_items=4, n_parts=2, n_split=1), F, None, None, 0,
+                               None) == nat.ERR_TILES
+  assert L.fwn_attn_fwd_launch(desc, F, F, F, _tiles(n_items=4, n_parts=2), F, None, None, 0, None) == nat.ERR_TILES
+
+
+def test_workspace_size_and_checks():
+  """Split schedules need n_parts * batch * heads * 128 * (2 * head_dim + 2) * 4 bytes of
+  256-byte-aligned workspace; launchers refuse a missing, short or misaligned one."""
+  import ctypes
+  L = nat.lib()
+  F = FAKE
+  desc = _desc(batch=2, heads=3, head_dim=64, stride_b=300 * 3 * 64, stride_n=3 * 64, stride_h=64)
+  split = _tiles(n_items=5, n_parts=3, n_split=1, split=F)
+  size = ctypes.c_uint64(0)
+  nat.check(L.fwn_attn_workspace_size(desc, split, ctypes.byref(size)))
+  need = 3 * 2 * 3 * 128 * (2 * 64 + 2) * 4
+  assert size.value == need
+  nat.check(L.fwn_attn_workspace_size(desc, _tiles(), ctypes.byref(size)))
+  assert size.value == 0
+  for ws, nbytes in [(None, need), (F + 16, need), (F, need - 1)]:
+    assert L.fwn_attn_fwd_launch(desc, F, F, F, split, F, None, ws, nbytes, None) == nat.ERR_INVALID_ARG
+    assert L.fwn_attn_bwd_dq_launch(desc, F, F, F, F, F, F, split, F, ws, nbytes, None) == nat.ERR_INVALID_ARG
+    assert L.fwn_attn_bwd_dkv_launch(desc, F, F, F, F, F, F, split, F, F, ws, nbytes, None) == nat.ERR_INVALID_ARG
+    assert "workspace" in L.fwn_last_error().decode()
 
 
 def test_enable_disable_and_unknown_option():
