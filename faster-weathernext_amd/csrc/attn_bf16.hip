@@ -225,15 +225,19 @@ __global__ void __launch_bounds__(NT, 2) fwd_kernel(KArgs a) {
 }
 
 // ------------------------------------------------------------------------------------------
-// dQ: per query block over the forward tile list (pallas_attn.py:161-184).
+// dQ: per work item of the forward tile list (pallas_attn.py:161-184).
 // P = where(valid, exp(s*scale - lse), 0); dS = P * (dP - delta); dQ = scale * dS K.
-
+//
+// Two workgroups per CU: single K and V buffers (64 KB at D = 128), refilled once every wave is
+// done with the tile, and at most 256 VGPRs per wave; the other resident workgroup computes while
+// the copy is in flight.
 template <int D>
-__global__ void __launch_bounds__(NT, min_blocks<D>()) dq_kernel(KArgs a) {
+__global__ void __launch_bounds__(NT, 2) dq_kernel(KArgs a) {
   constexpr int TB = Tile<D>::BYTES;
-  __shared__ __attribute__((aligned(1024))) char lds0[2 * TB];  // K | V
-  __shared__ __attribute__((aligned(1024))) char lds1[2 * TB];
-  lds_char* bufs[2] = {(lds_char*)lds0, (lds_char*)lds1};
+  __shared__ __attribute__((aligned(1024))) char lk[TB];
+  __shared__ __attribute__((aligned(1024))) char lv[TB];
+  lds_char* K = (lds_char*)lk;
+  lds_char* V = (lds_char*)lv;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int i = lane & 31, g = lane >> 5;
@@ -263,20 +267,13 @@ __global__ void __launch_bounds__(NT, min_blocks<D>()) dq_kernel(KArgs a) {
   tile_range(a, j, t0, t1);
   if (t0 < t1) {
     const int kb = ((ci32_ptr)a.col)[t0];
-    dma.issue(rK, bufs[0], w, kb * BLK, snb);
-    dma.issue(rV, bufs[0] + TB, w, kb * BLK, snb);
+    dma.issue(rK, K, w, kb * BLK, snb);
+    dma.issue(rV, V, w, kb * BLK, snb);
   }
-  auto step = [&](int tt, lds_char* cur, lds_char* nxt) {
+  for (int tt = t0; tt < t1; ++tt) {
     const int t = __builtin_amdgcn_readfirstlane(tt);
     wait_vmem();
     __syncthreads();
-    if (t + 1 < t1) {
-      const int kb = ((ci32_ptr)a.col)[t + 1];
-      dma.issue(rK, nxt, w, kb * BLK, snb);
-      dma.issue(rV, nxt + TB, w, kb * BLK, snb);
-    }
-    const lds_char* K = cur;
-    const lds_char* V = cur + TB;
     const cu64_ptr mk = tile_masks(a, t, w);
 #pragma unroll
     for (int sb = 0; sb < 4; ++sb) {
@@ -313,10 +310,12 @@ __global__ void __launch_bounds__(NT, min_blocks<D>()) dq_kernel(KArgs a) {
         acc[db] = mfma_bf16(kt[db][1], d1, acc[db]);
       }
     }
-  };
-  for (int tt = t0; tt < t1; tt += 2) {
-    step(tt, bufs[0], bufs[1]);
-    if (tt + 1 < t1) step(tt + 1, bufs[1], bufs[0]);
+    __syncthreads();  // every wave is done with K(t) and V(t)
+    if (t + 1 < t1) {
+      const int kb = ((ci32_ptr)a.col)[t + 1];
+      dma.issue(rK, K, w, kb * BLK, snb);
+      dma.issue(rV, V, w, kb * BLK, snb);
+    }
   }
   if (j.part >= 0) {
     store_bwd_partial<D>(a, j, 32 * w + i, acc, 0, g);
