@@ -110,13 +110,18 @@ struct Job {
   int64_t base;  // element offset of (b, h)
 };
 
-// Work items are visited longest first; the (batch, head) index varies fastest, so the heads of
-// one item run side by side and share its mask words in L2.
+// Workgroups are dealt round-robin over the 8 XCDs, each with its own L2. Jobs are ordered
+// (batch, head) major, then work items in block order, and XCD x gets a contiguous range of
+// them, so the workgroups resident on one XCD work on neighbouring blocks of one head and share
+// their K/V tiles in that XCD's L2. The map from workgroup id to job is a bijection for any count.
 __device__ __forceinline__ Job decode_job(const KArgs& a) {
   Job j;
-  const int bh_count = a.batch * a.heads;
-  const int slot = blockIdx.x / bh_count;
-  j.bh = blockIdx.x - slot * bh_count;
+  const int total = a.n_items * a.batch * a.heads;
+  const int pid = blockIdx.x, xcd = pid & 7, local = pid >> 3;
+  const int small = total >> 3, rem = total & 7;
+  const int job = xcd < rem ? xcd * (small + 1) + local : rem * (small + 1) + (xcd - rem) * small + local;
+  j.bh = job / a.n_items;
+  const int slot = job - j.bh * a.n_items;
   const ci32_ptr item = (ci32_ptr)a.items + 4 * slot;
   j.blk = item[0];
   j.t0 = item[1] < 0 ? 0 : item[1];

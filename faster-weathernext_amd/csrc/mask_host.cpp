@@ -402,8 +402,6 @@ int fwn_tiles_schedule_fill(int32_t n_blocks, const int32_t* tile_ptr, int32_t m
       t += len;
     }
   }
-  std::stable_sort(items, items + n_items,
-                   [](const fwn_item& x, const fwn_item& y) { return x.t1 - x.t0 > y.t1 - y.t0; });
   return FWN_OK;
 }
 

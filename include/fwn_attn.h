@@ -83,7 +83,7 @@ typedef struct fwn_tiles {
   int32_t n_parts;          /* partial slots (items with part >= 0) */
   int32_t n_split;          /* blocks cut into more than one item */
   int32_t reserved;         /* 0 */
-  const fwn_item* items;    /* [n_items], longest first */
+  const fwn_item* items;    /* [n_items], in block order */
   const int32_t* split;     /* [n_split * 3]: block, first partial slot, slot count */
 } fwn_tiles;
 
@@ -133,8 +133,9 @@ int fwn_tiles_prepare(int32_t n_blocks, int32_t n_tiles, int32_t n_cols, const i
  * runs of near-equal length (max_item_tiles <= 0 selects FWN_ITEM_TILES). The reference runs one
  * program per block (pallas_attn.py:244-247), so its launch lasts as long as its longest block;
  * splitting bounds every item. Two passes: fwn_tiles_schedule_count gives the sizes,
- * fwn_tiles_schedule_fill writes items[n_items] (longest first, ties by block) and
- * split[n_split * 3] (host buffers). */
+ * fwn_tiles_schedule_fill writes items[n_items] in block order (neighbouring blocks share most of
+ * their key tiles, so running them together keeps those tiles in L2) and split[n_split * 3]
+ * (host buffers). */
 #define FWN_ITEM_TILES 64
 int fwn_tiles_schedule_count(int32_t n_blocks, const int32_t* tile_ptr, int32_t max_item_tiles,
                              int32_t* n_items, int32_t* n_parts, int32_t* n_split);

@@ -146,7 +146,7 @@ def _schedule(tp, max_item_tiles):
 @pytest.mark.parametrize("max_item_tiles", [1, 2, 3, 7, 64, 0, -5])
 def test_schedule_covers_every_tile_once(max_item_tiles):
   """Work items partition each block's tile run into near-equal pieces of at most max_item_tiles
-  (default FWN_ITEM_TILES = 64 for max_item_tiles <= 0), longest first; split blocks own a
+  (default FWN_ITEM_TILES = 64 for max_item_tiles <= 0), in block order; split blocks own a
   contiguous range of partial slots."""
   rng = np.random.default_rng(3)
   counts = rng.integers(0, 200, 40)
@@ -156,7 +156,7 @@ def test_schedule_covers_every_tile_once(max_item_tiles):
   items, split, n_parts = _schedule(tp, max_item_tiles)
   cap = max_item_tiles if max_item_tiles > 0 else nat.ITEM_TILES
   lengths = items[:, 2] - items[:, 1]
-  assert (np.diff(lengths) <= 0).all()
+  assert (np.diff(items[:, 0]) >= 0).all() and (np.diff(items[:, 1]) >= 0).all()
   assert lengths.max() <= max(cap, 0) or (lengths.max() == 0)
   covered = np.zeros(tp[-1], np.int32)
   for blk, t0, t1, part in items:
