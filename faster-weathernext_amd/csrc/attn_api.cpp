@@ -93,7 +93,8 @@ int check_tiles(const fwn_attn_desc* d, const fwn_tiles* t, const char* name) {
   if (t->n_parts < 0 || t->n_split < 0 || (t->n_split > 0 && !t->split) || (t->n_split > 0) != (t->n_parts > 0))
     return fail(FWN_ERR_TILES, "%s: inconsistent split schedule (%d parts, %d split blocks)", name, t->n_parts,
                 t->n_split);
-  if ((int64_t)t->n_items * d->batch * d->heads > INT32_MAX || (int64_t)t->n_split * d->batch * d->heads > INT32_MAX)
+  if ((int64_t)t->n_items * d->batch * d->heads > INT32_MAX ||
+      (int64_t)t->n_split * d->batch * d->heads * (d->head_dim / 16) > INT32_MAX)
     return fail(FWN_ERR_INVALID_ARG, "%s: grid too large", name);
   return FWN_OK;
 }

@@ -7,8 +7,8 @@
 // tiles (pallas_attn.py:128-141). dQ, dK, dV: partial sums over disjoint tile ranges, added and
 // scaled as the kernels scale their direct outputs (pallas_attn.py:184, 214-215).
 //
-// One workgroup per (split block, batch, head); thread t handles row t / 2 and half t % 2 of the
-// columns, reading its 16-byte chunks of every slot.
+// Each thread handles 8 consecutive columns of one row; a (split block, batch, head) takes
+// 128 * D / 8 threads, D / 16 workgroups of 256.
 #include "attn_device.h"
 
 namespace fwn {
@@ -23,11 +23,11 @@ struct Split {
   bool ok;
 };
 
-__device__ __forceinline__ Split decode_split(const KArgs& a) {
+__device__ __forceinline__ Split decode_split(const KArgs& a, int job) {
   Split s;
   const int bh_count = a.batch * a.heads;
-  const int idx = blockIdx.x / bh_count;
-  s.bh = blockIdx.x - idx * bh_count;
+  const int idx = job / bh_count;
+  s.bh = job - idx * bh_count;
   const ci32_ptr e = (ci32_ptr)a.split + 3 * idx;
   s.blk = e[0];
   s.p0 = e[1];
@@ -59,60 +59,74 @@ __device__ __forceinline__ void store4(void* base, int64_t off, const f32x4& x) 
   }
 }
 
+// Workgroups per (split block, batch, head) and this thread's (row, first column).
+template <int D>
+struct Cell {
+  static constexpr int CH = D / 8;                 // 8-column chunks per row
+  static constexpr int WGS = 128 * CH / kThreads;  // D / 16
+  int job, r, d;
+  __device__ __forceinline__ Cell() {
+    job = blockIdx.x / WGS;
+    const int id = (blockIdx.x - job * WGS) * kThreads + threadIdx.x;
+    r = id / CH;
+    d = (id - r * CH) * 8;
+  }
+};
+
 template <typename T, int D>
 __global__ void __launch_bounds__(kThreads) fwd_combine_kernel(KArgs a) {
-  const Split s = decode_split(a);
-  const int r = threadIdx.x >> 1, half = threadIdx.x & 1;
+  const Cell<D> cell;
+  const Split s = decode_split(a, cell.job);
+  const int r = cell.r, d = cell.d;
   const int row = s.blk * BLK + r;
   if (!s.ok || row >= a.n) return;
   float M = -__builtin_inff();
   for (int c = 0; c < s.np; ++c) M = fmaxf(M, slot_ptr<D>(a, s, c)[128 * D + r]);
   const float base = M == -__builtin_inff() ? 0.f : M;
   float L = 0.f;
+  f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0;
   for (int c = 0; c < s.np; ++c) {
     const float* p = slot_ptr<D>(a, s, c);
-    L += p[128 * D + 128 + r] * fast_exp2(p[128 * D + r] - base);
+    const float wgt = fast_exp2(p[128 * D + r] - base);
+    L += p[128 * D + 128 + r] * wgt;
+    acc0 += wgt * *(const f32x4*)(p + r * D + d);
+    acc1 += wgt * *(const f32x4*)(p + r * D + d + 4);
   }
   const float inv = L > 0.f ? 1.f / L : 0.f;
-  const int64_t out_off = (int64_t)s.b * a.sb + (int64_t)s.h * a.sh + (int64_t)row * a.sn;
-#pragma unroll
-  for (int d = half * (D / 2); d < (half + 1) * (D / 2); d += 4) {
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (int c = 0; c < s.np; ++c) {
-      const float* p = slot_ptr<D>(a, s, c);
-      const float wgt = fast_exp2(p[128 * D + r] - base);
-      acc += wgt * *(const f32x4*)(p + r * D + d);
-    }
-    store4<T>(a.out0, out_off + d, acc * inv);
-  }
-  if (half == 0 && a.lse_out)
+  const int64_t out_off = (int64_t)s.b * a.sb + (int64_t)s.h * a.sh + (int64_t)row * a.sn + d;
+  store4<T>(a.out0, out_off, acc0 * inv);
+  store4<T>(a.out0, out_off + 4, acc1 * inv);
+  if (d == 0 && a.lse_out)
     a.lse_out[((int64_t)s.b * a.heads + s.h) * a.n + row] = (M + __builtin_amdgcn_logf(fmaxf(L, 1e-30f))) * LN2;
 }
 
 // dQ (one output, scaled) or dK/dV (two outputs: dK scaled, dV not).
 template <typename T, int D, int OUTS>
 __global__ void __launch_bounds__(kThreads) bwd_combine_kernel(KArgs a) {
-  const Split s = decode_split(a);
-  const int r = threadIdx.x >> 1, half = threadIdx.x & 1;
+  const Cell<D> cell;
+  const Split s = decode_split(a, cell.job);
+  const int r = cell.r, d = cell.d;
   const int row = s.blk * BLK + r;
   if (!s.ok || row >= a.n) return;
-  const int64_t out_off = (int64_t)s.b * a.sb + (int64_t)s.h * a.sh + (int64_t)row * a.sn;
+  const int64_t out_off = (int64_t)s.b * a.sb + (int64_t)s.h * a.sh + (int64_t)row * a.sn + d;
 #pragma unroll
   for (int o = 0; o < OUTS; ++o) {
+    f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0;
+    for (int c = 0; c < s.np; ++c) {
+      const float* p = slot_ptr<D>(a, s, c) + (o * 128 + r) * D + d;
+      acc0 += *(const f32x4*)p;
+      acc1 += *(const f32x4*)(p + 4);
+    }
     const float mul = o == 0 ? a.scale : 1.f;
     void* out = o == 0 ? a.out0 : a.out1;
-#pragma unroll
-    for (int d = half * (D / 2); d < (half + 1) * (D / 2); d += 4) {
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-      for (int c = 0; c < s.np; ++c) acc += *(const f32x4*)(slot_ptr<D>(a, s, c) + (o * 128 + r) * D + d);
-      store4<T>(out, out_off + d, acc * mul);
-    }
+    store4<T>(out, out_off, acc0 * mul);
+    store4<T>(out, out_off + 4, acc1 * mul);
   }
 }
 
 template <typename T, int D>
 hipError_t launch_td(Kind kind, const KArgs& a, hipStream_t stream) {
-  const dim3 grid((unsigned)a.n_split * (unsigned)(a.batch * a.heads)), block(kThreads);
+  const dim3 grid((unsigned)a.n_split * (unsigned)(a.batch * a.heads) * (unsigned)Cell<D>::WGS), block(kThreads);
   switch (kind) {
     case Kind::kFwdCombine: hipLaunchKernelGGL((fwd_combine_kernel<T, D>), grid, block, 0, stream, a); break;
     case Kind::kDqCombine: hipLaunchKernelGGL((bwd_combine_kernel<T, D, 1>), grid, block, 0, stream, a); break;
