@@ -63,10 +63,15 @@ struct TileDma {
   }
 
   __device__ __forceinline__ void issue(rsrc_t r, lds_char* tile, int w, int row0, uint32_t snb) const {
+    // The LDS destinations are loop-invariant; left visible, the compiler keeps all of them in
+    // SGPRs across the tile loop and spills other scalars. The empty asm makes the base opaque,
+    // so each destination is one scalar add at the copy.
+    uint32_t base = (uint32_t)(uintptr_t)tile + (uint32_t)w * 1024u;
+    asm volatile("" : "+s"(base));
 #pragma unroll
     for (int op = 0; op < Tile<D>::OPS_PER_WAVE; ++op) {
       const uint32_t vo = voff + (uint32_t)(row0 + op * 4 * RPO) * snb;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(tile + (op * 4 + w) * 1024),
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(uintptr_t)(base + op * 4096u),
                                                16, (int)vo, 0, 0, 0);
     }
   }
@@ -189,13 +194,19 @@ __global__ void __launch_bounds__(NT, 2) fwd_kernel(KArgs a) {
       for (int k = 0; k < D / 16; ++k) s[sb] = mfma_bf16(ka[k], qf[k], s[sb]);
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[sb][r] = select_lane(m.w[r], s[sb][r], -__builtin_inff());
+      // Apply this sub-block's mask words before the next sub-block's are loaded: all four
+      // sub-blocks' words (128 SGPRs) do not fit next to the kernel's other scalars. The empty asm
+      // consumes the masked values here, so the selects cannot sink to the max below.
+      asm volatile("" : "+v"(s[sb]));
     }
     wait_vmem();      // this wave's part of V(t)
     __syncthreads();  // all of V(t) landed; every wave is done reading K(t)
     if (t + 1 < t1) dma.issue(rK, K, w, ((ci32_ptr)a.col)[t + 1] * BLK, snb);
-    const float corr = softmax_tile(s, st, a.c2);
+    float corr;
+    if (softmax_tile(s, st, a.c2, corr)) {
 #pragma unroll
-    for (int db = 0; db < D / 32; ++db) o[db] *= corr;
+      for (int db = 0; db < D / 32; ++db) o[db] *= corr;
+    }
 #pragma unroll
     for (int sb = 0; sb < 4; ++sb) {
       u32x4 va[D / 32][2];

@@ -174,15 +174,21 @@ __device__ __forceinline__ cu64_ptr tile_masks(const KArgs& a, int t, int w) {
   return (cu64_ptr)a.lanes + ((int64_t)t * 4 + w) * 64;
 }
 
-// Online softmax of the forward kernels. s[sb][r] holds this lane's masked logits (raw q.k, -inf
-// where masked); on return it holds exp2(s*c2 - m). Returns the rescale factor of the running
-// sums.
+// Online softmax of the forward kernels (pallas_attn.py:125-131) with a lazily moved reference
+// max. s[sb][r] holds this lane's masked logits (raw q.k, -inf where masked); on return it holds
+// p = exp2(s*c2 - m) for the lane's reference max m. m moves only when some lane of the wave sees
+// a logit more than kLazyMax above its m (a wave-uniform decision); otherwise p <= 2^kLazyMax,
+// the accumulators keep their scale and the caller skips the rescale. O and l always share m, so
+// O / l and lse = m + log2 l are unchanged up to rounding. Returns true when m moved; `corr` is
+// then the factor the caller applies to its accumulators (l is rescaled here).
+constexpr float kLazyMax = 8.f;
+
 struct SoftmaxState {
-  float m;  // running max of s*c2 (log2 domain), -inf before the first valid key
+  float m;  // reference max of s*c2 (log2 domain), -inf before the first valid key
   float l;  // running sum of exp2(s*c2 - m) over this lane's half of the keys
 };
 
-__device__ __forceinline__ float softmax_tile(f32x16 (&s)[4], SoftmaxState& st, float c2) {
+__device__ __forceinline__ bool softmax_tile(f32x16 (&s)[4], SoftmaxState& st, float c2, float& corr) {
   const float ninf = -__builtin_inff();
   float mx = s[0][0];
 #pragma unroll
@@ -190,9 +196,16 @@ __device__ __forceinline__ float softmax_tile(f32x16 (&s)[4], SoftmaxState& st, 
 #pragma unroll
     for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[sb][r]);
   mx = fmaxf(mx, __shfl_xor(mx, 32));
-  const float m_new = fmaxf(st.m, mx * c2);
-  const float base = m_new == ninf ? 0.f : m_new;
-  const float corr = fast_exp2(st.m - base);
+  const float mxs = mx * c2;
+  corr = 1.f;
+  const bool moved = __builtin_amdgcn_ballot_w64(mxs > st.m + kLazyMax) != 0;
+  if (moved) {
+    const float m_new = fmaxf(st.m, mxs);
+    corr = fast_exp2(st.m - (m_new == ninf ? 0.f : m_new));
+    st.l *= corr;
+    st.m = m_new;
+  }
+  const float base = st.m == ninf ? 0.f : st.m;
   float sum = 0.f;
 #pragma unroll
   for (int sb = 0; sb < 4; ++sb)
@@ -202,9 +215,8 @@ __device__ __forceinline__ float softmax_tile(f32x16 (&s)[4], SoftmaxState& st, 
       s[sb][r] = p;
       sum += p;
     }
-  st.l = st.l * corr + sum;
-  st.m = m_new;
-  return corr;
+  st.l += sum;
+  return moved;
 }
 
 // Natural log-sum-exp of the scaled logits: (m + log2 l) * ln 2 (pallas_attn.py:140-141).

@@ -121,9 +121,11 @@ __global__ void __launch_bounds__(NT, 1) fwd_f32_kernel(KArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[sb][r] = select_lane(m.w[r], s[sb][r], -__builtin_inff());
     }
-    const float corr = softmax_tile(s, st, a.c2);
+    float corr;
+    if (softmax_tile(s, st, a.c2, corr)) {
 #pragma unroll
-    for (int db = 0; db < D / 32; ++db) o[db] *= corr;
+      for (int db = 0; db < D / 32; ++db) o[db] *= corr;
+    }
 #pragma unroll
     for (int sb = 0; sb < 4; ++sb)
 #pragma unroll
