@@ -170,34 +170,31 @@ __global__ void __launch_bounds__(NT, 2) fwd_kernel(KArgs a) {
 
   int t0, t1;
   tile_range(a, j, t0, t1);
+  u32x2 mbits = {0u, 0u};  // mask bits of the next tile, loaded a tile ahead
   if (t0 < t1) {
     const int kb = ((ci32_ptr)a.col)[t0];
+    mbits = tile_bits(a, t0, w, lane);
     dma.issue(rK, K, w, kb * BLK, snb);
-    wait_vmem();  // K(t0) and the Q fragment
+    wait_vmem();  // K(t0), its mask bits and the Q fragment
     dma.issue(rV, V, w, kb * BLK, snb);
   }
   __syncthreads();
   for (int tt = t0; tt < t1; ++tt) {
     const int t = __builtin_amdgcn_readfirstlane(tt);
     // K(t) is in LDS for every wave here; V(t) may still be in flight.
-    const cu64_ptr mk = tile_masks(a, t, w);
+    const u32x2 mb = mbits;
+    if (t + 1 < t1) mbits = tile_bits(a, t + 1, w, lane);
     f32x16 s[4];
 #pragma unroll
     for (int sb = 0; sb < 4; ++sb) {
       u32x4 ka[D / 16];
 #pragma unroll
       for (int k = 0; k < D / 16; ++k) ka[k] = row_read(K, off.row[k] + sb * 32 * (2 * D));
-      SubMask m;
-      m.load(mk, sb);
       s[sb] = zero16();
 #pragma unroll
       for (int k = 0; k < D / 16; ++k) s[sb] = mfma_bf16(ka[k], qf[k], s[sb]);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) s[sb][r] = select_lane(m.w[r], s[sb][r], -__builtin_inff());
-      // Apply this sub-block's mask words before the next sub-block's are loaded: all four
-      // sub-blocks' words (128 SGPRs) do not fit next to the kernel's other scalars. The empty asm
-      // consumes the masked values here, so the selects cannot sink to the max below.
-      asm volatile("" : "+v"(s[sb]));
+      for (int r = 0; r < 16; ++r) s[sb][r] = keep_or_ninf(s[sb][r], elem_keep(mb, sb, r));
     }
     wait_vmem();      // this wave's part of V(t)
     __syncthreads();  // all of V(t) landed; every wave is done reading K(t)
@@ -276,8 +273,10 @@ __global__ void __launch_bounds__(NT, 2) dq_kernel(KArgs a) {
 
   int t0, t1;
   tile_range(a, j, t0, t1);
+  u32x2 mbits = {0u, 0u};  // mask bits of the next tile, loaded with its copy
   if (t0 < t1) {
     const int kb = ((ci32_ptr)a.col)[t0];
+    mbits = tile_bits(a, t0, w, lane);
     dma.issue(rK, K, w, kb * BLK, snb);
     dma.issue(rV, V, w, kb * BLK, snb);
   }
@@ -285,7 +284,7 @@ __global__ void __launch_bounds__(NT, 2) dq_kernel(KArgs a) {
     const int t = __builtin_amdgcn_readfirstlane(tt);
     wait_vmem();
     __syncthreads();
-    const cu64_ptr mk = tile_masks(a, t, w);
+    const u32x2 mb = mbits;
 #pragma unroll
     for (int sb = 0; sb < 4; ++sb) {
       u32x4 ka[D / 16], va[D / 16];
@@ -294,8 +293,6 @@ __global__ void __launch_bounds__(NT, 2) dq_kernel(KArgs a) {
         ka[k] = row_read(K, off.row[k] + sb * 32 * (2 * D));
         va[k] = row_read(V, off.row[k] + sb * 32 * (2 * D));
       }
-      SubMask m;
-      m.load(mk, sb);
       __builtin_amdgcn_sched_barrier(0);
       f32x16 s = zero16(), dp = zero16();
 #pragma unroll
@@ -311,7 +308,7 @@ __global__ void __launch_bounds__(NT, 2) dq_kernel(KArgs a) {
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float p = select_lane(m.w[r], fast_exp2(fmaf(s[r], a.c2, -lse_t)), 0.f);
+        const float p = keep_or_zero(fast_exp2(fmaf(s[r], a.c2, -lse_t)), elem_keep(mb, sb, r));
         dp[r] = p * (dp[r] - delta);
       }
       const bf16x8 d0 = pack_bf16(dp, 0), d1 = pack_bf16(dp, 1);
@@ -324,6 +321,7 @@ __global__ void __launch_bounds__(NT, 2) dq_kernel(KArgs a) {
     __syncthreads();  // every wave is done with K(t) and V(t)
     if (t + 1 < t1) {
       const int kb = ((ci32_ptr)a.col)[t + 1];
+      mbits = tile_bits(a, t + 1, w, lane);
       dma.issue(rK, K, w, kb * BLK, snb);
       dma.issue(rV, V, w, kb * BLK, snb);
     }
@@ -393,7 +391,11 @@ __global__ void __launch_bounds__(NT, min_blocks<D>()) dkv_kernel(KArgs a) {
                                                (int)(lane < 32 ? kPastEnd : vo), 0, 0, 0);
     }
   };
-  if (t0 < t1) issue(t0, bufs[0]);
+  u32x2 mbits = {0u, 0u};  // mask bits of the next tile, loaded with its copy
+  if (t0 < t1) {
+    mbits = tile_bits(a, t0, w, lane);
+    issue(t0, bufs[0]);
+  }
   auto step = [&](int tt, lds_char* cur, lds_char* nxt) {
     const int t = __builtin_amdgcn_readfirstlane(tt);
     wait_vmem();
@@ -404,12 +406,15 @@ __global__ void __launch_bounds__(NT, min_blocks<D>()) dkv_kernel(KArgs a) {
       *l4 = *l4 * LOG2E;
     }
     __syncthreads();
-    if (t + 1 < t1) issue(t + 1, nxt);
+    const u32x2 mb = mbits;
+    if (t + 1 < t1) {
+      mbits = tile_bits(a, t + 1, w, lane);
+      issue(t + 1, nxt);
+    }
     const lds_char* Q = cur;
     const lds_char* O = cur + TB;
     const __attribute__((address_space(3))) float* L = (const __attribute__((address_space(3))) float*)(cur + 2 * TB);
     const __attribute__((address_space(3))) float* Dl = L + 2 * BLK;
-    const cu64_ptr mk = tile_masks(a, t, w);
 #pragma unroll
     for (int sb = 0; sb < 4; ++sb) {
       u32x4 qa[D / 16], oa[D / 16];
@@ -418,8 +423,6 @@ __global__ void __launch_bounds__(NT, min_blocks<D>()) dkv_kernel(KArgs a) {
         qa[k] = row_read(Q, off.row[k] + sb * 32 * (2 * D));
         oa[k] = row_read(O, off.row[k] + sb * 32 * (2 * D));
       }
-      SubMask m;
-      m.load(mk, sb);
       // Statistics of the 16 queries in this lane's accumulator rows: 32*sb + 16*c + 8*g + 0..7.
       f32x4 lr[4], dr[4];
 #pragma unroll
@@ -447,7 +450,7 @@ __global__ void __launch_bounds__(NT, min_blocks<D>()) dkv_kernel(KArgs a) {
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float p = select_lane(m.w[r], fast_exp2(fmaf(s[r], a.c2, -lr[r >> 2][r & 3])), 0.f);
+        const float p = keep_or_zero(fast_exp2(fmaf(s[r], a.c2, -lr[r >> 2][r & 3])), elem_keep(mb, sb, r));
         s[r] = p;
         dp[r] = p * (dp[r] - dr[r >> 2][r & 3]);
       }

@@ -11,8 +11,10 @@
 //     contraction. P and dS therefore go from accumulator to MFMA operand in registers.
 //   - Global memory is read through raw buffer resources, one per (batch, head) slice; the
 //     hardware range check returns zeros for rows >= n and drops their stores.
-//   - Tile masks are one 64-bit lane mask per accumulator element (fwn_tiles_prepare), loaded
-//     with scalar loads through the constant address space and applied with one v_cndmask.
+//   - Tile masks are one 64-bit word per lane and wave (fwn_tiles_prepare): bit e says whether
+//     accumulator element e (sub-block e / 16, register e % 16) of this lane is a valid key. A
+//     wave fetches its 512 bytes per tile with one coalesced vector load, issued a tile ahead;
+//     a valid element is kept with a sign-extracted bit and one AND or bitfield insert.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -67,13 +69,6 @@ __device__ __forceinline__ f32x16 zero16() {
   return z;
 }
 
-// Bit `lane` of the wave-uniform mask `sel` ? x : y. inverse_ballot turns the 64-bit SGPR mask
-// into the per-lane condition, so this is one v_cndmask with the SGPR pair as its selector, and
-// (unlike inline assembly) the compiler sees the operands and inserts the wait states an MFMA
-// result needs before a VALU read.
-__device__ __forceinline__ float select_lane(uint64_t sel, float x, float y) {
-  return __builtin_amdgcn_inverse_ballot_w64(sel) ? x : y;
-}
 
 // Waits for every outstanding vector-memory operation (s_waitcnt vmcnt(0); expcnt and lgkmcnt
 // left free).
@@ -160,18 +155,29 @@ __device__ __forceinline__ int64_t stat_index(const KArgs& a, const Job& j, int 
   return ((int64_t)j.b * a.heads + j.h) * a.n + row;
 }
 
-// The 16 lane masks of sub-block sb of a tile (scalar loads). Fully valid tiles hold all-ones
-// words, so masks are applied unconditionally: one v_cndmask per element and no branch.
-struct SubMask {
-  uint64_t w[16];
-  __device__ __forceinline__ void load(cu64_ptr mk, int sb) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) w[r] = mk[sb * 16 + r];
-  }
-};
+// This lane's validity bits for tile t (wave w): bit e = element e. Fully valid tiles hold
+// all-ones words, so masks are applied unconditionally (no branch).
+__device__ __forceinline__ u32x2 tile_bits(const KArgs& a, int t, int w, int lane) {
+  return *(const u32x2*)(a.lanes + ((int64_t)t * 4 + w) * 64 + lane);
+}
 
-__device__ __forceinline__ cu64_ptr tile_masks(const KArgs& a, int t, int w) {
-  return (cu64_ptr)a.lanes + ((int64_t)t * 4 + w) * 64;
+// All ones if element (sb, r) is valid for this lane, else 0: one v_bfe_i32 of one bit.
+__device__ __forceinline__ uint32_t elem_keep(const u32x2& bits, int sb, int r) {
+  const int e = 16 * sb + r;
+  return __builtin_amdgcn_sbfe(bits[e >> 5], (uint32_t)(e & 31), 1u);
+}
+
+// x where kept, -inf elsewhere (one v_bitop3_b32).
+__device__ __forceinline__ float keep_or_ninf(float x, uint32_t keep) {
+  return __builtin_bit_cast(float, (__builtin_bit_cast(uint32_t, x) & keep) | (0xff800000u & ~keep));
+}
+
+// x where kept, +0 elsewhere (one v_and_b32). The empty asm hides that `keep` is a sign-extended
+// bit; otherwise the compiler turns the AND into a bit test, a compare and a v_cndmask (three
+// instructions and a VCC hazard instead of one).
+__device__ __forceinline__ float keep_or_zero(float x, uint32_t keep) {
+  asm("" : "+v"(keep));
+  return __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, x) & keep);
 }
 
 // Online softmax of the forward kernels (pallas_attn.py:125-131) with a lazily moved reference

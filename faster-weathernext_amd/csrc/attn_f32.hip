@@ -101,16 +101,14 @@ __global__ void __launch_bounds__(NT, 1) fwd_f32_kernel(KArgs a) {
   for (int tt = t0; tt < t1; ++tt) {
     const int t = __builtin_amdgcn_readfirstlane(tt);
     const int kb = ((ci32_ptr)a.col)[t];
+    const u32x2 mb = tile_bits(a, t, w, lane);  // lands while the tile is staged
     __syncthreads();
     stage_rows_f32<D>(ldsK, rK, kb * BLK, snb, tid, true);
     stage_rows_f32<D>(ldsV, rV, kb * BLK, snb, tid, false);
     __syncthreads();
-    const cu64_ptr mk = (cu64_ptr)a.lanes + ((int64_t)t * 4 + w) * 64;
     f32x16 s[4];
 #pragma unroll
     for (int sb = 0; sb < 4; ++sb) {
-      SubMask m;
-      m.load(mk, sb);
       s[sb] = zero16();
 #pragma unroll
       for (int u = 0; u < D / 8; ++u) {
@@ -119,7 +117,7 @@ __global__ void __launch_bounds__(NT, 1) fwd_f32_kernel(KArgs a) {
         for (int e = 0; e < 4; ++e) s[sb] = mfma_f32(kx[e], qf[u][e], s[sb]);
       }
 #pragma unroll
-      for (int r = 0; r < 16; ++r) s[sb][r] = select_lane(m.w[r], s[sb][r], -__builtin_inff());
+      for (int r = 0; r < 16; ++r) s[sb][r] = keep_or_ninf(s[sb][r], elem_keep(mb, sb, r));
     }
     float corr;
     if (softmax_tile(s, st, a.c2, corr)) {
@@ -181,15 +179,13 @@ __global__ void __launch_bounds__(NT, 1) dq_f32_kernel(KArgs a) {
   for (int tt = t0; tt < t1; ++tt) {
     const int t = __builtin_amdgcn_readfirstlane(tt);
     const int kb = ((ci32_ptr)a.col)[t];
+    const u32x2 mb = tile_bits(a, t, w, lane);  // lands while the tile is staged
     __syncthreads();
     stage_rows_f32<D>(ldsK, rK, kb * BLK, snb, tid, true);
     stage_rows_f32<D>(ldsV, rV, kb * BLK, snb, tid, true);
     __syncthreads();
-    const cu64_ptr mk = (cu64_ptr)a.lanes + ((int64_t)t * 4 + w) * 64;
 #pragma unroll
     for (int sb = 0; sb < 4; ++sb) {
-      SubMask m;
-      m.load(mk, sb);
       f32x16 s = zero16(), dp = zero16();
 #pragma unroll
       for (int u = 0; u < D / 8; ++u) {
@@ -204,7 +200,7 @@ __global__ void __launch_bounds__(NT, 1) dq_f32_kernel(KArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         float p = fast_exp2(fmaf(s[r], a.c2, -lse_t));
-        p = select_lane(m.w[r], p, 0.f);
+        p = keep_or_zero(p, elem_keep(mb, sb, r));
         dp[r] = p * (dp[r] - delta);
       }
 #pragma unroll
@@ -260,6 +256,7 @@ __global__ void __launch_bounds__(NT, 1) dkv_f32_kernel(KArgs a) {
   for (int tt = t0; tt < t1; ++tt) {
     const int t = __builtin_amdgcn_readfirstlane(tt);
     const int qb = ((ci32_ptr)a.col)[t];
+    const u32x2 mb = tile_bits(a, t, w, lane);  // lands while the tile is staged
     __syncthreads();
     stage_rows_f32<D>(ldsQ, rQ, qb * BLK, snb, tid, true);
     stage_rows_f32<D>(ldsO, rO, qb * BLK, snb, tid, true);
@@ -270,11 +267,8 @@ __global__ void __launch_bounds__(NT, 1) dkv_f32_kernel(KArgs a) {
       (tid < BLK ? ldsL : ldsDl)[tid & (BLK - 1)] = stat;
     }
     __syncthreads();
-    const cu64_ptr mk = (cu64_ptr)a.lanes + ((int64_t)t * 4 + w) * 64;
 #pragma unroll
     for (int sb = 0; sb < 4; ++sb) {
-      SubMask m;
-      m.load(mk, sb);
       f32x16 s = zero16(), dp = zero16();
 #pragma unroll
       for (int u = 0; u < D / 8; ++u) {
@@ -290,7 +284,7 @@ __global__ void __launch_bounds__(NT, 1) dkv_f32_kernel(KArgs a) {
       for (int r = 0; r < 16; ++r) {
         const int qq = element_col(sb, r, g);
         float p = fast_exp2(fmaf(s[r], a.c2, -ldsL[qq]));
-        p = select_lane(m.w[r], p, 0.f);
+        p = keep_or_zero(p, elem_keep(mb, sb, r));
         s[r] = p;
         dp[r] = p * (dp[r] - ldsDl[qq]);
       }

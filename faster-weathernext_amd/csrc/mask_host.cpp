@@ -331,15 +331,14 @@ int fwn_tiles_prepare(int32_t n_blocks, int32_t n_tiles, int32_t n_cols, const i
         for (int32_t r = 32 * w; r < 32 * w + 32 && all; ++r)
           for (int32_t x = 0; x < words; ++x) all = all && bits[r * words + x] == 0xffffffffu;
         if (all) f |= 1u << w;
-        for (int32_t el = 0; el < 64; ++el) {
-          const int32_t sb = el >> 4, reg = el & 15;
+        for (int32_t lane = 0; lane < 64; ++lane) {
+          const int32_t row = 32 * w + (lane & 31);
           uint64_t word = 0;
-          for (int32_t lane = 0; lane < 64; ++lane) {
-            const int32_t row = 32 * w + (lane & 31);
-            const int32_t key = fwn::element_col(sb, reg, lane >> 5);
-            word |= (uint64_t)((bits[row * words + key / 32] >> (key % 32)) & 1u) << lane;
+          for (int32_t el = 0; el < 64; ++el) {
+            const int32_t key = fwn::element_col(el >> 4, el & 15, lane >> 5);
+            word |= (uint64_t)((bits[row * words + key / 32] >> (key % 32)) & 1u) << el;
           }
-          lanes[t * FWN_LANE_WORDS + w * 64 + el] = word;
+          lanes[t * FWN_LANE_WORDS + w * 64 + lane] = word;
         }
       }
       full[t] = f;

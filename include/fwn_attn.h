@@ -30,7 +30,7 @@ extern "C" {
 
 #define FWN_BLOCK 128
 #define FWN_WAVES 4                       /* waves per workgroup; each owns 32 rows of a block */
-#define FWN_LANE_WORDS (FWN_WAVES * 64)   /* uint64 lane-mask words per tile */
+#define FWN_LANE_WORDS (FWN_WAVES * 64)   /* uint64 mask words per tile: one per lane of each wave */
 
 typedef enum fwn_status {
   FWN_OK = 0,
@@ -77,7 +77,7 @@ typedef struct fwn_tiles {
   int32_t n_tiles;          /* live tiles */
   const int32_t* ptr;       /* [n_blocks + 1] */
   const int32_t* col;       /* [n_tiles] column block of each tile */
-  const uint64_t* lanes;    /* [n_tiles * FWN_LANE_WORDS] */
+  const uint64_t* lanes;    /* [n_tiles][FWN_WAVES][64 lanes]: bit e = accumulator element e of that lane */
   const uint32_t* full;     /* [n_tiles] bit w: rows 32w..32w+31 of the tile are all valid */
   int32_t n_items;          /* work items: every block appears, empty blocks included */
   int32_t n_parts;          /* partial slots (items with part >= 0) */

@@ -97,15 +97,15 @@ def test_tile_list_matches_oracle(n, density, permute):
 def _decode_lanes(lanes, n_tiles):
   """Inverse of fwn_tiles_prepare's lane layout, written from the layout's definition."""
   bits = np.zeros((n_tiles, 128, 128), bool)
-  lanes = lanes.reshape(n_tiles, 4, 4, 16)  # tile, wave, sub-block, register
+  lanes = lanes.reshape(n_tiles, 4, 64)  # tile, wave, lane; bit e = element e = (sub-block, register)
   for w in range(4):
-    for sb in range(4):
-      for r in range(16):
-        word = lanes[:, w, sb, r]
-        for lane in range(64):
-          row = 32 * w + (lane & 31)
+    for lane in range(64):
+      word = lanes[:, w, lane]
+      row = 32 * w + (lane & 31)
+      for sb in range(4):
+        for r in range(16):
           col = 32 * sb + 16 * (r >> 3) + 8 * (lane >> 5) + (r & 7)
-          bits[:, row, col] = (word >> np.uint64(lane)) & np.uint64(1)
+          bits[:, row, col] = (word >> np.uint64(16 * sb + r)) & np.uint64(1)
   return bits
 
 
