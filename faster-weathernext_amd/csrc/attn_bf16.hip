@@ -129,11 +129,6 @@ __device__ __forceinline__ void load_frag(u32x4 (&f)[D / 16], rsrc_t r, int row,
   for (int s = 0; s < D / 16; ++s) f[s] = bload16(r, (uint32_t)row * snb + (uint32_t)(32 * s + 16 * g));
 }
 
-template <int D>
-constexpr int min_blocks() {
-  return D <= 64 ? 2 : 1;
-}
-
 // ------------------------------------------------------------------------------------------
 // Forward: per work item (a run of a query block's live tiles), O^T += V^T P^T with an online
 // softmax (pallas_attn.py:112-141).
@@ -334,20 +329,30 @@ __global__ void __launch_bounds__(NT, 2) dq_kernel(KArgs a) {
 }
 
 // ------------------------------------------------------------------------------------------
-// dK/dV: per key block over the transposed tile list; each workgroup owns its dK/dV rows, so
-// there are no atomics (pallas_attn.py:187-215). The tile's 128 log-sum-exps and deltas are
-// copied next to its Q and dO tiles; the log-sum-exps are rescaled to the log2 domain once per
-// tile in LDS.
+// dK/dV: per work item of the transposed tile list; each workgroup owns its dK/dV rows, so there
+// are no atomics (pallas_attn.py:187-215). The tile's 128 log-sum-exps and deltas are copied next
+// to its Q and dO tiles; the log-sum-exps are rescaled to the log2 domain once per tile in LDS.
+//
+// The work is split by role over 8 waves. Waves w and w + 4 (one SIMD) own the same 32
+// keys: wave w computes S^T = K Q^T, P and dV += P^T dO; wave w + 4 computes dP^T = V dO^T and,
+// with wave w's P handed over through LDS, dS = P (dP - delta) and dK += dS^T Q. Each wave issues
+// half of the MFMAs and holds half of the persistent state, so two waves share each SIMD and one's
+// VALU work overlaps the other's MFMAs.
+constexpr int NT8 = 512;
 
 template <int D>
-__global__ void __launch_bounds__(NT, min_blocks<D>()) dkv_kernel(KArgs a) {
+__global__ void __launch_bounds__(NT8, 1) dkv_kernel(KArgs a) {
   constexpr int TB = Tile<D>::BYTES;
   constexpr int BUF = 2 * TB + 1536;
+  constexpr int PSLOT = 64 * 32;  // one wave's P of one sub-block: 64 lanes x 16 bf16
   __shared__ __attribute__((aligned(1024))) char lds0[BUF];  // Q | dO | lse[128] | gap | delta[128]
   __shared__ __attribute__((aligned(1024))) char lds1[BUF];
+  __shared__ __attribute__((aligned(1024))) char lp[4 * 2 * PSLOT];  // [key sub-block][parity]
   lds_char* bufs[2] = {(lds_char*)lds0, (lds_char*)lds1};
   const int tid = threadIdx.x, lane = tid & 63;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int w = wid & 3;        // key sub-block
+  const bool kw = wid >= 4;     // dK wave (else dV wave)
   const int i = lane & 31, g = lane >> 5;
   const Job j = decode_job(a);
   const uint32_t snb = (uint32_t)a.sn * 2;
@@ -357,32 +362,26 @@ __global__ void __launch_bounds__(NT, min_blocks<D>()) dkv_kernel(KArgs a) {
   const rsrc_t rD = make_rsrc(a.delta + stat_index(a, j, 0), (uint32_t)a.n * 4);
 
   const int krow = j.blk * BLK + 32 * w + i;  // this lane's key
-  u32x4 kf[D / 16], vf[D / 16];
-  load_frag<D>(kf, make_rsrc((const uint16_t*)a.k + j.base, a.slice_bytes), krow, snb, g);
-  load_frag<D>(vf, make_rsrc((const uint16_t*)a.v + j.base, a.slice_bytes), krow, snb, g);
+  u32x4 frag[D / 16];                          // K (dV waves) or V (dK waves)
+  load_frag<D>(frag, make_rsrc((const uint16_t*)(kw ? a.v : a.k) + j.base, a.slice_bytes), krow, snb, g);
   Off<D> off;
   off.init(lane);
   TileDma<D> dma;
   dma.init(w, lane, snb);
-  f32x16 dk[D / 32], dv[D / 32];
+  f32x16 acc[D / 32];
 #pragma unroll
-  for (int db = 0; db < D / 32; ++db) {
-    dk[db] = zero16();
-    dv[db] = zero16();
-  }
+  for (int db = 0; db < D / 32; ++db) acc[db] = zero16();
+  lds_char* pslot = (lds_char*)lp + w * 2 * PSLOT + lane * 32;
 
   int t0, t1;
   tile_range(a, j, t0, t1);
-  // Wave 0 also copies the tile's statistics with two full-wave copies and no branch: the first
-  // (log-sum-exps) lands at stats + 16 * lane, the second (deltas) at stats + 512 + 16 * lane.
-  // Lanes 0-31 of the first and 32-63 of the second carry the data; the other halves address
-  // past the end of their buffer, read zeros and land in the 512-byte gap.
   constexpr uint32_t kPastEnd = 0x7FFFFFF0u;
+  // The dV waves copy the tiles, their statistics and their mask bits.
   auto issue = [&](int t, lds_char* buf) {
     const int qb = ((ci32_ptr)a.col)[t];
     dma.issue(rQ, buf, w, qb * BLK, snb);
     dma.issue(rO, buf + TB, w, qb * BLK, snb);
-    if (w == 0) {
+    if (wid == 0) {
       const uint32_t vo = (uint32_t)(qb * BLK + 4 * (lane & 31)) * 4;
       lds_char* stats = buf + 2 * TB;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rL, (__attribute__((address_space(3))) void*)stats, 16,
@@ -391,17 +390,25 @@ __global__ void __launch_bounds__(NT, min_blocks<D>()) dkv_kernel(KArgs a) {
                                                (int)(lane < 32 ? kPastEnd : vo), 0, 0, 0);
     }
   };
-  u32x2 mbits = {0u, 0u};  // mask bits of the next tile, loaded with its copy
-  if (t0 < t1) {
+  auto stats4 = [&](const lds_char* cur, int off_bytes, int sb, f32x4 (&x)[4]) {
+    const __attribute__((address_space(3))) float* p =
+        (const __attribute__((address_space(3))) float*)(cur + 2 * TB + off_bytes);
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+        x[2 * c + hh] = *(const __attribute__((address_space(3))) f32x4*)(p + 32 * sb + 16 * c + 8 * g + 4 * hh);
+  };
+  u32x2 mbits = {0u, 0u};
+  if (t0 < t1 && !kw) {
     mbits = tile_bits(a, t0, w, lane);
     issue(t0, bufs[0]);
   }
-  auto step = [&](int tt, lds_char* cur, lds_char* nxt) {
+  // Per tile both roles pass 5 barriers: tile start, then one per sub-block (P written / read).
+  auto dv_step = [&](int tt, lds_char* cur, lds_char* nxt) {
     const int t = __builtin_amdgcn_readfirstlane(tt);
     wait_vmem();
-    if (w == 0 && lane < 32) {
-      // Wave 0 copied the statistics; it converts the 128 log-sum-exps to the log2 domain in
-      // place (one multiply per 4 rows here instead of one per element in every wave).
+    if (wid == 0 && lane < 32) {
       __attribute__((address_space(3))) f32x4* l4 = (__attribute__((address_space(3))) f32x4*)(cur + 2 * TB) + lane;
       *l4 = *l4 * LOG2E;
     }
@@ -413,69 +420,99 @@ __global__ void __launch_bounds__(NT, min_blocks<D>()) dkv_kernel(KArgs a) {
     }
     const lds_char* Q = cur;
     const lds_char* O = cur + TB;
-    const __attribute__((address_space(3))) float* L = (const __attribute__((address_space(3))) float*)(cur + 2 * TB);
-    const __attribute__((address_space(3))) float* Dl = L + 2 * BLK;
+    // P of sub-block sb, written to its LDS slot for the dK wave; kept in registers for dV.
+    auto make_p = [&](int sb, bf16x8& p0, bf16x8& p1) {
+      u32x4 qa[D / 16];
+#pragma unroll
+      for (int k = 0; k < D / 16; ++k) qa[k] = row_read(Q, off.row[k] + sb * 32 * (2 * D));
+      f32x4 lr[4];
+      stats4(cur, 0, sb, lr);
+      f32x16 sv = zero16();
+#pragma unroll
+      for (int k = 0; k < D / 16; ++k) sv = mfma_bf16(qa[k], frag[k], sv);
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        sv[r] = keep_or_zero(fast_exp2(fmaf(sv[r], a.c2, -lr[r >> 2][r & 3])), elem_keep(mb, sb, r));
+      p0 = pack_bf16(sv, 0);
+      p1 = pack_bf16(sv, 1);
+      lds_char* ps = pslot + (sb & 1) * PSLOT;
+      *(__attribute__((address_space(3))) bf16x8*)ps = p0;
+      *(__attribute__((address_space(3))) bf16x8*)(ps + 16) = p1;
+    };
+    // P runs one sub-block ahead: between two barriers this wave issues dV(sb) and S(sb + 1)
+    // while the dK wave issues dK(sb) and dP(sb + 1).
+    bf16x8 pc0, pc1;
+    make_p(0, pc0, pc1);
 #pragma unroll
     for (int sb = 0; sb < 4; ++sb) {
-      u32x4 qa[D / 16], oa[D / 16];
-#pragma unroll
-      for (int k = 0; k < D / 16; ++k) {
-        qa[k] = row_read(Q, off.row[k] + sb * 32 * (2 * D));
-        oa[k] = row_read(O, off.row[k] + sb * 32 * (2 * D));
-      }
-      // Statistics of the 16 queries in this lane's accumulator rows: 32*sb + 16*c + 8*g + 0..7.
-      f32x4 lr[4], dr[4];
-#pragma unroll
-      for (int c = 0; c < 2; ++c)
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          const int q0 = 32 * sb + 16 * c + 8 * g + 4 * hh;
-          lr[2 * c + hh] = *(const __attribute__((address_space(3))) f32x4*)(L + q0);
-          dr[2 * c + hh] = *(const __attribute__((address_space(3))) f32x4*)(Dl + q0);
-        }
-      f32x16 s = zero16(), dp = zero16();
-#pragma unroll
-      for (int k = 0; k < D / 16; ++k) {
-        s = mfma_bf16(qa[k], kf[k], s);
-        dp = mfma_bf16(oa[k], vf[k], dp);
-      }
-      u32x4 qt[D / 32][2], ot[D / 32][2];
+      u32x4 ot[D / 32][2];
 #pragma unroll
       for (int db = 0; db < D / 32; ++db)
 #pragma unroll
-        for (int c = 0; c < 2; ++c) {
-          qt[db][c] = tr_operand<D>(Q, off, db, sb, c);
-          ot[db][c] = tr_operand<D>(O, off, db, sb, c);
-        }
-      __builtin_amdgcn_sched_barrier(0);
+        for (int c = 0; c < 2; ++c) ot[db][c] = tr_operand<D>(O, off, db, sb, c);
+      __syncthreads();  // P(sb) is in LDS for the dK wave
+#pragma unroll
+      for (int db = 0; db < D / 32; ++db) {
+        acc[db] = mfma_bf16(ot[db][0], pc0, acc[db]);
+        acc[db] = mfma_bf16(ot[db][1], pc1, acc[db]);
+      }
+      if (sb < 3) make_p(sb + 1, pc0, pc1);
+    }
+  };
+  auto dk_step = [&](int tt, lds_char* cur) {
+    __syncthreads();
+    const lds_char* Q = cur;
+    const lds_char* O = cur + TB;
+#pragma unroll
+    for (int sb = 0; sb < 4; ++sb) {
+      u32x4 oa[D / 16];
+#pragma unroll
+      for (int k = 0; k < D / 16; ++k) oa[k] = row_read(O, off.row[k] + sb * 32 * (2 * D));
+      f32x4 dr[4];
+      stats4(cur, 1024, sb, dr);
+      f32x16 dp = zero16();
+#pragma unroll
+      for (int k = 0; k < D / 16; ++k) dp = mfma_bf16(oa[k], frag[k], dp);
+      u32x4 qt[D / 32][2];
+#pragma unroll
+      for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) qt[db][c] = tr_operand<D>(Q, off, db, sb, c);
+      __syncthreads();  // P(sb) written by the dV wave
+      const lds_char* ps = pslot + (sb & 1) * PSLOT;
+      const u32x4 pw0 = *(const __attribute__((address_space(3))) u32x4*)ps;
+      const u32x4 pw1 = *(const __attribute__((address_space(3))) u32x4*)(ps + 16);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float p = keep_or_zero(fast_exp2(fmaf(s[r], a.c2, -lr[r >> 2][r & 3])), elem_keep(mb, sb, r));
-        s[r] = p;
+        const uint32_t word = (r < 8 ? pw0 : pw1)[(r & 7) >> 1];
+        const float p = __builtin_bit_cast(float, (r & 1) ? (word & 0xffff0000u) : (word << 16));
         dp[r] = p * (dp[r] - dr[r >> 2][r & 3]);
       }
-      const bf16x8 p0 = pack_bf16(s, 0), p1 = pack_bf16(s, 1);
       const bf16x8 d0 = pack_bf16(dp, 0), d1 = pack_bf16(dp, 1);
 #pragma unroll
       for (int db = 0; db < D / 32; ++db) {
-        dv[db] = mfma_bf16(ot[db][0], p0, dv[db]);
-        dv[db] = mfma_bf16(ot[db][1], p1, dv[db]);
-        dk[db] = mfma_bf16(qt[db][0], d0, dk[db]);
-        dk[db] = mfma_bf16(qt[db][1], d1, dk[db]);
+        acc[db] = mfma_bf16(qt[db][0], d0, acc[db]);
+        acc[db] = mfma_bf16(qt[db][1], d1, acc[db]);
       }
     }
   };
-  for (int tt = t0; tt < t1; tt += 2) {
-    step(tt, bufs[0], bufs[1]);
-    if (tt + 1 < t1) step(tt + 1, bufs[1], bufs[0]);
+  if (!kw) {
+    for (int tt = t0; tt < t1; tt += 2) {
+      dv_step(tt, bufs[0], bufs[1]);
+      if (tt + 1 < t1) dv_step(tt + 1, bufs[1], bufs[0]);
+    }
+  } else {
+    for (int tt = t0; tt < t1; tt += 2) {
+      dk_step(tt, bufs[0]);
+      if (tt + 1 < t1) dk_step(tt + 1, bufs[1]);
+    }
   }
   if (j.part >= 0) {
-    store_bwd_partial<D>(a, j, 32 * w + i, dk, 0, g);
-    store_bwd_partial<D>(a, j, 32 * w + i, dv, 1, g);
+    store_bwd_partial<D>(a, j, 32 * w + i, acc, kw ? 0 : 1, g);
     return;
   }
-  store_acc_bf16<D>(make_rsrc((uint16_t*)a.out0 + j.base, a.slice_bytes), krow, snb, dk, a.scale, g);
-  store_acc_bf16<D>(make_rsrc((uint16_t*)a.out1 + j.base, a.slice_bytes), krow, snb, dv, 1.f, g);
+  store_acc_bf16<D>(make_rsrc((uint16_t*)(kw ? a.out0 : a.out1) + j.base, a.slice_bytes), krow, snb, acc,
+                    kw ? a.scale : 1.f, g);
 }
 
 template <int D>
@@ -484,7 +521,7 @@ hipError_t launch_d(Kind kind, const KArgs& a, hipStream_t stream) {
   switch (kind) {
     case Kind::kFwd: hipLaunchKernelGGL(fwd_kernel<D>, grid, block, 0, stream, a); break;
     case Kind::kDq: hipLaunchKernelGGL(dq_kernel<D>, grid, block, 0, stream, a); break;
-    case Kind::kDkv: hipLaunchKernelGGL(dkv_kernel<D>, grid, block, 0, stream, a); break;
+    case Kind::kDkv: hipLaunchKernelGGL(dkv_kernel<D>, grid, dim3(NT8), 0, stream, a); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
