@@ -194,11 +194,12 @@ struct SoftmaxState {
   float l;  // running sum of exp2(s*c2 - m) over this lane's half of the keys
 };
 
-__device__ __forceinline__ bool softmax_tile(f32x16 (&s)[4], SoftmaxState& st, float c2, float& corr) {
+template <int NSB>
+__device__ __forceinline__ bool softmax_tile(f32x16 (&s)[NSB], SoftmaxState& st, float c2, float& corr) {
   const float ninf = -__builtin_inff();
   float mx = s[0][0];
 #pragma unroll
-  for (int sb = 0; sb < 4; ++sb)
+  for (int sb = 0; sb < NSB; ++sb)
 #pragma unroll
     for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[sb][r]);
   mx = fmaxf(mx, __shfl_xor(mx, 32));
@@ -214,7 +215,7 @@ __device__ __forceinline__ bool softmax_tile(f32x16 (&s)[4], SoftmaxState& st, f
   const float base = st.m == ninf ? 0.f : st.m;
   float sum = 0.f;
 #pragma unroll
-  for (int sb = 0; sb < 4; ++sb)
+  for (int sb = 0; sb < NSB; ++sb)
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const float p = fast_exp2(fmaf(s[sb][r], c2, -base));
