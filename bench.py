@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the block-sparse masked mesh attention on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c3|c2|c4|c5] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c3|c2|c4|c5|c5mha] [--no-cpu]
 
 A step is one pass of the hot path over one batch of synthetic input: for the default workload
 (configuration 3 of BASELINE.json) the forward kernel plus the backward (delta pre-pass, dQ,
@@ -37,6 +37,10 @@ WORKLOADS = {
     "c5": dict(k_hop=32, heads=6, head_dim=128, batch=1, dtype="bf16", backward=False, reorder=True, sigma=1.0,
                desc="WN2 mesh-transformer attention shape: r6 mesh, 32-hop, Hilbert order, 6x128, bf16, "
                     "forward (one of 24 layers)"),
+    "c5mha": dict(k_hop=32, heads=6, head_dim=128, batch=1, dtype="bf16", backward=True, reorder=True, sigma=1.0,
+                  d_model=768,
+                  desc="WN2 attention block at C5 shape: fused q/k/v projection (768 -> 3x6x128), HIP attention "
+                       "read in place, mha_final projection; forward + backward, bf16, random-init weights"),
 }
 
 
@@ -97,6 +101,57 @@ def copy_calibration(mib, steps, warmup):
   return 0
 
 
+def mha_block(args):
+  """Times one attention block (projection, attention, final projection; forward + backward) with
+  the fused in-place layout and with separate contiguous q, k, v. The metric counts attention
+  FLOPs over live tiles only; the projections' GEMMs (rocBLAS/hipBLASLt) are in the step time."""
+  import numpy as np
+  import torch
+
+  import faster_weathernext_amd as fwn
+  cfg = WORKLOADS[args.workload]
+  D, H, B, dm = cfg["head_dim"], cfg["heads"], cfg["batch"], cfg["d_model"]
+  dev = torch.device("cuda:0")
+  torch.cuda.set_device(dev)
+  mask, lat, lon, perm = fwn.mesh_mask(6, cfg["k_hop"], reorder=cfg["reorder"])
+  tiles = fwn.TileList.from_mask(mask, perm, device=dev)
+  n, T = mask.shape[0], tiles.n_tiles
+  torch.manual_seed(0)
+  block = fwn.TiledMHA(dm, H, D, tiles, device=dev, dtype=torch.bfloat16)
+  x = torch.randn(B, n, dm, device=dev, dtype=torch.bfloat16, requires_grad=True)
+  g = torch.randn(B, n, dm, device=dev, dtype=torch.bfloat16)
+
+  def timed(fn):
+    for _ in range(args.warmup):
+      fn(x).backward(g)
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(args.steps):
+      fn(x).backward(g)
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / args.steps
+
+  ms_fused = timed(block.forward)
+  ms_unfused = timed(block.forward_unfused)
+  flops = 14 * D * 128 * 128 * T * B * H
+  value = flops / (ms_fused * 1e-3) / 1e12
+  result = {
+      "metric": METRIC, "value": round(value, 3), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+      "warmup": args.warmup, "ms_per_step": round(ms_fused, 4), "higher_is_better": True, "scaling": "weak",
+      "vs_baseline": None, "dtype": "bf16",
+      "data": "synthetic: N(0,1) node features and output gradients (torch seed 0), random-init torch weights, on "
+              "a generated icosahedral mesh; no checkpoints or datasets",
+      "config": {"workload": cfg["desc"], "mesh_refinement": 6, "n": n, "k_hop": cfg["k_hop"], "batch": B,
+                 "heads": H, "head_dim": D, "d_model": dm, "order": "hilbert", "live_tiles": T},
+      "ms_per_block_unfused": round(ms_unfused, 4),
+      "fused_speedup": round(ms_unfused / ms_fused, 4),
+  }
+  print(json.dumps(result), flush=True)
+  return 0
+
+
 def cpu_baseline(cfg, q, k, v, do, mask, tiles, scale, budget_s):
   """Times the restated reference XLA chunked path on whole query chunks until `budget_s` elapses."""
   import numpy as np
@@ -135,6 +190,8 @@ def main():
     return 2
   if args.copy_mib:
     return copy_calibration(args.copy_mib, args.steps, args.warmup)
+  if args.workload == "c5mha":
+    return mha_block(args)
   import numpy as np
   import torch
 

@@ -58,19 +58,24 @@ int check_desc(const fwn_attn_desc* d) {
   if (!(d->scale > 0.f) || !std::isfinite(d->scale))
     return fail(FWN_ERR_INVALID_ARG, "scale must be positive and finite");
   const int64_t vec = d->dtype == FWN_BF16 ? 8 : 4;  // elements per 16 bytes
-  if (d->stride_b < 0 || d->stride_n <= 0 || d->stride_h < 0 || d->stride_b % vec || d->stride_n % vec ||
-      d->stride_h % vec)
-    return fail(FWN_ERR_INVALID_ARG, "strides must be non-negative multiples of 16 bytes");
-  if (d->stride_n < d->head_dim || (d->heads > 1 && d->stride_h < d->head_dim))
-    return fail(FWN_ERR_INVALID_ARG, "strides overlap rows or heads");
   const int64_t n_blocks = (d->n + FWN_BLOCK - 1) / FWN_BLOCK;
   if (n_blocks * d->batch * d->heads > INT32_MAX)
     return fail(FWN_ERR_INVALID_ARG, "grid too large");
-  // Buffer offsets are 32-bit: every row of a (batch, head) slice, padding rows of the last block
-  // included, must be addressable below 2 GiB.
   const int64_t elem = d->dtype == FWN_BF16 ? 2 : 4;
-  if ((n_blocks * FWN_BLOCK + 1) * d->stride_n * elem >= ((int64_t)1 << 31))
-    return fail(FWN_ERR_INVALID_ARG, "a (batch, head) slice spans 2 GiB or more");
+  const bool same = d->ostride_b == 0 && d->ostride_n == 0 && d->ostride_h == 0;
+  for (int set = 0; set < (same ? 1 : 2); ++set) {
+    const int64_t sb = set ? d->ostride_b : d->stride_b, sn = set ? d->ostride_n : d->stride_n,
+                  sh = set ? d->ostride_h : d->stride_h;
+    const char* what = set ? "o/dout strides" : "strides";
+    if (sb < 0 || sn <= 0 || sh < 0 || sb % vec || sn % vec || sh % vec)
+      return fail(FWN_ERR_INVALID_ARG, "%s must be non-negative multiples of 16 bytes", what);
+    if (sn < d->head_dim || (d->heads > 1 && sh < d->head_dim))
+      return fail(FWN_ERR_INVALID_ARG, "%s overlap rows or heads", what);
+    // Buffer offsets are 32-bit: every row of a (batch, head) slice, padding rows of the last
+    // block included, must be addressable below 2 GiB.
+    if ((n_blocks * FWN_BLOCK + 1) * sn * elem >= ((int64_t)1 << 31))
+      return fail(FWN_ERR_INVALID_ARG, "a (batch, head) slice spans 2 GiB or more (%s)", what);
+  }
   return FWN_OK;
 }
 
@@ -123,7 +128,13 @@ KArgs base_args(const fwn_attn_desc* d) {
   a.sb = d->stride_b;
   a.sn = d->stride_n;
   a.sh = d->stride_h;
-  a.slice_bytes = (uint32_t)(((int64_t)(d->n - 1) * d->stride_n + d->head_dim) * (d->dtype == FWN_BF16 ? 2 : 4));
+  const bool same = d->ostride_b == 0 && d->ostride_n == 0 && d->ostride_h == 0;
+  a.osb = same ? d->stride_b : d->ostride_b;
+  a.osn = same ? d->stride_n : d->ostride_n;
+  a.osh = same ? d->stride_h : d->ostride_h;
+  const int64_t elem = d->dtype == FWN_BF16 ? 2 : 4;
+  a.slice_bytes = (uint32_t)(((int64_t)(d->n - 1) * a.sn + d->head_dim) * elem);
+  a.oslice_bytes = (uint32_t)(((int64_t)(d->n - 1) * a.osn + d->head_dim) * elem);
   a.scale = d->scale;
   a.c2 = (float)((double)d->scale * 1.4426950408889634);
   return a;

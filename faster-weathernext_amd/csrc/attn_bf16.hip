@@ -223,7 +223,7 @@ __global__ void __launch_bounds__(NT, 2) fwd_kernel(KArgs a) {
     return;
   }
   const float inv = ltot > 0.f ? 1.f / ltot : 0.f;
-  store_acc_bf16<D>(make_rsrc((uint16_t*)a.out0 + j.base, a.slice_bytes), qrow, snb, o, inv, g);
+  store_acc_bf16<D>(make_rsrc((uint16_t*)a.out0 + j.obase, a.oslice_bytes), qrow, (uint32_t)a.osn * 2, o, inv, g);
   if (g == 0) write_lse(a, j, qrow, st, ltot);
 }
 
@@ -252,7 +252,7 @@ __global__ void __launch_bounds__(NT, 2) dq_kernel(KArgs a) {
   const int qrow = j.blk * BLK + 32 * w + i;
   u32x4 qf[D / 16], df[D / 16];
   load_frag<D>(qf, make_rsrc((const uint16_t*)a.q + j.base, a.slice_bytes), qrow, snb, g);
-  load_frag<D>(df, make_rsrc((const uint16_t*)a.dout + j.base, a.slice_bytes), qrow, snb, g);
+  load_frag<D>(df, make_rsrc((const uint16_t*)a.dout + j.obase, a.oslice_bytes), qrow, (uint32_t)a.osn * 2, g);
   float lse_t = 0.f, delta = 0.f;
   if (qrow < a.n) {
     lse_t = a.lse[stat_index(a, j, qrow)] * LOG2E;
@@ -357,7 +357,8 @@ __global__ void __launch_bounds__(NT8, 1) dkv_kernel(KArgs a) {
   const Job j = decode_job(a);
   const uint32_t snb = (uint32_t)a.sn * 2;
   const rsrc_t rQ = make_rsrc((const uint16_t*)a.q + j.base, a.slice_bytes);
-  const rsrc_t rO = make_rsrc((const uint16_t*)a.dout + j.base, a.slice_bytes);
+  const rsrc_t rO = make_rsrc((const uint16_t*)a.dout + j.obase, a.oslice_bytes);
+  const uint32_t osnb = (uint32_t)a.osn * 2;
   const rsrc_t rL = make_rsrc(a.lse + stat_index(a, j, 0), (uint32_t)a.n * 4);
   const rsrc_t rD = make_rsrc(a.delta + stat_index(a, j, 0), (uint32_t)a.n * 4);
 
@@ -366,8 +367,9 @@ __global__ void __launch_bounds__(NT8, 1) dkv_kernel(KArgs a) {
   load_frag<D>(frag, make_rsrc((const uint16_t*)(kw ? a.v : a.k) + j.base, a.slice_bytes), krow, snb, g);
   Off<D> off;
   off.init(lane);
-  TileDma<D> dma;
+  TileDma<D> dma, dmaO;  // Q and dO tiles (their row strides may differ)
   dma.init(w, lane, snb);
+  dmaO.init(w, lane, osnb);
   f32x16 acc[D / 32];
 #pragma unroll
   for (int db = 0; db < D / 32; ++db) acc[db] = zero16();
@@ -380,7 +382,7 @@ __global__ void __launch_bounds__(NT8, 1) dkv_kernel(KArgs a) {
   auto issue = [&](int t, lds_char* buf) {
     const int qb = ((ci32_ptr)a.col)[t];
     dma.issue(rQ, buf, w, qb * BLK, snb);
-    dma.issue(rO, buf + TB, w, qb * BLK, snb);
+    dmaO.issue(rO, buf + TB, w, qb * BLK, osnb);
     if (wid == 0) {
       const uint32_t vo = (uint32_t)(qb * BLK + 4 * (lane & 31)) * 4;
       lds_char* stats = buf + 2 * TB;

@@ -93,7 +93,7 @@ __global__ void __launch_bounds__(kThreads) fwd_combine_kernel(KArgs a) {
     acc1 += wgt * *(const f32x4*)(p + r * D + d + 4);
   }
   const float inv = L > 0.f ? 1.f / L : 0.f;
-  const int64_t out_off = (int64_t)s.b * a.sb + (int64_t)s.h * a.sh + (int64_t)row * a.sn + d;
+  const int64_t out_off = (int64_t)s.b * a.osb + (int64_t)s.h * a.osh + (int64_t)row * a.osn + d;
   store4<T>(a.out0, out_off, acc0 * inv);
   store4<T>(a.out0, out_off + 4, acc1 * inv);
   if (d == 0 && a.lse_out)

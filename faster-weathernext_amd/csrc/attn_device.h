@@ -102,7 +102,8 @@ struct Job {
   int b, h, bh;
   int t0, t1;    // tile range of this work item, clamped to [0, n_tiles)
   int part;      // partial slot, or -1 when the item covers its whole block
-  int64_t base;  // element offset of (b, h)
+  int64_t base;   // element offset of (b, h) in q, k, v, dq, dk, dv
+  int64_t obase;  // element offset of (b, h) in o, dout
 };
 
 // Workgroups are dealt round-robin over the 8 XCDs, each with its own L2. Jobs are ordered
@@ -130,6 +131,7 @@ __device__ __forceinline__ Job decode_job(const KArgs& a) {
   j.b = j.bh / a.heads;
   j.h = j.bh - j.b * a.heads;
   j.base = (int64_t)j.b * a.sb + (int64_t)j.h * a.sh;
+  j.obase = (int64_t)j.b * a.osb + (int64_t)j.h * a.osh;
   return j;
 }
 

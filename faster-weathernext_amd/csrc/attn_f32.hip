@@ -139,7 +139,7 @@ __global__ void __launch_bounds__(NT, 1) fwd_f32_kernel(KArgs a) {
     return;
   }
   const float inv = ltot > 0.f ? 1.f / ltot : 0.f;
-  store_acc_f32<D>(make_rsrc((float*)a.out0 + j.base, a.slice_bytes), qrow, snb, o, inv, g);
+  store_acc_f32<D>(make_rsrc((float*)a.out0 + j.obase, a.oslice_bytes), qrow, (uint32_t)a.osn * 4, o, inv, g);
   if (g == 0) write_lse(a, j, qrow, st, ltot);
 }
 
@@ -161,7 +161,7 @@ __global__ void __launch_bounds__(NT, 1) dq_f32_kernel(KArgs a) {
   const int qrow = j.blk * BLK + 32 * w + i;
   f32x4 qf[D / 8], df[D / 8];
   load_frag_f32<D>(qf, make_rsrc((const float*)a.q + j.base, a.slice_bytes), qrow, snb, g);
-  load_frag_f32<D>(df, make_rsrc((const float*)a.dout + j.base, a.slice_bytes), qrow, snb, g);
+  load_frag_f32<D>(df, make_rsrc((const float*)a.dout + j.obase, a.oslice_bytes), qrow, (uint32_t)a.osn * 4, g);
   float lse_t = 0.f, delta = 0.f;
   if (qrow < a.n) {
     lse_t = a.lse[stat_index(a, j, qrow)] * LOG2E;
@@ -233,7 +233,8 @@ __global__ void __launch_bounds__(NT, 1) dkv_f32_kernel(KArgs a) {
   const Job j = decode_job(a);
   const uint32_t snb = (uint32_t)a.sn * 4;
   const rsrc_t rQ = make_rsrc((const float*)a.q + j.base, a.slice_bytes);
-  const rsrc_t rO = make_rsrc((const float*)a.dout + j.base, a.slice_bytes);
+  const rsrc_t rO = make_rsrc((const float*)a.dout + j.obase, a.oslice_bytes);
+  const uint32_t osnb = (uint32_t)a.osn * 4;
   const float* lse = a.lse + stat_index(a, j, 0);
   const float* dl = a.delta + stat_index(a, j, 0);
 
@@ -259,7 +260,7 @@ __global__ void __launch_bounds__(NT, 1) dkv_f32_kernel(KArgs a) {
     const u32x2 mb = tile_bits(a, t, w, lane);  // lands while the tile is staged
     __syncthreads();
     stage_rows_f32<D>(ldsQ, rQ, qb * BLK, snb, tid, true);
-    stage_rows_f32<D>(ldsO, rO, qb * BLK, snb, tid, true);
+    stage_rows_f32<D>(ldsO, rO, qb * BLK, osnb, tid, true);
     {
       const int row = qb * BLK + (tid & (BLK - 1));
       float stat = 0.f;
@@ -323,7 +324,7 @@ __global__ void __launch_bounds__(NT) delta_kernel(KArgs a) {
     const int row = (int)(item % a.n);
     const int64_t bh = item / a.n;
     const int h = (int)(bh % a.heads), b = (int)(bh / a.heads);
-    const int64_t off = (int64_t)b * a.sb + (int64_t)h * a.sh + (int64_t)row * a.sn + part * EPC;
+    const int64_t off = (int64_t)b * a.osb + (int64_t)h * a.osh + (int64_t)row * a.osn + part * EPC;
     const u32x4 x = *(const u32x4*)((const T*)a.o + off);
     const u32x4 y = *(const u32x4*)((const T*)a.dout + off);
     if constexpr (sizeof(T) == 4) {

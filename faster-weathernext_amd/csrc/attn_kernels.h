@@ -25,8 +25,10 @@ struct KArgs {
   const int32_t* split;   // [n_split * 3] block, first partial slot, slot count (combine pass)
   float* work;            // partial slots: [n_parts][batch * heads][128][2 * head_dim + 2] float32
   int32_t n, heads, batch, n_blocks, n_tiles, n_items, n_parts, n_split;
-  int64_t sb, sn, sh;
+  int64_t sb, sn, sh;     // strides of q, k, v, dq, dk, dv
+  int64_t osb, osn, osh;  // strides of o, dout
   uint32_t slice_bytes;   // bytes of one (batch, head) slice: ((n - 1) * sn + head_dim) * elem
+  uint32_t oslice_bytes;  // the same for o, dout
   float scale;            // softmax scale
   float c2;               // scale * log2(e)
 };

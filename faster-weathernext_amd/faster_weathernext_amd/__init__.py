@@ -10,8 +10,10 @@ op contract, computed by hand-written gfx950 HIP kernels behind a C ABI (include
 """
 
 from . import patch
-from .hip_attn import BLOCK_K, BLOCK_Q, TileList, attention_backward, attention_forward, tiled_flash_attention
+from .hip_attn import (BLOCK_K, BLOCK_Q, TileList, attention_backward, attention_forward, tiled_flash_attention,
+                       tiled_flash_attention_qkv)
 from .mesh import adjacency, build_tile_mask, hilbert_order, icosahedral_mesh, khop_mask, mesh_mask
+from .mha import TiledMHA
 
 __version__ = "0.1.0"
 

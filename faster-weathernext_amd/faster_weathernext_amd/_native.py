@@ -37,7 +37,8 @@ class FwnError(RuntimeError):
 class AttnDesc(ctypes.Structure):
   _fields_ = [("batch", ctypes.c_int32), ("n", ctypes.c_int32), ("heads", ctypes.c_int32),
               ("head_dim", ctypes.c_int32), ("dtype", ctypes.c_int32), ("scale", ctypes.c_float),
-              ("stride_b", ctypes.c_int64), ("stride_n", ctypes.c_int64), ("stride_h", ctypes.c_int64)]
+              ("stride_b", ctypes.c_int64), ("stride_n", ctypes.c_int64), ("stride_h", ctypes.c_int64),
+              ("ostride_b", ctypes.c_int64), ("ostride_n", ctypes.c_int64), ("ostride_h", ctypes.c_int64)]
 
 
 class Tiles(ctypes.Structure):

@@ -112,22 +112,42 @@ def _as_tiles(tiles, n, device):
     return hit[3]
 
 
-def _desc(q, scale):
+def _check(q):
   if q.dtype not in _DTYPES:
     raise TypeError(f"unsupported dtype {q.dtype}: float32 or bfloat16")
   if q.device.type != "cuda":
     raise ValueError("tiled_flash_attention runs on the GPU only (tensors are on %s)" % q.device)
-  if q.dim() != 4 or q.stride(-1) != 1:
-    raise ValueError("expected [batch, n, heads, head_dim] with head_dim contiguous")
+  if q.dim() != 4:
+    raise ValueError("expected [batch, n, heads, head_dim]")
+
+
+def _desc(q, scale, o=None):
+  """Call descriptor: q's strides for q, k, v, dq, dk, dv and o's for o, dout (0 = the same)."""
   b, n, h, d = q.shape
   sb, sn, sh, _ = q.stride()
-  return nat.AttnDesc(b, n, h, d, _DTYPES[q.dtype], float(scale), sb, sn, sh)
+  osb = osn = osh = 0
+  if o is not None and o.stride() != q.stride():
+    osb, osn, osh, _ = o.stride()
+  return nat.AttnDesc(b, n, h, d, _DTYPES[q.dtype], float(scale), sb, sn, sh, osb, osn, osh)
+
+
+def _in_place(x):
+  """x itself when the kernels can read it where it lies (head_dim contiguous, strides and base
+  16-byte aligned), else a contiguous copy."""
+  ok = (x.stride(-1) == 1 and x.data_ptr() % 16 == 0 and
+        all(st >= 0 and (st * x.element_size()) % 16 == 0 for st in x.stride()[:3]))
+  return x if ok else x.contiguous()
 
 
 def _same_layout(x, ref, name):
+  """x in ref's strides (the kernels share one set of strides over q, k, v)."""
   if x.shape != ref.shape or x.dtype != ref.dtype or x.device != ref.device:
     raise ValueError(f"{name} must match q in shape, dtype and device")
-  return x if x.stride() == ref.stride() else x.contiguous().as_strided(ref.shape, ref.stride())
+  if x.stride() == ref.stride():
+    return x
+  y = torch.empty_strided(ref.shape, ref.stride(), dtype=ref.dtype, device=ref.device)
+  y.copy_(x)
+  return y
 
 
 def _stream(device):
@@ -145,13 +165,18 @@ def _ws_args(ws):
 
 
 def attention_forward(q, k, v, tiles, scale, with_lse=True):
-  """Forward kernel: returns (out, lse) with lse float32 [batch, heads, n] (None if not requested)."""
-  q = q.contiguous()
+  """Forward kernel: returns (out, lse) with lse float32 [batch, heads, n] (None if not requested).
+
+  q, k, v are read where they lie when their strides allow it (e.g. views of one fused
+  projection); out is a new contiguous [batch, n, heads, head_dim] tensor.
+  """
+  _check(q)
+  q = _in_place(q)
   k = _same_layout(k, q, "k")
   v = _same_layout(v, q, "v")
-  desc = _desc(q, scale)
+  out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+  desc = _desc(q, scale, out)
   tl = _as_tiles(tiles, q.shape[1], q.device)
-  out = torch.empty_like(q)
   lse = torch.empty((q.shape[0], q.shape[2], q.shape[1]), dtype=torch.float32, device=q.device) if with_lse else None
   ws = workspace(desc, q.device, tl)
   nat.check(nat.lib().fwn_attn_fwd_launch(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), tl.struct, out.data_ptr(),
@@ -159,24 +184,30 @@ def attention_forward(q, k, v, tiles, scale, with_lse=True):
   return out, lse
 
 
-def attention_backward(q, k, v, out, lse, dout, tiles, tiles_t, scale):
-  """Backward kernels (delta pre-pass, dQ, dK/dV): returns (dq, dk, dv)."""
-  q = q.contiguous()
-  k = _same_layout(k, q, "k")
-  v = _same_layout(v, q, "v")
-  out = _same_layout(out, q, "out")
-  dout = _same_layout(dout, q, "dout")
-  desc = _desc(q, scale)
+def _backward_into(q, k, v, out, lse, dout, tiles, tiles_t, scale, dq, dk, dv):
+  """Backward kernels (delta pre-pass, dQ, dK/dV) writing dq, dk, dv (q's strides)."""
+  desc = _desc(q, scale, out)
   n = q.shape[1]
   tl = _as_tiles(tiles, n, q.device)
   tlt = tl if tiles_t is None else _as_tiles(tiles_t, n, q.device)
   delta = torch.empty_like(lse)
-  dq, dk, dv = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
   ws = workspace(desc, q.device, tl, tlt)
   nat.check(nat.lib().fwn_attn_bwd_launch(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
                                           dout.data_ptr(), lse.data_ptr(), delta.data_ptr(), tl.struct, tlt.struct,
                                           dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), *_ws_args(ws),
                                           _stream(q.device)))
+
+
+def attention_backward(q, k, v, out, lse, dout, tiles, tiles_t, scale):
+  """Backward kernels (delta pre-pass, dQ, dK/dV): returns contiguous (dq, dk, dv)."""
+  _check(q)
+  q = q.contiguous()  # dq, dk, dv are written in q's strides: keep them dense
+  k = _same_layout(k, q, "k")
+  v = _same_layout(v, q, "v")
+  out = _in_place(out)
+  dout = _same_layout(dout, out, "dout")
+  dq, dk, dv = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
+  _backward_into(q, k, v, out, lse, dout, tiles, tiles_t, scale, dq, dk, dv)
   return dq, dk, dv
 
 
@@ -198,6 +229,42 @@ class _TiledAttention(torch.autograd.Function):
     q, k, v, out, lse = ctx.saved_tensors
     dq, dk, dv = attention_backward(q, k, v, out, lse, dout, ctx.tiles, ctx.tiles_t, ctx.scale)
     return dq, dk, dv, None, None, None
+
+
+class _TiledAttentionQKV(torch.autograd.Function):
+  """The same custom VJP over one packed [batch, n, 3, heads, head_dim] q/k/v buffer: the kernels
+  read q, k, v where the projection wrote them and write dq, dk, dv into one packed gradient."""
+
+  @staticmethod
+  def forward(ctx, qkv, tiles, tiles_t, scale):
+    q, k, v = qkv.unbind(2)
+    need = ctx.needs_input_grad[0]
+    out, lse = attention_forward(q, k, v, tiles, scale, with_lse=need)
+    if need:
+      ctx.save_for_backward(qkv, out, lse)
+      ctx.tiles, ctx.tiles_t, ctx.scale = tiles, tiles_t, scale
+    return out
+
+  @staticmethod
+  def backward(ctx, dout):
+    qkv, out, lse = ctx.saved_tensors
+    q, k, v = qkv.unbind(2)
+    dqkv = torch.empty_like(qkv)
+    dq, dk, dv = dqkv.unbind(2)
+    _backward_into(q, k, v, out, lse, _same_layout(dout, out, "dout"), ctx.tiles, ctx.tiles_t, ctx.scale,
+                   dq, dk, dv)
+    return dqkv, None, None, None
+
+
+def tiled_flash_attention_qkv(qkv, tiles, *, scale, tiles_t=None):
+  """Attention over a packed qkv [batch, n, 3, heads, head_dim] (one fused projection's output,
+  contiguous) -> [batch, n, heads, head_dim], with no copy of q, k, v or of their gradients."""
+  _check(qkv[:, :, 0])
+  if qkv.dim() != 5 or qkv.shape[2] != 3 or not qkv.is_contiguous():
+    raise ValueError("expected a contiguous [batch, n, 3, heads, head_dim] tensor")
+  if tiles_t is not None and not isinstance(tiles_t, TileList):
+    tiles_t = tuple(tiles_t)
+  return _TiledAttentionQKV.apply(qkv, tiles, tiles_t, float(scale))
 
 
 def tiled_flash_attention(q, k, v, tile_ptr, tile_kb=None, tile_bits=None, *, scale, tiles_t=None):

@@ -14,7 +14,8 @@
  *     state, so they are re-entrant and safe under stream capture.
  *   - Tensors q, k, v, o, dout, dq, dk, dv are [batch, n, heads, head_dim] in the element strides
  *     of fwn_attn_desc (head_dim contiguous): node-major by default, read and written in place
- *     (the reference transposes to head-major and pads, pallas_attn.py:334-335; here no copy is made).
+ *     (the reference transposes to head-major and pads, pallas_attn.py:334-335; here no copy is
+ *     made). q, k, v, dq, dk, dv share one set of strides, o and dout another.
  *   - lse and delta are float32 [batch, heads, n], contiguous.
  *   - Rows are processed in blocks of FWN_BLOCK = 128 and key tiles are 128 wide
  *     (the reference uses 64 x 32, pallas_attn.py:30-31).
@@ -43,7 +44,10 @@ typedef enum fwn_status {
 typedef enum fwn_dtype { FWN_F32 = 0, FWN_BF16 = 1 } fwn_dtype;
 
 /* Shape of one attention call. scale multiplies q.k (the reference passes key_size**-0.5,
- * patch.py:174). Strides are in elements, shared by every [batch, n, heads, head_dim] tensor. */
+ * patch.py:174). Strides are in elements. stride_* apply to q, k, v and to dq, dk, dv;
+ * ostride_* to o and dout, or are all 0 to mean "the same as stride_*". Two layouts let a fused
+ * projection hand over q, k, v as views of one [batch, n, 3, heads, head_dim] buffer, and take
+ * dq, dk, dv back in the same buffer, while o and dout stay [batch, n, heads, head_dim]. */
 typedef struct fwn_attn_desc {
   int32_t batch;
   int32_t n;          /* nodes (queries = keys) */
@@ -54,6 +58,9 @@ typedef struct fwn_attn_desc {
   int64_t stride_b;
   int64_t stride_n;
   int64_t stride_h;
+  int64_t ostride_b;
+  int64_t ostride_n;
+  int64_t ostride_h;
 } fwn_attn_desc;
 
 /* One work item of a tile list: tiles [t0, t1) of row block `block`. With part < 0 the item

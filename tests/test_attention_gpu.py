@@ -325,6 +325,57 @@ def test_split_workspace_is_reused_across_calls():
     outs.append(out)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_packed_qkv_op_is_bitwise_the_unpacked_op(dtype):
+  """tiled_flash_attention_qkv reads q, k, v as views of one [B, n, 3, H, D] buffer and writes
+  one packed gradient; the kernels see the same values, so outputs and gradients match the
+  separate-tensor op bit for bit, and both match the dense oracle."""
+  rng = np.random.default_rng(50)
+  b, n, h, d = 2, 500, 2, 64
+  qkv_h = _rounded(rng.standard_normal((b, n, 3, h, d)), dtype)
+  do_h = _rounded(rng.standard_normal((b, n, h, d)), dtype)
+  m = _random_mask(n, 0.04, 51, symmetric=True)
+  tiles = fwn.TileList(*fwn.build_tile_mask(m), n, DEV, 2)  # split items as well
+  qkv = _dev(qkv_h, dtype, True)
+  out = fwn.tiled_flash_attention_qkv(qkv, tiles, scale=d ** -0.5)
+  out.backward(_dev(do_h, dtype))
+  q, k, v = (_dev(qkv_h[:, :, i], dtype, True) for i in range(3))
+  ref = fwn.tiled_flash_attention(q, k, v, tiles, scale=d ** -0.5)
+  ref.backward(_dev(do_h, dtype))
+  torch.cuda.synchronize()
+  np.testing.assert_array_equal(_np(out), _np(ref))
+  for i, t in enumerate((q, k, v)):
+    np.testing.assert_array_equal(_np(qkv.grad[:, :, i]), _np(t.grad))
+  dense = A.dense_attention(qkv_h[:, :, 0], qkv_h[:, :, 1], qkv_h[:, :, 2], m.toarray(), d ** -0.5)
+  _check(_np(out), dense, dtype, "out")
+  grads = A.dense_grads(qkv_h[:, :, 0], qkv_h[:, :, 1], qkv_h[:, :, 2], do_h, m.toarray(), d ** -0.5)
+  for i, name in enumerate(("dq", "dk", "dv")):
+    _check(_np(qkv.grad[:, :, i]), grads[i], dtype, name)
+
+
+def test_tiled_mha_block_matches_unfused_block():
+  """TiledMHA (fused projection, in-place kernels) equals the unfused block (separate contiguous
+  q, k, v) bit for bit in the output and in every parameter gradient."""
+  torch.manual_seed(0)
+  b, n, h, d, dm = 1, 700, 2, 64, 128
+  m = _random_mask(n, 0.05, 52, symmetric=True)
+  tiles = fwn.TileList.from_mask(m, device=DEV)
+  block = fwn.TiledMHA(dm, h, d, tiles, device=DEV, dtype=torch.bfloat16)
+  x = torch.randn(b, n, dm, device=DEV, dtype=torch.bfloat16)
+  grads = []
+  outs = []
+  for fn in (block.forward, block.forward_unfused):
+    block.zero_grad()
+    y = fn(x)
+    y.float().square().sum().backward()
+    outs.append(_np(y))
+    grads.append([_np(p.grad) for p in block.parameters()])
+  torch.cuda.synchronize()
+  np.testing.assert_array_equal(outs[0], outs[1])
+  for g0, g1 in zip(*grads):
+    np.testing.assert_array_equal(g0, g1)
+
+
 def test_exp2_based_softmax_accuracy():
   """The softmax uses V_EXP_F32 (2^x) with log2(e) folded into the scale: rows must sum to one and
   the log-sum-exp must match float64 to single-precision accuracy."""

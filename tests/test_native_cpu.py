@@ -254,6 +254,22 @@ def test_launchers_reject_bad_pointers_and_tiles():
   assert L.fwn_attn_fwd_launch(desc, F, F, F, _tiles(n_items=4, n_parts=2), F, None, None, 0, None) == nat.ERR_TILES
 
 
+def test_output_strides_are_validated_separately():
+  """o/dout strides (ostride_*) are checked like the q/k/v strides; all zero means 'the same'."""
+  L = nat.lib()
+  F = FAKE
+  good = _tiles()
+  packed = _desc(stride_b=300 * 3 * 2 * 64, stride_n=3 * 2 * 64, stride_h=64)  # q, k, v views of [B, n, 3, H, D]
+  assert L.fwn_attn_fwd_launch(packed, F, F, F, _tiles(n_blocks=5), F, None, None, 0, None) == nat.ERR_TILES
+  for bad in (dict(ostride_b=300 * 128, ostride_n=66, ostride_h=64),      # not a multiple of 16 bytes
+              dict(ostride_b=300 * 128, ostride_n=32, ostride_h=64),      # rows overlap
+              dict(ostride_b=0, ostride_n=1 << 21, ostride_h=64)):        # slice beyond 2 GiB offsets
+    d = _desc(**bad)
+    assert L.fwn_attn_fwd_launch(d, F, F, F, good, F, None, None, 0, None) == nat.ERR_INVALID_ARG
+    assert "o/dout" in L.fwn_last_error().decode()
+    assert L.fwn_attn_bwd_delta_launch(d, F, F, F, None) == nat.ERR_INVALID_ARG
+
+
 def test_workspace_size_and_checks():
   """Split schedules need n_parts * batch * heads * 128 * (2 * head_dim + 2) * 4 bytes of
   256-byte-aligned workspace; launchers refuse a missing, short or misaligned one."""
