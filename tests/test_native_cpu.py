@@ -310,3 +310,51 @@ def test_public_op_refuses_cpu_tensors():
   tp, kb, bits = fwn.build_tile_mask(sparse.identity(10, dtype=bool, format="csr"))
   with pytest.raises(ValueError, match="GPU"):
     fwn.tiled_flash_attention(q, q, q, tp, kb, bits, scale=1.0)
+
+
+def test_tile_cache_round_trip_and_invalidation(tmp_path):
+  """The cache returns the built tile list bit for bit on a hit; another k, a changed adjacency, a
+  corrupt or truncated file are misses and are rebuilt."""
+  from faster_weathernext_amd import tile_cache
+  v, f, lat, lon = fwn.icosahedral_mesh(3)
+  adj = fwn.adjacency(f, len(v))
+  perm = fwn.hilbert_order(lat, lon)
+  ref = fwn.build_tile_mask(fwn.khop_mask(adj, 2), perm)
+  got = tile_cache.cached_khop_tiles(adj, 2, perm, cache_dir=str(tmp_path))
+  assert not got[3]
+  for a, b in zip(got[:3], ref):
+    np.testing.assert_array_equal(a, b)
+  hit = tile_cache.cached_khop_tiles(adj, 2, perm, cache_dir=str(tmp_path))
+  assert hit[3]
+  for a, b in zip(hit[:3], ref):
+    np.testing.assert_array_equal(a, b)
+  assert not tile_cache.cached_khop_tiles(adj, 3, perm, cache_dir=str(tmp_path))[3]   # other k
+  assert not tile_cache.cached_khop_tiles(adj, 2, None, cache_dir=str(tmp_path))[3]   # other order
+  (path,) = [p for p in tmp_path.iterdir() if p.name.startswith("khop2_") and
+             p.name.endswith(f"{tile_cache.mask_key(adj, perm, 2):016x}.fwnt")]
+  raw = path.read_bytes()
+  path.write_bytes(raw[:-4])                                                          # truncated
+  assert not tile_cache.cached_khop_tiles(adj, 2, perm, cache_dir=str(tmp_path))[3]
+  bad = bytearray(path.read_bytes())
+  bad[0:8] = b"XXXXXXXX"                                                               # wrong magic
+  path.write_bytes(bytes(bad))
+  assert not tile_cache.cached_khop_tiles(adj, 2, perm, cache_dir=str(tmp_path))[3]
+  assert tile_cache.cached_khop_tiles(adj, 2, perm, cache_dir=str(tmp_path))[3]
+  # header fields as documented
+  head = tile_cache._HEADER.unpack_from(path.read_bytes())
+  assert head[0] == b"FWNTILES" and head[1] == 1 and head[2] == head[3] == len(v) and head[4] == 2 and head[5] == 1
+  assert head[6] == 128 and head[8] == len(ref[0]) - 1 and head[9] == len(ref[1])
+
+
+def test_tile_mask_cache_keys_on_content(tmp_path):
+  from faster_weathernext_amd import tile_cache
+  m = _random_mask(400, 0.03, 7)
+  a = tile_cache.cached_tile_mask(m, cache_dir=str(tmp_path))
+  assert not a[3] and tile_cache.cached_tile_mask(m, cache_dir=str(tmp_path))[3]
+  m2 = m.tolil()
+  m2[0, 399] = not m2[0, 399]
+  b = tile_cache.cached_tile_mask(m2.tocsr(), cache_dir=str(tmp_path))
+  assert not b[3]
+  ref = fwn.build_tile_mask(m2.tocsr())
+  for x, y in zip(b[:3], ref):
+    np.testing.assert_array_equal(x, y)
