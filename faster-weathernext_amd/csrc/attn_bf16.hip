@@ -179,9 +179,12 @@ __global__ void __launch_bounds__(NT, 2) fwd_kernel(KArgs a) {
     // K(t) is in LDS for every wave here; V(t) may still be in flight.
     const u32x2 mb = mbits;
     if (t + 1 < t1) mbits = tile_bits(a, t + 1, w, lane);
+    // Sub-blocks with no valid element for this wave are skipped: they would add p = 0.
+    const uint32_t live = live_subblocks(mb);
     f32x16 s[4];
 #pragma unroll
     for (int sb = 0; sb < 4; ++sb) {
+      if (!(live >> sb & 1u)) continue;
       u32x4 ka[D / 16];
 #pragma unroll
       for (int k = 0; k < D / 16; ++k) ka[k] = row_read(K, off.row[k] + sb * 32 * (2 * D));
@@ -195,12 +198,13 @@ __global__ void __launch_bounds__(NT, 2) fwd_kernel(KArgs a) {
     __syncthreads();  // all of V(t) landed; every wave is done reading K(t)
     if (t + 1 < t1) dma.issue(rK, K, w, ((ci32_ptr)a.col)[t + 1] * BLK, snb);
     float corr;
-    if (softmax_tile(s, st, a.c2, corr)) {
+    if (live != 0u && softmax_live(s, live, st, a.c2, corr)) {
 #pragma unroll
       for (int db = 0; db < D / 32; ++db) o[db] *= corr;
     }
 #pragma unroll
     for (int sb = 0; sb < 4; ++sb) {
+      if (!(live >> sb & 1u)) continue;
       u32x4 va[D / 32][2];
 #pragma unroll
       for (int db = 0; db < D / 32; ++db)
@@ -280,8 +284,10 @@ __global__ void __launch_bounds__(NT, 2) dq_kernel(KArgs a) {
     wait_vmem();
     __syncthreads();
     const u32x2 mb = mbits;
+    const uint32_t live = live_subblocks(mb);  // sub-blocks with p = 0 throughout add nothing
 #pragma unroll
     for (int sb = 0; sb < 4; ++sb) {
+      if (!(live >> sb & 1u)) continue;
       u32x4 ka[D / 16], va[D / 16];
 #pragma unroll
       for (int k = 0; k < D / 16; ++k) {
@@ -374,6 +380,7 @@ __global__ void __launch_bounds__(NT8, 1) dkv_kernel(KArgs a) {
 #pragma unroll
   for (int db = 0; db < D / 32; ++db) acc[db] = zero16();
   lds_char* pslot = (lds_char*)lp + w * 2 * PSLOT + lane * 32;
+  __shared__ __attribute__((aligned(16))) uint32_t live_sets[2 * 4];  // [tile parity][key group]
 
   int t0, t1;
   tile_range(a, j, t0, t1);
@@ -406,24 +413,37 @@ __global__ void __launch_bounds__(NT8, 1) dkv_kernel(KArgs a) {
     mbits = tile_bits(a, t0, w, lane);
     issue(t0, bufs[0]);
   }
-  // Per tile both roles pass 5 barriers: tile start, then one per sub-block (P written / read).
+  // Query sub-blocks (32 queries) of a tile with no valid element for any of the 4 key groups are
+  // skipped by every wave; the others cost one barrier each. A pair (w, w + 4) computes only the
+  // sub-blocks in which its own 32 keys have a valid element (the rest would add p = 0). The dV
+  // wave publishes its pair's set before the tile barrier, double-buffered by tile parity.
+  // Per tile each wave passes 1 + (number of sub-blocks live for any pair) barriers.
+  auto tile_sets = [&](int tt, uint32_t& any, uint32_t& own) {
+    const u32x4 lw = *(const __attribute__((address_space(3))) u32x4*)(live_sets + 4 * (tt & 1));
+    any = __builtin_amdgcn_readfirstlane(lw[0] | lw[1] | lw[2] | lw[3]);
+    own = __builtin_amdgcn_readfirstlane(w == 0 ? lw[0] : w == 1 ? lw[1] : w == 2 ? lw[2] : lw[3]);
+  };
   auto dv_step = [&](int tt, lds_char* cur, lds_char* nxt) {
     const int t = __builtin_amdgcn_readfirstlane(tt);
     wait_vmem();
+    const u32x2 mb = mbits;
+    const uint32_t pair_live = live_subblocks(mb);  // ballots: the whole wave takes part
+    if (lane == 0) live_sets[4 * (tt & 1) + w] = pair_live;
     if (wid == 0 && lane < 32) {
       __attribute__((address_space(3))) f32x4* l4 = (__attribute__((address_space(3))) f32x4*)(cur + 2 * TB) + lane;
       *l4 = *l4 * LOG2E;
     }
     __syncthreads();
-    const u32x2 mb = mbits;
+    uint32_t any, own;
+    tile_sets(tt, any, own);
     if (t + 1 < t1) {
       mbits = tile_bits(a, t + 1, w, lane);
       issue(t + 1, nxt);
     }
     const lds_char* Q = cur;
     const lds_char* O = cur + TB;
-    // P of sub-block sb, written to its LDS slot for the dK wave; kept in registers for dV.
-    auto make_p = [&](int sb, bf16x8& p0, bf16x8& p1) {
+    // P of sub-block sb, written to LDS slot `slot` for the dK wave; kept in registers for dV.
+    auto make_p = [&](int sb, int slot, bf16x8& p0, bf16x8& p1) {
       u32x4 qa[D / 16];
 #pragma unroll
       for (int k = 0; k < D / 16; ++k) qa[k] = row_read(Q, off.row[k] + sb * 32 * (2 * D));
@@ -437,65 +457,104 @@ __global__ void __launch_bounds__(NT8, 1) dkv_kernel(KArgs a) {
         sv[r] = keep_or_zero(fast_exp2(fmaf(sv[r], a.c2, -lr[r >> 2][r & 3])), elem_keep(mb, sb, r));
       p0 = pack_bf16(sv, 0);
       p1 = pack_bf16(sv, 1);
-      lds_char* ps = pslot + (sb & 1) * PSLOT;
+      lds_char* ps = pslot + slot * PSLOT;
       *(__attribute__((address_space(3))) bf16x8*)ps = p0;
       *(__attribute__((address_space(3))) bf16x8*)(ps + 16) = p1;
     };
-    // P runs one sub-block ahead: between two barriers this wave issues dV(sb) and S(sb + 1)
-    // while the dK wave issues dK(sb) and dP(sb + 1).
+    // P runs one live sub-block ahead: between two barriers this wave issues dV(sb) and S(next)
+    // while the dK wave issues dK(sb) and dP(next). P(sb) goes to slot (its rank in `any`) & 1.
+    // make_p is instantiated per sub-block so its LDS offsets stay constants.
+#ifdef FWN_PSWITCH
+    auto make_p_at = [&](uint32_t sb, int slot, bf16x8& p0, bf16x8& p1) {
+      switch (sb) {
+        case 0: make_p(0, slot, p0, p1); break;
+        case 1: make_p(1, slot, p0, p1); break;
+        case 2: make_p(2, slot, p0, p1); break;
+        default: make_p(3, slot, p0, p1); break;
+      }
+    };
+#else
+    auto make_p_at = [&](uint32_t sb, int slot, bf16x8& p0, bf16x8& p1) { make_p((int)sb, slot, p0, p1); };
+#endif
     bf16x8 pc0, pc1;
-    make_p(0, pc0, pc1);
+    {
+      const uint32_t first = (uint32_t)__builtin_ctz(any | 16u);
+      if (own >> first & 1u) make_p_at(first, 0, pc0, pc1);
+    }
+    int rank = 0;
 #pragma unroll
     for (int sb = 0; sb < 4; ++sb) {
+      if (!(any >> sb & 1u)) continue;
+      const bool mine = own >> sb & 1u;
       u32x4 ot[D / 32][2];
+      if (mine) {
 #pragma unroll
-      for (int db = 0; db < D / 32; ++db)
+        for (int db = 0; db < D / 32; ++db)
 #pragma unroll
-        for (int c = 0; c < 2; ++c) ot[db][c] = tr_operand<D>(O, off, db, sb, c);
-      __syncthreads();  // P(sb) is in LDS for the dK wave
-#pragma unroll
-      for (int db = 0; db < D / 32; ++db) {
-        acc[db] = mfma_bf16(ot[db][0], pc0, acc[db]);
-        acc[db] = mfma_bf16(ot[db][1], pc1, acc[db]);
+          for (int c = 0; c < 2; ++c) ot[db][c] = tr_operand<D>(O, off, db, sb, c);
       }
-      if (sb < 3) make_p(sb + 1, pc0, pc1);
+      __syncthreads();  // P(sb) is in LDS for the dK wave
+      if (mine) {
+#pragma unroll
+        for (int db = 0; db < D / 32; ++db) {
+          acc[db] = mfma_bf16(ot[db][0], pc0, acc[db]);
+          acc[db] = mfma_bf16(ot[db][1], pc1, acc[db]);
+        }
+      }
+      ++rank;
+      if (sb < 3) {
+        const uint32_t later = any & (0xeu << sb);
+        const uint32_t next = (uint32_t)__builtin_ctz(later | 16u);
+        if (later != 0u && (own >> next & 1u)) make_p_at(next, rank & 1, pc0, pc1);
+      }
     }
   };
   auto dk_step = [&](int tt, lds_char* cur) {
     __syncthreads();
+    uint32_t any, own;
+    tile_sets(tt, any, own);
     const lds_char* Q = cur;
     const lds_char* O = cur + TB;
+    int rank = 0;
 #pragma unroll
     for (int sb = 0; sb < 4; ++sb) {
-      u32x4 oa[D / 16];
-#pragma unroll
-      for (int k = 0; k < D / 16; ++k) oa[k] = row_read(O, off.row[k] + sb * 32 * (2 * D));
+      if (!(any >> sb & 1u)) continue;
+      const bool mine = own >> sb & 1u;
       f32x4 dr[4];
-      stats4(cur, 1024, sb, dr);
-      f32x16 dp = zero16();
-#pragma unroll
-      for (int k = 0; k < D / 16; ++k) dp = mfma_bf16(oa[k], frag[k], dp);
+      f32x16 dp;
       u32x4 qt[D / 32][2];
+      if (mine) {
+        u32x4 oa[D / 16];
 #pragma unroll
-      for (int db = 0; db < D / 32; ++db)
+        for (int k = 0; k < D / 16; ++k) oa[k] = row_read(O, off.row[k] + sb * 32 * (2 * D));
+        stats4(cur, 1024, sb, dr);
+        dp = zero16();
 #pragma unroll
-        for (int c = 0; c < 2; ++c) qt[db][c] = tr_operand<D>(Q, off, db, sb, c);
+        for (int k = 0; k < D / 16; ++k) dp = mfma_bf16(oa[k], frag[k], dp);
+#pragma unroll
+        for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+          for (int c = 0; c < 2; ++c) qt[db][c] = tr_operand<D>(Q, off, db, sb, c);
+      }
       __syncthreads();  // P(sb) written by the dV wave
-      const lds_char* ps = pslot + (sb & 1) * PSLOT;
-      const u32x4 pw0 = *(const __attribute__((address_space(3))) u32x4*)ps;
-      const u32x4 pw1 = *(const __attribute__((address_space(3))) u32x4*)(ps + 16);
+      if (mine) {
+        const lds_char* ps = pslot + (rank & 1) * PSLOT;
+        const u32x4 pw0 = *(const __attribute__((address_space(3))) u32x4*)ps;
+        const u32x4 pw1 = *(const __attribute__((address_space(3))) u32x4*)(ps + 16);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const uint32_t word = (r < 8 ? pw0 : pw1)[(r & 7) >> 1];
-        const float p = __builtin_bit_cast(float, (r & 1) ? (word & 0xffff0000u) : (word << 16));
-        dp[r] = p * (dp[r] - dr[r >> 2][r & 3]);
-      }
-      const bf16x8 d0 = pack_bf16(dp, 0), d1 = pack_bf16(dp, 1);
+        for (int r = 0; r < 16; ++r) {
+          const uint32_t word = (r < 8 ? pw0 : pw1)[(r & 7) >> 1];
+          const float p = __builtin_bit_cast(float, (r & 1) ? (word & 0xffff0000u) : (word << 16));
+          dp[r] = p * (dp[r] - dr[r >> 2][r & 3]);
+        }
+        const bf16x8 d0 = pack_bf16(dp, 0), d1 = pack_bf16(dp, 1);
 #pragma unroll
-      for (int db = 0; db < D / 32; ++db) {
-        acc[db] = mfma_bf16(qt[db][0], d0, acc[db]);
-        acc[db] = mfma_bf16(qt[db][1], d1, acc[db]);
+        for (int db = 0; db < D / 32; ++db) {
+          acc[db] = mfma_bf16(qt[db][0], d0, acc[db]);
+          acc[db] = mfma_bf16(qt[db][1], d1, acc[db]);
+        }
       }
+      ++rank;
     }
   };
   if (!kw) {

@@ -169,6 +169,18 @@ __device__ __forceinline__ uint32_t elem_keep(const u32x2& bits, int sb, int r) 
   return __builtin_amdgcn_sbfe(bits[e >> 5], (uint32_t)(e & 31), 1u);
 }
 
+// Sub-blocks of a tile's 32-key groups that hold at least one valid element for this wave: bit sb
+// is set when some lane's 16 bits for sb are nonzero (a wave-uniform value).
+__device__ __forceinline__ uint32_t live_subblocks(const u32x2& bits) {
+  uint32_t live = 0;
+#pragma unroll
+  for (int sb = 0; sb < 4; ++sb) {
+    const uint32_t f = (bits[sb >> 1] >> (16 * (sb & 1))) & 0xffffu;
+    if (__builtin_amdgcn_ballot_w64(f != 0u) != 0) live |= 1u << sb;
+  }
+  return live;
+}
+
 // x where kept, -inf elsewhere (one v_bitop3_b32).
 __device__ __forceinline__ float keep_or_ninf(float x, uint32_t keep) {
   return __builtin_bit_cast(float, (__builtin_bit_cast(uint32_t, x) & keep) | (0xff800000u & ~keep));
@@ -196,12 +208,15 @@ struct SoftmaxState {
   float l;  // running sum of exp2(s*c2 - m) over this lane's half of the keys
 };
 
-template <int NSB>
-__device__ __forceinline__ bool softmax_tile(f32x16 (&s)[NSB], SoftmaxState& st, float c2, float& corr) {
+// The first NSB entries of s take part (all of them by default).
+template <int NSB = -1, int CAP>
+__device__ __forceinline__ bool softmax_tile(f32x16 (&s)[CAP], SoftmaxState& st, float c2, float& corr) {
+  constexpr int N = NSB < 0 ? CAP : NSB;
+  static_assert(N >= 1 && N <= CAP, "sub-block count");
   const float ninf = -__builtin_inff();
   float mx = s[0][0];
 #pragma unroll
-  for (int sb = 0; sb < NSB; ++sb)
+  for (int sb = 0; sb < N; ++sb)
 #pragma unroll
     for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[sb][r]);
   mx = fmaxf(mx, __shfl_xor(mx, 32));
@@ -217,12 +232,50 @@ __device__ __forceinline__ bool softmax_tile(f32x16 (&s)[NSB], SoftmaxState& st,
   const float base = st.m == ninf ? 0.f : st.m;
   float sum = 0.f;
 #pragma unroll
-  for (int sb = 0; sb < NSB; ++sb)
+  for (int sb = 0; sb < N; ++sb)
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const float p = fast_exp2(fmaf(s[sb][r], c2, -base));
       s[sb][r] = p;
       sum += p;
+    }
+  st.l += sum;
+  return moved;
+}
+
+// softmax_tile over the sub-blocks in `live` only (a nonzero wave-uniform set); the others are
+// neither read nor written.
+__device__ __forceinline__ bool softmax_live(f32x16 (&s)[4], uint32_t live, SoftmaxState& st, float c2,
+                                             float& corr) {
+  const float ninf = -__builtin_inff();
+  float mx = ninf;
+#pragma unroll
+  for (int sb = 0; sb < 4; ++sb)
+    if (live >> sb & 1u) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[sb][r]);
+    }
+  mx = fmaxf(mx, __shfl_xor(mx, 32));
+  const float mxs = mx * c2;
+  corr = 1.f;
+  const bool moved = __builtin_amdgcn_ballot_w64(mxs > st.m + kLazyMax) != 0;
+  if (moved) {
+    const float m_new = fmaxf(st.m, mxs);
+    corr = fast_exp2(st.m - (m_new == ninf ? 0.f : m_new));
+    st.l *= corr;
+    st.m = m_new;
+  }
+  const float base = st.m == ninf ? 0.f : st.m;
+  float sum = 0.f;
+#pragma unroll
+  for (int sb = 0; sb < 4; ++sb)
+    if (live >> sb & 1u) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = fast_exp2(fmaf(s[sb][r], c2, -base));
+        s[sb][r] = p;
+        sum += p;
+      }
     }
   st.l += sum;
   return moved;
