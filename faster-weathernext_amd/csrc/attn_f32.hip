@@ -106,9 +106,11 @@ __global__ void __launch_bounds__(NT, 1) fwd_f32_kernel(KArgs a) {
     stage_rows_f32<D>(ldsK, rK, kb * BLK, snb, tid, true);
     stage_rows_f32<D>(ldsV, rV, kb * BLK, snb, tid, false);
     __syncthreads();
+    const uint32_t live = live_subblocks(mb);  // sub-blocks with p = 0 throughout are skipped
     f32x16 s[4];
 #pragma unroll
     for (int sb = 0; sb < 4; ++sb) {
+      if (!(live >> sb & 1u)) continue;
       s[sb] = zero16();
 #pragma unroll
       for (int u = 0; u < D / 8; ++u) {
@@ -120,18 +122,20 @@ __global__ void __launch_bounds__(NT, 1) fwd_f32_kernel(KArgs a) {
       for (int r = 0; r < 16; ++r) s[sb][r] = keep_or_ninf(s[sb][r], elem_keep(mb, sb, r));
     }
     float corr;
-    if (softmax_tile(s, st, a.c2, corr)) {
+    if (live != 0u && softmax_live(s, live, st, a.c2, corr)) {
 #pragma unroll
       for (int db = 0; db < D / 32; ++db) o[db] *= corr;
     }
 #pragma unroll
-    for (int sb = 0; sb < 4; ++sb)
+    for (int sb = 0; sb < 4; ++sb) {
+      if (!(live >> sb & 1u)) continue;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
 #pragma unroll
         for (int db = 0; db < D / 32; ++db)
           o[db] = mfma_f32(*(const float*)(ldsV + off.el_plain + off.el_imm(sb, r, db)), s[sb][r], o[db]);
       }
+    }
   }
   const float ltot = st.l + __shfl_xor(st.l, 32);
   if (j.part >= 0) {
@@ -184,8 +188,10 @@ __global__ void __launch_bounds__(NT, 1) dq_f32_kernel(KArgs a) {
     stage_rows_f32<D>(ldsK, rK, kb * BLK, snb, tid, true);
     stage_rows_f32<D>(ldsV, rV, kb * BLK, snb, tid, true);
     __syncthreads();
+    const uint32_t live = live_subblocks(mb);  // sub-blocks with p = 0 throughout are skipped
 #pragma unroll
     for (int sb = 0; sb < 4; ++sb) {
+      if (!(live >> sb & 1u)) continue;
       f32x16 s = zero16(), dp = zero16();
 #pragma unroll
       for (int u = 0; u < D / 8; ++u) {
@@ -268,8 +274,10 @@ __global__ void __launch_bounds__(NT, 1) dkv_f32_kernel(KArgs a) {
       (tid < BLK ? ldsL : ldsDl)[tid & (BLK - 1)] = stat;
     }
     __syncthreads();
+    const uint32_t live = live_subblocks(mb);  // sub-blocks with p = 0 throughout are skipped
 #pragma unroll
     for (int sb = 0; sb < 4; ++sb) {
+      if (!(live >> sb & 1u)) continue;
       f32x16 s = zero16(), dp = zero16();
 #pragma unroll
       for (int u = 0; u < D / 8; ++u) {
