@@ -90,7 +90,7 @@ int check_tiles(const fwn_attn_desc* d, const fwn_tiles* t, const char* name) {
   const int32_t n_blocks = (d->n + FWN_BLOCK - 1) / FWN_BLOCK;
   if (t->n_blocks != n_blocks)
     return fail(FWN_ERR_TILES, "%s has %d row blocks, expected %d for n = %d", name, t->n_blocks, n_blocks, d->n);
-  if (t->n_tiles < 0 || !t->ptr || (t->n_tiles > 0 && (!t->col || !t->lanes || !t->full)))
+  if (t->n_tiles < 0 || !t->ptr || (t->n_tiles > 0 && (!t->col || !t->lanes || !t->groups)))
     return fail(FWN_ERR_TILES, "%s: missing device arrays", name);
   if (t->n_items < n_blocks || !t->items)
     return fail(FWN_ERR_TILES, "%s: %d work items for %d blocks (every block needs at least one)", name, t->n_items,
@@ -137,6 +137,7 @@ KArgs base_args(const fwn_attn_desc* d) {
   a.oslice_bytes = (uint32_t)(((int64_t)(d->n - 1) * a.osn + d->head_dim) * elem);
   a.scale = d->scale;
   a.c2 = (float)((double)d->scale * 1.4426950408889634);
+  a.nlse_mul = (float)(-1.0 / (double)d->scale);
   return a;
 }
 
@@ -144,7 +145,7 @@ void set_tiles(KArgs& a, const fwn_tiles* t, void* ws) {
   a.ptr = t->ptr;
   a.col = t->col;
   a.lanes = t->lanes;
-  a.full = t->full;
+  a.groups = t->groups;
   a.items = (const int32_t*)t->items;
   a.split = t->split;
   a.n_tiles = t->n_tiles;

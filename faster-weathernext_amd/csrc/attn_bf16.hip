@@ -62,7 +62,10 @@ struct TileDma {
     voff = (uint32_t)row * snb + (uint32_t)((((lane % C) ^ swz<C>(row))) << 4);
   }
 
-  __device__ __forceinline__ void issue(rsrc_t r, lds_char* tile, int w, int row0, uint32_t snb) const {
+  // Copies the rows of the tile's 32-row groups in `live` (bit c: rows 32c..32c+31, a
+  // wave-uniform set); the rows of the other groups keep stale data and must not be read.
+  __device__ __forceinline__ void issue(rsrc_t r, lds_char* tile, int w, int row0, uint32_t snb,
+                                        uint32_t live = 15u) const {
     // The LDS destinations are loop-invariant; left visible, the compiler keeps all of them in
     // SGPRs across the tile loop and spills other scalars. The empty asm makes the base opaque,
     // so each destination is one scalar add at the copy.
@@ -70,6 +73,7 @@ struct TileDma {
     asm volatile("" : "+s"(base));
 #pragma unroll
     for (int op = 0; op < Tile<D>::OPS_PER_WAVE; ++op) {
+      if (!(live >> ((op * 4 * RPO + w * RPO) >> 5) & 1u)) continue;  // this op's rows lie in one group
       const uint32_t vo = voff + (uint32_t)(row0 + op * 4 * RPO) * snb;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(uintptr_t)(base + op * 4096u),
                                                16, (int)vo, 0, 0, 0);
@@ -166,11 +170,13 @@ __global__ void __launch_bounds__(NT, 2) fwd_kernel(KArgs a) {
   int t0, t1;
   tile_range(a, j, t0, t1);
   u32x2 mbits = {0u, 0u};  // mask bits of the next tile, loaded a tile ahead
+  uint32_t gnext = 0u;     // group bits of the next tile, loaded a tile ahead
   if (t0 < t1) {
     const int kb = ((ci32_ptr)a.col)[t0];
     mbits = tile_bits(a, t0, w, lane);
+    gnext = tile_groups(a, t0);
     dma.issue(rK, K, w, kb * BLK, snb);
-    wait_vmem();  // K(t0), its mask bits and the Q fragment
+    wait_vmem();  // K(t0), its mask and group bits and the Q fragment
     dma.issue(rV, V, w, kb * BLK, snb);
   }
   __syncthreads();
@@ -178,9 +184,14 @@ __global__ void __launch_bounds__(NT, 2) fwd_kernel(KArgs a) {
     const int t = __builtin_amdgcn_readfirstlane(tt);
     // K(t) is in LDS for every wave here; V(t) may still be in flight.
     const u32x2 mb = mbits;
-    if (t + 1 < t1) mbits = tile_bits(a, t + 1, w, lane);
-    // Sub-blocks with no valid element for this wave are skipped: they would add p = 0.
-    const uint32_t live = live_subblocks(mb);
+    const uint32_t gt = gnext;
+    if (t + 1 < t1) {
+      mbits = tile_bits(a, t + 1, w, lane);
+      gnext = tile_groups(a, t + 1);
+    }
+    // Key groups with no valid element for this wave are skipped: they would add p = 0. Key
+    // groups with none for any wave are not copied either.
+    const uint32_t live = gt >> (4 * w) & 15u;
     f32x16 s[4];
 #pragma unroll
     for (int sb = 0; sb < 4; ++sb) {
@@ -194,9 +205,10 @@ __global__ void __launch_bounds__(NT, 2) fwd_kernel(KArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[sb][r] = keep_or_ninf(s[sb][r], elem_keep(mb, sb, r));
     }
-    wait_vmem();      // this wave's part of V(t)
+    wait_vmem();      // this wave's part of V(t); the next tile's group bits
     __syncthreads();  // all of V(t) landed; every wave is done reading K(t)
-    if (t + 1 < t1) dma.issue(rK, K, w, ((ci32_ptr)a.col)[t + 1] * BLK, snb);
+    const uint32_t copy_next = any_rows(gnext);
+    if (t + 1 < t1) dma.issue(rK, K, w, ((ci32_ptr)a.col)[t + 1] * BLK, snb, copy_next);
     float corr;
     if (live != 0u && softmax_live(s, live, st, a.c2, corr)) {
 #pragma unroll
@@ -219,7 +231,7 @@ __global__ void __launch_bounds__(NT, 2) fwd_kernel(KArgs a) {
     }
     wait_vmem();      // this wave's part of K(t+1)
     __syncthreads();  // all of K(t+1) landed; every wave is done reading V(t)
-    if (t + 1 < t1) dma.issue(rV, V, w, ((ci32_ptr)a.col)[t + 1] * BLK, snb);
+    if (t + 1 < t1) dma.issue(rV, V, w, ((ci32_ptr)a.col)[t + 1] * BLK, snb, copy_next);
   }
   const float ltot = st.l + __shfl_xor(st.l, 32);
   if (j.part >= 0) {
@@ -273,9 +285,11 @@ __global__ void __launch_bounds__(NT, 2) dq_kernel(KArgs a) {
   int t0, t1;
   tile_range(a, j, t0, t1);
   u32x2 mbits = {0u, 0u};  // mask bits of the next tile, loaded with its copy
+  uint32_t gnext = 0u;     // group bits of the next tile, loaded a tile ahead of its copy
   if (t0 < t1) {
     const int kb = ((ci32_ptr)a.col)[t0];
     mbits = tile_bits(a, t0, w, lane);
+    gnext = tile_groups(a, t0);
     dma.issue(rK, K, w, kb * BLK, snb);
     dma.issue(rV, V, w, kb * BLK, snb);
   }
@@ -284,7 +298,11 @@ __global__ void __launch_bounds__(NT, 2) dq_kernel(KArgs a) {
     wait_vmem();
     __syncthreads();
     const u32x2 mb = mbits;
-    const uint32_t live = live_subblocks(mb);  // sub-blocks with p = 0 throughout add nothing
+    const uint32_t gt = gnext;
+    if (t + 1 < t1) gnext = tile_groups(a, t + 1);
+    // Key groups with no valid element for this wave are skipped (p = 0 throughout); key groups
+    // with none for any wave are not copied either.
+    const uint32_t live = gt >> (4 * w) & 15u;
 #pragma unroll
     for (int sb = 0; sb < 4; ++sb) {
       if (!(live >> sb & 1u)) continue;
@@ -322,9 +340,10 @@ __global__ void __launch_bounds__(NT, 2) dq_kernel(KArgs a) {
     __syncthreads();  // every wave is done with K(t) and V(t)
     if (t + 1 < t1) {
       const int kb = ((ci32_ptr)a.col)[t + 1];
+      const uint32_t copy = any_rows(gnext);
       mbits = tile_bits(a, t + 1, w, lane);
-      dma.issue(rK, K, w, kb * BLK, snb);
-      dma.issue(rV, V, w, kb * BLK, snb);
+      dma.issue(rK, K, w, kb * BLK, snb, copy);
+      dma.issue(rV, V, w, kb * BLK, snb, copy);
     }
   }
   if (j.part >= 0) {
@@ -379,17 +398,18 @@ __global__ void __launch_bounds__(NT8, 1) dkv_kernel(KArgs a) {
   f32x16 acc[D / 32];
 #pragma unroll
   for (int db = 0; db < D / 32; ++db) acc[db] = zero16();
-  lds_char* pslot = (lds_char*)lp + w * 2 * PSLOT + lane * 32;
-  __shared__ __attribute__((aligned(16))) uint32_t live_sets[2 * 4];  // [tile parity][key group]
+  // A P slot holds the two 8-element halves of every lane, each half 64 lanes x 16 bytes
+  // contiguous, so the slot's b128 writes and reads are free of bank conflicts.
+  lds_char* pslot = (lds_char*)lp + w * 2 * PSLOT + lane * 16;
 
   int t0, t1;
   tile_range(a, j, t0, t1);
   constexpr uint32_t kPastEnd = 0x7FFFFFF0u;
   // The dV waves copy the tiles, their statistics and their mask bits.
-  auto issue = [&](int t, lds_char* buf) {
+  auto issue = [&](int t, lds_char* buf, uint32_t copy) {
     const int qb = ((ci32_ptr)a.col)[t];
-    dma.issue(rQ, buf, w, qb * BLK, snb);
-    dmaO.issue(rO, buf + TB, w, qb * BLK, osnb);
+    dma.issue(rQ, buf, w, qb * BLK, snb, copy);
+    dmaO.issue(rO, buf + TB, w, qb * BLK, osnb, copy);
     if (wid == 0) {
       const uint32_t vo = (uint32_t)(qb * BLK + 4 * (lane & 31)) * 4;
       lds_char* stats = buf + 2 * TB;
@@ -408,38 +428,40 @@ __global__ void __launch_bounds__(NT8, 1) dkv_kernel(KArgs a) {
       for (int hh = 0; hh < 2; ++hh)
         x[2 * c + hh] = *(const __attribute__((address_space(3))) f32x4*)(p + 32 * sb + 16 * c + 8 * g + 4 * hh);
   };
+  // Query groups (32 queries) of a tile with no valid element for any of the 4 key groups are
+  // skipped by every wave and not copied (they would add p = 0); the others cost one barrier each,
+  // so per tile each wave passes 1 + (number of live query groups) barriers. A dK wave also skips
+  // the live groups in which its own 32 keys have no valid element (its P is zero there), which
+  // saves LDS reads; the dV waves compute every live group (skipping there too costs more
+  // registers than a wave has). Group bits are loaded a tile ahead of their use (two tiles ahead
+  // of the copy for dV waves).
   u32x2 mbits = {0u, 0u};
+  uint32_t gcur = 0u, gnext = 0u;  // group bits of the current and (dV waves) the next tile
+  if (t0 < t1) gcur = tile_groups(a, t0);
   if (t0 < t1 && !kw) {
     mbits = tile_bits(a, t0, w, lane);
-    issue(t0, bufs[0]);
+    if (t0 + 1 < t1) gnext = tile_groups(a, t0 + 1);
+    issue(t0, bufs[0], 15u);
   }
-  // Query sub-blocks (32 queries) of a tile with no valid element for any of the 4 key groups are
-  // skipped by every wave; the others cost one barrier each. A pair (w, w + 4) computes only the
-  // sub-blocks in which its own 32 keys have a valid element (the rest would add p = 0). The dV
-  // wave publishes its pair's set before the tile barrier, double-buffered by tile parity.
-  // Per tile each wave passes 1 + (number of sub-blocks live for any pair) barriers.
-  auto tile_sets = [&](int tt, uint32_t& any, uint32_t& own) {
-    const u32x4 lw = *(const __attribute__((address_space(3))) u32x4*)(live_sets + 4 * (tt & 1));
-    any = __builtin_amdgcn_readfirstlane(lw[0] | lw[1] | lw[2] | lw[3]);
-    own = __builtin_amdgcn_readfirstlane(w == 0 ? lw[0] : w == 1 ? lw[1] : w == 2 ? lw[2] : lw[3]);
-  };
   auto dv_step = [&](int tt, lds_char* cur, lds_char* nxt) {
     const int t = __builtin_amdgcn_readfirstlane(tt);
     wait_vmem();
     const u32x2 mb = mbits;
-    const uint32_t pair_live = live_subblocks(mb);  // ballots: the whole wave takes part
-    if (lane == 0) live_sets[4 * (tt & 1) + w] = pair_live;
-    if (wid == 0 && lane < 32) {
-      __attribute__((address_space(3))) f32x4* l4 = (__attribute__((address_space(3))) f32x4*)(cur + 2 * TB) + lane;
-      *l4 = *l4 * LOG2E;
+    if (wid == 0) {
+      // lse -> -lse / scale and delta -> -delta, the initial values of the S^T and dP^T
+      // accumulators: (s - lse / scale) * c2 = s * c2 - lse * log2(e), and dP - delta.
+      __attribute__((address_space(3))) f32x4* x =
+          (__attribute__((address_space(3))) f32x4*)(cur + 2 * TB + (lane < 32 ? 0 : 512) + 16 * lane);
+      *x = *x * (lane < 32 ? a.nlse_mul : -1.f);
     }
     __syncthreads();
-    uint32_t any, own;
-    tile_sets(tt, any, own);
+    const uint32_t any = any_rows(gcur);
     if (t + 1 < t1) {
       mbits = tile_bits(a, t + 1, w, lane);
-      issue(t + 1, nxt);
+      issue(t + 1, nxt, any_rows(gnext));
     }
+    gcur = gnext;
+    if (t + 2 < t1) gnext = tile_groups(a, t + 2);
     const lds_char* Q = cur;
     const lds_char* O = cur + TB;
     // P of sub-block sb, written to LDS slot `slot` for the dK wave; kept in registers for dV.
@@ -449,70 +471,47 @@ __global__ void __launch_bounds__(NT8, 1) dkv_kernel(KArgs a) {
       for (int k = 0; k < D / 16; ++k) qa[k] = row_read(Q, off.row[k] + sb * 32 * (2 * D));
       f32x4 lr[4];
       stats4(cur, 0, sb, lr);
-      f32x16 sv = zero16();
+      f32x16 sv;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sv[r] = lr[r >> 2][r & 3];  // -lse / scale of the element's query
 #pragma unroll
       for (int k = 0; k < D / 16; ++k) sv = mfma_bf16(qa[k], frag[k], sv);
 #pragma unroll
-      for (int r = 0; r < 16; ++r)
-        sv[r] = keep_or_zero(fast_exp2(fmaf(sv[r], a.c2, -lr[r >> 2][r & 3])), elem_keep(mb, sb, r));
+      for (int r = 0; r < 16; ++r) sv[r] = keep_or_zero(fast_exp2(sv[r] * a.c2), elem_keep(mb, sb, r));
       p0 = pack_bf16(sv, 0);
       p1 = pack_bf16(sv, 1);
       lds_char* ps = pslot + slot * PSLOT;
       *(__attribute__((address_space(3))) bf16x8*)ps = p0;
-      *(__attribute__((address_space(3))) bf16x8*)(ps + 16) = p1;
+      *(__attribute__((address_space(3))) bf16x8*)(ps + 1024) = p1;
     };
     // P runs one live sub-block ahead: between two barriers this wave issues dV(sb) and S(next)
     // while the dK wave issues dK(sb) and dP(next). P(sb) goes to slot (its rank in `any`) & 1.
-    // make_p is instantiated per sub-block so its LDS offsets stay constants.
-#ifdef FWN_PSWITCH
-    auto make_p_at = [&](uint32_t sb, int slot, bf16x8& p0, bf16x8& p1) {
-      switch (sb) {
-        case 0: make_p(0, slot, p0, p1); break;
-        case 1: make_p(1, slot, p0, p1); break;
-        case 2: make_p(2, slot, p0, p1); break;
-        default: make_p(3, slot, p0, p1); break;
-      }
-    };
-#else
-    auto make_p_at = [&](uint32_t sb, int slot, bf16x8& p0, bf16x8& p1) { make_p((int)sb, slot, p0, p1); };
-#endif
     bf16x8 pc0, pc1;
-    {
-      const uint32_t first = (uint32_t)__builtin_ctz(any | 16u);
-      if (own >> first & 1u) make_p_at(first, 0, pc0, pc1);
-    }
+    if (any != 0u) make_p(__builtin_ctz(any), 0, pc0, pc1);
     int rank = 0;
 #pragma unroll
     for (int sb = 0; sb < 4; ++sb) {
       if (!(any >> sb & 1u)) continue;
-      const bool mine = own >> sb & 1u;
       u32x4 ot[D / 32][2];
-      if (mine) {
 #pragma unroll
-        for (int db = 0; db < D / 32; ++db)
+      for (int db = 0; db < D / 32; ++db)
 #pragma unroll
-          for (int c = 0; c < 2; ++c) ot[db][c] = tr_operand<D>(O, off, db, sb, c);
-      }
+        for (int c = 0; c < 2; ++c) ot[db][c] = tr_operand<D>(O, off, db, sb, c);
       __syncthreads();  // P(sb) is in LDS for the dK wave
-      if (mine) {
 #pragma unroll
-        for (int db = 0; db < D / 32; ++db) {
-          acc[db] = mfma_bf16(ot[db][0], pc0, acc[db]);
-          acc[db] = mfma_bf16(ot[db][1], pc1, acc[db]);
-        }
+      for (int db = 0; db < D / 32; ++db) {
+        acc[db] = mfma_bf16(ot[db][0], pc0, acc[db]);
+        acc[db] = mfma_bf16(ot[db][1], pc1, acc[db]);
       }
       ++rank;
-      if (sb < 3) {
-        const uint32_t later = any & (0xeu << sb);
-        const uint32_t next = (uint32_t)__builtin_ctz(later | 16u);
-        if (later != 0u && (own >> next & 1u)) make_p_at(next, rank & 1, pc0, pc1);
-      }
+      const uint32_t later = sb < 3 ? any & (0xeu << sb) : 0u;
+      if (later != 0u) make_p(__builtin_ctz(later), rank & 1, pc0, pc1);
     }
   };
   auto dk_step = [&](int tt, lds_char* cur) {
     __syncthreads();
-    uint32_t any, own;
-    tile_sets(tt, any, own);
+    const uint32_t any = any_rows(gcur), own = gcur >> (4 * w) & 15u;
+    if (tt + 1 < t1) gcur = tile_groups(a, tt + 1);
     const lds_char* Q = cur;
     const lds_char* O = cur + TB;
     int rank = 0;
@@ -520,15 +519,16 @@ __global__ void __launch_bounds__(NT8, 1) dkv_kernel(KArgs a) {
     for (int sb = 0; sb < 4; ++sb) {
       if (!(any >> sb & 1u)) continue;
       const bool mine = own >> sb & 1u;
-      f32x4 dr[4];
       f32x16 dp;
       u32x4 qt[D / 32][2];
       if (mine) {
         u32x4 oa[D / 16];
 #pragma unroll
         for (int k = 0; k < D / 16; ++k) oa[k] = row_read(O, off.row[k] + sb * 32 * (2 * D));
+        f32x4 dr[4];
         stats4(cur, 1024, sb, dr);
-        dp = zero16();
+#pragma unroll
+        for (int r = 0; r < 16; ++r) dp[r] = dr[r >> 2][r & 3];  // -delta of the element's query
 #pragma unroll
         for (int k = 0; k < D / 16; ++k) dp = mfma_bf16(oa[k], frag[k], dp);
 #pragma unroll
@@ -540,12 +540,12 @@ __global__ void __launch_bounds__(NT8, 1) dkv_kernel(KArgs a) {
       if (mine) {
         const lds_char* ps = pslot + (rank & 1) * PSLOT;
         const u32x4 pw0 = *(const __attribute__((address_space(3))) u32x4*)ps;
-        const u32x4 pw1 = *(const __attribute__((address_space(3))) u32x4*)(ps + 16);
+        const u32x4 pw1 = *(const __attribute__((address_space(3))) u32x4*)(ps + 1024);
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const uint32_t word = (r < 8 ? pw0 : pw1)[(r & 7) >> 1];
           const float p = __builtin_bit_cast(float, (r & 1) ? (word & 0xffff0000u) : (word << 16));
-          dp[r] = p * (dp[r] - dr[r >> 2][r & 3]);
+          dp[r] = p * dp[r];
         }
         const bf16x8 d0 = pack_bf16(dp, 0), d1 = pack_bf16(dp, 1);
 #pragma unroll

@@ -169,17 +169,17 @@ __device__ __forceinline__ uint32_t elem_keep(const u32x2& bits, int sb, int r) 
   return __builtin_amdgcn_sbfe(bits[e >> 5], (uint32_t)(e & 31), 1u);
 }
 
-// Sub-blocks of a tile's 32-key groups that hold at least one valid element for this wave: bit sb
-// is set when some lane's 16 bits for sb are nonzero (a wave-uniform value).
-__device__ __forceinline__ uint32_t live_subblocks(const u32x2& bits) {
-  uint32_t live = 0;
-#pragma unroll
-  for (int sb = 0; sb < 4; ++sb) {
-    const uint32_t f = (bits[sb >> 1] >> (16 * (sb & 1))) & 0xffffu;
-    if (__builtin_amdgcn_ballot_w64(f != 0u) != 0) live |= 1u << sb;
-  }
-  return live;
+// The tile's 16 group bits: bit 4r + c is set when rows 32r..32r+31 have a valid element in
+// columns 32c..32c+31. A wave owning row group r computes only the column groups in
+// (bits >> 4r) & 15; the others would add p = 0.
+// Read through the constant address space, so a uniform index becomes a scalar load and the
+// value an SGPR (the kernels branch on it).
+__device__ __forceinline__ uint32_t tile_groups(const KArgs& a, int t) {
+  return ((const __attribute__((address_space(4))) uint32_t*)a.groups)[t];
 }
+
+// Column groups with a valid element in any row group.
+__device__ __forceinline__ uint32_t any_rows(uint32_t g) { return (g | g >> 4 | g >> 8 | g >> 12) & 15u; }
 
 // x where kept, -inf elsewhere (one v_bitop3_b32).
 __device__ __forceinline__ float keep_or_ninf(float x, uint32_t keep) {

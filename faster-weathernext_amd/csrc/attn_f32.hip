@@ -19,12 +19,17 @@ __device__ __forceinline__ int swz_row3(int row) { return (row & 3) | (((row >> 
 // ------------------------------------------------------------------------------------------
 // fp32 staging: linear chunk mapping (coalesced), row-major tiles in LDS, optionally swizzled.
 
+// Only the rows of the 32-row groups in `live` (a uniform set) are copied; the others keep stale
+// data and must not be read.
 template <int D>
-__device__ __forceinline__ void stage_rows_f32(char* lds, rsrc_t r, int row0, uint32_t snb, int tid, bool swizzle) {
+__device__ __forceinline__ void stage_rows_f32(char* lds, rsrc_t r, int row0, uint32_t snb, int tid, bool swizzle,
+                                               uint32_t live) {
   constexpr int C = D / 4;
   constexpr int PER = BLK * C / NT;
+  static_assert(NT % C == 0 && 32 % (NT / C) == 0, "an iteration's rows lie in one group");
 #pragma unroll
   for (int it = 0; it < PER; ++it) {
+    if (!(live >> (it * (NT / C) / 32) & 1u)) continue;
     const int id = tid + it * NT;
     const int row = id / C, ch = id % C;
     const u32x4 x = bload16(r, (uint32_t)(row0 + row) * snb + (uint32_t)(16 * ch));
@@ -98,15 +103,18 @@ __global__ void __launch_bounds__(NT, 1) fwd_f32_kernel(KArgs a) {
 
   int t0, t1;
   tile_range(a, j, t0, t1);
+  uint32_t gnext = t0 < t1 ? tile_groups(a, t0) : 0u;  // group bits, loaded a tile ahead
   for (int tt = t0; tt < t1; ++tt) {
     const int t = __builtin_amdgcn_readfirstlane(tt);
     const int kb = ((ci32_ptr)a.col)[t];
     const u32x2 mb = tile_bits(a, t, w, lane);  // lands while the tile is staged
+    const uint32_t gt = gnext;
+    if (t + 1 < t1) gnext = tile_groups(a, t + 1);
     __syncthreads();
-    stage_rows_f32<D>(ldsK, rK, kb * BLK, snb, tid, true);
-    stage_rows_f32<D>(ldsV, rV, kb * BLK, snb, tid, false);
+    stage_rows_f32<D>(ldsK, rK, kb * BLK, snb, tid, true, any_rows(gt));
+    stage_rows_f32<D>(ldsV, rV, kb * BLK, snb, tid, false, any_rows(gt));
     __syncthreads();
-    const uint32_t live = live_subblocks(mb);  // sub-blocks with p = 0 throughout are skipped
+    const uint32_t live = gt >> (4 * w) & 15u;  // key groups with p = 0 throughout are skipped
     f32x16 s[4];
 #pragma unroll
     for (int sb = 0; sb < 4; ++sb) {
@@ -180,15 +188,18 @@ __global__ void __launch_bounds__(NT, 1) dq_f32_kernel(KArgs a) {
 
   int t0, t1;
   tile_range(a, j, t0, t1);
+  uint32_t gnext = t0 < t1 ? tile_groups(a, t0) : 0u;  // group bits, loaded a tile ahead
   for (int tt = t0; tt < t1; ++tt) {
     const int t = __builtin_amdgcn_readfirstlane(tt);
     const int kb = ((ci32_ptr)a.col)[t];
     const u32x2 mb = tile_bits(a, t, w, lane);  // lands while the tile is staged
+    const uint32_t gt = gnext;
+    if (t + 1 < t1) gnext = tile_groups(a, t + 1);
     __syncthreads();
-    stage_rows_f32<D>(ldsK, rK, kb * BLK, snb, tid, true);
-    stage_rows_f32<D>(ldsV, rV, kb * BLK, snb, tid, true);
+    stage_rows_f32<D>(ldsK, rK, kb * BLK, snb, tid, true, any_rows(gt));
+    stage_rows_f32<D>(ldsV, rV, kb * BLK, snb, tid, true, any_rows(gt));
     __syncthreads();
-    const uint32_t live = live_subblocks(mb);  // sub-blocks with p = 0 throughout are skipped
+    const uint32_t live = gt >> (4 * w) & 15u;  // key groups with p = 0 throughout are skipped
 #pragma unroll
     for (int sb = 0; sb < 4; ++sb) {
       if (!(live >> sb & 1u)) continue;
@@ -260,13 +271,16 @@ __global__ void __launch_bounds__(NT, 1) dkv_f32_kernel(KArgs a) {
 
   int t0, t1;
   tile_range(a, j, t0, t1);
+  uint32_t gnext = t0 < t1 ? tile_groups(a, t0) : 0u;  // group bits, loaded a tile ahead
   for (int tt = t0; tt < t1; ++tt) {
     const int t = __builtin_amdgcn_readfirstlane(tt);
     const int qb = ((ci32_ptr)a.col)[t];
     const u32x2 mb = tile_bits(a, t, w, lane);  // lands while the tile is staged
+    const uint32_t gt = gnext;
+    if (t + 1 < t1) gnext = tile_groups(a, t + 1);
     __syncthreads();
-    stage_rows_f32<D>(ldsQ, rQ, qb * BLK, snb, tid, true);
-    stage_rows_f32<D>(ldsO, rO, qb * BLK, osnb, tid, true);
+    stage_rows_f32<D>(ldsQ, rQ, qb * BLK, snb, tid, true, any_rows(gt));
+    stage_rows_f32<D>(ldsO, rO, qb * BLK, osnb, tid, true, any_rows(gt));
     {
       const int row = qb * BLK + (tid & (BLK - 1));
       float stat = 0.f;
@@ -274,11 +288,13 @@ __global__ void __launch_bounds__(NT, 1) dkv_f32_kernel(KArgs a) {
       (tid < BLK ? ldsL : ldsDl)[tid & (BLK - 1)] = stat;
     }
     __syncthreads();
-    const uint32_t live = live_subblocks(mb);  // sub-blocks with p = 0 throughout are skipped
+    const uint32_t live = gt >> (4 * w) & 15u;  // query groups with p = 0 throughout are skipped
 #pragma unroll
     for (int sb = 0; sb < 4; ++sb) {
       if (!(live >> sb & 1u)) continue;
-      f32x16 s = zero16(), dp = zero16();
+      f32x16 s = zero16(), dp;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) dp[r] = -ldsDl[element_col(sb, r, g)];  // dP^T - delta accumulates directly
 #pragma unroll
       for (int u = 0; u < D / 8; ++u) {
         const f32x4 qx = *(const f32x4*)(ldsQ + off.row[u & 3] + off.row_imm(sb, u));
@@ -295,7 +311,7 @@ __global__ void __launch_bounds__(NT, 1) dkv_f32_kernel(KArgs a) {
         float p = fast_exp2(fmaf(s[r], a.c2, -ldsL[qq]));
         p = keep_or_zero(p, elem_keep(mb, sb, r));
         s[r] = p;
-        dp[r] = p * (dp[r] - ldsDl[qq]);
+        dp[r] = p * dp[r];
       }
 #pragma unroll
       for (int r = 0; r < 16; ++r) {

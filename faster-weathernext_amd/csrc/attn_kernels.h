@@ -20,7 +20,7 @@ struct KArgs {
   const int32_t* ptr;
   const int32_t* col;
   const uint64_t* lanes;
-  const uint32_t* full;
+  const uint32_t* groups;  // per tile: bit 4r + c = rows 32r.. have a valid element in columns 32c..
   const int32_t* items;   // fwn_item[n_items] as int32 quadruples (block, t0, t1, part)
   const int32_t* split;   // [n_split * 3] block, first partial slot, slot count (combine pass)
   float* work;            // partial slots: [n_parts][batch * heads][128][2 * head_dim + 2] float32
@@ -31,6 +31,7 @@ struct KArgs {
   uint32_t oslice_bytes;  // the same for o, dout
   float scale;            // softmax scale
   float c2;               // scale * log2(e)
+  float nlse_mul;         // -1 / scale: turns a saved lse into the initial value of an S accumulator
 };
 
 enum class Kind { kFwd, kDq, kDkv, kDelta, kFwdCombine, kDqCombine, kDkvCombine };

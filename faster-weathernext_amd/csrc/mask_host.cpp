@@ -307,10 +307,10 @@ int fwn_tiles_fill(int32_t n_rows, int32_t n_cols, const int64_t* row_ptr, const
 
 int fwn_tiles_prepare(int32_t n_blocks, int32_t n_tiles, int32_t n_cols, const int32_t* tile_ptr,
                       const int32_t* tile_col, const uint32_t* tile_bits, uint64_t* lanes,
-                      uint32_t* full) {
+                      uint32_t* groups) {
   fwn::clear_error();
   if (n_blocks <= 0 || n_tiles < 0 || n_cols <= 0 || !tile_ptr || (n_tiles > 0 && (!tile_col || !tile_bits)) ||
-      (n_tiles > 0 && (!lanes || !full)))
+      (n_tiles > 0 && (!lanes || !groups)))
     return fwn::fail(FWN_ERR_INVALID_ARG, "fwn_tiles_prepare: null or empty argument");
   if (int rc = fwn::check_tile_list(n_blocks, n_tiles, n_cols, tile_ptr, tile_col)) return rc;
   const int32_t words = FWN_BLOCK / 32;
@@ -327,10 +327,9 @@ int fwn_tiles_prepare(int32_t n_blocks, int32_t n_tiles, int32_t n_cols, const i
       }
       uint32_t f = 0;
       for (int32_t w = 0; w < FWN_WAVES; ++w) {
-        bool all = true;
-        for (int32_t r = 32 * w; r < 32 * w + 32 && all; ++r)
-          for (int32_t x = 0; x < words; ++x) all = all && bits[r * words + x] == 0xffffffffu;
-        if (all) f |= 1u << w;
+        for (int32_t r = 32 * w; r < 32 * w + 32; ++r)
+          for (int32_t x = 0; x < words; ++x)
+            if (bits[r * words + x]) f |= 1u << (4 * w + x);
         for (int32_t lane = 0; lane < 64; ++lane) {
           const int32_t row = 32 * w + (lane & 31);
           uint64_t word = 0;
@@ -341,7 +340,7 @@ int fwn_tiles_prepare(int32_t n_blocks, int32_t n_tiles, int32_t n_cols, const i
           lanes[t * FWN_LANE_WORDS + w * 64 + lane] = word;
         }
       }
-      full[t] = f;
+      groups[t] = f;
     }
   });
   if (bad) return fwn::fail(FWN_ERR_TILES, "fwn_tiles_prepare: a tile has bits set beyond n_cols");

@@ -43,7 +43,7 @@ class AttnDesc(ctypes.Structure):
 
 class Tiles(ctypes.Structure):
   _fields_ = [("n_blocks", ctypes.c_int32), ("n_tiles", ctypes.c_int32), ("ptr", ctypes.c_void_p),
-              ("col", ctypes.c_void_p), ("lanes", ctypes.c_void_p), ("full", ctypes.c_void_p),
+              ("col", ctypes.c_void_p), ("lanes", ctypes.c_void_p), ("groups", ctypes.c_void_p),
               ("n_items", ctypes.c_int32), ("n_parts", ctypes.c_int32), ("n_split", ctypes.c_int32),
               ("reserved", ctypes.c_int32), ("items", ctypes.c_void_p), ("split", ctypes.c_void_p)]
 

@@ -47,9 +47,9 @@ class TileList:
     self.n_cols = int(n_cols)
     L = nat.lib()
     lanes = np.zeros((self.n_tiles, nat.LANE_WORDS), np.uint64)
-    full = np.zeros(self.n_tiles, np.uint32)
+    groups = np.zeros(self.n_tiles, np.uint32)
     nat.check(L.fwn_tiles_prepare(self.n_blocks, self.n_tiles, self.n_cols, nat.ptr(tile_ptr), nat.ptr(tile_kb),
-                                  nat.ptr(tile_bits), nat.ptr(lanes), nat.ptr(full)))
+                                  nat.ptr(tile_bits), nat.ptr(lanes), nat.ptr(groups)))
     # Work items: each block's run of tiles cut into pieces of at most max_item_tiles (split-K).
     counts = np.zeros(3, np.int32)
     nat.check(L.fwn_tiles_schedule_count(self.n_blocks, nat.ptr(tile_ptr), int(max_item_tiles), nat.ptr(counts[0:]),
@@ -66,14 +66,15 @@ class TileList:
     self.ptr = put(tile_ptr)
     self.col = put(tile_kb)
     self.lanes = put(lanes.view(np.int64))
-    self.full = put(full.view(np.int32))
+    self.groups = put(groups.view(np.int32))
+    self.groups_host = groups
     self.items = put(items)
     self.split = put(split)
     self.counts = np.diff(tile_ptr)
     self.nnz = int(np.unpackbits(tile_bits.view(np.uint8)).sum()) if self.n_tiles else 0
     addr = lambda t: t.data_ptr() if t.numel() else None
     self.struct = nat.Tiles(self.n_blocks, self.n_tiles, addr(self.ptr), addr(self.col), addr(self.lanes),
-                            addr(self.full), self.n_items, self.n_parts, self.n_split, 0, addr(self.items),
+                            addr(self.groups), self.n_items, self.n_parts, self.n_split, 0, addr(self.items),
                             addr(self.split) if self.n_split else None)
 
   def workspace_bytes(self, desc):

@@ -76,7 +76,7 @@ typedef struct fwn_item {
 
 /* Device view of a prepared tile list (see fwn_tiles_prepare, fwn_tiles_schedule_fill).
  * `ptr`/`col` are the CSR tile list of pallas_attn.build_tile_mask (pallas_attn.py:85-109) at
- * 128 x 128; `lanes` and `full` hold its bitmasks in the kernels' register layout. For the dK/dV
+ * 128 x 128; `lanes` and `groups` hold its bitmasks in the kernels' layout. For the dK/dV
  * launcher the list must be the transposed mask's (rows = keys, columns = queries), as the
  * reference's tiles_t (pallas_attn.py:297-310; equal to the forward list for symmetric masks). */
 typedef struct fwn_tiles {
@@ -85,7 +85,8 @@ typedef struct fwn_tiles {
   const int32_t* ptr;       /* [n_blocks + 1] */
   const int32_t* col;       /* [n_tiles] column block of each tile */
   const uint64_t* lanes;    /* [n_tiles][FWN_WAVES][64 lanes]: bit e = accumulator element e of that lane */
-  const uint32_t* full;     /* [n_tiles] bit w: rows 32w..32w+31 of the tile are all valid */
+  const uint32_t* groups;   /* [n_tiles] bit 4r + c: rows 32r..32r+31 of the tile have a valid
+                               element in columns 32c..32c+31 (the kernels skip the others) */
   int32_t n_items;          /* work items: every block appears, empty blocks included */
   int32_t n_parts;          /* partial slots (items with part >= 0) */
   int32_t n_split;          /* blocks cut into more than one item */
@@ -130,11 +131,11 @@ int fwn_tiles_fill(int32_t n_rows, int32_t n_cols, const int64_t* row_ptr, const
                    uint32_t* tile_bits);
 
 /* Validates a canonical tile list (tile_ptr, tile_col, tile_bits as above, n_cols columns) and
- * converts it into the kernels' layout: lanes[n_tiles * FWN_LANE_WORDS] and full[n_tiles]
+ * converts it into the kernels' layout: lanes[n_tiles * FWN_LANE_WORDS] and groups[n_tiles]
  * (host buffers; the caller copies them to the device). */
 int fwn_tiles_prepare(int32_t n_blocks, int32_t n_tiles, int32_t n_cols, const int32_t* tile_ptr,
                       const int32_t* tile_col, const uint32_t* tile_bits, uint64_t* lanes,
-                      uint32_t* full);
+                      uint32_t* groups);
 
 /* Work items of a tile list: the tiles of each block are cut into ceil(count / max_item_tiles)
  * runs of near-equal length (max_item_tiles <= 0 selects FWN_ITEM_TILES). The reference runs one

@@ -118,16 +118,43 @@ def test_prepare_layout_roundtrip():
   tp, kb, bits = fwn.build_tile_mask(m)
   T, nb = len(kb), len(tp) - 1
   lanes = np.zeros((T, nat.LANE_WORDS), np.uint64)
-  full = np.zeros(T, np.uint32)
+  groups = np.zeros(T, np.uint32)
   nat.check(nat.lib().fwn_tiles_prepare(nb, T, n, nat.ptr(tp), nat.ptr(kb), nat.ptr(bits), nat.ptr(lanes),
-                                        nat.ptr(full)))
+                                        nat.ptr(groups)))
   dense = ((bits[:, :, :, None] >> np.arange(32, dtype=np.uint32)) & 1).astype(bool).reshape(T, 128, 128)
   np.testing.assert_array_equal(_decode_lanes(lanes, T), dense)
-  expect_full = np.zeros(T, np.uint32)
-  for w in range(4):
-    expect_full |= dense[:, 32 * w:32 * w + 32].reshape(T, -1).all(1).astype(np.uint32) << w
-  np.testing.assert_array_equal(full, expect_full)
-  assert full.max() == 15
+  # groups: bit 4r + c set iff the 32 x 32 block (rows 32r.., columns 32c..) has a valid element.
+  expect = np.zeros(T, np.uint32)
+  for r in range(4):
+    for c in range(4):
+      expect |= dense[:, 32 * r:32 * r + 32, 32 * c:32 * c + 32].reshape(T, -1).any(1).astype(np.uint32) << (4 * r + c)
+  np.testing.assert_array_equal(groups, expect)
+  full_tile = np.flatnonzero((tp[0] <= np.arange(T)) & (np.arange(T) < tp[1]) & (kb == 1))
+  assert groups[full_tile[0]] == 0xFFFF
+  assert 0 < np.mean(groups != 0xFFFF)  # the random tiles leave some blocks empty
+
+
+def test_prepare_groups_single_elements():
+  # One valid element per tile at (row, column): exactly bit 4 * (row // 32) + column // 32.
+  n = 512
+  rows, cols = [5, 40, 70, 127, 300, 511], [100, 3, 64, 127, 33, 500]
+  from scipy import sparse
+  m = sparse.csr_matrix((np.ones(len(rows), bool), (rows, cols)), shape=(n, n))
+  tp, kb, bits = fwn.build_tile_mask(m)
+  T, nb = len(kb), len(tp) - 1
+  lanes = np.zeros((T, nat.LANE_WORDS), np.uint64)
+  groups = np.zeros(T, np.uint32)
+  nat.check(nat.lib().fwn_tiles_prepare(nb, T, n, nat.ptr(tp), nat.ptr(kb), nat.ptr(bits), nat.ptr(lanes),
+                                        nat.ptr(groups)))
+  got = {}
+  for qb in range(nb):
+    for t in range(tp[qb], tp[qb + 1]):
+      got[(qb, int(kb[t]))] = int(groups[t])
+  expect = {}
+  for r, c in zip(rows, cols):
+    key = (r // 128, c // 128)
+    expect[key] = expect.get(key, 0) | 1 << (4 * ((r % 128) // 32) + (c % 128) // 32)
+  assert got == expect
 
 
 def _schedule(tp, max_item_tiles):
@@ -198,9 +225,9 @@ def test_prepare_rejects_malformed_lists(case):
     bits[last, 0, 3] |= np.uint32(1 << 31)  # column 2*128 + 127 >= n
   T, nb = len(kb), len(tp) - 1
   lanes = np.zeros((T, nat.LANE_WORDS), np.uint64)
-  full = np.zeros(T, np.uint32)
+  groups = np.zeros(T, np.uint32)
   status = nat.lib().fwn_tiles_prepare(nb, T, n, nat.ptr(tp), nat.ptr(kb), nat.ptr(bits), nat.ptr(lanes),
-                                       nat.ptr(full))
+                                       nat.ptr(groups))
   assert status == nat.ERR_TILES
   assert nat.lib().fwn_last_error()
 
