@@ -294,6 +294,7 @@ def main():
       "config": {"workload": cfg["desc"], "mesh_refinement": 6, "n": n, "k_hop": cfg["k_hop"], "batch": B,
                  "heads": H, "head_dim": D, "order": "hilbert" if cfg["reorder"] else "subdivision",
                  "sigma": cfg["sigma"], "live_tiles": T, "tile_density": round(tiles.density, 4),
+                 "live_group_fraction": round(tiles.group_fraction, 4),
                  "valid_entries": int(mask.nnz)},
       "roofline": {"bound": "mfma", "kernel": dominant, "achieved": round(achieved, 3), "peak": peak,
                    "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": traffic,

@@ -94,6 +94,15 @@ class TileList:
     """Fraction of valid entries in the live tiles."""
     return self.nnz / max(1, self.n_tiles * nat.BLOCK * nat.BLOCK)
 
+  @property
+  def group_fraction(self):
+    """Fraction of the live tiles' 32 x 32 groups that hold a valid element: the share of the
+    live-tile work the kernels execute (the other groups are skipped)."""
+    if not self.n_tiles:
+      return 0.0
+    bits = np.unpackbits(self.groups_host.astype('<u4').view(np.uint8)).sum()
+    return float(bits) / (16 * self.n_tiles)
+
 
 _cache_lock = threading.Lock()
 _cache = {}
