@@ -284,67 +284,79 @@ __global__ void __launch_bounds__(NT, 2) dq_kernel(KArgs a) {
 
   int t0, t1;
   tile_range(a, j, t0, t1);
-  u32x2 mbits = {0u, 0u};  // mask bits of the next tile, loaded with its copy
-  uint32_t gnext = 0u;     // group bits of the next tile, loaded a tile ahead of its copy
+  // Each tile is copied in two halves: rows 0-63 (key groups 0-1) and rows 64-127 (groups 2-3).
+  // A half of tile t+1 is copied while the other half of tile t is computed, so every copy has
+  // half a tile of work to hide behind. Per tile: wait + barrier, copy the second half of t,
+  // groups 0-1 of t, wait + barrier, copy the first half of t+1, groups 2-3 of t.
+  u32x2 mbits = {0u, 0u};  // mask bits of the next tile, loaded with its first half
+  uint32_t gcur = 0u, gnext = 0u;
   if (t0 < t1) {
     const int kb = ((ci32_ptr)a.col)[t0];
     mbits = tile_bits(a, t0, w, lane);
-    gnext = tile_groups(a, t0);
-    dma.issue(rK, K, w, kb * BLK, snb);
-    dma.issue(rV, V, w, kb * BLK, snb);
+    gcur = tile_groups(a, t0);
+    dma.issue(rK, K, w, kb * BLK, snb, 3u);
+    dma.issue(rV, V, w, kb * BLK, snb, 3u);
   }
+  auto group = [&](int sb, const u32x2& mb) {
+    u32x4 ka[D / 16], va[D / 16];
+#pragma unroll
+    for (int k = 0; k < D / 16; ++k) {
+      ka[k] = row_read(K, off.row[k] + sb * 32 * (2 * D));
+      va[k] = row_read(V, off.row[k] + sb * 32 * (2 * D));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    f32x16 s = zero16(), dp = zero16();
+#pragma unroll
+    for (int k = 0; k < D / 16; ++k) {
+      s = mfma_bf16(ka[k], qf[k], s);
+      dp = mfma_bf16(va[k], df[k], dp);
+    }
+    u32x4 kt[D / 32][2];
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+      for (int c = 0; c < 2; ++c) kt[db][c] = tr_operand<D>(K, off, db, sb, c);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float p = keep_or_zero(fast_exp2(fmaf(s[r], a.c2, -lse_t)), elem_keep(mb, sb, r));
+      dp[r] = p * (dp[r] - delta);
+    }
+    const bf16x8 d0 = pack_bf16(dp, 0), d1 = pack_bf16(dp, 1);
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db) {
+      acc[db] = mfma_bf16(kt[db][0], d0, acc[db]);
+      acc[db] = mfma_bf16(kt[db][1], d1, acc[db]);
+    }
+  };
   for (int tt = t0; tt < t1; ++tt) {
     const int t = __builtin_amdgcn_readfirstlane(tt);
-    wait_vmem();
-    __syncthreads();
+    const int kb = ((ci32_ptr)a.col)[t];
+    wait_vmem();      // this wave's part of rows 0-63 of tile t and its mask bits
+    __syncthreads();  // all of rows 0-63 landed; every wave is done with rows 64-127 of tile t-1
     const u32x2 mb = mbits;
-    const uint32_t gt = gnext;
+    const uint32_t gt = gcur;
     if (t + 1 < t1) gnext = tile_groups(a, t + 1);
+    const uint32_t copy = any_rows(gt);
+    dma.issue(rK, K, w, kb * BLK, snb, copy & 12u);
+    dma.issue(rV, V, w, kb * BLK, snb, copy & 12u);
     // Key groups with no valid element for this wave are skipped (p = 0 throughout); key groups
     // with none for any wave are not copied either.
     const uint32_t live = gt >> (4 * w) & 15u;
-#pragma unroll
-    for (int sb = 0; sb < 4; ++sb) {
-      if (!(live >> sb & 1u)) continue;
-      u32x4 ka[D / 16], va[D / 16];
-#pragma unroll
-      for (int k = 0; k < D / 16; ++k) {
-        ka[k] = row_read(K, off.row[k] + sb * 32 * (2 * D));
-        va[k] = row_read(V, off.row[k] + sb * 32 * (2 * D));
-      }
-      __builtin_amdgcn_sched_barrier(0);
-      f32x16 s = zero16(), dp = zero16();
-#pragma unroll
-      for (int k = 0; k < D / 16; ++k) {
-        s = mfma_bf16(ka[k], qf[k], s);
-        dp = mfma_bf16(va[k], df[k], dp);
-      }
-      u32x4 kt[D / 32][2];
-#pragma unroll
-      for (int db = 0; db < D / 32; ++db)
-#pragma unroll
-        for (int c = 0; c < 2; ++c) kt[db][c] = tr_operand<D>(K, off, db, sb, c);
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = keep_or_zero(fast_exp2(fmaf(s[r], a.c2, -lse_t)), elem_keep(mb, sb, r));
-        dp[r] = p * (dp[r] - delta);
-      }
-      const bf16x8 d0 = pack_bf16(dp, 0), d1 = pack_bf16(dp, 1);
-#pragma unroll
-      for (int db = 0; db < D / 32; ++db) {
-        acc[db] = mfma_bf16(kt[db][0], d0, acc[db]);
-        acc[db] = mfma_bf16(kt[db][1], d1, acc[db]);
-      }
-    }
-    __syncthreads();  // every wave is done with K(t) and V(t)
+    if (live & 1u) group(0, mb);
+    if (live & 2u) group(1, mb);
+    wait_vmem();      // this wave's part of rows 64-127 of tile t
+    __syncthreads();  // all of rows 64-127 landed; every wave is done with rows 0-63 of tile t
     if (t + 1 < t1) {
-      const int kb = ((ci32_ptr)a.col)[t + 1];
-      const uint32_t copy = any_rows(gnext);
+      const int kb1 = ((ci32_ptr)a.col)[t + 1];
+      const uint32_t copy1 = any_rows(gnext);
       mbits = tile_bits(a, t + 1, w, lane);
-      dma.issue(rK, K, w, kb * BLK, snb, copy);
-      dma.issue(rV, V, w, kb * BLK, snb, copy);
+      dma.issue(rK, K, w, kb1 * BLK, snb, copy1 & 3u);
+      dma.issue(rV, V, w, kb1 * BLK, snb, copy1 & 3u);
     }
+    if (live & 4u) group(2, mb);
+    if (live & 8u) group(3, mb);
+    gcur = gnext;
   }
   if (j.part >= 0) {
     store_bwd_partial<D>(a, j, 32 * w + i, acc, 0, g);
