@@ -1,4 +1,4 @@
-"""ctypes binding of libfwn_attn.so (the C ABI declared in include/fwn_attn.h).
+"""ctypes binding of libfwn_attn.so (the C ABI declared in include/fwn_attn.h and include/fwn_rows.h).
 
 The library is loaded on first use from ``_lib/libfwn_attn.so`` next to this file. There is no
 fallback: if it is missing or does not export every declared symbol, ``lib()`` raises.
@@ -51,12 +51,21 @@ class Tiles(ctypes.Structure):
 ITEM_TILES = 64  # FWN_ITEM_TILES: default longest run of tiles per work item
 
 
+class RowsDesc(ctypes.Structure):
+  _fields_ = [("batch", ctypes.c_int32), ("n", ctypes.c_int32), ("channels", ctypes.c_int32),
+              ("dtype", ctypes.c_int32), ("eps", ctypes.c_float)]
+
+
+ROWS_MAX_CHANNELS = 4096  # FWN_ROWS_MAX_CHANNELS
+
+
 _P = ctypes.c_void_p
 _I32, _I64, _U64, _F = ctypes.c_int32, ctypes.c_int64, ctypes.c_uint64, ctypes.c_float
 _DESC = ctypes.POINTER(AttnDesc)
 _TILES = ctypes.POINTER(Tiles)
+_ROWS = ctypes.POINTER(RowsDesc)
 
-# name -> argtypes, every entry point of include/fwn_attn.h
+# name -> argtypes, every entry point of include/fwn_attn.h and include/fwn_rows.h
 SIGNATURES = {
     "fwn_last_error": [],
     "fwn_khop_count": [_I32, _P, _P, _I32, _P],
@@ -73,6 +82,8 @@ SIGNATURES = {
     "fwn_attn_bwd_dq_launch": [_DESC, _P, _P, _P, _P, _P, _P, _TILES, _P, _P, _U64, _P],
     "fwn_attn_bwd_dkv_launch": [_DESC, _P, _P, _P, _P, _P, _P, _TILES, _P, _P, _P, _U64, _P],
     "fwn_attn_bwd_launch": [_DESC, _P, _P, _P, _P, _P, _P, _P, _TILES, _TILES, _P, _P, _P, _P, _U64, _P],
+    "fwn_rows_gather_norm_launch": [_ROWS, _P, _P, _P, _P, _P],
+    "fwn_rows_norm_scatter_launch": [_ROWS, _P, _P, _P, _P, _P, _P],
 }
 
 _lock = threading.Lock()

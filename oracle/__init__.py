@@ -9,6 +9,8 @@ This package restates, on the CPU and in float64 where it matters, what the refe
 * ``attention`` dense masked softmax attention and its analytic gradients
                 (``tests/test_pallas_kernel.py:15-21, 58-69``), and the reference XLA chunked path
                 (``patch.py:106-162``, ``scripts/attn_bench.py:55-77``) with its backward.
+* ``rows``      the Hilbert gather/scatter of the node features either side of the layer loop
+                and the layer norms next to them (``patch.py:244, 274-276, 288-292``).
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
 import this package, and only as the checker or the timed CPU baseline. The product
@@ -31,4 +33,8 @@ How each function is pinned (checks live in ``tests/test_oracle.py``):
   ``tests/test_masks.py:39-52``.
 * ``tiles.build_tile_mask``: dense round trip and distinct non-empty tiles per block
   (``tests/test_masks.py:25-36``).
+* ``rows.gather`` / ``scatter``: scatter inverts gather for the same permutation, and gather
+  with the identity is the identity. ``rows.layer_norm``: every row has mean 0 and variance
+  var / (var + eps); it is invariant to adding a constant to a row and to scaling it by a
+  positive factor when eps = 0; on a two-value row it reduces to +-1 in closed form.
 """

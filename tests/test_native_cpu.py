@@ -24,7 +24,7 @@ def _random_mask(n, density, seed, symmetric=False):
 
 
 def test_library_exports_every_declared_symbol():
-  header = open(os.path.join(ROOT, "include", "fwn_attn.h")).read()
+  header = "".join(open(os.path.join(ROOT, "include", h)).read() for h in ("fwn_attn.h", "fwn_rows.h"))
   declared = set(re.findall(r"^(?:int|const char\*)\s+(fwn_\w+)\(", header, re.M))
   assert declared == set(nat.SIGNATURES), declared ^ set(nat.SIGNATURES)
   lib = ctypes.CDLL(nat.LIB_PATH)
@@ -385,3 +385,64 @@ def test_tile_mask_cache_keys_on_content(tmp_path):
   ref = fwn.build_tile_mask(m2.tocsr())
   for x, y in zip(b[:3], ref):
     np.testing.assert_array_equal(x, y)
+
+
+# ---- row permutation passes (include/fwn_rows.h): host validation, no GPU calls ----
+
+_ROW_PTR = 1 << 20  # an aligned fake device address: validation fails before any launch
+
+
+def _rows_desc(**kw):
+  d = dict(batch=1, n=64, channels=768, dtype=nat.F32, eps=1e-5)
+  d.update(kw)
+  return nat.RowsDesc(d["batch"], d["n"], d["channels"], d["dtype"], d["eps"])
+
+
+@pytest.mark.parametrize("kw, code", [
+    (dict(channels=0), nat.ERR_INVALID_ARG),
+    (dict(channels=12), nat.ERR_INVALID_ARG),                 # not a multiple of 8
+    (dict(channels=nat.ROWS_MAX_CHANNELS + 8), nat.ERR_INVALID_ARG),
+    (dict(n=-1), nat.ERR_INVALID_ARG),
+    (dict(batch=-2), nat.ERR_INVALID_ARG),
+    (dict(dtype=7), nat.ERR_UNSUPPORTED),
+    (dict(eps=float("nan")), nat.ERR_INVALID_ARG),
+    (dict(eps=-1.0), nat.ERR_INVALID_ARG),
+])
+def test_rows_launchers_reject_bad_descriptors(kw, code):
+  L = nat.lib()
+  d = _rows_desc(**kw)
+  P = _ROW_PTR
+  assert L.fwn_rows_gather_norm_launch(d, P, P + (1 << 24), P + (2 << 24), P + (3 << 24), None) == code
+  assert L.fwn_rows_norm_scatter_launch(d, P, P + (1 << 24), None, None, P + (2 << 24), None) == code
+  assert L.fwn_last_error()
+
+
+def test_rows_launchers_reject_bad_pointers():
+  L = nat.lib()
+  d = _rows_desc()
+  P, Q, R, S = _ROW_PTR, _ROW_PTR + (1 << 24), _ROW_PTR + (2 << 24), _ROW_PTR + (3 << 24)
+  bad = nat.ERR_INVALID_ARG
+  assert L.fwn_rows_gather_norm_launch(None, P, Q, R, S, None) == bad
+  assert L.fwn_rows_gather_norm_launch(d, None, Q, R, S, None) == bad   # x
+  assert L.fwn_rows_gather_norm_launch(d, P, None, R, S, None) == bad   # perm
+  assert L.fwn_rows_gather_norm_launch(d, P, Q, None, S, None) == bad   # x_out
+  assert L.fwn_rows_gather_norm_launch(d, P + 4, Q, R, S, None) == bad  # misaligned x
+  assert L.fwn_rows_gather_norm_launch(d, P, Q, R, S + 8, None) == bad  # misaligned norm_out
+  assert L.fwn_rows_gather_norm_launch(d, P, Q, P + 64, S, None) == bad  # x_out overlaps x
+  assert L.fwn_rows_gather_norm_launch(d, P, Q, R, R + 64, None) == bad  # norm_out overlaps x_out
+  assert L.fwn_rows_norm_scatter_launch(d, P, Q, None, None, None, None) == bad  # out
+  assert L.fwn_rows_norm_scatter_launch(d, P, Q, R + 4, None, S, None) == bad    # misaligned mul
+  assert L.fwn_rows_norm_scatter_launch(d, P, Q, None, R + 4, S, None) == bad    # misaligned add
+  assert L.fwn_rows_norm_scatter_launch(d, P, Q, None, None, P + 64, None) == bad  # out overlaps x
+  assert b"overlap" in L.fwn_last_error()
+
+
+def test_rows_python_wrappers_reject_cpu_tensors():
+  import torch
+  from faster_weathernext_amd import rows
+  x = torch.zeros(1, 16, 64)
+  perm = torch.arange(16)
+  with pytest.raises(ValueError):
+    rows.gather_layer_norm(x, perm)
+  with pytest.raises(ValueError):
+    rows.layer_norm_scatter(x, perm)

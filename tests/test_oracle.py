@@ -10,7 +10,7 @@ import pytest
 from scipy import sparse
 
 from oracle import attention as A
-from oracle import mesh, tiles
+from oracle import mesh, rows, tiles
 
 
 def _random_mask(n, density, seed, symmetric=False):
@@ -257,3 +257,37 @@ def test_sampled_attention_equals_dense():
   np.testing.assert_allclose(got["dq"], dq[:, rows], atol=1e-12)
   np.testing.assert_allclose(got["dk"], dk[:, keys], atol=1e-12)
   np.testing.assert_allclose(got["dv"], dv[:, keys], atol=1e-12)
+
+
+# ---- oracle.rows: the gather/scatter either side of the layer loop and the layer norm ----
+
+def test_rows_scatter_inverts_gather():
+  rng = np.random.default_rng(0)
+  x = rng.standard_normal((2, 50, 24))
+  perm = rng.permutation(50)
+  np.testing.assert_array_equal(rows.scatter(rows.gather(x, perm), perm), x)
+  np.testing.assert_array_equal(rows.gather(rows.scatter(x, perm), perm), x)
+  np.testing.assert_array_equal(rows.gather(x, np.arange(50)), x)
+  # scatter with perm is take(., argsort(perm)) (patch.py:291-292)
+  np.testing.assert_array_equal(rows.scatter(x, perm), np.take(x, np.argsort(perm), axis=1))
+
+
+def test_rows_layer_norm_closed_forms():
+  rng = np.random.default_rng(1)
+  x = rng.standard_normal((3, 7, 40)) * 5 + 2
+  eps = 1e-5
+  y = rows.layer_norm(x, eps)
+  var = x.var(-1)
+  np.testing.assert_allclose(y.mean(-1), 0, atol=1e-12)
+  np.testing.assert_allclose(y.var(-1), var / (var + eps), rtol=1e-12)
+  # shift invariance, and scale invariance at eps = 0
+  np.testing.assert_allclose(rows.layer_norm(x + 3.5, eps), y, atol=1e-12)
+  np.testing.assert_allclose(rows.layer_norm(4 * x, 0.0), rows.layer_norm(x, 0.0), atol=1e-12)
+  # a row of equally many a's and b's normalises to -1 / +1 (eps = 0)
+  two = np.array([[[1.0, 3.0] * 8]])
+  np.testing.assert_allclose(rows.layer_norm(two, 0.0), [[[-1.0, 1.0] * 8]], atol=1e-15)
+  # a constant row has zero variance and normalises to 0
+  np.testing.assert_array_equal(rows.layer_norm(np.full((1, 1, 8), 2.0), eps), 0.0)
+  # the affine is applied per (batch, channel)
+  mul, add = rng.standard_normal((3, 40)), rng.standard_normal((3, 40))
+  np.testing.assert_allclose(rows.norm_affine(x, mul, add, eps), y * mul[:, None] + add[:, None], rtol=1e-15)
