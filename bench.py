@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the block-sparse masked mesh attention on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c3|c2|c4|c5|c5mha] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c3|c2|c4|c5|c5mha|rows] [--no-cpu]
 
 A step is one pass of the hot path over one batch of synthetic input: for the default workload
 (configuration 3 of BASELINE.json) the forward kernel plus the backward (delta pre-pass, dQ,
@@ -41,6 +41,9 @@ WORKLOADS = {
                   d_model=768,
                   desc="WN2 attention block at C5 shape: fused q/k/v projection (768 -> 3x6x128), HIP attention "
                        "read in place, mha_final projection; forward + backward, bf16, random-init weights"),
+    "rows": dict(dtype="f32", channels=768, batch=1,
+                 desc="Hilbert gather + first layer norm and final layer norm + affine + scatter of the node "
+                      "features [1, 40962, 768] float32, once each per step (patch.py:244, 274-276, 288-292)"),
 }
 
 
@@ -152,6 +155,81 @@ def mha_block(args):
   return 0
 
 
+def row_passes(args):
+  """Times the two fused row passes of a step (gather + layer norm, layer norm + affine + scatter)
+  against the same work as separate torch operations. The metric is HBM GB/s over the passes'
+  algorithmic bytes: x read once and x_out, norm_out written (gather), x read and out written
+  (scatter), 5 tensors of [batch, n, channels] per step (the [batch, channels] affine and the
+  permutation are negligible)."""
+  import numpy as np
+  import torch
+
+  import faster_weathernext_amd as fwn
+  from faster_weathernext_amd import rows
+  cfg = WORKLOADS[args.workload]
+  dev = torch.device("cuda:0")
+  torch.cuda.set_device(dev)
+  v, f, lat, lon = fwn.icosahedral_mesh(6)
+  perm = torch.from_numpy(np.asarray(fwn.hilbert_order(lat, lon), np.int64)).to(dev)
+  inv = torch.argsort(perm)
+  B, n, C = cfg["batch"], len(lat), cfg["channels"]
+  dtype = torch.float32 if cfg["dtype"] == "f32" else torch.bfloat16
+  g = torch.Generator(device=dev).manual_seed(0)
+  x = torch.randn(B, n, C, device=dev, generator=g).to(dtype)
+  mul = 1 + 0.1 * torch.randn(B, C, device=dev, generator=g)
+  add = torch.randn(B, C, device=dev, generator=g)
+  stream = torch.cuda.current_stream(dev)
+
+  def fused():
+    xp, yp = rows.gather_layer_norm_forward(x, perm)
+    return rows.layer_norm_scatter_forward(xp, perm, mul, add)
+
+  def unfused():
+    xp = torch.index_select(x, 1, perm)
+    yp = torch.nn.functional.layer_norm(xp, (C,), eps=1e-5)
+    z = torch.nn.functional.layer_norm(xp, (C,), eps=1e-5) * mul[:, None].to(dtype) + add[:, None].to(dtype)
+    return torch.index_select(z, 1, inv), yp
+
+  def timed(fn):
+    for _ in range(args.warmup):
+      fn()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(args.steps):
+      fn()
+    stop.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / args.steps
+
+  # Per-pass durations on the launch stream (the roofline entry): each pass launched `steps` times
+  # back to back between two events, so host-side call overhead overlaps the kernels.
+  xp, _ = rows.gather_layer_norm_forward(x, perm)
+  t_gather = timed(lambda: rows.gather_layer_norm_forward(x, perm))
+  t_scatter = timed(lambda: rows.layer_norm_scatter_forward(xp, perm, mul, add))
+  ms_fused = timed(fused)
+  ms_unfused = timed(unfused)
+  row_bytes = B * n * C * x.element_size()
+  value = 5 * row_bytes / (ms_fused * 1e-3) / 1e9
+  achieved = 3 * row_bytes / (t_gather * 1e-3) / 1e9
+  result = {
+      "metric": "HBM GB/s of the fused Hilbert gather/scatter + layer-norm passes (algorithmic bytes), 1 GPU",
+      "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+      "ms_per_step": round(ms_fused, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+      "dtype": cfg["dtype"], "data": "synthetic: N(0,1) node features (torch seed 0) on a generated icosahedral mesh",
+      "config": {"workload": cfg["desc"], "mesh_refinement": 6, "n": n, "batch": B, "channels": C},
+      "roofline": {"bound": "hbm", "kernel": "gather_norm", "achieved": round(achieved, 1), "peak": 8000.0,
+                   "unit": "GB/s", "frac": round(achieved / 8000.0, 4),
+                   "traffic": measured_traffic(args.workload, "gather_norm")[0],
+                   "traffic_source": measured_traffic(args.workload, "gather_norm")[1]},
+      "passes_ms": {"gather_norm": round(t_gather, 4), "norm_scatter": round(t_scatter, 4)},
+      "ms_per_step_torch_separate_ops": round(ms_unfused, 4),
+      "speedup_vs_torch": round(ms_unfused / ms_fused, 3),
+  }
+  print(json.dumps(result), flush=True)
+  return 0
+
+
 def cpu_baseline(cfg, q, k, v, do, mask, tiles, scale, budget_s):
   """Times the restated reference XLA chunked path on whole query chunks until `budget_s` elapses."""
   import numpy as np
@@ -192,6 +270,8 @@ def main():
     return copy_calibration(args.copy_mib, args.steps, args.warmup)
   if args.workload == "c5mha":
     return mha_block(args)
+  if args.workload == "rows":
+    return row_passes(args)
   import numpy as np
   import torch
 

