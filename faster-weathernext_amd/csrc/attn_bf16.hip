@@ -193,6 +193,8 @@ __global__ void __launch_bounds__(NT, 2) fwd_kernel(KArgs a) {
     // groups with none for any wave are not copied either.
     const uint32_t live = gt >> (4 * w) & 15u;
     f32x16 s[4];
+    // MFMAs of every live group first, then the masks: a group's mask VALU work then waits on
+    // MFMAs issued several groups earlier rather than on its own.
 #pragma unroll
     for (int sb = 0; sb < 4; ++sb) {
       if (!(live >> sb & 1u)) continue;
@@ -202,6 +204,10 @@ __global__ void __launch_bounds__(NT, 2) fwd_kernel(KArgs a) {
       s[sb] = zero16();
 #pragma unroll
       for (int k = 0; k < D / 16; ++k) s[sb] = mfma_bf16(ka[k], qf[k], s[sb]);
+    }
+#pragma unroll
+    for (int sb = 0; sb < 4; ++sb) {
+      if (!(live >> sb & 1u)) continue;
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[sb][r] = keep_or_ninf(s[sb][r], elem_keep(mb, sb, r));
     }
@@ -210,10 +216,14 @@ __global__ void __launch_bounds__(NT, 2) fwd_kernel(KArgs a) {
     const uint32_t copy_next = any_rows(gnext);
     if (t + 1 < t1) dma.issue(rK, K, w, ((ci32_ptr)a.col)[t + 1] * BLK, snb, copy_next);
     float corr;
-    if (live != 0u && softmax_live(s, live, st, a.c2, corr)) {
+    // The row max and the lazy rescale first; then per group the exponentials and its PV MFMAs,
+    // so one group's VALU work overlaps the previous group's MFMAs.
+    if (live != 0u && softmax_rebase(s, live, st, a.c2, corr)) {
 #pragma unroll
       for (int db = 0; db < D / 32; ++db) o[db] *= corr;
     }
+    const float base = softmax_base(st);
+    float sum = 0.f;
 #pragma unroll
     for (int sb = 0; sb < 4; ++sb) {
       if (!(live >> sb & 1u)) continue;
@@ -222,6 +232,12 @@ __global__ void __launch_bounds__(NT, 2) fwd_kernel(KArgs a) {
       for (int db = 0; db < D / 32; ++db)
 #pragma unroll
         for (int c = 0; c < 2; ++c) va[db][c] = tr_operand<D>(V, off, db, sb, c);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = fast_exp2(fmaf(s[sb][r], a.c2, -base));
+        s[sb][r] = p;
+        sum += p;
+      }
       const bf16x8 p0 = pack_bf16(s[sb], 0), p1 = pack_bf16(s[sb], 1);
 #pragma unroll
       for (int db = 0; db < D / 32; ++db) {
@@ -229,6 +245,7 @@ __global__ void __launch_bounds__(NT, 2) fwd_kernel(KArgs a) {
         o[db] = mfma_bf16(va[db][1], p1, o[db]);
       }
     }
+    st.l += sum;
     wait_vmem();      // this wave's part of K(t+1)
     __syncthreads();  // all of K(t+1) landed; every wave is done reading V(t)
     if (t + 1 < t1) dma.issue(rV, V, w, ((ci32_ptr)a.col)[t + 1] * BLK, snb, copy_next);

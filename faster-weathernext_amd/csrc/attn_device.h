@@ -243,6 +243,37 @@ __device__ __forceinline__ bool softmax_tile(f32x16 (&s)[CAP], SoftmaxState& st,
   return moved;
 }
 
+// First half of softmax_live: the row max over the sub-blocks in `live`, the lazy move of the
+// reference max and the rescale of l. Returns whether m moved (`corr` rescales the caller's
+// accumulators); the caller then computes p = exp2(s * c2 - base) per sub-block with
+// base = softmax_base(st) and adds the row sums to st.l itself.
+__device__ __forceinline__ bool softmax_rebase(const f32x16 (&s)[4], uint32_t live, SoftmaxState& st, float c2,
+                                               float& corr) {
+  const float ninf = -__builtin_inff();
+  float mx = ninf;
+#pragma unroll
+  for (int sb = 0; sb < 4; ++sb)
+    if (live >> sb & 1u) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[sb][r]);
+    }
+  mx = fmaxf(mx, __shfl_xor(mx, 32));
+  const float mxs = mx * c2;
+  corr = 1.f;
+  const bool moved = __builtin_amdgcn_ballot_w64(mxs > st.m + kLazyMax) != 0;
+  if (moved) {
+    const float m_new = fmaxf(st.m, mxs);
+    corr = fast_exp2(st.m - (m_new == ninf ? 0.f : m_new));
+    st.l *= corr;
+    st.m = m_new;
+  }
+  return moved;
+}
+
+__device__ __forceinline__ float softmax_base(const SoftmaxState& st) {
+  return st.m == -__builtin_inff() ? 0.f : st.m;
+}
+
 // softmax_tile over the sub-blocks in `live` only (a nonzero wave-uniform set); the others are
 // neither read nor written.
 __device__ __forceinline__ bool softmax_live(f32x16 (&s)[4], uint32_t live, SoftmaxState& st, float c2,
