@@ -55,6 +55,8 @@ def parse():
   p.add_argument("--workload", default="c3", choices=sorted(WORKLOADS))
   p.add_argument("--cpu-seconds", type=float, default=12.0, help="bounded CPU-baseline sample length")
   p.add_argument("--no-cpu", action="store_true")
+  p.add_argument("--item-tiles", type=int, default=0,
+                 help="longest run of tiles per work item (0: the library default, FWN_ITEM_TILES)")
   p.add_argument("--copy-mib", type=int, default=0,
                  help="instead of the attention step, time a plain device-to-device copy of this many MiB "
                       "(the known-size kernel that scales the FETCH_SIZE / WRITE_SIZE counters)")
@@ -288,7 +290,7 @@ def main():
   mask, lat, lon, perm = fwn.mesh_mask(6, cfg["k_hop"], reorder=cfg["reorder"])
   t_mask = time.perf_counter() - t0
   t0 = time.perf_counter()
-  tiles = fwn.TileList.from_mask(mask, perm, device=dev)
+  tiles = fwn.TileList.from_mask(mask, perm, device=dev, max_item_tiles=args.item_tiles or nat.ITEM_TILES)
   t_tiles = time.perf_counter() - t0
   n = mask.shape[0]
   if perm is not None:

@@ -218,6 +218,65 @@ def test_rows_without_keys_are_zero_and_finite():
     np.testing.assert_array_equal(res[name][:, empty], 0.0)
 
 
+def _group_pattern_mask(seed):
+  """n = 512 mask built from 32 x 32 groups so that the group skipping meets every case: per
+  tile, waves (row groups) with different live column groups, waves with none, column groups
+  live for no wave (not copied), full groups, groups holding a single element, and
+  non-symmetric structure (the dK/dV list is the transposed mask's). Every row has a key."""
+  rng = np.random.default_rng(seed)
+  m = np.zeros((512, 512), bool)
+
+  def group(rb, cb, rg, cg, density=None, single=None):
+    r0, c0 = 128 * rb + 32 * rg, 128 * cb + 32 * cg
+    if single is not None:
+      m[r0 + single[0], c0 + single[1]] = True
+      return
+    g = rng.random((32, 32)) < density if density < 1 else np.ones((32, 32), bool)
+    g[np.arange(32), rng.integers(0, 32, 32)] = True  # every row of the group has a key
+    m[r0:r0 + 32, c0:c0 + 32] |= g
+
+  for rg in range(4):                       # tile (0, 0): one different column group per wave
+    group(0, 0, rg, (rg + 1) % 4, density=0.3)
+  group(0, 1, 2, 0, single=(5, 3))          # tile (0, 1): only wave 2, two single elements
+  group(0, 1, 2, 3, single=(20, 31))
+  group(1, 1, 1, 2, density=1.0)            # tile (1, 1): one full group ...
+  for rg in (0, 2, 3):                      # ... and single elements for the other waves
+    for r in range(32):
+      m[128 + 32 * rg + r, 128 + (r * 7) % 32] = True
+  for rg in range(4):                       # tile (2, 3): column group 1 dead for every wave
+    for cg in (0, 2, 3):
+      group(2, 3, rg, cg, density=0.2)
+  for r in range(32):                       # tile (3, 0): wave 0 only, one key per row
+    m[384 + r, 96 + r] = True
+  for rg in (1, 2, 3):                      # tile (3, 2): waves 1-3, column group 1
+    group(3, 2, rg, 1, density=0.25)
+  assert m.any(1).all()
+  return sparse.csr_matrix(m)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("d", [64, 128])
+def test_group_skipping_patterns(d, dtype):
+  print(f"group patterns d={d} {dtype}", flush=True)
+  m = _group_pattern_mask(21)
+  tiles, tiles_t = fwn.TileList.from_mask(m), fwn.TileList.from_mask(m.T.tocsr())
+  # the designed tiles skip what they should: (0, 1) has only wave 2's bits, (2, 3) no column 1
+  kb = tiles.col.cpu().numpy()
+  ptr = tiles.ptr.cpu().numpy()
+  g01 = tiles.groups_host[ptr[0] + int(np.flatnonzero(kb[ptr[0]:ptr[1]] == 1)[0])]
+  assert g01 == (1 << 8) | (1 << 11)
+  g23 = tiles.groups_host[ptr[2] + int(np.flatnonzero(kb[ptr[2]:ptr[3]] == 3)[0])]
+  assert g23 & 0x2222 == 0 and g23 & 0xDDDD == 0xDDDD
+  rng = np.random.default_rng(22)
+  n, h = 512, 2
+  q, k, v, do = (_rounded(rng.standard_normal((1, n, h, d)), dtype) for _ in range(4))
+  res = _run(q, k, v, do, tiles, d ** -0.5, dtype, tiles_t)
+  dense = m.toarray()
+  _check(res["out"], A.dense_attention(q, k, v, dense, d ** -0.5), dtype, "out")
+  for name, r in zip(("dq", "dk", "dv"), A.dense_grads(q, k, v, do, dense, d ** -0.5)):
+    _check(res[name], r, dtype, name)
+
+
 def test_packed_qkv_strides_through_c_abi():
   """q, k, v as strided views of one [B, n, 3, H, D] buffer, read in place by the kernels."""
   rng = np.random.default_rng(10)
