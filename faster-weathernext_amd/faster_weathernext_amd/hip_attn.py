@@ -194,18 +194,45 @@ def attention_forward(q, k, v, tiles, scale, with_lse=True):
   return out, lse
 
 
+_side_lock = threading.Lock()
+_side_streams = {}
+
+
+def _side_stream(device):
+  """One extra stream per device (default priority) for the dK/dV kernel."""
+  with _side_lock:
+    s = _side_streams.get(device.index)
+    if s is None:
+      s = _side_streams[device.index] = torch.cuda.Stream(device)
+  return s
+
+
 def _backward_into(q, k, v, out, lse, dout, tiles, tiles_t, scale, dq, dk, dv):
-  """Backward kernels (delta pre-pass, dQ, dK/dV) writing dq, dk, dv (q's strides)."""
+  """Backward kernels writing dq, dk, dv (q's strides): the delta pre-pass, then dQ on the current
+  stream and dK/dV on a side stream at the same time (each with its own workspace), joined
+  before returning. The two kernels are independent; run side by side, each fills the CUs the
+  other's last workgroups leave idle (C3: 1.89 -> 1.79 ms per fwd+bwd step). The sequence is
+  what fwn_attn_bwd_launch enqueues on one stream, with the dQ and dK/dV launches overlapped."""
   desc = _desc(q, scale, out)
   n = q.shape[1]
   tl = _as_tiles(tiles, n, q.device)
   tlt = tl if tiles_t is None else _as_tiles(tiles_t, n, q.device)
   delta = torch.empty_like(lse)
-  ws = workspace(desc, q.device, tl, tlt)
-  nat.check(nat.lib().fwn_attn_bwd_launch(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
-                                          dout.data_ptr(), lse.data_ptr(), delta.data_ptr(), tl.struct, tlt.struct,
-                                          dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), *_ws_args(ws),
-                                          _stream(q.device)))
+  ws_q, ws_kv = workspace(desc, q.device, tl), workspace(desc, q.device, tlt)
+  L = nat.lib()
+  main = torch.cuda.current_stream(q.device)
+  nat.check(L.fwn_attn_bwd_delta_launch(desc, out.data_ptr(), dout.data_ptr(), delta.data_ptr(), main.cuda_stream))
+  side = _side_stream(q.device)
+  side.wait_stream(main)
+  nat.check(L.fwn_attn_bwd_dkv_launch(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), dout.data_ptr(),
+                                      lse.data_ptr(), delta.data_ptr(), tlt.struct, dk.data_ptr(), dv.data_ptr(),
+                                      *_ws_args(ws_kv), side.cuda_stream))
+  nat.check(L.fwn_attn_bwd_dq_launch(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), dout.data_ptr(),
+                                     lse.data_ptr(), delta.data_ptr(), tl.struct, dq.data_ptr(), *_ws_args(ws_q),
+                                     main.cuda_stream))
+  # Everything the side stream used was allocated on `main`; ordering main after it keeps the
+  # caching allocator from handing those blocks out while the dK/dV kernel still runs.
+  main.wait_stream(side)
 
 
 def attention_backward(q, k, v, out, lse, dout, tiles, tiles_t, scale):

@@ -192,7 +192,11 @@ int fwn_attn_bwd_dkv_launch(const fwn_attn_desc* desc, const void* q, const void
 /* Whole backward: delta, dq, then dk/dv, in stream order (pallas_attn._attention_bwd,
  * pallas_attn.py:274-311). delta is caller-provided scratch of [batch, heads, n] floats; the
  * workspace must hold the larger of the two lists' sizes (dq and dk/dv run one after the other
- * on `stream` and share it). */
+ * on `stream` and share it). The dq and dk/dv launches only read what delta and the forward
+ * wrote, so a caller with two streams may instead enqueue delta, then dq and dk/dv on different
+ * streams, each with its own workspace, and join them: the two kernels then fill each other's
+ * idle CUs (the Python package does this; 1.89 -> 1.80 ms per fwd+bwd step at refinement 6,
+ * 16-hop, 4 x 128, bf16). */
 int fwn_attn_bwd_launch(const fwn_attn_desc* desc, const void* q, const void* k, const void* v,
                         const void* o, const void* dout, const float* lse, float* delta,
                         const fwn_tiles* tiles, const fwn_tiles* tiles_t, void* dq, void* dk,
