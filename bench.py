@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the block-sparse masked mesh attention on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c3|c2|c4|c5|c5mha|rows] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c3|c2|c4|c5|c5mha|c5stack|rows] [--no-cpu]
 
 A step is one pass of the hot path over one batch of synthetic input: for the default workload
 (configuration 3 of BASELINE.json) the forward kernel plus the backward (delta pre-pass, then dQ
@@ -42,6 +42,11 @@ WORKLOADS = {
                   d_model=768,
                   desc="WN2 attention block at C5 shape: fused q/k/v projection (768 -> 3x6x128), HIP attention "
                        "read in place, mha_final projection; forward + backward, bf16, random-init weights"),
+    "c5stack": dict(k_hop=32, heads=6, head_dim=128, batch=1, dtype="bf16", reorder=True, d_model=768, layers=24,
+                    ffw_hidden=3072, cond_size=32,
+                    desc="WN2 mesh transformer (processor) forward at C5 shape: 24 blocks (conditioned layer norms, "
+                         "fused-QKV HIP attention, GELU MLP 768-3072-768), Hilbert gather/scatter fused with the "
+                         "first and last layer norms; bf16, random-init weights"),
     "rows": dict(dtype="f32", channels=768, batch=1,
                  desc="Hilbert gather + first layer norm and final layer norm + affine + scatter of the node "
                       "features [1, 40962, 768] float32, once each per step (patch.py:244, 274-276, 288-292)"),
@@ -233,6 +238,56 @@ def row_passes(args):
   return 0
 
 
+def mesh_stack(args):
+  """Times one forward of the 24-layer mesh transformer (``transformer.MeshTransformer``) at the
+  C5 shape: the part of a WN2 0.25-degree step that the attention path sits in. The GNN encoder
+  and decoder and the data pipeline are not part of this build, so this is not the whole step."""
+  import torch
+
+  import faster_weathernext_amd as fwn
+  cfg = WORKLOADS[args.workload]
+  dev = torch.device("cuda:0")
+  torch.cuda.set_device(dev)
+  torch.manual_seed(0)
+  t0 = time.perf_counter()
+  model = fwn.MeshTransformer(6, cfg["k_hop"], cfg["layers"], cfg["d_model"], cfg["heads"], cfg["head_dim"],
+                              cfg["ffw_hidden"], cfg["cond_size"], cfg["reorder"], device=dev, dtype=torch.bfloat16)
+  t_build = time.perf_counter() - t0
+  n, B, T = model.n, cfg["batch"], model.tiles.n_tiles
+  x = torch.randn(B, n, cfg["d_model"], device=dev, dtype=torch.bfloat16)
+  cond = torch.randn(B, cfg["cond_size"], device=dev, dtype=torch.bfloat16)
+  stream = torch.cuda.current_stream(dev)
+  with torch.no_grad():
+    for _ in range(args.warmup):
+      model(x, cond)
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(args.steps):
+      model(x, cond)
+    stop.record(stream)
+    torch.cuda.synchronize()
+  ms = start.elapsed_time(stop) / args.steps
+  attn_flops = cfg["layers"] * 4 * cfg["head_dim"] * 128 * 128 * T * B * cfg["heads"]
+  result = {
+      "metric": "seconds per forward of the 24-layer WN2 mesh transformer at 0.25 deg (the attention path's "
+                "share of a 6-h step), 1 GPU",
+      "value": round(ms * 1e-3, 5), "unit": "s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+      "ms_per_step": round(ms, 3), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+      "dtype": "bf16",
+      "data": "synthetic: N(0,1) node features and conditioning (torch seed 0), random-init torch weights, on a "
+              "generated icosahedral mesh; no checkpoints or datasets",
+      "config": {"workload": cfg["desc"], "mesh_refinement": 6, "n": n, "k_hop": cfg["k_hop"], "batch": B,
+                 "layers": cfg["layers"], "heads": cfg["heads"], "head_dim": cfg["head_dim"],
+                 "d_model": cfg["d_model"], "ffw_hidden": cfg["ffw_hidden"], "live_tiles": T},
+      "attention_effective_tflops": round(attn_flops / (ms * 1e-3) / 1e12, 3),
+      "model_build_s": round(t_build, 2),
+      "reference_step_s_rtx5090": {"full_step_tf32": 0.78, "source": "README.md:38, 87 (whole 0.25-deg step)"},
+  }
+  print(json.dumps(result), flush=True)
+  return 0
+
+
 def cpu_baseline(cfg, q, k, v, do, mask, tiles, scale, budget_s):
   """Times the restated reference XLA chunked path on whole query chunks until `budget_s` elapses."""
   import numpy as np
@@ -275,6 +330,8 @@ def main():
     return mha_block(args)
   if args.workload == "rows":
     return row_passes(args)
+  if args.workload == "c5stack":
+    return mesh_stack(args)
   import numpy as np
   import torch
 

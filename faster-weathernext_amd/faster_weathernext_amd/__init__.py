@@ -15,6 +15,7 @@ from .hip_attn import (BLOCK_K, BLOCK_Q, TileList, attention_backward, attention
 from .mesh import adjacency, build_tile_mask, hilbert_order, icosahedral_mesh, khop_mask, mesh_mask
 from .mha import TiledMHA
 from .rows import gather_layer_norm, layer_norm_scatter
+from .transformer import MeshBlock, MeshTransformer
 from .tile_cache import cached_khop_tiles, cached_tile_mask
 
 __version__ = "0.1.0"

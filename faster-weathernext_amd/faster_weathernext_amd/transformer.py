@@ -1,0 +1,111 @@
+"""The mesh transformer around the attention kernels: the reference's patched
+``ChunkedTransformer`` / ``ChunkedBlock`` (``patch.py:193-293``) in PyTorch.
+
+Structure, as the reference wires it:
+
+* at construction, the k-hop mask of the refined icosahedral mesh, the optional Hilbert
+  permutation and the live-tile list, built once and shared by every layer
+  (``_transformer_init``, ``patch.py:193-226``; ``optimization_barrier``, ``:263-266``);
+* before the layers, the gather of the node features into Hilbert order (``:274-276``), here
+  fused with block 0's first layer norm (``rows.gather_layer_norm``);
+* per block (``ChunkedBlock.__call__``, ``:233-253``):
+  ``x = x + mha(cond_norm(layernorm(x)))`` then ``x = x + ffw(cond_norm(layernorm(x)))``, with the
+  attention ``TiledMHA`` (``tiled_mha``, ``:165-177``) on the HIP kernels;
+* after the layers, the final layer norm, its conditioning and the scatter back to mesh order
+  (``:288-292``), fused into one pass (``rows.layer_norm_scatter``).
+
+Two parts live in weathernext, which is not vendored, so their exact form is not pinned here:
+``LinearNormConditioning`` is implemented as published with GenCast (a linear map of the
+conditioning vector, zero-initialised, giving a per-channel scale-minus-one and offset:
+``x * (1 + scale) + offset``), and ``st.ffw`` as a two-layer GELU MLP of width ``ffw_hidden``.
+Parameters are random-initialised torch parameters; official checkpoints are Haiku parameters of
+the JAX model, which this package does not load.
+"""
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+from .hip_attn import TileList
+from .mesh import mesh_mask
+from .mha import TiledMHA
+from .rows import gather_layer_norm, layer_norm_scatter
+
+
+class NormConditioning(torch.nn.Module):
+  """x * (1 + scale(cond)) + offset(cond) per channel; the linear map starts at zero."""
+
+  def __init__(self, d_model, cond_size, device=None, dtype=None):
+    super().__init__()
+    self.linear = torch.nn.Linear(cond_size, 2 * d_model, device=device, dtype=dtype)
+    torch.nn.init.zeros_(self.linear.weight)
+    torch.nn.init.zeros_(self.linear.bias)
+
+  def affine(self, cond):
+    """(multiplier, offset), each [batch, d_model]."""
+    scale_m1, offset = self.linear(cond).chunk(2, dim=-1)
+    return 1 + scale_m1, offset
+
+  def forward(self, x, cond):
+    mul, add = self.affine(cond)
+    return x * mul[:, None, :] + add[:, None, :]
+
+
+class MeshBlock(torch.nn.Module):
+  """One transformer block (``ChunkedBlock``, ``patch.py:229-253``)."""
+
+  def __init__(self, d_model, num_heads, key_size, ffw_hidden, cond_size, tiles, tiles_t=None, *, device=None,
+               dtype=None, eps=1e-5):
+    super().__init__()
+    self.eps = eps
+    kw = dict(device=device, dtype=dtype)
+    self.norm_mha = NormConditioning(d_model, cond_size, **kw)
+    self.mha = TiledMHA(d_model, num_heads, key_size, tiles, tiles_t, **kw)
+    self.norm_ffw = NormConditioning(d_model, cond_size, **kw)
+    self.ffw = torch.nn.Sequential(torch.nn.Linear(d_model, ffw_hidden, **kw), torch.nn.GELU(),
+                                   torch.nn.Linear(ffw_hidden, d_model, **kw))
+
+  def forward(self, x, cond, normed=None):
+    """`normed` is layernorm(x) when the caller has it already (block 0 gets it from the fused
+    gather)."""
+    d = x.shape[-1]
+    if normed is None:
+      normed = F.layer_norm(x, (d,), eps=self.eps)
+    x = x + self.mha(self.norm_mha(normed, cond))
+    return x + self.ffw(self.norm_ffw(F.layer_norm(x, (d,), eps=self.eps), cond))
+
+
+class MeshTransformer(torch.nn.Module):
+  """The 24-layer mesh transformer of WeatherNext 2's processor, node features [batch, n, d_model]
+  in mesh (subdivision) order in and out; the attention runs in Hilbert order when `reorder`."""
+
+  def __init__(self, refinement=6, k_hop=32, num_layers=24, d_model=768, num_heads=6, key_size=128,
+               ffw_hidden=3072, cond_size=32, reorder=True, *, device="cuda", dtype=torch.bfloat16, tiles=None,
+               eps=1e-5):
+    super().__init__()
+    mask, lat, lon, perm = mesh_mask(refinement, k_hop, reorder=reorder)
+    self.n = mask.shape[0]
+    self.eps = eps
+    # One tile list for every layer; the k-hop mask of the symmetric mesh adjacency is symmetric,
+    # so it also serves the backward (patch.py:214-218).
+    self.tiles = tiles if tiles is not None else TileList.from_mask(mask, perm, device=device)
+    self.register_buffer("perm", None if perm is None else torch.from_numpy(np.asarray(perm, np.int64)).to(device),
+                         persistent=False)
+    self.blocks = torch.nn.ModuleList(
+        MeshBlock(d_model, num_heads, key_size, ffw_hidden, cond_size, self.tiles, device=device, dtype=dtype,
+                  eps=eps)
+        for _ in range(num_layers))
+    self.final_norm = NormConditioning(d_model, cond_size, device=device, dtype=dtype)
+
+  def forward(self, x, cond):
+    d = x.shape[-1]
+    normed = None
+    if self.perm is not None:
+      x, normed = gather_layer_norm(x, self.perm, eps=self.eps)
+    elif len(self.blocks):
+      normed = F.layer_norm(x, (d,), eps=self.eps)
+    for i, block in enumerate(self.blocks):
+      x = block(x, cond, normed if i == 0 else None)
+    mul, add = self.final_norm.affine(cond)
+    if self.perm is not None:
+      return layer_norm_scatter(x, self.perm, mul=mul.float().contiguous(), add=add.float().contiguous(), eps=self.eps)
+    return F.layer_norm(x, (d,), eps=self.eps) * mul[:, None, :] + add[:, None, :]

@@ -1,0 +1,68 @@
+"""The mesh transformer wiring (``transformer.MeshTransformer``) against the same model written
+with plain torch operations: a dense masked softmax in place of the HIP attention, and separate
+gather / layer-norm / scatter steps in place of the fused row passes (``patch.py:233-292``).
+Same weights; float32; the check is max rel RMS over the output and the input gradient."""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import faster_weathernext_amd as fwn
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _reference(model, mask, x, cond):
+  d = x.shape[-1]
+  perm = model.perm
+  xp = x[:, perm] if perm is not None else x
+  allowed = torch.from_numpy(mask).to(x.device)
+  for blk in model.blocks:
+    h = blk.norm_mha(F.layer_norm(xp, (d,), eps=model.eps), cond)
+    b, n, _ = h.shape
+    H, Dk = blk.mha.num_heads, blk.mha.key_size
+    q, k, v = blk.mha.qkv(h).view(b, n, 3, H, Dk).unbind(2)
+    s = torch.einsum("bnhd,bmhd->bhnm", q, k) * Dk ** -0.5
+    p = torch.softmax(s.masked_fill(~allowed, float("-inf")), dim=-1)
+    o = torch.einsum("bhnm,bmhd->bnhd", p, v).reshape(b, n, H * Dk)
+    xp = xp + blk.mha.final(o)
+    xp = xp + blk.ffw(blk.norm_ffw(F.layer_norm(xp, (d,), eps=model.eps), cond))
+  mul, add = model.final_norm.affine(cond)
+  y = F.layer_norm(xp, (d,), eps=model.eps) * mul[:, None] + add[:, None]
+  if perm is None:
+    return y
+  out = torch.empty_like(y)
+  out[:, perm] = y
+  return out
+
+
+def _rel_rms(a, b):
+  return float((a - b).square().mean().sqrt() / b.std())
+
+
+@pytest.mark.parametrize("reorder", [True, False])
+def test_mesh_transformer_matches_plain_torch(reorder):
+  print(f"mesh transformer reorder={reorder}", flush=True)
+  torch.manual_seed(0)
+  model = fwn.MeshTransformer(refinement=3, k_hop=2, num_layers=3, d_model=64, num_heads=2, key_size=32,
+                              ffw_hidden=128, cond_size=8, reorder=reorder, device=DEV, dtype=torch.float32)
+  with torch.no_grad():  # the conditioning starts at zero; give it weights so it is exercised
+    for mod in model.modules():
+      if isinstance(mod, fwn.transformer.NormConditioning):
+        mod.linear.weight.normal_(0, 0.1)
+        mod.linear.bias.normal_(0, 0.1)
+  mask, lat, lon, perm = fwn.mesh_mask(3, 2, reorder=reorder)
+  dense = (mask[perm][:, perm] if perm is not None else mask).toarray()
+  n = mask.shape[0]
+  x = torch.randn(2, n, 64, device=DEV, requires_grad=True)
+  cond = torch.randn(2, 8, device=DEV)
+  g = torch.randn(2, n, 64, device=DEV)
+  out = model(x, cond)
+  out.backward(g)
+  gx = x.grad.clone()
+  x.grad = None
+  ref = _reference(model, dense, x, cond)
+  ref.backward(g)
+  assert _rel_rms(out.detach(), ref.detach()) <= 1e-5
+  assert _rel_rms(gx, x.grad) <= 1e-5
