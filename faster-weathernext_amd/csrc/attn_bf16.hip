@@ -192,6 +192,7 @@ __global__ void __launch_bounds__(NT, 2) fwd_kernel(KArgs a) {
     // Key groups with no valid element for this wave are skipped: they would add p = 0. Key
     // groups with none for any wave are not copied either.
     const uint32_t live = gt >> (4 * w) & 15u;
+    const uint32_t full = gt >> (16 + 4 * w) & 15u;  // groups with every element valid: no mask
     f32x16 s[4];
     // MFMAs of every live group first, then the masks: a group's mask VALU work then waits on
     // MFMAs issued several groups earlier rather than on its own.
@@ -207,7 +208,7 @@ __global__ void __launch_bounds__(NT, 2) fwd_kernel(KArgs a) {
     }
 #pragma unroll
     for (int sb = 0; sb < 4; ++sb) {
-      if (!(live >> sb & 1u)) continue;
+      if (!(live >> sb & 1u) || (full >> sb & 1u)) continue;
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[sb][r] = keep_or_ninf(s[sb][r], elem_keep(mb, sb, r));
     }
@@ -314,7 +315,7 @@ __global__ void __launch_bounds__(NT, 2) dq_kernel(KArgs a) {
     dma.issue(rK, K, w, kb * BLK, snb, 3u);
     dma.issue(rV, V, w, kb * BLK, snb, 3u);
   }
-  auto group = [&](int sb, const u32x2& mb) {
+  auto group = [&](int sb, const u32x2& mb, bool full) {
     u32x4 ka[D / 16], va[D / 16];
 #pragma unroll
     for (int k = 0; k < D / 16; ++k) {
@@ -334,10 +335,15 @@ __global__ void __launch_bounds__(NT, 2) dq_kernel(KArgs a) {
 #pragma unroll
       for (int c = 0; c < 2; ++c) kt[db][c] = tr_operand<D>(K, off, db, sb, c);
     __builtin_amdgcn_sched_barrier(0);
+    if (full) {  // every element of the group is valid
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const float p = keep_or_zero(fast_exp2(fmaf(s[r], a.c2, -lse_t)), elem_keep(mb, sb, r));
-      dp[r] = p * (dp[r] - delta);
+      for (int r = 0; r < 16; ++r) dp[r] = fast_exp2(fmaf(s[r], a.c2, -lse_t)) * (dp[r] - delta);
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = keep_or_zero(fast_exp2(fmaf(s[r], a.c2, -lse_t)), elem_keep(mb, sb, r));
+        dp[r] = p * (dp[r] - delta);
+      }
     }
     const bf16x8 d0 = pack_bf16(dp, 0), d1 = pack_bf16(dp, 1);
 #pragma unroll
@@ -360,8 +366,9 @@ __global__ void __launch_bounds__(NT, 2) dq_kernel(KArgs a) {
     // Key groups with no valid element for this wave are skipped (p = 0 throughout); key groups
     // with none for any wave are not copied either.
     const uint32_t live = gt >> (4 * w) & 15u;
-    if (live & 1u) group(0, mb);
-    if (live & 2u) group(1, mb);
+    const uint32_t full = gt >> (16 + 4 * w) & 15u;  // groups with every element valid: no mask
+    if (live & 1u) group(0, mb, full & 1u);
+    if (live & 2u) group(1, mb, full & 2u);
     wait_vmem();      // this wave's part of rows 64-127 of tile t
     __syncthreads();  // all of rows 64-127 landed; every wave is done with rows 0-63 of tile t
     if (t + 1 < t1) {
@@ -371,8 +378,8 @@ __global__ void __launch_bounds__(NT, 2) dq_kernel(KArgs a) {
       dma.issue(rK, K, w, kb1 * BLK, snb, copy1 & 3u);
       dma.issue(rV, V, w, kb1 * BLK, snb, copy1 & 3u);
     }
-    if (live & 4u) group(2, mb);
-    if (live & 8u) group(3, mb);
+    if (live & 4u) group(2, mb, full & 4u);
+    if (live & 8u) group(3, mb, full & 8u);
     gcur = gnext;
   }
   if (j.part >= 0) {
@@ -485,6 +492,7 @@ __global__ void __launch_bounds__(NT8, 1) dkv_kernel(KArgs a) {
     }
     __syncthreads();
     const uint32_t any = any_rows(gcur);
+    const uint32_t full = gcur >> (16 + 4 * w) & 15u;  // query groups with every element valid
     if (t + 1 < t1) {
       mbits = tile_bits(a, t + 1, w, lane);
       issue(t + 1, nxt, any_rows(gnext));
@@ -505,8 +513,13 @@ __global__ void __launch_bounds__(NT8, 1) dkv_kernel(KArgs a) {
       for (int r = 0; r < 16; ++r) sv[r] = lr[r >> 2][r & 3];  // -lse / scale of the element's query
 #pragma unroll
       for (int k = 0; k < D / 16; ++k) sv = mfma_bf16(qa[k], frag[k], sv);
+      if (full >> sb & 1u) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) sv[r] = keep_or_zero(fast_exp2(sv[r] * a.c2), elem_keep(mb, sb, r));
+        for (int r = 0; r < 16; ++r) sv[r] = fast_exp2(sv[r] * a.c2);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sv[r] = keep_or_zero(fast_exp2(sv[r] * a.c2), elem_keep(mb, sb, r));
+      }
       p0 = pack_bf16(sv, 0);
       p1 = pack_bf16(sv, 1);
       lds_char* ps = pslot + slot * PSLOT;

@@ -327,9 +327,15 @@ int fwn_tiles_prepare(int32_t n_blocks, int32_t n_tiles, int32_t n_cols, const i
       }
       uint32_t f = 0;
       for (int32_t w = 0; w < FWN_WAVES; ++w) {
-        for (int32_t r = 32 * w; r < 32 * w + 32; ++r)
-          for (int32_t x = 0; x < words; ++x)
-            if (bits[r * words + x]) f |= 1u << (4 * w + x);
+        for (int32_t x = 0; x < words; ++x) {
+          bool any = false, all = true;
+          for (int32_t r = 32 * w; r < 32 * w + 32; ++r) {
+            any = any || bits[r * words + x] != 0u;
+            all = all && bits[r * words + x] == 0xffffffffu;
+          }
+          if (any) f |= 1u << (4 * w + x);
+          if (all) f |= 1u << (16 + 4 * w + x);
+        }
         for (int32_t lane = 0; lane < 64; ++lane) {
           const int32_t row = 32 * w + (lane & 31);
           uint64_t word = 0;

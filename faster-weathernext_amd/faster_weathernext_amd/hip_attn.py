@@ -100,7 +100,7 @@ class TileList:
     live-tile work the kernels execute (the other groups are skipped)."""
     if not self.n_tiles:
       return 0.0
-    bits = np.unpackbits(self.groups_host.astype('<u4').view(np.uint8)).sum()
+    bits = np.unpackbits((self.groups_host & 0xFFFF).astype('<u4').view(np.uint8)).sum()
     return float(bits) / (16 * self.n_tiles)
 
 

@@ -86,7 +86,9 @@ typedef struct fwn_tiles {
   const int32_t* col;       /* [n_tiles] column block of each tile */
   const uint64_t* lanes;    /* [n_tiles][FWN_WAVES][64 lanes]: bit e = accumulator element e of that lane */
   const uint32_t* groups;   /* [n_tiles] bit 4r + c: rows 32r..32r+31 of the tile have a valid
-                               element in columns 32c..32c+31 (the kernels skip the others) */
+                               element in columns 32c..32c+31 (the kernels skip the others);
+                               bit 16 + 4r + c: every element of that 32 x 32 group is valid
+                               (the kernels apply no mask there) */
   int32_t n_items;          /* work items: every block appears, empty blocks included */
   int32_t n_parts;          /* partial slots (items with part >= 0) */
   int32_t n_split;          /* blocks cut into more than one item */

@@ -123,15 +123,19 @@ def test_prepare_layout_roundtrip():
                                         nat.ptr(groups)))
   dense = ((bits[:, :, :, None] >> np.arange(32, dtype=np.uint32)) & 1).astype(bool).reshape(T, 128, 128)
   np.testing.assert_array_equal(_decode_lanes(lanes, T), dense)
-  # groups: bit 4r + c set iff the 32 x 32 block (rows 32r.., columns 32c..) has a valid element.
+  # groups: bit 4r + c set iff the 32 x 32 block (rows 32r.., columns 32c..) has a valid element,
+  # bit 16 + 4r + c iff every element of it is valid.
   expect = np.zeros(T, np.uint32)
   for r in range(4):
     for c in range(4):
-      expect |= dense[:, 32 * r:32 * r + 32, 32 * c:32 * c + 32].reshape(T, -1).any(1).astype(np.uint32) << (4 * r + c)
+      blk = dense[:, 32 * r:32 * r + 32, 32 * c:32 * c + 32].reshape(T, -1)
+      expect |= blk.any(1).astype(np.uint32) << (4 * r + c)
+      expect |= blk.all(1).astype(np.uint32) << (16 + 4 * r + c)
   np.testing.assert_array_equal(groups, expect)
   full_tile = np.flatnonzero((tp[0] <= np.arange(T)) & (np.arange(T) < tp[1]) & (kb == 1))
-  assert groups[full_tile[0]] == 0xFFFF
-  assert 0 < np.mean(groups != 0xFFFF)  # the random tiles leave some blocks empty
+  assert groups[full_tile[0]] == 0xFFFFFFFF
+  assert 0 < np.mean((groups & 0xFFFF) != 0xFFFF)  # the random tiles leave some blocks empty
+  assert np.all((groups >> 16) & ~groups & 0xFFFF == 0)  # full implies live
 
 
 def test_prepare_groups_single_elements():
