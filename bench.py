@@ -63,6 +63,9 @@ def parse():
   p.add_argument("--no-cpu", action="store_true")
   p.add_argument("--item-tiles", type=int, default=0,
                  help="longest run of tiles per work item (0: the library default, FWN_ITEM_TILES)")
+  p.add_argument("--layout", default="node", choices=["node", "head"],
+                 help="storage of q, k, v, o, dO, dq, dk, dv: node-major [B, n, H, D] (the reference's "
+                      "interface) or head-major [B, H, n, D] passed as strided views")
   p.add_argument("--copy-mib", type=int, default=0,
                  help="instead of the attention step, time a plain device-to-device copy of this many MiB "
                       "(the known-size kernel that scales the FETCH_SIZE / WRITE_SIZE counters)")
@@ -363,6 +366,10 @@ def main():
     members.append(xs + [rng.standard_normal((n, H, D)).astype(np.float32)])
   host = [np.stack([mem[i] for mem in members]) for i in range(4)]
   q, k, v, do = (torch.from_numpy(x).to(dev).to(dtype) for x in host)
+  if args.layout == "head":
+    # [batch, n, heads, head_dim] views of head-major storage: a 32-row group of one head is one
+    # contiguous run instead of 32 rows at the node stride.
+    q, k, v, do = (x.permute(0, 2, 1, 3).contiguous().permute(0, 2, 1, 3) for x in (q, k, v, do))
   scale = D ** -0.5
   desc = nat.AttnDesc(B, n, H, D, nat.BF16 if dtype == torch.bfloat16 else nat.F32, scale, *q.stride()[:3])
   out = torch.empty_like(q)
