@@ -208,6 +208,21 @@ struct SoftmaxState {
   float l;  // running sum of exp2(s*c2 - m) over this lane's half of the keys
 };
 
+// The lazy move itself, from this lane's max over its half of the row's logits. Lanes i and
+// i + 32 hold one row and share m, and x * c2 is monotonic, so "some lane's half-row max exceeds
+// m + kLazyMax" is exactly "some row's max does": the wave-uniform decision needs no cross-lane
+// step, and the row max (one lane exchange) is formed only when m moves.
+__device__ __forceinline__ bool lazy_move(float mx_half, SoftmaxState& st, float c2, float& corr) {
+  corr = 1.f;
+  if (__builtin_amdgcn_ballot_w64(mx_half * c2 > st.m + kLazyMax) == 0) return false;
+  const float mxs = fmaxf(mx_half, __shfl_xor(mx_half, 32)) * c2;
+  const float m_new = fmaxf(st.m, mxs);
+  corr = fast_exp2(st.m - (m_new == -__builtin_inff() ? 0.f : m_new));
+  st.l *= corr;
+  st.m = m_new;
+  return true;
+}
+
 // The first NSB entries of s take part (all of them by default).
 template <int NSB = -1, int CAP>
 __device__ __forceinline__ bool softmax_tile(f32x16 (&s)[CAP], SoftmaxState& st, float c2, float& corr) {
@@ -219,16 +234,7 @@ __device__ __forceinline__ bool softmax_tile(f32x16 (&s)[CAP], SoftmaxState& st,
   for (int sb = 0; sb < N; ++sb)
 #pragma unroll
     for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[sb][r]);
-  mx = fmaxf(mx, __shfl_xor(mx, 32));
-  const float mxs = mx * c2;
-  corr = 1.f;
-  const bool moved = __builtin_amdgcn_ballot_w64(mxs > st.m + kLazyMax) != 0;
-  if (moved) {
-    const float m_new = fmaxf(st.m, mxs);
-    corr = fast_exp2(st.m - (m_new == ninf ? 0.f : m_new));
-    st.l *= corr;
-    st.m = m_new;
-  }
+  const bool moved = lazy_move(mx, st, c2, corr);
   const float base = st.m == ninf ? 0.f : st.m;
   float sum = 0.f;
 #pragma unroll
@@ -257,16 +263,7 @@ __device__ __forceinline__ bool softmax_rebase(const f32x16 (&s)[4], uint32_t li
 #pragma unroll
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[sb][r]);
     }
-  mx = fmaxf(mx, __shfl_xor(mx, 32));
-  const float mxs = mx * c2;
-  corr = 1.f;
-  const bool moved = __builtin_amdgcn_ballot_w64(mxs > st.m + kLazyMax) != 0;
-  if (moved) {
-    const float m_new = fmaxf(st.m, mxs);
-    corr = fast_exp2(st.m - (m_new == ninf ? 0.f : m_new));
-    st.l *= corr;
-    st.m = m_new;
-  }
+  const bool moved = lazy_move(mx, st, c2, corr);
   return moved;
 }
 
@@ -286,16 +283,7 @@ __device__ __forceinline__ bool softmax_live(f32x16 (&s)[4], uint32_t live, Soft
 #pragma unroll
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[sb][r]);
     }
-  mx = fmaxf(mx, __shfl_xor(mx, 32));
-  const float mxs = mx * c2;
-  corr = 1.f;
-  const bool moved = __builtin_amdgcn_ballot_w64(mxs > st.m + kLazyMax) != 0;
-  if (moved) {
-    const float m_new = fmaxf(st.m, mxs);
-    corr = fast_exp2(st.m - (m_new == ninf ? 0.f : m_new));
-    st.l *= corr;
-    st.m = m_new;
-  }
+  const bool moved = lazy_move(mx, st, c2, corr);
   const float base = st.m == ninf ? 0.f : st.m;
   float sum = 0.f;
 #pragma unroll
