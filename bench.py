@@ -63,6 +63,8 @@ def parse():
   p.add_argument("--no-cpu", action="store_true")
   p.add_argument("--item-tiles", type=int, default=0,
                  help="longest run of tiles per work item (0: the library default, FWN_ITEM_TILES)")
+  p.add_argument("--serial-bwd", action="store_true",
+                 help="run dQ and then dK/dV on one stream instead of side by side on two streams")
   p.add_argument("--layout", default="node", choices=["node", "head"],
                  help="storage of q, k, v, o, dO, dq, dk, dv: node-major [B, n, H, D] (the reference's "
                       "interface) or head-major [B, H, n, D] passed as strided views")
@@ -408,11 +410,16 @@ def main():
   # (name, launch, stream it runs on); dkv runs on the side stream after delta.
   kernels = [("fwd", fwd, stream)]
   if cfg["backward"]:
-    kernels += [("delta", bwd_delta, stream), ("dkv", bwd_dkv, side), ("dq", bwd_dq, stream)]
+    if args.serial_bwd:
+      # One stream, dQ then dK/dV (fwn_attn_bwd_launch's order): each kernel has the GPU alone.
+      ws2p, ws2n, sidep = wsp, wsn, sp
+      kernels += [("delta", bwd_delta, stream), ("dq", bwd_dq, stream), ("dkv", bwd_dkv, stream)]
+    else:
+      kernels += [("delta", bwd_delta, stream), ("dkv", bwd_dkv, side), ("dq", bwd_dq, stream)]
 
   def step(ev=None):
     for i, (name, fn, st) in enumerate(kernels):
-      if name == "dkv":
+      if name == "dkv" and st is side:
         side.wait_stream(stream)
       if ev is not None:
         ev[i][0].record(st)

@@ -146,6 +146,7 @@ void set_tiles(KArgs& a, const fwn_tiles* t, void* ws) {
   a.col = t->col;
   a.lanes = t->lanes;
   a.groups = t->groups;
+  a.halves = t->halves;
   a.items = (const int32_t*)t->items;
   a.split = t->split;
   a.n_tiles = t->n_tiles;

@@ -307,15 +307,18 @@ __global__ void __launch_bounds__(NT, 2) dq_kernel(KArgs a) {
   // half a tile of work to hide behind. Per tile: wait + barrier, copy the second half of t,
   // groups 0-1 of t, wait + barrier, copy the first half of t+1, groups 2-3 of t.
   u32x2 mbits = {0u, 0u};  // mask bits of the next tile, loaded with its first half
-  uint32_t gcur = 0u, gnext = 0u;
+  uint32_t gcur = 0u, gnext = 0u, hcur = 0u, hnext = 0u;
   if (t0 < t1) {
     const int kb = ((ci32_ptr)a.col)[t0];
     mbits = tile_bits(a, t0, w, lane);
     gcur = tile_groups(a, t0);
+    hcur = tile_halves(a, t0);
     dma.issue(rK, K, w, kb * BLK, snb, 3u);
     dma.issue(rV, V, w, kb * BLK, snb, 3u);
   }
-  auto group = [&](int sb, const u32x2& mb, bool full) {
+  // hv: this wave's live 16-key halves of the group (bit h); a clear half gets no dS work and
+  // no dQ MFMAs (its dS is zero).
+  auto group = [&](int sb, const u32x2& mb, bool full, uint32_t hv) {
     u32x4 ka[D / 16], va[D / 16];
 #pragma unroll
     for (int k = 0; k < D / 16; ++k) {
@@ -329,27 +332,26 @@ __global__ void __launch_bounds__(NT, 2) dq_kernel(KArgs a) {
       s = mfma_bf16(ka[k], qf[k], s);
       dp = mfma_bf16(va[k], df[k], dp);
     }
-    u32x4 kt[D / 32][2];
 #pragma unroll
-    for (int db = 0; db < D / 32; ++db)
+    for (int h = 0; h < 2; ++h) {
+      if (!(hv >> h & 1u)) continue;
+      u32x4 kt[D / 32];
 #pragma unroll
-      for (int c = 0; c < 2; ++c) kt[db][c] = tr_operand<D>(K, off, db, sb, c);
-    __builtin_amdgcn_sched_barrier(0);
-    if (full) {  // every element of the group is valid
+      for (int db = 0; db < D / 32; ++db) kt[db] = tr_operand<D>(K, off, db, sb, h);
+      __builtin_amdgcn_sched_barrier(0);
+      if (full) {  // every element of the group is valid
 #pragma unroll
-      for (int r = 0; r < 16; ++r) dp[r] = fast_exp2(fmaf(s[r], a.c2, -lse_t)) * (dp[r] - delta);
-    } else {
+        for (int r = 8 * h; r < 8 * h + 8; ++r) dp[r] = fast_exp2(fmaf(s[r], a.c2, -lse_t)) * (dp[r] - delta);
+      } else {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = keep_or_zero(fast_exp2(fmaf(s[r], a.c2, -lse_t)), elem_keep(mb, sb, r));
-        dp[r] = p * (dp[r] - delta);
+        for (int r = 8 * h; r < 8 * h + 8; ++r) {
+          const float p = keep_or_zero(fast_exp2(fmaf(s[r], a.c2, -lse_t)), elem_keep(mb, sb, r));
+          dp[r] = p * (dp[r] - delta);
+        }
       }
-    }
-    const bf16x8 d0 = pack_bf16(dp, 0), d1 = pack_bf16(dp, 1);
+      const bf16x8 dh = pack_bf16(dp, h);
 #pragma unroll
-    for (int db = 0; db < D / 32; ++db) {
-      acc[db] = mfma_bf16(kt[db][0], d0, acc[db]);
-      acc[db] = mfma_bf16(kt[db][1], d1, acc[db]);
+      for (int db = 0; db < D / 32; ++db) acc[db] = mfma_bf16(kt[db], dh, acc[db]);
     }
   };
   for (int tt = t0; tt < t1; ++tt) {
@@ -359,7 +361,11 @@ __global__ void __launch_bounds__(NT, 2) dq_kernel(KArgs a) {
     __syncthreads();  // all of rows 0-63 landed; every wave is done with rows 64-127 of tile t-1
     const u32x2 mb = mbits;
     const uint32_t gt = gcur;
-    if (t + 1 < t1) gnext = tile_groups(a, t + 1);
+    const uint32_t hw = hcur >> (8 * w) & 0xffu;  // this wave's live halves: bit 2sb + h
+    if (t + 1 < t1) {
+      gnext = tile_groups(a, t + 1);
+      hnext = tile_halves(a, t + 1);
+    }
     const uint32_t copy = any_rows(gt);
     dma.issue(rK, K, w, kb * BLK, snb, copy & 12u);
     dma.issue(rV, V, w, kb * BLK, snb, copy & 12u);
@@ -367,8 +373,8 @@ __global__ void __launch_bounds__(NT, 2) dq_kernel(KArgs a) {
     // with none for any wave are not copied either.
     const uint32_t live = gt >> (4 * w) & 15u;
     const uint32_t full = gt >> (16 + 4 * w) & 15u;  // groups with every element valid: no mask
-    if (live & 1u) group(0, mb, full & 1u);
-    if (live & 2u) group(1, mb, full & 2u);
+    if (live & 1u) group(0, mb, full & 1u, hw & 3u);
+    if (live & 2u) group(1, mb, full & 2u, hw >> 2 & 3u);
     wait_vmem();      // this wave's part of rows 64-127 of tile t
     __syncthreads();  // all of rows 64-127 landed; every wave is done with rows 0-63 of tile t
     if (t + 1 < t1) {
@@ -378,9 +384,10 @@ __global__ void __launch_bounds__(NT, 2) dq_kernel(KArgs a) {
       dma.issue(rK, K, w, kb1 * BLK, snb, copy1 & 3u);
       dma.issue(rV, V, w, kb1 * BLK, snb, copy1 & 3u);
     }
-    if (live & 4u) group(2, mb, full & 4u);
-    if (live & 8u) group(3, mb, full & 8u);
+    if (live & 4u) group(2, mb, full & 4u, hw >> 4 & 3u);
+    if (live & 8u) group(3, mb, full & 8u, hw >> 6 & 3u);
     gcur = gnext;
+    hcur = hnext;
   }
   if (j.part >= 0) {
     store_bwd_partial<D>(a, j, 32 * w + i, acc, 0, g);

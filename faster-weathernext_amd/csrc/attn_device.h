@@ -178,6 +178,14 @@ __device__ __forceinline__ uint32_t tile_groups(const KArgs& a, int t) {
   return ((const __attribute__((address_space(4))) uint32_t*)a.groups)[t];
 }
 
+// The tile's 32 half bits: bit 8r + 2c + h is set when rows 32r..32r+31 have a valid element in
+// columns 32c + 16h .. +15. Accumulator registers 8h..8h+7 of sub-block c hold exactly those 16
+// columns (element_col), so a clear bit skips their dS work and the dQ MFMAs they feed; they
+// would add exact zeros. Lists prepared without halves read all ones.
+__device__ __forceinline__ uint32_t tile_halves(const KArgs& a, int t) {
+  return a.halves ? ((const __attribute__((address_space(4))) uint32_t*)a.halves)[t] : ~0u;
+}
+
 // Column groups with a valid element in any row group.
 __device__ __forceinline__ uint32_t any_rows(uint32_t g) { return (g | g >> 4 | g >> 8 | g >> 12) & 15u; }
 

@@ -21,6 +21,7 @@ struct KArgs {
   const int32_t* col;
   const uint64_t* lanes;
   const uint32_t* groups;  // per tile: bit 4r + c = rows 32r.. have a valid element in columns 32c..
+  const uint32_t* halves;  // per tile: bit 8r + 2c + h = ... in columns 32c + 16h..; NULL = all live
   const int32_t* items;   // fwn_item[n_items] as int32 quadruples (block, t0, t1, part)
   const int32_t* split;   // [n_split * 3] block, first partial slot, slot count (combine pass)
   float* work;            // partial slots: [n_parts][batch * heads][128][2 * head_dim + 2] float32

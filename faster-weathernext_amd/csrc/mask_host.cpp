@@ -307,7 +307,7 @@ int fwn_tiles_fill(int32_t n_rows, int32_t n_cols, const int64_t* row_ptr, const
 
 int fwn_tiles_prepare(int32_t n_blocks, int32_t n_tiles, int32_t n_cols, const int32_t* tile_ptr,
                       const int32_t* tile_col, const uint32_t* tile_bits, uint64_t* lanes,
-                      uint32_t* groups) {
+                      uint32_t* groups, uint32_t* halves) {
   fwn::clear_error();
   if (n_blocks <= 0 || n_tiles < 0 || n_cols <= 0 || !tile_ptr || (n_tiles > 0 && (!tile_col || !tile_bits)) ||
       (n_tiles > 0 && (!lanes || !groups)))
@@ -325,16 +325,21 @@ int fwn_tiles_prepare(int32_t n_blocks, int32_t n_tiles, int32_t n_cols, const i
           for (int32_t j = tail; j < FWN_BLOCK; ++j)
             if ((bits[r * words + j / 32] >> (j % 32)) & 1u) bad = true;
       }
-      uint32_t f = 0;
+      uint32_t f = 0, hv = 0;
       for (int32_t w = 0; w < FWN_WAVES; ++w) {
         for (int32_t x = 0; x < words; ++x) {
           bool any = false, all = true;
+          uint32_t lo = 0, hi = 0;
           for (int32_t r = 32 * w; r < 32 * w + 32; ++r) {
             any = any || bits[r * words + x] != 0u;
             all = all && bits[r * words + x] == 0xffffffffu;
+            lo |= bits[r * words + x] & 0xffffu;
+            hi |= bits[r * words + x] >> 16;
           }
           if (any) f |= 1u << (4 * w + x);
           if (all) f |= 1u << (16 + 4 * w + x);
+          if (lo) hv |= 1u << (8 * w + 2 * x);
+          if (hi) hv |= 1u << (8 * w + 2 * x + 1);
         }
         for (int32_t lane = 0; lane < 64; ++lane) {
           const int32_t row = 32 * w + (lane & 31);
@@ -347,6 +352,7 @@ int fwn_tiles_prepare(int32_t n_blocks, int32_t n_tiles, int32_t n_cols, const i
         }
       }
       groups[t] = f;
+      if (halves) halves[t] = hv;
     }
   });
   if (bad) return fwn::fail(FWN_ERR_TILES, "fwn_tiles_prepare: a tile has bits set beyond n_cols");

@@ -45,7 +45,8 @@ class Tiles(ctypes.Structure):
   _fields_ = [("n_blocks", ctypes.c_int32), ("n_tiles", ctypes.c_int32), ("ptr", ctypes.c_void_p),
               ("col", ctypes.c_void_p), ("lanes", ctypes.c_void_p), ("groups", ctypes.c_void_p),
               ("n_items", ctypes.c_int32), ("n_parts", ctypes.c_int32), ("n_split", ctypes.c_int32),
-              ("reserved", ctypes.c_int32), ("items", ctypes.c_void_p), ("split", ctypes.c_void_p)]
+              ("reserved", ctypes.c_int32), ("items", ctypes.c_void_p), ("split", ctypes.c_void_p),
+              ("halves", ctypes.c_void_p)]
 
 
 ITEM_TILES = 64  # FWN_ITEM_TILES: default longest run of tiles per work item
@@ -73,7 +74,7 @@ SIGNATURES = {
     "fwn_hilbert_order": [_I64, _P, _P, _I32, _P],
     "fwn_tiles_count": [_I32, _I32, _P, _P, _P, _P],
     "fwn_tiles_fill": [_I32, _I32, _P, _P, _P, _P, _P, _P],
-    "fwn_tiles_prepare": [_I32, _I32, _I32, _P, _P, _P, _P, _P],
+    "fwn_tiles_prepare": [_I32, _I32, _I32, _P, _P, _P, _P, _P, _P],
     "fwn_tiles_schedule_count": [_I32, _P, _I32, _P, _P, _P],
     "fwn_tiles_schedule_fill": [_I32, _P, _I32, _P, _P],
     "fwn_attn_workspace_size": [_DESC, _TILES, _P],

@@ -48,8 +48,9 @@ class TileList:
     L = nat.lib()
     lanes = np.zeros((self.n_tiles, nat.LANE_WORDS), np.uint64)
     groups = np.zeros(self.n_tiles, np.uint32)
+    halves = np.zeros(self.n_tiles, np.uint32)
     nat.check(L.fwn_tiles_prepare(self.n_blocks, self.n_tiles, self.n_cols, nat.ptr(tile_ptr), nat.ptr(tile_kb),
-                                  nat.ptr(tile_bits), nat.ptr(lanes), nat.ptr(groups)))
+                                  nat.ptr(tile_bits), nat.ptr(lanes), nat.ptr(groups), nat.ptr(halves)))
     # Work items: each block's run of tiles cut into pieces of at most max_item_tiles (split-K).
     counts = np.zeros(3, np.int32)
     nat.check(L.fwn_tiles_schedule_count(self.n_blocks, nat.ptr(tile_ptr), int(max_item_tiles), nat.ptr(counts[0:]),
@@ -68,6 +69,8 @@ class TileList:
     self.lanes = put(lanes.view(np.int64))
     self.groups = put(groups.view(np.int32))
     self.groups_host = groups
+    self.halves = put(halves.view(np.int32))
+    self.halves_host = halves
     self.items = put(items)
     self.split = put(split)
     self.counts = np.diff(tile_ptr)
@@ -75,7 +78,7 @@ class TileList:
     addr = lambda t: t.data_ptr() if t.numel() else None
     self.struct = nat.Tiles(self.n_blocks, self.n_tiles, addr(self.ptr), addr(self.col), addr(self.lanes),
                             addr(self.groups), self.n_items, self.n_parts, self.n_split, 0, addr(self.items),
-                            addr(self.split) if self.n_split else None)
+                            addr(self.split) if self.n_split else None, addr(self.halves))
 
   def workspace_bytes(self, desc):
     """Workspace the launchers need for this list and the call shape `desc` (0 if nothing is split)."""

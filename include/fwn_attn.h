@@ -95,6 +95,10 @@ typedef struct fwn_tiles {
   int32_t reserved;         /* 0 */
   const fwn_item* items;    /* [n_items], in block order */
   const int32_t* split;     /* [n_split * 3]: block, first partial slot, slot count */
+  const uint32_t* halves;   /* [n_tiles] or NULL: bit 8r + 2c + h set when rows 32r..32r+31 of the
+                               tile have a valid element in columns 32c + 16h .. +15; the bf16 dq
+                               kernel skips the other 16-column halves of live groups (NULL:
+                               every half of a live group is processed) */
 } fwn_tiles;
 
 /* Thread-local message of the last failure on this thread ("" if none). */
@@ -133,11 +137,11 @@ int fwn_tiles_fill(int32_t n_rows, int32_t n_cols, const int64_t* row_ptr, const
                    uint32_t* tile_bits);
 
 /* Validates a canonical tile list (tile_ptr, tile_col, tile_bits as above, n_cols columns) and
- * converts it into the kernels' layout: lanes[n_tiles * FWN_LANE_WORDS] and groups[n_tiles]
- * (host buffers; the caller copies them to the device). */
+ * converts it into the kernels' layout: lanes[n_tiles * FWN_LANE_WORDS], groups[n_tiles] and,
+ * when non-NULL, halves[n_tiles] (host buffers; the caller copies them to the device). */
 int fwn_tiles_prepare(int32_t n_blocks, int32_t n_tiles, int32_t n_cols, const int32_t* tile_ptr,
                       const int32_t* tile_col, const uint32_t* tile_bits, uint64_t* lanes,
-                      uint32_t* groups);
+                      uint32_t* groups, uint32_t* halves);
 
 /* Work items of a tile list: the tiles of each block are cut into ceil(count / max_item_tiles)
  * runs of near-equal length (max_item_tiles <= 0 selects FWN_ITEM_TILES). The reference runs one

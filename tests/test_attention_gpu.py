@@ -277,6 +277,42 @@ def test_group_skipping_patterns(d, dtype):
     _check(res[name], r, dtype, name)
 
 
+def _without_halves(tiles):
+  """The same prepared list with its half bits dropped (every half of a live group processed)."""
+  import copy
+  t = copy.copy(tiles)
+  t.struct = nat.Tiles.from_buffer_copy(tiles.struct)
+  t.struct.halves = None
+  return t
+
+
+@pytest.mark.parametrize("d", [32, 64, 128])
+def test_half_skipping_is_exact(d):
+  """Skipping the 16-column halves of live 32 x 32 groups that hold no valid element (the bf16
+  dQ kernel) only drops terms that are exact zeros: outputs and gradients are bitwise those of
+  the same list without half bits, and both match the dense oracle. The designed pattern has
+  live groups with one dead half; the random sparse mask has many."""
+  print(f"half skipping d={d}", flush=True)
+  dtype = torch.bfloat16
+  rng = np.random.default_rng(70 + d)
+  for m in (_group_pattern_mask(21), _random_mask(640, 0.004, 71, symmetric=True)):
+    n = m.shape[0]
+    tiles, tiles_t = fwn.TileList.from_mask(m), fwn.TileList.from_mask(m.T.tocsr())
+    hv, g = tiles.halves_host, tiles.groups_host
+    live_halves = sum(bin(int(x)).count("1") for x in hv)
+    live_groups = sum(bin(int(x) & 0xFFFF).count("1") for x in g)
+    assert live_halves < 2 * live_groups  # some live group has a dead half
+    q, k, v, do = (_rounded(rng.standard_normal((2, n, 2, d)), dtype) for _ in range(4))
+    got = _run(q, k, v, do, tiles, d ** -0.5, dtype, tiles_t)
+    ref = _run(q, k, v, do, _without_halves(tiles), d ** -0.5, dtype, _without_halves(tiles_t))
+    for name in got:
+      np.testing.assert_array_equal(got[name], ref[name], err_msg=name)
+    dense = m.toarray()
+    _check(got["out"], A.dense_attention(q, k, v, dense, d ** -0.5), dtype, "out")
+    for name, r in zip(("dq", "dk", "dv"), A.dense_grads(q, k, v, do, dense, d ** -0.5)):
+      _check(got[name], r, dtype, name)
+
+
 def test_packed_qkv_strides_through_c_abi():
   """q, k, v as strided views of one [B, n, 3, H, D] buffer, read in place by the kernels."""
   rng = np.random.default_rng(10)

@@ -119,10 +119,26 @@ def test_prepare_layout_roundtrip():
   T, nb = len(kb), len(tp) - 1
   lanes = np.zeros((T, nat.LANE_WORDS), np.uint64)
   groups = np.zeros(T, np.uint32)
+  halves = np.zeros(T, np.uint32)
   nat.check(nat.lib().fwn_tiles_prepare(nb, T, n, nat.ptr(tp), nat.ptr(kb), nat.ptr(bits), nat.ptr(lanes),
-                                        nat.ptr(groups)))
+                                        nat.ptr(groups), nat.ptr(halves)))
   dense = ((bits[:, :, :, None] >> np.arange(32, dtype=np.uint32)) & 1).astype(bool).reshape(T, 128, 128)
   np.testing.assert_array_equal(_decode_lanes(lanes, T), dense)
+  # halves: bit 8r + 2c + h set iff rows 32r.. have a valid element in columns 32c + 16h .. +15.
+  want = np.zeros(T, np.uint32)
+  for r in range(4):
+    for c in range(4):
+      for h in range(2):
+        blk = dense[:, 32 * r:32 * r + 32, 32 * c + 16 * h:32 * c + 16 * h + 16].reshape(T, -1)
+        want |= blk.any(1).astype(np.uint32) << (8 * r + 2 * c + h)
+  np.testing.assert_array_equal(halves, want)
+  assert 0 < np.mean(halves != 0xFFFFFFFF)
+  # a live group has at least one live half, a dead group none
+  for r in range(4):
+    for c in range(4):
+      live = (groups >> (4 * r + c)) & 1
+      hv = (halves >> (8 * r + 2 * c)) & 3
+      np.testing.assert_array_equal(live.astype(bool), hv != 0)
   # groups: bit 4r + c set iff the 32 x 32 block (rows 32r.., columns 32c..) has a valid element,
   # bit 16 + 4r + c iff every element of it is valid.
   expect = np.zeros(T, np.uint32)
@@ -149,7 +165,7 @@ def test_prepare_groups_single_elements():
   lanes = np.zeros((T, nat.LANE_WORDS), np.uint64)
   groups = np.zeros(T, np.uint32)
   nat.check(nat.lib().fwn_tiles_prepare(nb, T, n, nat.ptr(tp), nat.ptr(kb), nat.ptr(bits), nat.ptr(lanes),
-                                        nat.ptr(groups)))
+                                        nat.ptr(groups), None))
   got = {}
   for qb in range(nb):
     for t in range(tp[qb], tp[qb + 1]):
@@ -231,7 +247,7 @@ def test_prepare_rejects_malformed_lists(case):
   lanes = np.zeros((T, nat.LANE_WORDS), np.uint64)
   groups = np.zeros(T, np.uint32)
   status = nat.lib().fwn_tiles_prepare(nb, T, n, nat.ptr(tp), nat.ptr(kb), nat.ptr(bits), nat.ptr(lanes),
-                                       nat.ptr(groups))
+                                       nat.ptr(groups), None)
   assert status == nat.ERR_TILES
   assert nat.lib().fwn_last_error()
 
