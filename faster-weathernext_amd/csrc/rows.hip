@@ -140,7 +140,7 @@ __global__ void __launch_bounds__(64 * kWaves) norm_scatter_kernel(RowArgs a) {
   const int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
   if (row >= (int64_t)a.batch * a.n) return;
   const int64_t b = row / a.n, i = row - b * a.n;
-  const int64_t dst = a.perm[i];
+  const int64_t dst = a.perm ? a.perm[i] : i;  // no permutation: the conditioned layer norm alone
   if (dst < 0 || dst >= a.n) return;
   const size_t c = (size_t)a.channels;
   const int nv = a.channels / E;

@@ -13,15 +13,17 @@ namespace {
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
-int check_rows(const fwn_rows_desc* d, const void* x, const int64_t* perm, const char* what) {
-  if (!d || !x || !perm) return fail(FWN_ERR_INVALID_ARG, "%s: null descriptor, x or perm", what);
+// perm may be NULL only when `permuted` is false (the conditioned layer norm without a scatter).
+int check_rows(const fwn_rows_desc* d, const void* x, const int64_t* perm, const char* what, bool permuted = true) {
+  if (!d || !x || (permuted && !perm)) return fail(FWN_ERR_INVALID_ARG, "%s: null descriptor, x or perm", what);
   if (d->batch < 0 || d->n < 0) return fail(FWN_ERR_INVALID_ARG, "%s: negative batch or n", what);
   if (d->channels <= 0 || d->channels % 8 != 0 || d->channels > FWN_ROWS_MAX_CHANNELS)
     return fail(FWN_ERR_INVALID_ARG, "%s: channels must be a positive multiple of 8 up to %d (got %d)", what,
                 FWN_ROWS_MAX_CHANNELS, d->channels);
   if (d->dtype != FWN_F32 && d->dtype != FWN_BF16) return fail(FWN_ERR_UNSUPPORTED, "%s: dtype must be f32 or bf16", what);
   if (!(d->eps >= 0.f) || !std::isfinite(d->eps)) return fail(FWN_ERR_INVALID_ARG, "%s: eps must be finite and >= 0", what);
-  if (!aligned16(x) || !aligned16(perm)) return fail(FWN_ERR_INVALID_ARG, "%s: x and perm must be 16-byte aligned", what);
+  if (!aligned16(x) || (perm && !aligned16(perm)))
+    return fail(FWN_ERR_INVALID_ARG, "%s: x and perm must be 16-byte aligned", what);
   return FWN_OK;
 }
 
@@ -83,6 +85,22 @@ int fwn_rows_norm_scatter_launch(const fwn_rows_desc* d, const void* x, const in
     return fail(FWN_ERR_INVALID_ARG, "%s: out (and mul, add) must be non-null and 16-byte aligned", what);
   if (overlap(x, out, bytes(d))) return fail(FWN_ERR_INVALID_ARG, "%s: x and out must not overlap", what);
   RowArgs a = base(d, x, perm);
+  a.mul = mul;
+  a.add = add;
+  a.out = out;
+  return status(launch_rows(RowPass::kNormScatter, d->dtype, a, (hipStream_t)stream), what);
+}
+
+int fwn_rows_norm_affine_launch(const fwn_rows_desc* d, const void* x, const float* mul, const float* add, void* out,
+                                void* stream) {
+  using namespace fwn;
+  clear_error();
+  const char* what = "fwn_rows_norm_affine_launch";
+  if (int rc = check_rows(d, x, nullptr, what, false)) return rc;
+  if (!out || !aligned16(out) || (mul && !aligned16(mul)) || (add && !aligned16(add)))
+    return fail(FWN_ERR_INVALID_ARG, "%s: out (and mul, add) must be non-null and 16-byte aligned", what);
+  if (overlap(x, out, bytes(d))) return fail(FWN_ERR_INVALID_ARG, "%s: x and out must not overlap", what);
+  RowArgs a = base(d, x, nullptr);
   a.mul = mul;
   a.add = add;
   a.out = out;

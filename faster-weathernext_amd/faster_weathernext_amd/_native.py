@@ -85,6 +85,7 @@ SIGNATURES = {
     "fwn_attn_bwd_launch": [_DESC, _P, _P, _P, _P, _P, _P, _P, _TILES, _TILES, _P, _P, _P, _P, _U64, _P],
     "fwn_rows_gather_norm_launch": [_ROWS, _P, _P, _P, _P, _P],
     "fwn_rows_norm_scatter_launch": [_ROWS, _P, _P, _P, _P, _P, _P],
+    "fwn_rows_norm_affine_launch": [_ROWS, _P, _P, _P, _P, _P],
 }
 
 _lock = threading.Lock()

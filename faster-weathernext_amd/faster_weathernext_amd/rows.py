@@ -11,7 +11,9 @@ layers and back after them (``patch.py:274-276, 288-292``):
 
 ``gather_layer_norm`` does the first gather together with block 0's layer norm, and
 ``layer_norm_scatter`` the final layer norm, its per-member affine and the scatter, each as one
-HIP pass over [batch, n, channels] (``include/fwn_rows.h``). The affine's scale and offset come
+HIP pass over [batch, n, channels] (``include/fwn_rows.h``). ``layer_norm_affine`` is the same
+pass without a permutation: each block's conditioned layer norm in front of the attention and
+the feed-forward (``patch.py:240-244, 250-251``). The affine's scale and offset come
 from the conditioning vector through LinearNormConditioning's own projections, which the caller
 evaluates: pass ``mul`` (its multiplier of the normalised features) and ``add``.
 
@@ -90,6 +92,17 @@ def layer_norm_scatter_forward(x, perm, mul=None, add=None, eps=1e-5):
   return out
 
 
+def layer_norm_affine_forward(x, mul=None, add=None, eps=1e-5):
+  """layer_norm(x) * mul[:, None] + add[:, None], one HIP pass (no autograd)."""
+  d = _desc(x, eps)
+  mul = _affine(mul, x, "mul")
+  add = _affine(add, x, "add")
+  out = torch.empty_like(x)
+  with torch.cuda.device(x.device):
+    nat.check(nat.lib().fwn_rows_norm_affine_launch(d, _addr(x), _addr(mul), _addr(add), _addr(out), _stream(x)))
+  return out
+
+
 def _norm_stats(x, eps):
   xf = x.float()
   mean = xf.mean(-1, keepdim=True)
@@ -133,7 +146,10 @@ class _GatherNorm(torch.autograd.Function):
 class _NormScatter(torch.autograd.Function):
   @staticmethod
   def forward(ctx, x, perm, mul, add, eps):
-    out = layer_norm_scatter_forward(x, perm, mul, add, eps)
+    if perm is None:
+      out = layer_norm_affine_forward(x, mul, add, eps)
+    else:
+      out = layer_norm_scatter_forward(x, perm, mul, add, eps)
     ctx.save_for_backward(x, perm, mul)
     ctx.eps = eps
     ctx.has_add = add is not None
@@ -142,7 +158,7 @@ class _NormScatter(torch.autograd.Function):
   @staticmethod
   def backward(ctx, g_out):
     x, perm, mul = ctx.saved_tensors
-    g_y = g_out[:, perm].float()  # gradient of the un-scattered rows
+    g_y = (g_out if perm is None else g_out[:, perm]).float()  # gradient of the un-scattered rows
     xhat, rstd = _norm_stats(x, ctx.eps)
     g_mul = (g_y * xhat).sum(1) if mul is not None and ctx.needs_input_grad[2] else None
     g_add = g_y.sum(1) if ctx.has_add and ctx.needs_input_grad[3] else None
@@ -164,3 +180,11 @@ def layer_norm_scatter(x, perm, *, mul=None, add=None, eps=1e-5):
   order (``patch.py:288-292``) in one pass. mul and add are float32 [batch, channels] (None: 1
   and 0). Differentiable in x, mul and add."""
   return _NormScatter.apply(x, perm, mul, add, float(eps))
+
+
+def layer_norm_affine(x, *, mul=None, add=None, eps=1e-5):
+  """x [batch, n, channels] -> layer_norm(x) * mul[:, None] + add[:, None] in one pass: a block's
+  ``norm_conditioning_layer(st.layernorm(x, create_scale=False, create_offset=False))``
+  (``patch.py:240-244, 250-251``). mul and add are float32 [batch, channels] (None: 1 and 0).
+  Differentiable in x, mul and add."""
+  return _NormScatter.apply(x, None, mul, add, float(eps))

@@ -17,7 +17,11 @@ Structure, as the reference wires it:
 Two parts live in weathernext, which is not vendored, so their exact form is not pinned here:
 ``LinearNormConditioning`` is implemented as published with GenCast (a linear map of the
 conditioning vector, zero-initialised, giving a per-channel scale-minus-one and offset:
-``x * (1 + scale) + offset``), and ``st.ffw`` as a two-layer GELU MLP of width ``ffw_hidden``.
+``x * (1 + scale) + offset``), and ``st.ffw`` as a two-layer GELU MLP of width ``ffw_hidden``
+with the tanh form of GELU (``jax.nn.gelu``'s default). Without autograd, the first layer's bias
+and GELU run in the epilogue of its GEMM (``torch._addmm_activation``, which has no derivative),
+so the [n, ffw_hidden] activations make one trip to HBM instead of three; with autograd the same
+function runs as Linear, GELU, Linear.
 Parameters are random-initialised torch parameters; official checkpoints are Haiku parameters of
 the JAX model, which this package does not load.
 """
@@ -28,7 +32,7 @@ import torch.nn.functional as F
 from .hip_attn import TileList
 from .mesh import mesh_mask
 from .mha import TiledMHA
-from .rows import gather_layer_norm, layer_norm_scatter
+from .rows import gather_layer_norm, layer_norm_affine, layer_norm_scatter
 
 
 class NormConditioning(torch.nn.Module):
@@ -49,6 +53,11 @@ class NormConditioning(torch.nn.Module):
     mul, add = self.affine(cond)
     return x * mul[:, None, :] + add[:, None, :]
 
+  def norm(self, x, cond, eps):
+    """forward(layer_norm(x), cond) as one HIP pass (statistics and affine in float32)."""
+    mul, add = self.affine(cond)
+    return layer_norm_affine(x, mul=mul.float().contiguous(), add=add.float().contiguous(), eps=eps)
+
 
 class MeshBlock(torch.nn.Module):
   """One transformer block (``ChunkedBlock``, ``patch.py:229-253``)."""
@@ -61,17 +70,24 @@ class MeshBlock(torch.nn.Module):
     self.norm_mha = NormConditioning(d_model, cond_size, **kw)
     self.mha = TiledMHA(d_model, num_heads, key_size, tiles, tiles_t, **kw)
     self.norm_ffw = NormConditioning(d_model, cond_size, **kw)
-    self.ffw = torch.nn.Sequential(torch.nn.Linear(d_model, ffw_hidden, **kw), torch.nn.GELU(),
+    self.ffw = torch.nn.Sequential(torch.nn.Linear(d_model, ffw_hidden, **kw), torch.nn.GELU(approximate="tanh"),
                                    torch.nn.Linear(ffw_hidden, d_model, **kw))
+
+  def feed_forward(self, h):
+    """self.ffw(h); without autograd, the first layer's bias and GELU are fused into its GEMM."""
+    l1, l2 = self.ffw[0], self.ffw[2]
+    if torch.is_grad_enabled() and (h.requires_grad or any(p.requires_grad for p in self.ffw.parameters())):
+      return self.ffw(h)
+    lead = h.shape[:-1]
+    y = torch._addmm_activation(l1.bias, h.reshape(-1, h.shape[-1]), l1.weight.t(), use_gelu=True)
+    return F.linear(y, l2.weight, l2.bias).view(*lead, l2.out_features)
 
   def forward(self, x, cond, normed=None):
     """`normed` is layernorm(x) when the caller has it already (block 0 gets it from the fused
-    gather)."""
-    d = x.shape[-1]
-    if normed is None:
-      normed = F.layer_norm(x, (d,), eps=self.eps)
-    x = x + self.mha(self.norm_mha(normed, cond))
-    return x + self.ffw(self.norm_ffw(F.layer_norm(x, (d,), eps=self.eps), cond))
+    gather). Otherwise each conditioned layer norm is one fused pass (``layer_norm_affine``)."""
+    h = self.norm_mha(normed, cond) if normed is not None else self.norm_mha.norm(x, cond, self.eps)
+    x = x + self.mha(h)
+    return x + self.feed_forward(self.norm_ffw.norm(x, cond, self.eps))
 
 
 class MeshTransformer(torch.nn.Module):

@@ -52,6 +52,16 @@ int fwn_rows_gather_norm_launch(const fwn_rows_desc* d, const void* x, const int
 int fwn_rows_norm_scatter_launch(const fwn_rows_desc* d, const void* x, const int64_t* perm,
                                  const float* mul, const float* add, void* out, void* stream);
 
+/* out[b, i, :] = layer_norm(x[b, i, :]) * mul[b, :] + add[b, :] (mul and add float32
+ * [batch, channels], NULL meaning 1 and 0): the block's conditioned layer norm in one pass, the
+ * fwn_rows_norm_scatter_launch pass without a permutation. Replaces
+ * norm_conditioning_layer(st.layernorm(x, create_scale=False, create_offset=False)) in front of
+ * the attention and of the feed-forward of every block (patch.py:240-244, 250-251), whose
+ * LinearNormConditioning scale and offset the caller evaluates from the conditioning vector.
+ * x and out must not overlap. */
+int fwn_rows_norm_affine_launch(const fwn_rows_desc* d, const void* x, const float* mul,
+                                const float* add, void* out, void* stream);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

@@ -434,6 +434,7 @@ def test_rows_launchers_reject_bad_descriptors(kw, code):
   P = _ROW_PTR
   assert L.fwn_rows_gather_norm_launch(d, P, P + (1 << 24), P + (2 << 24), P + (3 << 24), None) == code
   assert L.fwn_rows_norm_scatter_launch(d, P, P + (1 << 24), None, None, P + (2 << 24), None) == code
+  assert L.fwn_rows_norm_affine_launch(d, P, None, None, P + (2 << 24), None) == code
   assert L.fwn_last_error()
 
 
@@ -454,6 +455,11 @@ def test_rows_launchers_reject_bad_pointers():
   assert L.fwn_rows_norm_scatter_launch(d, P, Q, R + 4, None, S, None) == bad    # misaligned mul
   assert L.fwn_rows_norm_scatter_launch(d, P, Q, None, R + 4, S, None) == bad    # misaligned add
   assert L.fwn_rows_norm_scatter_launch(d, P, Q, None, None, P + 64, None) == bad  # out overlaps x
+  assert L.fwn_rows_norm_affine_launch(d, None, None, None, S, None) == bad     # x
+  assert L.fwn_rows_norm_affine_launch(d, P, None, None, None, None) == bad     # out
+  assert L.fwn_rows_norm_affine_launch(d, P, R + 4, None, S, None) == bad       # misaligned mul
+  assert L.fwn_rows_norm_affine_launch(d, P, None, R + 4, S, None) == bad       # misaligned add
+  assert L.fwn_rows_norm_affine_launch(d, P, None, None, P + 64, None) == bad   # out overlaps x
   assert b"overlap" in L.fwn_last_error()
 
 

@@ -76,6 +76,45 @@ def test_layer_norm_scatter_matches_oracle(dtype, affine):
     assert _rel_rms(got, ref) <= 5e-3
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("b,n,c", [(1, 1, 8), (2, 257, 768), (3, 33, 1000), (1, 9, 4096)])
+def test_layer_norm_affine_matches_oracle(dtype, b, n, c):
+  """The block's conditioned layer norm (fwn_rows_norm_affine_launch) against the float64 oracle,
+  with and without the affine; rows stay in place."""
+  print(f"layer_norm_affine {dtype} b={b} n={n} c={c}", flush=True)
+  x, _ = _inputs(b, n, c, dtype, seed=11 + n)
+  g = torch.Generator().manual_seed(12)
+  mul, add = 1 + 0.1 * torch.randn(b, c, generator=g), torch.randn(b, c, generator=g)
+  for m, a in ((mul, add), (None, None), (mul, None)):
+    out = rows.layer_norm_affine_forward(x.to(DEV), None if m is None else m.to(DEV), None if a is None else a.to(DEV),
+                                         eps=1e-5)
+    torch.cuda.synchronize()
+    ref = orows.norm_affine(x.float().numpy(), None if m is None else m.numpy(), None if a is None else a.numpy(),
+                            1e-5)
+    got = out.float().cpu().numpy()
+    if dtype == torch.float32:
+      assert _rel_rms(got, ref) <= 1e-5
+    else:
+      np.testing.assert_allclose(got, _bf16_round(ref), rtol=2 ** -7, atol=1e-5)
+      assert _rel_rms(got, ref) <= 5e-3
+
+
+def test_layer_norm_affine_gradients_match_torch():
+  """Gradients in x, mul and add against the float64 torch composite of the same map."""
+  b, n, c = 2, 50, 256
+  x, _ = _inputs(b, n, c, torch.float32, seed=13)
+  g = torch.Generator().manual_seed(14)
+  mul, add = 1 + 0.1 * torch.randn(b, c, generator=g), torch.randn(b, c, generator=g)
+  gout = torch.randn(b, n, c, generator=g)
+  xs, ms, as_ = (t.to(DEV).requires_grad_(True) for t in (x, mul, add))
+  rows.layer_norm_affine(xs, mul=ms, add=as_, eps=1e-5).backward(gout.to(DEV))
+  xr, mr, ar = (t.double().requires_grad_(True) for t in (x, mul, add))
+  ref = torch.nn.functional.layer_norm(xr, (c,), eps=1e-5) * mr[:, None] + ar[:, None]
+  ref.backward(gout.double())
+  for got, want in ((xs.grad, xr.grad), (ms.grad, mr.grad), (as_.grad, ar.grad)):
+    assert _rel_rms(got.cpu().numpy(), want.numpy()) <= 1e-5
+
+
 def test_gather_without_norm_and_invalid_entries():
   b, n, c = 2, 40, 64
   x, _ = _inputs(b, n, c, torch.float32, seed=3)

@@ -1,7 +1,8 @@
 """The mesh transformer wiring (``transformer.MeshTransformer``) against the same model written
 with plain torch operations: a dense masked softmax in place of the HIP attention, and separate
 gather / layer-norm / scatter steps in place of the fused row passes (``patch.py:233-292``).
-Same weights; float32; the check is max rel RMS over the output and the input gradient."""
+Same weights; float32; the check is max rel RMS over the output, the input gradient and every
+parameter gradient."""
 import numpy as np
 import pytest
 import torch
@@ -61,8 +62,16 @@ def test_mesh_transformer_matches_plain_torch(reorder):
   out = model(x, cond)
   out.backward(g)
   gx = x.grad.clone()
+  grads = {name: p.grad.clone() for name, p in model.named_parameters()}
   x.grad = None
+  model.zero_grad(set_to_none=True)
   ref = _reference(model, dense, x, cond)
   ref.backward(g)
   assert _rel_rms(out.detach(), ref.detach()) <= 1e-5
   assert _rel_rms(gx, x.grad) <= 1e-5
+  with torch.no_grad():  # inference path: GELU in the feed-forward GEMM's epilogue
+    assert _rel_rms(model(x, cond), ref.detach()) <= 1e-5
+  # every parameter, the conditioning projections included (their gradients flow through the
+  # fused conditioned layer norms)
+  for name, p in model.named_parameters():
+    assert _rel_rms(grads[name], p.grad) <= 1e-5, name
