@@ -170,7 +170,8 @@ def mha_block(args):
 
 def row_passes(args):
   """Times the two fused row passes of a step (gather + layer norm, layer norm + affine + scatter)
-  against the same work as separate torch operations. The metric is HBM GB/s over the passes'
+  against the same work as separate torch operations, and the blocks' conditioned layer norm
+  (the same pass without a permutation) against torch's layer norm, multiply and add. The metric is HBM GB/s over the passes'
   algorithmic bytes: x read once and x_out, norm_out written (gather), x read and out written
   (scatter), 5 tensors of [batch, n, channels] per step (the [batch, channels] affine and the
   permutation are negligible)."""
@@ -220,6 +221,11 @@ def row_passes(args):
   xp, _ = rows.gather_layer_norm_forward(x, perm)
   t_gather = timed(lambda: rows.gather_layer_norm_forward(x, perm))
   t_scatter = timed(lambda: rows.layer_norm_scatter_forward(xp, perm, mul, add))
+  # The block's conditioned layer norm (the same pass without a permutation) against torch's
+  # layer norm, multiply and add (2 [batch, n, channels] tensors of algorithmic traffic).
+  t_affine = timed(lambda: rows.layer_norm_affine_forward(xp, mul, add))
+  mul_t, add_t = mul[:, None].to(dtype), add[:, None].to(dtype)
+  t_affine_torch = timed(lambda: torch.nn.functional.layer_norm(xp, (C,), eps=1e-5) * mul_t + add_t)
   ms_fused = timed(fused)
   ms_unfused = timed(unfused)
   row_bytes = B * n * C * x.element_size()
@@ -236,6 +242,8 @@ def row_passes(args):
                    "traffic": measured_traffic(args.workload, "gather_norm")[0],
                    "traffic_source": measured_traffic(args.workload, "gather_norm")[1]},
       "passes_ms": {"gather_norm": round(t_gather, 4), "norm_scatter": round(t_scatter, 4)},
+      "norm_affine": {"ms": round(t_affine, 4), "gbps": round(2 * row_bytes / (t_affine * 1e-3) / 1e9, 1),
+                      "ms_torch_layer_norm_mul_add": round(t_affine_torch, 4)},
       "ms_per_step_torch_separate_ops": round(ms_unfused, 4),
       "speedup_vs_torch": round(ms_unfused / ms_fused, 3),
   }
@@ -479,7 +487,7 @@ def main():
                    "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": traffic,
                    "traffic_source": traffic_src,
                    **({"note": "dkv's duration is measured while dq runs beside it on the other stream"}
-                      if dominant in ("dkv", "dq") and cfg["backward"] else {})},
+                      if dominant in ("dkv", "dq") and cfg["backward"] and not args.serial_bwd else {})},
       **({"backward_pair": {
           "ms": round(pair_ms, 4), "kernels": ["dq", "dkv"],
           "achieved": round((algo["dq"] + algo["dkv"]) / (pair_ms * 1e-3) / 1e12, 3), "unit": "TFLOP/s",
