@@ -401,26 +401,29 @@ __global__ void __launch_bounds__(NT, 2) dq_kernel(KArgs a) {
 // are no atomics (pallas_attn.py:187-215). The tile's 128 log-sum-exps and deltas are copied next
 // to its Q and dO tiles; the log-sum-exps are rescaled to the log2 domain once per tile in LDS.
 //
-// The work is split by role over 8 waves. Waves w and w + 4 (one SIMD) own the same 32
-// keys: wave w computes S^T = K Q^T, P and dV += P^T dO; wave w + 4 computes dP^T = V dO^T and,
-// with wave w's P handed over through LDS, dS = P (dP - delta) and dK += dS^T Q. Each wave issues
-// half of the MFMAs and holds half of the persistent state, so two waves share each SIMD and one's
-// VALU work overlaps the other's MFMAs.
+// The work is split by role over 8 waves. Waves w and w + 4 share one SIMD and own the same 32
+// keys. Wave w (the P wave) holds the K fragment and computes S^T = K Q^T and P, hands P over
+// to wave w + 4 through LDS and accumulates the first half of dV's columns. Wave w + 4 holds the
+// V fragment and computes dP^T = V dO^T, dS = P (dP - delta), dK += dS^T Q and the second half
+// of dV's columns (all of them at D = 32). Splitting dV moves MFMAs off the P wave, whose
+// exponentials otherwise keep the other wave waiting at every hand-over.
 constexpr int NT8 = 512;
+constexpr int PSLOT = 2048;  // one P slot: 32 keys x 32 queries bf16
 
 template <int D>
 __global__ void __launch_bounds__(NT8, 1) dkv_kernel(KArgs a) {
   constexpr int TB = Tile<D>::BYTES;
-  constexpr int BUF = 2 * TB + 1536;
-  constexpr int PSLOT = 64 * 32;  // one wave's P of one sub-block: 64 lanes x 16 bf16
-  __shared__ __attribute__((aligned(1024))) char lds0[BUF];  // Q | dO | lse[128] | gap | delta[128]
-  __shared__ __attribute__((aligned(1024))) char lds1[BUF];
-  __shared__ __attribute__((aligned(1024))) char lp[4 * 2 * PSLOT];  // [key sub-block][parity]
+  constexpr int NB = D / 32;     // 32-column blocks of dK and dV
+  constexpr int NV0 = NB / 2;    // dV blocks of the P wave (none at D = 32)
+  constexpr int NV1 = NB - NV0;  // dV blocks of the dK wave
+  __shared__ __attribute__((aligned(1024))) char lds0[2 * TB + 1536];  // Q | dO | lse[128] | gap | delta[128]
+  __shared__ __attribute__((aligned(1024))) char lds1[2 * TB + 1536];
+  __shared__ __attribute__((aligned(1024))) char lp[4 * 2 * PSLOT];  // 2 P slots per key sub-block
   lds_char* bufs[2] = {(lds_char*)lds0, (lds_char*)lds1};
   const int tid = threadIdx.x, lane = tid & 63;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int w = wid & 3;        // key sub-block
-  const bool kw = wid >= 4;     // dK wave (else dV wave)
+  const bool kw = wid >= 4;     // dK wave (else P wave)
   const int i = lane & 31, g = lane >> 5;
   const Job j = decode_job(a);
   const uint32_t snb = (uint32_t)a.sn * 2;
@@ -431,16 +434,19 @@ __global__ void __launch_bounds__(NT8, 1) dkv_kernel(KArgs a) {
   const rsrc_t rD = make_rsrc(a.delta + stat_index(a, j, 0), (uint32_t)a.n * 4);
 
   const int krow = j.blk * BLK + 32 * w + i;  // this lane's key
-  u32x4 frag[D / 16];                          // K (dV waves) or V (dK waves)
+  u32x4 frag[D / 16];                          // K (P waves) or V (dK waves)
   load_frag<D>(frag, make_rsrc((const uint16_t*)(kw ? a.v : a.k) + j.base, a.slice_bytes), krow, snb, g);
   Off<D> off;
   off.init(lane);
   TileDma<D> dma, dmaO;  // Q and dO tiles (their row strides may differ)
   dma.init(w, lane, snb);
   dmaO.init(w, lane, osnb);
-  f32x16 acc[D / 32];
+  f32x16 acc[NB];    // dK (dK waves) or dV blocks 0 .. NV0 - 1 (P waves)
+  f32x16 accv[NV1];  // dV blocks NV0 .. NB - 1 (dK waves)
 #pragma unroll
-  for (int db = 0; db < D / 32; ++db) acc[db] = zero16();
+  for (int db = 0; db < NB; ++db) acc[db] = zero16();
+#pragma unroll
+  for (int db = 0; db < NV1; ++db) accv[db] = zero16();
   // A P slot holds the two 8-element halves of every lane, each half 64 lanes x 16 bytes
   // contiguous, so the slot's b128 writes and reads are free of bank conflicts.
   lds_char* pslot = (lds_char*)lp + w * 2 * PSLOT + lane * 16;
@@ -448,7 +454,7 @@ __global__ void __launch_bounds__(NT8, 1) dkv_kernel(KArgs a) {
   int t0, t1;
   tile_range(a, j, t0, t1);
   constexpr uint32_t kPastEnd = 0x7FFFFFF0u;
-  // The dV waves copy the tiles, their statistics and their mask bits.
+  // The P waves copy the tiles, their statistics and their mask bits.
   auto issue = [&](int t, lds_char* buf, uint32_t copy) {
     const int qb = ((ci32_ptr)a.col)[t];
     dma.issue(rQ, buf, w, qb * BLK, snb, copy);
@@ -474,19 +480,19 @@ __global__ void __launch_bounds__(NT8, 1) dkv_kernel(KArgs a) {
   // Query groups (32 queries) of a tile with no valid element for any of the 4 key groups are
   // skipped by every wave and not copied (they would add p = 0); the others cost one barrier each,
   // so per tile each wave passes 1 + (number of live query groups) barriers. A dK wave also skips
-  // the live groups in which its own 32 keys have no valid element (its P is zero there), which
-  // saves LDS reads; the dV waves compute every live group (skipping there too costs more
-  // registers than a wave has). Group bits are loaded a tile ahead of their use (two tiles ahead
-  // of the copy for dV waves).
+  // the live groups in which its own 32 keys have no valid element (its P is zero there). The P
+  // waves compute every live group: the barriers pace all 8 waves, so a skip there would only
+  // move the wait to another wave. Group bits are loaded a tile ahead of their use (two tiles
+  // ahead of the copy for P waves).
   u32x2 mbits = {0u, 0u};
-  uint32_t gcur = 0u, gnext = 0u;  // group bits of the current and (dV waves) the next tile
+  uint32_t gcur = 0u, gnext = 0u;  // group bits of the current and (P waves) the next tile
   if (t0 < t1) gcur = tile_groups(a, t0);
   if (t0 < t1 && !kw) {
     mbits = tile_bits(a, t0, w, lane);
     if (t0 + 1 < t1) gnext = tile_groups(a, t0 + 1);
     issue(t0, bufs[0], 15u);
   }
-  auto dv_step = [&](int tt, lds_char* cur, lds_char* nxt) {
+  auto pv_step = [&](int tt, lds_char* cur, lds_char* nxt) {
     const int t = __builtin_amdgcn_readfirstlane(tt);
     wait_vmem();
     const u32x2 mb = mbits;
@@ -495,11 +501,12 @@ __global__ void __launch_bounds__(NT8, 1) dkv_kernel(KArgs a) {
       // accumulators: (s - lse / scale) * c2 = s * c2 - lse * log2(e), and dP - delta.
       __attribute__((address_space(3))) f32x4* x =
           (__attribute__((address_space(3))) f32x4*)(cur + 2 * TB + (lane < 32 ? 0 : 512) + 16 * lane);
-      *x = *x * (lane < 32 ? a.nlse_mul : -1.f);
+      float m = lane < 32 ? a.nlse_mul : -1.f;
+      asm volatile("" : "+v"(m));  // computed here: hoisted, the compiler keeps it as spilled vectors
+      *x = *x * m;
     }
-    __syncthreads();
+    __syncthreads();  // tile t is in LDS; every wave is done with tile t - 1 (buffer nxt)
     const uint32_t any = any_rows(gcur);
-    const uint32_t full = gcur >> (16 + 4 * w) & 15u;  // query groups with every element valid
     if (t + 1 < t1) {
       mbits = tile_bits(a, t + 1, w, lane);
       issue(t + 1, nxt, any_rows(gnext));
@@ -508,8 +515,8 @@ __global__ void __launch_bounds__(NT8, 1) dkv_kernel(KArgs a) {
     if (t + 2 < t1) gnext = tile_groups(a, t + 2);
     const lds_char* Q = cur;
     const lds_char* O = cur + TB;
-    // P of sub-block sb, written to LDS slot `slot` for the dK wave; kept in registers for dV.
-    auto make_p = [&](int sb, int slot, bf16x8& p0, bf16x8& p1) {
+    // S^T of query group sb, started at -lse / scale of the element's query.
+    auto s_chain = [&](int sb) {
       u32x4 qa[D / 16];
 #pragma unroll
       for (int k = 0; k < D / 16; ++k) qa[k] = row_read(Q, off.row[k] + sb * 32 * (2 * D));
@@ -517,44 +524,84 @@ __global__ void __launch_bounds__(NT8, 1) dkv_kernel(KArgs a) {
       stats4(cur, 0, sb, lr);
       f32x16 sv;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) sv[r] = lr[r >> 2][r & 3];  // -lse / scale of the element's query
+      for (int r = 0; r < 16; ++r) sv[r] = lr[r >> 2][r & 3];
 #pragma unroll
       for (int k = 0; k < D / 16; ++k) sv = mfma_bf16(qa[k], frag[k], sv);
-      if (full >> sb & 1u) {
+      return sv;
+    };
+    // P = exp2(S c2) (masked), packed to bf16 and written to LDS slot `slot` for the dK wave.
+    auto finish_p = [&](f32x16& sv, int sb, int slot, bf16x8& p0, bf16x8& p1) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) sv[r] = fast_exp2(sv[r] * a.c2);
-      } else {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) sv[r] = keep_or_zero(fast_exp2(sv[r] * a.c2), elem_keep(mb, sb, r));
-      }
+      for (int r = 0; r < 16; ++r) sv[r] = keep_or_zero(fast_exp2(sv[r] * a.c2), elem_keep(mb, sb, r));
       p0 = pack_bf16(sv, 0);
       p1 = pack_bf16(sv, 1);
       lds_char* ps = pslot + slot * PSLOT;
       *(__attribute__((address_space(3))) bf16x8*)ps = p0;
       *(__attribute__((address_space(3))) bf16x8*)(ps + 1024) = p1;
     };
-    // P runs one live sub-block ahead: between two barriers this wave issues dV(sb) and S(next)
-    // while the dK wave issues dK(sb) and dP(next). P(sb) goes to slot (its rank in `any`) & 1.
+    // P runs one live query group ahead. Between two barriers this wave computes S(next), then
+    // issues its dV(sb) MFMAs one at a time between slices of next's exponentials, so that the
+    // VALU work runs while the MFMA pipe is busy; the dK wave meanwhile issues dK(sb), its dV(sb)
+    // and dP(next). P(sb) goes to slot (its rank in `any`) & 1.
     bf16x8 pc0, pc1;
-    if (any != 0u) make_p(__builtin_ctz(any), 0, pc0, pc1);
+    if (any != 0u) {
+      const int sb0 = __builtin_ctz(any);
+      f32x16 sv = s_chain(sb0);
+      finish_p(sv, sb0, 0, pc0, pc1);
+    }
     int rank = 0;
 #pragma unroll
     for (int sb = 0; sb < 4; ++sb) {
       if (!(any >> sb & 1u)) continue;
-      u32x4 ot[D / 32][2];
-#pragma unroll
-      for (int db = 0; db < D / 32; ++db)
-#pragma unroll
-        for (int c = 0; c < 2; ++c) ot[db][c] = tr_operand<D>(O, off, db, sb, c);
-      __syncthreads();  // P(sb) is in LDS for the dK wave
-#pragma unroll
-      for (int db = 0; db < D / 32; ++db) {
-        acc[db] = mfma_bf16(ot[db][0], pc0, acc[db]);
-        acc[db] = mfma_bf16(ot[db][1], pc1, acc[db]);
-      }
+      lds_barrier();  // P(sb) is in LDS for the dK wave
       ++rank;
       const uint32_t later = sb < 3 ? any & (0xeu << sb) : 0u;
-      if (later != 0u) make_p(__builtin_ctz(later), rank & 1, pc0, pc1);
+      u32x4 ot[NV0 > 0 ? NV0 : 1][2];
+      if (later != 0u) {
+        const int nsb = __builtin_ctz(later);
+        f32x16 sv = s_chain(nsb);
+#pragma unroll
+        for (int db = 0; db < NV0; ++db)
+#pragma unroll
+          for (int c = 0; c < 2; ++c) ot[db][c] = tr_operand<D>(O, off, db, sb, c);
+        // Order: the Q and stats reads; the S chain with the dO^T reads between its MFMAs
+        // (they take the registers the Q operands free); then the dV MFMAs with slices of the
+        // exponential work between them; the P slot writes.
+        __builtin_amdgcn_sched_group_barrier(0x100, D / 16 + 4, 0);
+#pragma unroll
+        for (int m = 0; m < D / 16; ++m) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          if (m < 4 * NV0) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        bf16x8 pn0, pn1;
+#pragma unroll
+        for (int db = 0; db < NV0; ++db) {
+          acc[db] = mfma_bf16(ot[db][0], pc0, acc[db]);
+          acc[db] = mfma_bf16(ot[db][1], pc1, acc[db]);
+        }
+        finish_p(sv, nsb, rank & 1, pn0, pn1);
+        if constexpr (NV0 > 0) {
+#pragma unroll
+          for (int m = 0; m < 2 * NV0; ++m) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+            __builtin_amdgcn_sched_group_barrier(0x002, 80 / (2 * NV0), 1);
+          }
+          __builtin_amdgcn_sched_group_barrier(0x200, 2, 1);
+        }
+        pc0 = pn0;
+        pc1 = pn1;
+      } else {
+#pragma unroll
+        for (int db = 0; db < NV0; ++db)
+#pragma unroll
+          for (int c = 0; c < 2; ++c) ot[db][c] = tr_operand<D>(O, off, db, sb, c);
+#pragma unroll
+        for (int db = 0; db < NV0; ++db) {
+          acc[db] = mfma_bf16(ot[db][0], pc0, acc[db]);
+          acc[db] = mfma_bf16(ot[db][1], pc1, acc[db]);
+        }
+      }
     }
   };
   auto dk_step = [&](int tt, lds_char* cur) {
@@ -569,7 +616,7 @@ __global__ void __launch_bounds__(NT8, 1) dkv_kernel(KArgs a) {
       if (!(any >> sb & 1u)) continue;
       const bool mine = own >> sb & 1u;
       f32x16 dp;
-      u32x4 qt[D / 32][2];
+      u32x4 qt[NB][2];
       if (mine) {
         u32x4 oa[D / 16];
 #pragma unroll
@@ -581,15 +628,20 @@ __global__ void __launch_bounds__(NT8, 1) dkv_kernel(KArgs a) {
 #pragma unroll
         for (int k = 0; k < D / 16; ++k) dp = mfma_bf16(oa[k], frag[k], dp);
 #pragma unroll
-        for (int db = 0; db < D / 32; ++db)
+        for (int db = 0; db < NB; ++db)
 #pragma unroll
           for (int c = 0; c < 2; ++c) qt[db][c] = tr_operand<D>(Q, off, db, sb, c);
       }
-      __syncthreads();  // P(sb) written by the dV wave
+      lds_barrier();  // P(sb) written by the P wave
       if (mine) {
         const lds_char* ps = pslot + (rank & 1) * PSLOT;
         const u32x4 pw0 = *(const __attribute__((address_space(3))) u32x4*)ps;
         const u32x4 pw1 = *(const __attribute__((address_space(3))) u32x4*)(ps + 1024);
+        u32x4 ot[NV1][2];
+#pragma unroll
+        for (int db = 0; db < NV1; ++db)
+#pragma unroll
+          for (int c = 0; c < 2; ++c) ot[db][c] = tr_operand<D>(O, off, NV0 + db, sb, c);
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const uint32_t word = (r < 8 ? pw0 : pw1)[(r & 7) >> 1];
@@ -598,9 +650,15 @@ __global__ void __launch_bounds__(NT8, 1) dkv_kernel(KArgs a) {
         }
         const bf16x8 d0 = pack_bf16(dp, 0), d1 = pack_bf16(dp, 1);
 #pragma unroll
-        for (int db = 0; db < D / 32; ++db) {
+        for (int db = 0; db < NB; ++db) {
           acc[db] = mfma_bf16(qt[db][0], d0, acc[db]);
           acc[db] = mfma_bf16(qt[db][1], d1, acc[db]);
+        }
+        const bf16x8 p0 = __builtin_bit_cast(bf16x8, pw0), p1 = __builtin_bit_cast(bf16x8, pw1);
+#pragma unroll
+        for (int db = 0; db < NV1; ++db) {
+          accv[db] = mfma_bf16(ot[db][0], p0, accv[db]);
+          accv[db] = mfma_bf16(ot[db][1], p1, accv[db]);
         }
       }
       ++rank;
@@ -608,8 +666,8 @@ __global__ void __launch_bounds__(NT8, 1) dkv_kernel(KArgs a) {
   };
   if (!kw) {
     for (int tt = t0; tt < t1; tt += 2) {
-      dv_step(tt, bufs[0], bufs[1]);
-      if (tt + 1 < t1) dv_step(tt + 1, bufs[1], bufs[0]);
+      pv_step(tt, bufs[0], bufs[1]);
+      if (tt + 1 < t1) pv_step(tt + 1, bufs[1], bufs[0]);
     }
   } else {
     for (int tt = t0; tt < t1; tt += 2) {
@@ -617,12 +675,25 @@ __global__ void __launch_bounds__(NT8, 1) dkv_kernel(KArgs a) {
       if (tt + 1 < t1) dk_step(tt + 1, bufs[1]);
     }
   }
-  if (j.part >= 0) {
-    store_bwd_partial<D>(a, j, 32 * w + i, acc, kw ? 0 : 1, g);
-    return;
+  const rsrc_t rV = make_rsrc((uint16_t*)a.out1 + j.base, a.slice_bytes);
+  if (kw) {
+    if (j.part >= 0) {
+      store_bwd_partial<D>(a, j, 32 * w + i, acc, 0, g);
+      store_bwd_partial<D, NV1>(a, j, 32 * w + i, accv, 1, g, NV0);
+      return;
+    }
+    store_acc_bf16<D>(make_rsrc((uint16_t*)a.out0 + j.base, a.slice_bytes), krow, snb, acc, a.scale, g);
+    store_acc_bf16<D, NV1>(rV, krow, snb, accv, 1.f, g, NV0);
+  } else if constexpr (NV0 > 0) {
+    f32x16 dv[NV0];
+#pragma unroll
+    for (int db = 0; db < NV0; ++db) dv[db] = acc[db];
+    if (j.part >= 0) {
+      store_bwd_partial<D, NV0>(a, j, 32 * w + i, dv, 1, g, 0);
+      return;
+    }
+    store_acc_bf16<D, NV0>(rV, krow, snb, dv, 1.f, g, 0);
   }
-  store_acc_bf16<D>(make_rsrc((uint16_t*)(kw ? a.out0 : a.out1) + j.base, a.slice_bytes), krow, snb, acc,
-                    kw ? a.scale : 1.f, g);
 }
 
 template <int D>

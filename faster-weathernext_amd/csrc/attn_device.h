@@ -77,6 +77,15 @@ __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70)
 // 2^x on the hardware transcendental unit (V_EXP_F32); callers fold log2(e) into their scales.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Workgroup barrier for hand-overs through LDS: orders and waits for this wave's LDS operations
+// only. __syncthreads() also waits for every outstanding global load, including a prefetch
+// copy into the other LDS buffer that no wave reads before the next tile.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 __device__ __forceinline__ bf16x8 pack_bf16(const f32x16& v, int half) {
   bf16x8 r;
 #pragma unroll
@@ -316,15 +325,16 @@ __device__ __forceinline__ void write_lse(const KArgs& a, const Job& j, int row,
   }
 }
 
-// Stores a transposed accumulator (rows d, column = this lane's row) as bf16, times `mul`.
-template <int D>
-__device__ __forceinline__ void store_acc_bf16(rsrc_t r, int row, uint32_t snb, const f32x16 (&acc)[D / 32],
-                                               float mul, int g) {
+// Stores a transposed accumulator (rows d, column = this lane's row) as bf16, times `mul`. The
+// NB accumulators hold the 32-column blocks db0 .. db0 + NB - 1.
+template <int D, int NB = D / 32>
+__device__ __forceinline__ void store_acc_bf16(rsrc_t r, int row, uint32_t snb, const f32x16 (&acc)[NB],
+                                               float mul, int g, int db0 = 0) {
 #pragma unroll
-  for (int db = 0; db < D / 32; ++db) {
+  for (int db = 0; db < NB; ++db) {
 #pragma unroll
     for (int k4 = 0; k4 < 4; ++k4) {
-      const int d = 32 * db + 8 * k4 + 4 * g;
+      const int d = 32 * (db0 + db) + 8 * k4 + 4 * g;
       u32x2 w;
 #pragma unroll
       for (int h2 = 0; h2 < 2; ++h2) {
@@ -337,15 +347,15 @@ __device__ __forceinline__ void store_acc_bf16(rsrc_t r, int row, uint32_t snb, 
   }
 }
 
-// Stores a transposed accumulator as float32, times `mul`.
-template <int D>
-__device__ __forceinline__ void store_acc_f32(rsrc_t r, int row, uint32_t snb, const f32x16 (&acc)[D / 32], float mul,
-                                              int g) {
+// Stores a transposed accumulator as float32, times `mul` (blocks db0 .. db0 + NB - 1).
+template <int D, int NB = D / 32>
+__device__ __forceinline__ void store_acc_f32(rsrc_t r, int row, uint32_t snb, const f32x16 (&acc)[NB], float mul,
+                                              int g, int db0 = 0) {
 #pragma unroll
-  for (int db = 0; db < D / 32; ++db) {
+  for (int db = 0; db < NB; ++db) {
 #pragma unroll
     for (int k4 = 0; k4 < 4; ++k4) {
-      const int d = 32 * db + 8 * k4 + 4 * g;
+      const int d = 32 * (db0 + db) + 8 * k4 + 4 * g;
       f32x4 w;
 #pragma unroll
       for (int e = 0; e < 4; ++e) w[e] = acc[db][4 * k4 + e] * mul;
@@ -370,10 +380,10 @@ __device__ __forceinline__ void store_fwd_partial(const KArgs& a, const Job& j, 
 
 // Backward partial epilogue: unscaled accumulator rows into the first (which = 0: dQ, dK) or
 // second (which = 1: dV) half of the slot.
-template <int D>
-__device__ __forceinline__ void store_bwd_partial(const KArgs& a, const Job& j, int row, const f32x16 (&acc)[D / 32],
-                                                  int which, int g) {
-  store_acc_f32<D>(part_slot<D>(a, j), row + 128 * which, D * 4, acc, 1.f, g);
+template <int D, int NB = D / 32>
+__device__ __forceinline__ void store_bwd_partial(const KArgs& a, const Job& j, int row, const f32x16 (&acc)[NB],
+                                                  int which, int g, int db0 = 0) {
+  store_acc_f32<D, NB>(part_slot<D>(a, j), row + 128 * which, D * 4, acc, 1.f, g, db0);
 }
 
 }  // namespace dev
