@@ -18,6 +18,37 @@ import torch
 
 from .hip_attn import TileList, tiled_flash_attention, tiled_flash_attention_qkv
 
+# hipBLASLt's bf16 GEMMs on MI355X run much faster when the row count is a multiple of 512: for
+# the block's four GEMMs at n = 40,962 nodes, 680 us per block against 519 us at 40,960 rows.
+ROW_QUANTUM = 512
+
+
+def linear_rows(x, weight, bias=None, gelu=False):
+  """x [M, K] @ weight[N, K]^T (+ bias) (then tanh GELU when `gelu`), without autograd.
+
+  Runs as two GEMMs into one output: the largest multiple of ROW_QUANTUM rows, then the rest,
+  so most rows get the fast kernels (for M = 40,962: 556 us per block instead of 680). The
+  bias and GELU run in the GEMM epilogue. Row results do not depend on the split beyond the
+  GEMM kernels' own accumulation order.
+  """
+  m_all = x.shape[0]
+  out = torch.empty((m_all, weight.shape[0]), device=x.device, dtype=x.dtype)
+  m = m_all - m_all % ROW_QUANTUM
+  for lo, hi in ((0, m), (m, m_all)) if 0 < m < m_all else ((0, m_all),):
+    xs, o = x[lo:hi], out[lo:hi]
+    if gelu:
+      torch._addmm_activation(bias, xs, weight.t(), use_gelu=True, out=o)
+    elif bias is not None:
+      torch.addmm(bias, xs, weight.t(), out=o)
+    else:
+      torch.mm(xs, weight.t(), out=o)
+  return out
+
+
+def needs_grad(x, module):
+  """True when autograd has to see this module's computation on x."""
+  return torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in module.parameters()))
+
 
 class TiledMHA(torch.nn.Module):
   """x [batch, n, d_model] -> x's attention update [batch, n, d_model].
@@ -34,10 +65,16 @@ class TiledMHA(torch.nn.Module):
     self.final = torch.nn.Linear(num_heads * key_size, d_model, device=device, dtype=dtype)
 
   def forward(self, x):
-    b, n, _ = x.shape
-    qkv = self.qkv(x).view(b, n, 3, self.num_heads, self.key_size)
+    b, n, d = x.shape
+    hd = self.num_heads * self.key_size
+    if needs_grad(x, self):
+      qkv = self.qkv(x).view(b, n, 3, self.num_heads, self.key_size)
+      out = tiled_flash_attention_qkv(qkv, self.tiles, scale=self.key_size ** -0.5, tiles_t=self.tiles_t)
+      return self.final(out.view(b, n, hd))
+    # Without autograd the projections run through linear_rows (the faster GEMM row split).
+    qkv = linear_rows(x.reshape(b * n, d), self.qkv.weight).view(b, n, 3, self.num_heads, self.key_size)
     out = tiled_flash_attention_qkv(qkv, self.tiles, scale=self.key_size ** -0.5, tiles_t=self.tiles_t)
-    return self.final(out.view(b, n, self.num_heads * self.key_size))
+    return linear_rows(out.reshape(b * n, hd), self.final.weight, self.final.bias).view(b, n, -1)
 
   def forward_unfused(self, x):
     """The same block with separate q, k, v tensors copied to contiguous [batch, n, heads,

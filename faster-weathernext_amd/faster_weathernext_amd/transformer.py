@@ -20,8 +20,9 @@ conditioning vector, zero-initialised, giving a per-channel scale-minus-one and 
 ``x * (1 + scale) + offset``), and ``st.ffw`` as a two-layer GELU MLP of width ``ffw_hidden``
 with the tanh form of GELU (``jax.nn.gelu``'s default). Without autograd, the first layer's bias
 and GELU run in the epilogue of its GEMM (``torch._addmm_activation``, which has no derivative),
-so the [n, ffw_hidden] activations make one trip to HBM instead of three; with autograd the same
-function runs as Linear, GELU, Linear.
+so the [n, ffw_hidden] activations make one trip to HBM instead of three, and every block GEMM
+splits its rows at a multiple of 512 (``mha.linear_rows``); with autograd the same functions run
+as plain Linear, GELU, Linear.
 Parameters are random-initialised torch parameters; official checkpoints are Haiku parameters of
 the JAX model, which this package does not load.
 """
@@ -31,7 +32,7 @@ import torch.nn.functional as F
 
 from .hip_attn import TileList
 from .mesh import mesh_mask
-from .mha import TiledMHA
+from .mha import TiledMHA, linear_rows, needs_grad
 from .rows import gather_layer_norm, layer_norm_affine, layer_norm_scatter
 
 
@@ -74,13 +75,14 @@ class MeshBlock(torch.nn.Module):
                                    torch.nn.Linear(ffw_hidden, d_model, **kw))
 
   def feed_forward(self, h):
-    """self.ffw(h); without autograd, the first layer's bias and GELU are fused into its GEMM."""
+    """self.ffw(h); without autograd, the first layer's bias and GELU are fused into its GEMM and
+    both GEMMs use the faster row split (``linear_rows``)."""
     l1, l2 = self.ffw[0], self.ffw[2]
-    if torch.is_grad_enabled() and (h.requires_grad or any(p.requires_grad for p in self.ffw.parameters())):
+    if needs_grad(h, self.ffw):
       return self.ffw(h)
     lead = h.shape[:-1]
-    y = torch._addmm_activation(l1.bias, h.reshape(-1, h.shape[-1]), l1.weight.t(), use_gelu=True)
-    return F.linear(y, l2.weight, l2.bias).view(*lead, l2.out_features)
+    y = linear_rows(h.reshape(-1, h.shape[-1]), l1.weight, l1.bias, gelu=True)
+    return linear_rows(y, l2.weight, l2.bias).view(*lead, l2.out_features)
 
   def forward(self, x, cond, normed=None):
     """`normed` is layernorm(x) when the caller has it already (block 0 gets it from the fused
