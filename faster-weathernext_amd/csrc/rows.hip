@@ -1,7 +1,8 @@
 // Row permutation passes fused with layer norms (gfx950): the gather of the node features into
 // Hilbert order before the mesh transformer's layers together with the first block's layer
 // norm, and the final layer norm with its per-member affine together with the scatter back
-// (patch.py:244, 274-276, 288-292).
+// (patch.py:244, 274-276, 288-292). The second pass without a permutation is each block's
+// conditioned layer norm, optionally with the residual add in front of it (patch.py:240-253).
 //
 // Both passes are HBM-bound streaming: one wave per row, 16 bytes per lane per load, so each
 // wave-wide load or store covers 1 KB of one row. A row stays in registers between its
@@ -71,10 +72,13 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
-// Loads one row (VPL vectors per lane, vector lane + 64k) and returns its mean and 1/std.
+// Loads one row (VPL vectors per lane, vector lane + 64k) and returns its mean and 1/std. With
+// `row2`, the row is row + row2, added in float32 and rounded once to T (as a separate
+// elementwise add would store it); v then holds that sum and the statistics are the sum's.
 template <typename T, int VPL>
 __device__ __forceinline__ void load_row(const T* row, bool ok, int nv, int channels, float eps, int lane,
-                                         u32x4 (&v)[VPL], float (&f)[VPL][Vec<T>::E], float& mean, float& rstd) {
+                                         u32x4 (&v)[VPL], float (&f)[VPL][Vec<T>::E], float& mean, float& rstd,
+                                         const T* row2 = nullptr) {
   constexpr int E = Vec<T>::E;
   float sum = 0.f;
 #pragma unroll
@@ -83,6 +87,16 @@ __device__ __forceinline__ void load_row(const T* row, bool ok, int nv, int chan
     v[k] = u32x4{0u, 0u, 0u, 0u};
     if (ok && idx < nv) v[k] = *(const u32x4*)(row + (size_t)idx * E);
     Vec<T>::unpack(v[k], f[k]);
+    if (row2) {
+      u32x4 w = u32x4{0u, 0u, 0u, 0u};
+      if (ok && idx < nv) w = *(const u32x4*)(row2 + (size_t)idx * E);
+      float g[E];
+      Vec<T>::unpack(w, g);
+#pragma unroll
+      for (int e = 0; e < E; ++e) f[k][e] += g[e];
+      v[k] = Vec<T>::pack(f[k]);
+      Vec<T>::unpack(v[k], f[k]);
+    }
 #pragma unroll
     for (int e = 0; e < E; ++e) sum += f[k][e];
   }
@@ -147,7 +161,14 @@ __global__ void __launch_bounds__(64 * kWaves) norm_scatter_kernel(RowArgs a) {
   u32x4 v[VPL];
   float f[VPL][E];
   float mean, rstd;
-  load_row<T, VPL>((const T*)a.x + (size_t)row * c, true, nv, a.channels, a.eps, lane, v, f, mean, rstd);
+  load_row<T, VPL>((const T*)a.x + (size_t)row * c, true, nv, a.channels, a.eps, lane, v, f, mean, rstd,
+                   a.addend ? (const T*)a.addend + (size_t)row * c : nullptr);
+  if (a.x_out) {  // the sum x + addend, in place of x's row (the whole row is in registers)
+    T* so = (T*)a.x_out + (size_t)row * c;
+#pragma unroll
+    for (int k = 0; k < VPL; ++k)
+      if (lane + 64 * k < nv) store16(so + (size_t)(lane + 64 * k) * E, v[k]);
+  }
   T* o = (T*)a.out + (size_t)(b * a.n + dst) * c;
   const float* mul = a.mul ? a.mul + (size_t)b * c : nullptr;
   const float* add = a.add ? a.add + (size_t)b * c : nullptr;

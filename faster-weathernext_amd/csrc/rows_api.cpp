@@ -107,4 +107,29 @@ int fwn_rows_norm_affine_launch(const fwn_rows_desc* d, const void* x, const flo
   return status(launch_rows(RowPass::kNormScatter, d->dtype, a, (hipStream_t)stream), what);
 }
 
+int fwn_rows_add_norm_affine_launch(const fwn_rows_desc* d, const void* x, const void* y, const float* mul,
+                                    const float* add, void* sum, void* out, void* stream) {
+  using namespace fwn;
+  clear_error();
+  const char* what = "fwn_rows_add_norm_affine_launch";
+  if (int rc = check_rows(d, x, nullptr, what, false)) return rc;
+  if (!y || !sum || !out || !aligned16(y) || !aligned16(sum) || !aligned16(out) || (mul && !aligned16(mul)) ||
+      (add && !aligned16(add)))
+    return fail(FWN_ERR_INVALID_ARG, "%s: y, sum and out (and mul, add) must be non-null and 16-byte aligned", what);
+  const uint64_t nb = bytes(d);
+  if (overlap(x, out, nb) || overlap(y, out, nb) || overlap(sum, out, nb))
+    return fail(FWN_ERR_INVALID_ARG, "%s: out must not overlap x, y or sum", what);
+  // sum may be x or y itself (each row is read whole before its sum is written), but no other
+  // overlap: a shifted alias would read rows another wave has already overwritten.
+  if ((sum != x && overlap(sum, x, nb)) || (sum != y && overlap(sum, y, nb)))
+    return fail(FWN_ERR_INVALID_ARG, "%s: sum must be x, y or disjoint from both", what);
+  RowArgs a = base(d, x, nullptr);
+  a.addend = y;
+  a.x_out = sum;
+  a.mul = mul;
+  a.add = add;
+  a.out = out;
+  return status(launch_rows(RowPass::kNormScatter, d->dtype, a, (hipStream_t)stream), what);
+}
+
 }  // extern "C"

@@ -86,6 +86,7 @@ SIGNATURES = {
     "fwn_rows_gather_norm_launch": [_ROWS, _P, _P, _P, _P, _P],
     "fwn_rows_norm_scatter_launch": [_ROWS, _P, _P, _P, _P, _P, _P],
     "fwn_rows_norm_affine_launch": [_ROWS, _P, _P, _P, _P, _P],
+    "fwn_rows_add_norm_affine_launch": [_ROWS, _P, _P, _P, _P, _P, _P, _P],
 }
 
 _lock = threading.Lock()

@@ -13,7 +13,8 @@ layers and back after them (``patch.py:274-276, 288-292``):
 ``layer_norm_scatter`` the final layer norm, its per-member affine and the scatter, each as one
 HIP pass over [batch, n, channels] (``include/fwn_rows.h``). ``layer_norm_affine`` is the same
 pass without a permutation: each block's conditioned layer norm in front of the attention and
-the feed-forward (``patch.py:240-244, 250-251``). The affine's scale and offset come
+the feed-forward (``patch.py:240-244, 250-251``), and ``add_layer_norm_affine`` adds the
+residual in front of it in the same pass. The affine's scale and offset come
 from the conditioning vector through LinearNormConditioning's own projections, which the caller
 evaluates: pass ``mul`` (its multiplier of the normalised features) and ``add``.
 
@@ -101,6 +102,29 @@ def layer_norm_affine_forward(x, mul=None, add=None, eps=1e-5):
   with torch.cuda.device(x.device):
     nat.check(nat.lib().fwn_rows_norm_affine_launch(d, _addr(x), _addr(mul), _addr(add), _addr(out), _stream(x)))
   return out
+
+
+def add_layer_norm_affine(x, y, *, mul=None, add=None, eps=1e-5, inplace=False):
+  """(x + y, layer_norm(x + y) * mul[:, None] + add[:, None]) in one HIP pass: a block's residual
+  add fused with the conditioned layer norm that reads it (``patch.py:240-253``). The sum is
+  added in float32 and rounded once to x's dtype, as ``x + y`` stores it, and the norm is the
+  sum's. With ``inplace`` the sum is written into x. mul and add are float32 [batch, channels]
+  (None: 1 and 0). Forward only: it refuses inputs that autograd would need to differentiate."""
+  if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (x, y, mul, add)):
+    raise RuntimeError("add_layer_norm_affine has no derivative; use x + y and layer_norm_affine under autograd")
+  d = _desc(x, eps)
+  if not isinstance(y, torch.Tensor) or y.shape != x.shape or y.dtype != x.dtype or y.device != x.device:
+    raise ValueError("y must be a tensor of x's shape, dtype and device")
+  if not y.is_contiguous():
+    raise ValueError("y must be contiguous")
+  mul = _affine(mul, x, "mul")
+  add = _affine(add, x, "add")
+  s = x if inplace else torch.empty_like(x)
+  out = torch.empty_like(x)
+  with torch.cuda.device(x.device):
+    nat.check(nat.lib().fwn_rows_add_norm_affine_launch(d, _addr(x), _addr(y), _addr(mul), _addr(add), _addr(s),
+                                                        _addr(out), _stream(x)))
+  return s, out
 
 
 def _norm_stats(x, eps):

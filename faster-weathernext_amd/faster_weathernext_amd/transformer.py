@@ -20,9 +20,10 @@ conditioning vector, zero-initialised, giving a per-channel scale-minus-one and 
 ``x * (1 + scale) + offset``), and ``st.ffw`` as a two-layer GELU MLP of width ``ffw_hidden``
 with the tanh form of GELU (``jax.nn.gelu``'s default). Without autograd, the first layer's bias
 and GELU run in the epilogue of its GEMM (``torch._addmm_activation``, which has no derivative),
-so the [n, ffw_hidden] activations make one trip to HBM instead of three, and every block GEMM
-splits its rows at a multiple of 512 (``mha.linear_rows``); with autograd the same functions run
-as plain Linear, GELU, Linear.
+so the [n, ffw_hidden] activations make one trip to HBM instead of three, every block GEMM
+splits its rows at a multiple of 512 (``mha.linear_rows``), and each residual add runs in one
+pass with the conditioned layer norm after it (``rows.add_layer_norm_affine``); with autograd the
+same functions run as plain Linear, GELU, Linear and separate adds.
 Parameters are random-initialised torch parameters; official checkpoints are Haiku parameters of
 the JAX model, which this package does not load.
 """
@@ -33,7 +34,7 @@ import torch.nn.functional as F
 from .hip_attn import TileList
 from .mesh import mesh_mask
 from .mha import TiledMHA, linear_rows, needs_grad
-from .rows import gather_layer_norm, layer_norm_affine, layer_norm_scatter
+from .rows import add_layer_norm_affine, gather_layer_norm, layer_norm_affine, layer_norm_scatter
 
 
 class NormConditioning(torch.nn.Module):
@@ -58,6 +59,11 @@ class NormConditioning(torch.nn.Module):
     """forward(layer_norm(x), cond) as one HIP pass (statistics and affine in float32)."""
     mul, add = self.affine(cond)
     return layer_norm_affine(x, mul=mul.float().contiguous(), add=add.float().contiguous(), eps=eps)
+
+  def add_norm(self, x, y, cond, eps):
+    """(x + y, forward(layer_norm(x + y), cond)) as one HIP pass, without autograd."""
+    mul, add = self.affine(cond)
+    return add_layer_norm_affine(x, y, mul=mul.float().contiguous(), add=add.float().contiguous(), eps=eps)
 
 
 class MeshBlock(torch.nn.Module):
@@ -91,6 +97,17 @@ class MeshBlock(torch.nn.Module):
     x = x + self.mha(h)
     return x + self.feed_forward(self.norm_ffw.norm(x, cond, self.eps))
 
+  def forward_fused(self, x, h, cond, next_norm=None):
+    """The block without autograd, from h = norm_mha(layernorm(x)) already computed: each residual
+    add runs in one pass with the conditioned layer norm that reads it (``add_layer_norm_affine``),
+    the feed-forward's own and, when `next_norm` is given, the next block's. Returns (x, the next
+    block's h or None)."""
+    x, h = self.norm_ffw.add_norm(x, self.mha(h), cond, self.eps)
+    f = self.feed_forward(h)
+    if next_norm is None:
+      return x + f, None
+    return next_norm.add_norm(x, f, cond, self.eps)
+
 
 class MeshTransformer(torch.nn.Module):
   """The 24-layer mesh transformer of WeatherNext 2's processor, node features [batch, n, d_model]
@@ -121,8 +138,14 @@ class MeshTransformer(torch.nn.Module):
       x, normed = gather_layer_norm(x, self.perm, eps=self.eps)
     elif len(self.blocks):
       normed = F.layer_norm(x, (d,), eps=self.eps)
-    for i, block in enumerate(self.blocks):
-      x = block(x, cond, normed if i == 0 else None)
+    if len(self.blocks) and not needs_grad(x, self):
+      # Without autograd the residual adds are fused into the conditioned layer norms after them.
+      h = self.blocks[0].norm_mha(normed, cond)
+      for i, block in enumerate(self.blocks):
+        x, h = block.forward_fused(x, h, cond, self.blocks[i + 1].norm_mha if i + 1 < len(self.blocks) else None)
+    else:
+      for i, block in enumerate(self.blocks):
+        x = block(x, cond, normed if i == 0 else None)
     mul, add = self.final_norm.affine(cond)
     if self.perm is not None:
       return layer_norm_scatter(x, self.perm, mul=mul.float().contiguous(), add=add.float().contiguous(), eps=self.eps)

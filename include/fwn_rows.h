@@ -62,6 +62,17 @@ int fwn_rows_norm_scatter_launch(const fwn_rows_desc* d, const void* x, const in
 int fwn_rows_norm_affine_launch(const fwn_rows_desc* d, const void* x, const float* mul,
                                 const float* add, void* out, void* stream);
 
+/* sum[b, i, :] = x[b, i, :] + y[b, i, :] (added in float32, rounded once to the dtype) and
+ * out[b, i, :] = layer_norm(sum[b, i, :]) * mul[b, :] + add[b, :]: the block's residual add
+ * fused with the conditioned layer norm that reads its result. Replaces `x = x + mha(...)`
+ * followed by the feed-forward's norm_conditioning_layer(st.layernorm(x)), and the feed-forward
+ * residual followed by the next block's conditioned layer norm (patch.py:240-253). sum may be x
+ * or y itself (an in-place residual update) or disjoint from both; out must not overlap x, y or
+ * sum. */
+int fwn_rows_add_norm_affine_launch(const fwn_rows_desc* d, const void* x, const void* y,
+                                    const float* mul, const float* add, void* sum, void* out,
+                                    void* stream);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

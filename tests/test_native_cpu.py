@@ -435,6 +435,7 @@ def test_rows_launchers_reject_bad_descriptors(kw, code):
   assert L.fwn_rows_gather_norm_launch(d, P, P + (1 << 24), P + (2 << 24), P + (3 << 24), None) == code
   assert L.fwn_rows_norm_scatter_launch(d, P, P + (1 << 24), None, None, P + (2 << 24), None) == code
   assert L.fwn_rows_norm_affine_launch(d, P, None, None, P + (2 << 24), None) == code
+  assert L.fwn_rows_add_norm_affine_launch(d, P, P + (1 << 24), None, None, P + (3 << 24), P + (2 << 24), None) == code
   assert L.fwn_last_error()
 
 
@@ -461,6 +462,17 @@ def test_rows_launchers_reject_bad_pointers():
   assert L.fwn_rows_norm_affine_launch(d, P, None, R + 4, S, None) == bad       # misaligned add
   assert L.fwn_rows_norm_affine_launch(d, P, None, None, P + 64, None) == bad   # out overlaps x
   assert b"overlap" in L.fwn_last_error()
+  add_norm = L.fwn_rows_add_norm_affine_launch  # (d, x, y, mul, add, sum, out, stream)
+  assert add_norm(d, P, None, None, None, R, S, None) == bad        # y
+  assert add_norm(d, P, Q, None, None, None, S, None) == bad        # sum
+  assert add_norm(d, P, Q, None, None, R, None, None) == bad        # out
+  assert add_norm(d, P, Q + 4, None, None, R, S, None) == bad       # misaligned y
+  assert add_norm(d, P, Q, R + 4, None, R, S, None) == bad          # misaligned mul
+  assert add_norm(d, P, Q, None, None, R, Q + 64, None) == bad      # out overlaps y
+  assert add_norm(d, P, Q, None, None, S, S, None) == bad           # out overlaps sum
+  assert add_norm(d, P, Q, None, None, P + 64, S, None) == bad      # sum shifted against x
+  assert add_norm(d, P, Q, None, None, Q + 64, S, None) == bad      # sum shifted against y
+  assert b"sum must be x, y or disjoint" in L.fwn_last_error()
 
 
 def test_rows_python_wrappers_reject_cpu_tensors():

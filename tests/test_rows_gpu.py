@@ -99,6 +99,49 @@ def test_layer_norm_affine_matches_oracle(dtype, b, n, c):
       assert _rel_rms(got, ref) <= 5e-3
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("b,n,c", [(1, 1, 8), (2, 257, 768), (1, 9, 4096)])
+def test_add_layer_norm_affine_matches_separate_ops(dtype, b, n, c):
+  """The residual add fused with the conditioned layer norm (fwn_rows_add_norm_affine_launch):
+  the sum equals torch's x + y bit for bit (float32 add, one rounding), the normed output equals
+  the unfused pass on that sum bit for bit and the float64 oracle to the dtype's bar; also with
+  the sum written over x or over y."""
+  print(f"add_layer_norm_affine {dtype} b={b} n={n} c={c}", flush=True)
+  x, _ = _inputs(b, n, c, dtype, seed=21 + n)
+  y, _ = _inputs(b, n, c, dtype, seed=22 + n)
+  g = torch.Generator().manual_seed(23)
+  mul, add = (1 + 0.1 * torch.randn(b, c, generator=g)).to(DEV), torch.randn(b, c, generator=g).to(DEV)
+  xd, yd = x.to(DEV), y.to(DEV)
+  want_sum = xd + yd
+  want_out = rows.layer_norm_affine_forward(want_sum, mul, add, eps=1e-5)
+  with torch.no_grad():
+    s, out = rows.add_layer_norm_affine(xd, yd, mul=mul, add=add, eps=1e-5)
+    torch.cuda.synchronize()
+    assert torch.equal(s, want_sum)
+    assert torch.equal(out, want_out)
+    ref = orows.norm_affine(want_sum.float().cpu().numpy(), mul.cpu().numpy(), add.cpu().numpy(), 1e-5)
+    tol = 1e-5 if dtype == torch.float32 else 5e-3
+    assert _rel_rms(out.float().cpu().numpy(), ref) <= tol
+    x2 = xd.clone()
+    s2, out2 = rows.add_layer_norm_affine(x2, yd, mul=mul, add=add, eps=1e-5, inplace=True)  # sum over x
+    torch.cuda.synchronize()
+    assert s2.data_ptr() == x2.data_ptr() and torch.equal(x2, want_sum) and torch.equal(out2, want_out)
+    y2 = yd.clone()
+    L, d = rows.nat.lib(), rows._desc(xd, 1e-5)
+    o3 = torch.empty_like(xd)
+    rows.nat.check(L.fwn_rows_add_norm_affine_launch(d, xd.data_ptr(), y2.data_ptr(), mul.data_ptr(),
+                                                     add.data_ptr(), y2.data_ptr(), o3.data_ptr(),
+                                                     rows._stream(xd)))  # sum over y
+    torch.cuda.synchronize()
+    assert torch.equal(y2, want_sum) and torch.equal(o3, want_out)
+
+
+def test_add_layer_norm_affine_refuses_autograd():
+  x = torch.zeros(1, 4, 8, device=DEV, requires_grad=True)
+  with pytest.raises(RuntimeError, match="no derivative"):
+    rows.add_layer_norm_affine(x, torch.zeros(1, 4, 8, device=DEV))
+
+
 def test_layer_norm_affine_gradients_match_torch():
   """Gradients in x, mul and add against the float64 torch composite of the same map."""
   b, n, c = 2, 50, 256
