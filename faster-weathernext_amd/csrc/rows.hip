@@ -147,7 +147,9 @@ __global__ void __launch_bounds__(64 * kWaves) gather_norm_kernel(RowArgs a) {
   }
 }
 
-template <typename T, int VPL>
+// ADD: a.addend is added to x first and the sum written to a.x_out (a compile-time switch, so
+// the plain pass carries no test for it).
+template <typename T, int VPL, bool ADD>
 __global__ void __launch_bounds__(64 * kWaves) norm_scatter_kernel(RowArgs a) {
   constexpr int E = Vec<T>::E;
   const int lane = threadIdx.x & 63;
@@ -162,8 +164,8 @@ __global__ void __launch_bounds__(64 * kWaves) norm_scatter_kernel(RowArgs a) {
   float f[VPL][E];
   float mean, rstd;
   load_row<T, VPL>((const T*)a.x + (size_t)row * c, true, nv, a.channels, a.eps, lane, v, f, mean, rstd,
-                   a.addend ? (const T*)a.addend + (size_t)row * c : nullptr);
-  if (a.x_out) {  // the sum x + addend, in place of x's row (the whole row is in registers)
+                   ADD ? (const T*)a.addend + (size_t)row * c : nullptr);
+  if constexpr (ADD) {  // the sum x + addend, in place of x's row (the whole row is in registers)
     T* so = (T*)a.x_out + (size_t)row * c;
 #pragma unroll
     for (int k = 0; k < VPL; ++k)
@@ -205,8 +207,10 @@ hipError_t launch_tv(RowPass pass, const RowArgs& a, hipStream_t stream) {
   const dim3 grid((unsigned)((rows + kWaves - 1) / kWaves)), block(64 * kWaves);
   if (pass == RowPass::kGatherNorm)
     hipLaunchKernelGGL((gather_norm_kernel<T, VPL>), grid, block, 0, stream, a);
+  else if (a.addend)
+    hipLaunchKernelGGL((norm_scatter_kernel<T, VPL, true>), grid, block, 0, stream, a);
   else
-    hipLaunchKernelGGL((norm_scatter_kernel<T, VPL>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((norm_scatter_kernel<T, VPL, false>), grid, block, 0, stream, a);
   return hipGetLastError();
 }
 

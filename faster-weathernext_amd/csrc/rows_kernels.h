@@ -14,7 +14,7 @@ struct RowArgs {
   const float* mul;  // scatter: [batch, channels] or null
   const float* add;  // scatter: [batch, channels] or null
   void* out;         // scatter: output
-  const void* addend;  // scatter: added to x before the norm (the sum goes to x_out), or null
+  const void* addend;  // scatter: added to x before the norm (the sum goes to x_out, required then), or null
   int32_t batch, n, channels;
   float eps;
 };
