@@ -62,7 +62,7 @@ def parse():
   p.add_argument("--cpu-seconds", type=float, default=12.0, help="bounded CPU-baseline sample length")
   p.add_argument("--no-cpu", action="store_true")
   p.add_argument("--item-tiles", type=int, default=0,
-                 help="longest run of tiles per work item (0: the library default, FWN_ITEM_TILES)")
+                 help="longest run of tiles per work item (0: chosen per launch by the library)")
   p.add_argument("--serial-bwd", action="store_true",
                  help="run dQ and then dK/dV on one stream instead of side by side on two streams")
   p.add_argument("--layout", default="node", choices=["node", "head"],
@@ -130,7 +130,7 @@ def mha_block(args):
   dev = torch.device("cuda:0")
   torch.cuda.set_device(dev)
   mask, lat, lon, perm = fwn.mesh_mask(6, cfg["k_hop"], reorder=cfg["reorder"])
-  tiles = fwn.TileList.from_mask(mask, perm, device=dev)
+  tiles = fwn.TileList.from_mask(mask, perm, device=dev, max_item_tiles=args.item_tiles or None)
   n, T = mask.shape[0], tiles.n_tiles
   torch.manual_seed(0)
   block = fwn.TiledMHA(dm, H, D, tiles, device=dev, dtype=torch.bfloat16)
@@ -261,10 +261,15 @@ def mesh_stack(args):
   cfg = WORKLOADS[args.workload]
   dev = torch.device("cuda:0")
   torch.cuda.set_device(dev)
+  tiles = None
+  if args.item_tiles:  # one split-K cap for every launch instead of the library's per-launch choice
+    mask, _, _, perm = fwn.mesh_mask(6, cfg["k_hop"], reorder=cfg["reorder"])
+    tiles = fwn.TileList.from_mask(mask, perm, device=dev, max_item_tiles=args.item_tiles)
   torch.manual_seed(0)
   t0 = time.perf_counter()
   model = fwn.MeshTransformer(6, cfg["k_hop"], cfg["layers"], cfg["d_model"], cfg["heads"], cfg["head_dim"],
-                              cfg["ffw_hidden"], cfg["cond_size"], cfg["reorder"], device=dev, dtype=torch.bfloat16)
+                              cfg["ffw_hidden"], cfg["cond_size"], cfg["reorder"], device=dev, dtype=torch.bfloat16,
+                              tiles=tiles)
   t_build = time.perf_counter() - t0
   n, B, T = model.n, cfg["batch"], model.tiles.n_tiles
   x = torch.randn(B, n, cfg["d_model"], device=dev, dtype=torch.bfloat16)
@@ -361,7 +366,7 @@ def main():
   mask, lat, lon, perm = fwn.mesh_mask(6, cfg["k_hop"], reorder=cfg["reorder"])
   t_mask = time.perf_counter() - t0
   t0 = time.perf_counter()
-  tiles = fwn.TileList.from_mask(mask, perm, device=dev, max_item_tiles=args.item_tiles or nat.ITEM_TILES)
+  tiles = fwn.TileList.from_mask(mask, perm, device=dev, max_item_tiles=args.item_tiles or None)
   t_tiles = time.perf_counter() - t0
   n = mask.shape[0]
   if perm is not None:
@@ -389,7 +394,7 @@ def main():
   L = nat.lib()
   stream = torch.cuda.current_stream(dev)
   sp = stream.cuda_stream
-  ts = tiles.struct
+  ts = tiles.struct_for(B, H)
   ws = fwn.hip_attn.workspace(desc, dev, tiles)
   wsp, wsn = (ws.data_ptr(), ws.numel()) if ws is not None else (None, 0)
   # dK/dV runs on a second stream beside dQ (as the package's backward does), with its own

@@ -30,15 +30,50 @@ BLOCK_K = nat.BLOCK
 _DTYPES = {torch.float32: nat.F32, torch.bfloat16: nat.BF16}
 
 
+# Work items (split-K): each block's run of live tiles is cut into items of at most a cap. A long
+# cap leaves fewer partial results to combine; a short one balances the launch better when there
+# are few jobs. With no cap given, a TileList picks per launch from the unsplit job count
+# blocks x batch x heads: WIDE_ITEM_TILES from WIDE_JOBS (6 jobs per CU of the 256) up, else
+# nat.ITEM_TILES. Measured on MI355X (TFLOP/s): C3 (1,284 jobs) 1063 at 64 against 1028 at 96;
+# C5 forward (1,926 jobs) 0.903 ms at 64 against 0.870 at 128; C4 (10,272 jobs) 1435 at 64
+# against 1458 at 128.
+WIDE_ITEM_TILES = 128
+WIDE_JOBS = 1536
+
+
+class _Schedule:
+  """One split-K schedule of a TileList: its work items, split records and C struct."""
+
+  def __init__(self, tl, tile_ptr, cap):
+    L = nat.lib()
+    counts = np.zeros(3, np.int32)
+    nat.check(L.fwn_tiles_schedule_count(tl.n_blocks, nat.ptr(tile_ptr), int(cap), nat.ptr(counts[0:]),
+                                         nat.ptr(counts[1:]), nat.ptr(counts[2:])))
+    self.n_items, self.n_parts, self.n_split = (int(c) for c in counts)
+    items = np.zeros((self.n_items, 4), np.int32)
+    split = np.zeros((max(self.n_split, 1), 3), np.int32)
+    nat.check(L.fwn_tiles_schedule_fill(tl.n_blocks, nat.ptr(tile_ptr), int(cap), nat.ptr(items), nat.ptr(split)))
+    self.items_host = items
+    self.split_host = split[:self.n_split]
+    self.items = torch.from_numpy(items).to(tl.device)
+    self.split = torch.from_numpy(split).to(tl.device)
+    addr = lambda t: t.data_ptr() if t.numel() else None
+    self.struct = nat.Tiles(tl.n_blocks, tl.n_tiles, addr(tl.ptr), addr(tl.col), addr(tl.lanes), addr(tl.groups),
+                            self.n_items, self.n_parts, self.n_split, 0, addr(self.items),
+                            addr(self.split) if self.n_split else None, addr(tl.halves))
+
+
 class TileList:
   """A tile list prepared for the kernels and resident on one device.
 
   Built from the canonical arrays of ``build_tile_mask`` (validated on the host, converted to the
   kernels' per-lane mask layout by ``fwn_tiles_prepare`` and copied once), then shared by every
   call, as the reference shares one device copy of the mask across layers (``patch.py:263-266``).
+  ``max_item_tiles`` fixes the split-K cap; None lets each launch pick it (``struct_for``).
+  ``struct`` is the schedule with the fixed cap, or nat.ITEM_TILES.
   """
 
-  def __init__(self, tile_ptr, tile_kb, tile_bits, n_cols, device="cuda", max_item_tiles=nat.ITEM_TILES):
+  def __init__(self, tile_ptr, tile_kb, tile_bits, n_cols, device="cuda", max_item_tiles=None):
     tile_ptr = nat.as_c(tile_ptr, np.int32)
     tile_kb = nat.as_c(tile_kb, np.int32)
     tile_bits = nat.as_c(tile_bits, np.uint32).reshape(len(tile_kb), nat.BLOCK, nat.BLOCK // 32)
@@ -51,17 +86,6 @@ class TileList:
     halves = np.zeros(self.n_tiles, np.uint32)
     nat.check(L.fwn_tiles_prepare(self.n_blocks, self.n_tiles, self.n_cols, nat.ptr(tile_ptr), nat.ptr(tile_kb),
                                   nat.ptr(tile_bits), nat.ptr(lanes), nat.ptr(groups), nat.ptr(halves)))
-    # Work items: each block's run of tiles cut into pieces of at most max_item_tiles (split-K).
-    counts = np.zeros(3, np.int32)
-    nat.check(L.fwn_tiles_schedule_count(self.n_blocks, nat.ptr(tile_ptr), int(max_item_tiles), nat.ptr(counts[0:]),
-                                         nat.ptr(counts[1:]), nat.ptr(counts[2:])))
-    self.n_items, self.n_parts, self.n_split = (int(c) for c in counts)
-    items = np.zeros((self.n_items, 4), np.int32)
-    split = np.zeros((max(self.n_split, 1), 3), np.int32)
-    nat.check(L.fwn_tiles_schedule_fill(self.n_blocks, nat.ptr(tile_ptr), int(max_item_tiles), nat.ptr(items),
-                                        nat.ptr(split)))
-    self.items_host = items
-    self.split_host = split[:self.n_split]
     self.device = torch.device(device)
     put = lambda a: torch.from_numpy(a).to(self.device)
     self.ptr = put(tile_ptr)
@@ -71,23 +95,42 @@ class TileList:
     self.groups_host = groups
     self.halves = put(halves.view(np.int32))
     self.halves_host = halves
-    self.items = put(items)
-    self.split = put(split)
     self.counts = np.diff(tile_ptr)
     self.nnz = int(np.unpackbits(tile_bits.view(np.uint8)).sum()) if self.n_tiles else 0
-    addr = lambda t: t.data_ptr() if t.numel() else None
-    self.struct = nat.Tiles(self.n_blocks, self.n_tiles, addr(self.ptr), addr(self.col), addr(self.lanes),
-                            addr(self.groups), self.n_items, self.n_parts, self.n_split, 0, addr(self.items),
-                            addr(self.split) if self.n_split else None, addr(self.halves))
+    self._tile_ptr = tile_ptr
+    self._fixed_cap = None if max_item_tiles is None else int(max_item_tiles)
+    self._schedules = {}
+    base = self._schedule(nat.ITEM_TILES if self._fixed_cap is None else self._fixed_cap)
+    self.n_items, self.n_parts, self.n_split = base.n_items, base.n_parts, base.n_split
+    self.items_host, self.split_host = base.items_host, base.split_host
+    self.items, self.split = base.items, base.split
+    self.struct = base.struct
+
+  def _schedule(self, cap):
+    cap = int(cap) if cap > 0 else nat.ITEM_TILES
+    if cap not in self._schedules:
+      self._schedules[cap] = _Schedule(self, self._tile_ptr, cap)
+    return self._schedules[cap]
+
+  def struct_for(self, batch, heads):
+    """The C struct to launch a call of `batch` x `heads` with (the schedule chosen for it)."""
+    if self._fixed_cap is not None:
+      return self.struct
+    wide = self.n_blocks * int(batch) * int(heads) >= WIDE_JOBS
+    return self._schedule(WIDE_ITEM_TILES if wide else nat.ITEM_TILES).struct
 
   def workspace_bytes(self, desc):
-    """Workspace the launchers need for this list and the call shape `desc` (0 if nothing is split)."""
-    n = ctypes.c_uint64(0)
-    nat.check(nat.lib().fwn_attn_workspace_size(desc, self.struct, ctypes.byref(n)))
-    return int(n.value)
+    """Workspace the launchers need for this list and the call shape `desc` (0 if nothing is split),
+    with either `struct` or the schedule ``struct_for`` picks for it."""
+    size = 0
+    for st in (self.struct, self.struct_for(desc.batch, desc.heads)):
+      n = ctypes.c_uint64(0)
+      nat.check(nat.lib().fwn_attn_workspace_size(desc, st, ctypes.byref(n)))
+      size = max(size, int(n.value))
+    return size
 
   @classmethod
-  def from_mask(cls, mask, perm=None, device="cuda", max_item_tiles=nat.ITEM_TILES):
+  def from_mask(cls, mask, perm=None, device="cuda", max_item_tiles=None):
     """Tile list of a boolean scipy/numpy [n, n] mask (optionally permuted as mask[perm][:, perm])."""
     tp, kb, bits = build_tile_mask(mask, perm)
     return cls(tp, kb, bits, mask.shape[1], device, max_item_tiles)
@@ -192,7 +235,8 @@ def attention_forward(q, k, v, tiles, scale, with_lse=True):
   tl = _as_tiles(tiles, q.shape[1], q.device)
   lse = torch.empty((q.shape[0], q.shape[2], q.shape[1]), dtype=torch.float32, device=q.device) if with_lse else None
   ws = workspace(desc, q.device, tl)
-  nat.check(nat.lib().fwn_attn_fwd_launch(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), tl.struct, out.data_ptr(),
+  ts = tl.struct_for(desc.batch, desc.heads)
+  nat.check(nat.lib().fwn_attn_fwd_launch(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), ts, out.data_ptr(),
                                           lse.data_ptr() if with_lse else None, *_ws_args(ws), _stream(q.device)))
   return out, lse
 
@@ -227,11 +271,12 @@ def _backward_into(q, k, v, out, lse, dout, tiles, tiles_t, scale, dq, dk, dv):
   nat.check(L.fwn_attn_bwd_delta_launch(desc, out.data_ptr(), dout.data_ptr(), delta.data_ptr(), main.cuda_stream))
   side = _side_stream(q.device)
   side.wait_stream(main)
+  ts, tst = tl.struct_for(desc.batch, desc.heads), tlt.struct_for(desc.batch, desc.heads)
   nat.check(L.fwn_attn_bwd_dkv_launch(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), dout.data_ptr(),
-                                      lse.data_ptr(), delta.data_ptr(), tlt.struct, dk.data_ptr(), dv.data_ptr(),
+                                      lse.data_ptr(), delta.data_ptr(), tst, dk.data_ptr(), dv.data_ptr(),
                                       *_ws_args(ws_kv), side.cuda_stream))
   nat.check(L.fwn_attn_bwd_dq_launch(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), dout.data_ptr(),
-                                     lse.data_ptr(), delta.data_ptr(), tl.struct, dq.data_ptr(), *_ws_args(ws_q),
+                                     lse.data_ptr(), delta.data_ptr(), ts, dq.data_ptr(), *_ws_args(ws_q),
                                      main.cuda_stream))
   # Everything the side stream used was allocated on `main`; ordering main after it keeps the
   # caching allocator from handing those blocks out while the dK/dV kernel still runs.

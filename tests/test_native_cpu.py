@@ -484,3 +484,30 @@ def test_rows_python_wrappers_reject_cpu_tensors():
     rows.gather_layer_norm(x, perm)
   with pytest.raises(ValueError):
     rows.layer_norm_scatter(x, perm)
+
+
+def test_tile_list_picks_the_split_schedule_per_launch():
+  """With no cap given, a TileList launches short items (nat.ITEM_TILES) for few jobs and long
+  ones (WIDE_ITEM_TILES) from WIDE_JOBS = blocks x batch x heads up; a given cap is always used."""
+  from faster_weathernext_amd import hip_attn
+  nb = 130  # block 0 has all 130 column tiles (3 items at cap 64, 2 at 128), the others their diagonal
+  tp = np.concatenate([[0], nb + np.arange(nb, dtype=np.int32)]).astype(np.int32)
+  kb = np.concatenate([np.arange(nb), np.arange(1, nb)]).astype(np.int32)
+  bits = np.full((len(kb), nat.BLOCK, nat.BLOCK // 32), 0xFFFFFFFF, np.uint32)
+  n = nb * nat.BLOCK
+  tl = hip_attn.TileList(tp, kb, bits, n, device="cpu")
+  assert tl.struct.n_items == tl.n_items == nb + 2 and tl.struct.n_parts == 3
+  jobs = -(-hip_attn.WIDE_JOBS // nb)  # batch members that reach WIDE_JOBS with one head
+  assert tl.struct_for(jobs - 1, 1).n_items == nb + 2
+  wide = tl.struct_for(jobs, 1)
+  assert wide.n_items == nb + 1 and wide.n_parts == 2
+  assert tl.struct_for(jobs, 1) is wide  # built once
+  fixed = hip_attn.TileList(tp, kb, bits, n, device="cpu", max_item_tiles=32)
+  assert fixed.struct_for(8, 64).n_items == fixed.struct.n_items == nb + 4
+  desc = nat.AttnDesc(jobs, n, 1, 128, nat.BF16, 0.1, n * 128, 128, 128, n * 128, 128, 128)  # [jobs, n, 1, 128]
+  sizes = []
+  for st in (tl.struct, wide):
+    size = ctypes.c_uint64(0)
+    nat.check(nat.lib().fwn_attn_workspace_size(desc, st, ctypes.byref(size)))
+    sizes.append(int(size.value))
+  assert tl.workspace_bytes(desc) == max(sizes) > 0
