@@ -15,6 +15,7 @@ the gfx950 kernels, and there is no interpreter or CPU path.
 All compute runs in the HIP kernels of libfwn_attn.so through its C ABI; torch only provides
 device memory and the stream. Tensors must be on a ROCm device: there is no CPU fallback.
 """
+import collections
 import ctypes
 import threading
 
@@ -76,7 +77,16 @@ class TileList:
   def __init__(self, tile_ptr, tile_kb, tile_bits, n_cols, device="cuda", max_item_tiles=None):
     tile_ptr = nat.as_c(tile_ptr, np.int32)
     tile_kb = nat.as_c(tile_kb, np.int32)
-    tile_bits = nat.as_c(tile_bits, np.uint32).reshape(len(tile_kb), nat.BLOCK, nat.BLOCK // 32)
+    tile_bits = nat.as_c(tile_bits, np.uint32)
+    if tile_ptr.ndim != 1 or tile_kb.ndim != 1 or len(tile_ptr) < 1:
+      raise ValueError("tile_ptr and tile_kb must be 1-D int32 arrays (tile_ptr of length n_blocks + 1)")
+    want = (len(tile_kb), nat.BLOCK, nat.BLOCK // 32)
+    if tile_bits.size != int(np.prod(want)):
+      # The reference's own lists are 64 x 32 tiles (uint32[T, 64], pallas_attn.py:93); these
+      # kernels take 128 x 128 tiles only (uint32[T, 128, 4]), from this package's build_tile_mask.
+      raise ValueError(f"tile_bits has shape {tuple(tile_bits.shape)}; expected {want}: 128 x 128 tiles "
+                       "(bit j of word w of row r = key 32w + j), as build_tile_mask here writes them")
+    tile_bits = tile_bits.reshape(want)
     self.n_blocks = len(tile_ptr) - 1
     self.n_tiles = len(tile_kb)
     self.n_cols = int(n_cols)
@@ -112,22 +122,27 @@ class TileList:
       self._schedules[cap] = _Schedule(self, self._tile_ptr, cap)
     return self._schedules[cap]
 
+  def item_cap_for(self, batch, heads):
+    """Longest run of tiles per work item for a call of `batch` x `heads`."""
+    if self._fixed_cap is not None:
+      return self._fixed_cap if self._fixed_cap > 0 else nat.ITEM_TILES
+    wide = self.n_blocks * int(batch) * int(heads) >= WIDE_JOBS
+    return WIDE_ITEM_TILES if wide else nat.ITEM_TILES
+
+  def schedule_for(self, batch, heads):
+    """The split-K schedule a call of `batch` x `heads` launches (items, split blocks, C struct)."""
+    return self._schedule(self.item_cap_for(batch, heads))
+
   def struct_for(self, batch, heads):
     """The C struct to launch a call of `batch` x `heads` with (the schedule chosen for it)."""
-    if self._fixed_cap is not None:
-      return self.struct
-    wide = self.n_blocks * int(batch) * int(heads) >= WIDE_JOBS
-    return self._schedule(WIDE_ITEM_TILES if wide else nat.ITEM_TILES).struct
+    return self.schedule_for(batch, heads).struct
 
   def workspace_bytes(self, desc):
-    """Workspace the launchers need for this list and the call shape `desc` (0 if nothing is split),
-    with either `struct` or the schedule ``struct_for`` picks for it."""
-    size = 0
-    for st in (self.struct, self.struct_for(desc.batch, desc.heads)):
-      n = ctypes.c_uint64(0)
-      nat.check(nat.lib().fwn_attn_workspace_size(desc, st, ctypes.byref(n)))
-      size = max(size, int(n.value))
-    return size
+    """Workspace the launchers need for this list and the call shape `desc`: the size for the
+    schedule ``struct_for`` picks for it (0 if that schedule splits no block)."""
+    n = ctypes.c_uint64(0)
+    nat.check(nat.lib().fwn_attn_workspace_size(desc, self.struct_for(desc.batch, desc.heads), ctypes.byref(n)))
+    return int(n.value)
 
   @classmethod
   def from_mask(cls, mask, perm=None, device="cuda", max_item_tiles=None):
@@ -151,12 +166,23 @@ class TileList:
 
 
 _cache_lock = threading.Lock()
-_cache = {}
+_cache = collections.OrderedDict()
+# Prepared lists kept for array triples passed directly to the op (least recently used first out).
+# Each holds its device arrays (about 38 MB at refinement 6, 32-hop); callers that build arrays
+# anew for every call should build a TileList once and pass that instead.
+CACHE_LISTS = 4
 
 
 def _as_tiles(tiles, n, device):
-  """A TileList from a TileList or a (tile_ptr, tile_kb, tile_bits) tuple (prepared once, cached)."""
+  """A TileList from a TileList or a (tile_ptr, tile_kb, tile_bits) tuple (prepared once, cached).
+
+  A TileList is checked against the call: its column count must be n (a list built for more
+  columns would address keys past n) and it must live on the call's device."""
   if isinstance(tiles, TileList):
+    if tiles.n_cols != n:
+      raise ValueError(f"tile list built for {tiles.n_cols} columns, but the call has n = {n} keys")
+    if tiles.device.type != device.type or (tiles.device.index or 0) != (device.index or 0):
+      raise ValueError(f"tile list lives on {tiles.device}, the tensors on {device}")
     return tiles
   tp, kb, bits = tiles
   key = (id(tp), id(kb), id(bits), n, str(device))
@@ -165,6 +191,9 @@ def _as_tiles(tiles, n, device):
     if hit is None or hit[0] is not tp or hit[1] is not kb or hit[2] is not bits:
       hit = (tp, kb, bits, TileList(np.asarray(tp), np.asarray(kb), np.asarray(bits), n, device))
       _cache[key] = hit
+    _cache.move_to_end(key)
+    while len(_cache) > CACHE_LISTS:
+      _cache.popitem(last=False)
     return hit[3]
 
 

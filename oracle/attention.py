@@ -14,6 +14,9 @@ a boolean [n, n] (query row, key column) shared by every batch element and head
   autodiff of that path computes (chunks rematerialised, ``scripts/attn_bench.py:76``):
   dS = P * (dP - rowsum(dP * P)), dQ = dS K s, dK += dS^T Q s, dV += P^T dO per window.
   These run in the input's float dtype (float32 for the CPU baseline).
+* ``block_attention`` / ``sampled_attention``: the dense closed form evaluated only at whole
+  128-row / 128-key blocks, or at single rows and keys, of masks too large for ``dense_*``
+  (refinement-6 meshes); pinned against ``dense_*`` on small masks.
 """
 
 import numpy as np
@@ -167,6 +170,84 @@ def max_rel_err(got, ref):
   got = np.asarray(got, np.float64)
   ref = np.asarray(ref, np.float64)
   return float(np.abs(got - ref).max() / np.abs(ref).max())
+
+
+def block_attention(q, k, v, do, mask, scale, row_blocks=(), key_blocks=(), block=128):
+  """Exact float64 results for whole blocks of 128 rows and of 128 keys of a large sparse mask.
+
+  The closed form of ``dense_attention`` / ``dense_grads``, evaluated one query block at a time
+  over the distinct keys that block's rows attend to (the 128-row unit of the kernels' tile list,
+  ``pallas_attn.py:85-109``): for query block b, S = Q_b K_C^T scale over its key set C, the masked
+  softmax P, O = P V_C and lse; delta_i = dO_i . O_i (= rowsum(P o dP)); dP = dO V^T, dS =
+  P (dP - delta). ``row_blocks`` receive out, lse and dq of all their rows. ``key_blocks`` receive
+  dk = scale dS^T Q and dv = P^T dO summed over every query block with a row that attends to one
+  of their keys (each query block is evaluated once for all requested key blocks). Rows with no
+  valid key get zero output and gradients (the kernels' convention).
+
+  Returns a dict: out/dq [B, rows, H, D] and lse [B, H, rows] over the concatenated rows of
+  ``row_blocks`` (ragged last block included as far as n), dk/dv [B, keys, H, D] over the
+  concatenated keys of ``key_blocks``; ``rows`` and ``keys`` hold the node indices.
+  """
+  mask = sparse.csr_matrix(mask).astype(bool)
+  n = mask.shape[0]
+  hm = lambda x: np.ascontiguousarray(np.asarray(x, np.float64).transpose(0, 2, 1, 3))  # [B, H, n, D]
+  qh, kh, vh, doh = hm(q), hm(k), hm(v), hm(do)
+  span = lambda b: np.arange(b * block, min(n, (b + 1) * block))
+  rows = np.concatenate([span(b) for b in row_blocks]) if len(row_blocks) else np.zeros(0, np.int64)
+  keys = np.concatenate([span(b) for b in key_blocks]) if len(key_blocks) else np.zeros(0, np.int64)
+  B, H, _, D = qh.shape
+  out = np.zeros((B, H, len(rows), D))
+  dq = np.zeros_like(out)
+  lse = np.zeros((B, H, len(rows)))
+  dk = np.zeros((B, H, len(keys), D))
+  dv = np.zeros_like(dk)
+  # Query blocks holding a row that attends to one of the requested keys.
+  need = set(int(b) for b in row_blocks)
+  for kb in key_blocks:
+    hit = mask[:, kb * block:min(n, (kb + 1) * block)].tocoo().row
+    need.update(int(b) for b in np.unique(hit // block))
+  row_pos = {int(b): i for i, b in enumerate(row_blocks)}
+  key_pos = np.full(n, -1, np.int64)
+  key_pos[keys] = np.arange(len(keys))
+  row_off = np.concatenate([[0], np.cumsum([len(span(b)) for b in row_blocks])]).astype(int)
+  for qb in sorted(need):
+    r = span(qb)
+    sub = mask[r[0]:r[-1] + 1]
+    cols = np.unique(sub.indices)
+    if len(cols) == 0:
+      continue
+    valid = sub[:, cols].toarray()                                           # [rows, C]
+    p = np.matmul(qh[:, :, r], kh[:, :, cols].transpose(0, 1, 3, 2))         # [B, H, rows, C]
+    p *= scale
+    np.copyto(p, -np.inf, where=~valid)
+    mx = p.max(-1, keepdims=True)
+    has = np.isfinite(mx)
+    mx[~has] = 0.0
+    p -= mx
+    np.exp(p, out=p)
+    tot = p.sum(-1, keepdims=True)
+    tot[~has] = 1.0
+    p /= tot
+    o = np.matmul(p, vh[:, :, cols])                                         # [B, H, rows, D]
+    delta = (o * doh[:, :, r]).sum(-1, keepdims=True)
+    if qb in row_pos:
+      a, b_ = row_off[row_pos[qb]], row_off[row_pos[qb] + 1]
+      dp = np.matmul(doh[:, :, r], vh[:, :, cols].transpose(0, 1, 3, 2))
+      out[:, :, a:b_] = o
+      dq[:, :, a:b_] = np.matmul(p * (dp - delta), kh[:, :, cols]) * scale
+      lse[:, :, a:b_] = np.where(has, mx + np.log(tot), -np.inf)[..., 0]
+    # Contributions of this query block to the requested keys it attends to.
+    sel = np.flatnonzero(key_pos[cols] >= 0)
+    if len(sel) == 0:
+      continue
+    kpos = key_pos[cols[sel]]
+    psel = p[..., sel]                                                       # [B, H, rows, S]
+    dpsel = np.matmul(doh[:, :, r], vh[:, :, cols[sel]].transpose(0, 1, 3, 2))
+    dssel = psel * (dpsel - delta)
+    dk[:, :, kpos] += np.matmul(dssel.transpose(0, 1, 3, 2), qh[:, :, r]) * scale
+    dv[:, :, kpos] += np.matmul(psel.transpose(0, 1, 3, 2), doh[:, :, r])
+  nm = lambda x: x.transpose(0, 2, 1, 3)
+  return {"out": nm(out), "dq": nm(dq), "lse": lse, "dk": nm(dk), "dv": nm(dv), "rows": rows, "keys": keys}
 
 
 def sampled_attention(q, k, v, do, mask, scale, rows, keys=()):

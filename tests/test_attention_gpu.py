@@ -486,100 +486,3 @@ def test_exp2_based_softmax_accuracy():
   np.testing.assert_allclose(_np(out), 1.0, rtol=0, atol=4e-6)
   ref = A.dense_lse(q, k, m.toarray(), d ** -0.5)
   np.testing.assert_allclose(_np(lse), ref, rtol=2e-6, atol=2e-6)
-
-
-# ---------------------------------------------------------------------------------------------
-# model scale (refinement-6 mesh, 40,962 nodes)
-
-
-@pytest.fixture(scope="module")
-def r6_masks():
-  masks = {}
-  for k in (8, 16):
-    mask, lat, lon, perm = fwn.mesh_mask(6, k, reorder=True)
-    masks[k] = (mask, perm)
-  return masks
-
-
-def _sample(n, count, seed):
-  return np.sort(np.random.default_rng(seed).choice(n, count, replace=False))
-
-
-@pytest.mark.parametrize("sigma", [128 ** -0.5, 1.0])
-def test_c2_fp32_forward_model_scale(r6_masks, sigma):
-  """Configuration 2: 8-hop mask, 4 heads x 128, float32 MFMA, forward."""
-  mask, _ = r6_masks[8]
-  n = mask.shape[0]
-  rng = np.random.default_rng(0)
-  q, k, v = (sigma * rng.standard_normal((1, n, 4, 128)).astype(np.float32) for _ in range(3))
-  tiles = fwn.TileList.from_mask(mask)
-  out, lse = fwn.attention_forward(*(_dev(x, torch.float32) for x in (q, k, v)), tiles, 128 ** -0.5)
-  rows = _sample(n, 512, 1)
-  ref = A.sampled_attention(q, k, v, np.zeros_like(q), mask, 128 ** -0.5, rows)
-  _check(_np(out)[:, rows], ref["out"], torch.float32, "out")
-  np.testing.assert_allclose(_np(lse)[:, :, rows], ref["lse"], rtol=0, atol=1e-5)
-
-
-def test_c3_bf16_forward_backward_model_scale(r6_masks):
-  """Configuration 3: 16-hop mask, 4 heads x 128, bf16 with fp32 accumulation, fwd + bwd."""
-  mask, _ = r6_masks[16]
-  n = mask.shape[0]
-  rng = np.random.default_rng(0)
-  q, k, v, do = (_rounded(rng.standard_normal((1, n, 4, 128)), torch.bfloat16) for _ in range(4))
-  tiles = fwn.TileList.from_mask(mask)
-  res = _run(q, k, v, do, tiles, 128 ** -0.5, torch.bfloat16)
-  rows, keys = _sample(n, 128, 2), _sample(n, 6, 3)
-  ref = A.sampled_attention(q, k, v, do, mask, 128 ** -0.5, rows, keys)
-  _check(res["out"][:, rows], ref["out"], torch.bfloat16, "out")
-  _check(res["dq"][:, rows], ref["dq"], torch.bfloat16, "dq")
-  _check(res["dk"][:, keys], ref["dk"], torch.bfloat16, "dk")
-  _check(res["dv"][:, keys], ref["dv"], torch.bfloat16, "dv")
-  # Size-independent identities over all 40,962 nodes: rows of P sum to one, so sum_j dV_j equals
-  # sum_i dO_i; rows of dS sum to zero, so sum_j dK_j = 0.
-  scale_dv = np.abs(do).sum(1)
-  np.testing.assert_allclose(res["dv"].astype(np.float64).sum(1), do.astype(np.float64).sum(1),
-                             rtol=0, atol=float(5e-3 * scale_dv.max()))
-  assert np.abs(res["dk"].astype(np.float64).sum(1)).max() <= 5e-3 * np.abs(res["dk"]).sum(1).max()
-
-
-def test_c4_bf16_ensemble_batch(r6_masks):
-  """Configuration 4: 8 members sharing one 8-hop tile list, bf16; member m drawn from seed m."""
-  mask, _ = r6_masks[8]
-  n = mask.shape[0]
-  members = [np.random.default_rng(m) for m in range(8)]
-  q, k, v = (np.concatenate([_rounded(r.standard_normal((1, n, 4, 128)), torch.bfloat16) for r in members])
-             for _ in range(3))
-  tiles = fwn.TileList.from_mask(mask)
-  res = _run(q, k, v, None, tiles, 128 ** -0.5, torch.bfloat16)
-  rows = _sample(n, 64, 4)
-  for m in (0, 5, 7):
-    ref = A.sampled_attention(q[m:m + 1], k[m:m + 1], v[m:m + 1], np.zeros_like(q[:1]), mask, 128 ** -0.5, rows)
-    _check(res["out"][m:m + 1, rows], ref["out"], torch.bfloat16, ("out", m))
-  # The library picks longer split-K items for the 8-member launch (10,272 jobs) than for one
-  # member (1,284), so member 5 alone differs from member 5 in the batch only by the rounding of the split
-  # combine; with the item cap pinned the launch size changes nothing, bit for bit.
-  one = _run(q[5:6], k[5:6], v[5:6], None, tiles, 128 ** -0.5, torch.bfloat16)
-  assert tiles.struct_for(8, 4).n_items < tiles.struct_for(1, 4).n_items
-  np.testing.assert_allclose(res["out"][5:6].astype(np.float32), one["out"].astype(np.float32), rtol=0,
-                             atol=float(2 ** -7 * np.abs(one["out"].astype(np.float32)).max()))
-  pinned = fwn.TileList.from_mask(mask, max_item_tiles=nat.ITEM_TILES)
-  batch = _run(q, k, v, None, pinned, 128 ** -0.5, torch.bfloat16)
-  one = _run(q[5:6], k[5:6], v[5:6], None, pinned, 128 ** -0.5, torch.bfloat16)
-  np.testing.assert_array_equal(batch["out"][5:6], one["out"])
-
-
-def test_hilbert_reordering_is_exact_up_to_rounding(r6_masks):
-  """Attention on Hilbert-permuted nodes with the permuted mask, un-permuted, equals attention in
-  subdivision order (patch.py:275-292 relies on this)."""
-  mask, perm = r6_masks[8]
-  n = mask.shape[0]
-  rng = np.random.default_rng(5)
-  q, k, v = (rng.standard_normal((1, n, 2, 64)).astype(np.float32) for _ in range(3))
-  plain = fwn.TileList.from_mask(mask)
-  hil = fwn.TileList.from_mask(mask, perm)
-  assert hil.n_tiles < plain.n_tiles
-  a, _ = fwn.attention_forward(*(_dev(x, torch.float32) for x in (q, k, v)), plain, 64 ** -0.5, with_lse=False)
-  b, _ = fwn.attention_forward(*(_dev(x[:, perm], torch.float32) for x in (q, k, v)), hil, 64 ** -0.5,
-                               with_lse=False)
-  inv = np.argsort(perm)
-  assert A.rel_rms(_np(b)[:, inv], _np(a)) <= 1e-6

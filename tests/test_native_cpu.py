@@ -504,10 +504,43 @@ def test_tile_list_picks_the_split_schedule_per_launch():
   assert tl.struct_for(jobs, 1) is wide  # built once
   fixed = hip_attn.TileList(tp, kb, bits, n, device="cpu", max_item_tiles=32)
   assert fixed.struct_for(8, 64).n_items == fixed.struct.n_items == nb + 4
-  desc = nat.AttnDesc(jobs, n, 1, 128, nat.BF16, 0.1, n * 128, 128, 128, n * 128, 128, 128)  # [jobs, n, 1, 128]
-  sizes = []
-  for st in (tl.struct, wide):
+  assert tl.schedule_for(jobs, 1).struct is wide and tl.item_cap_for(jobs, 1) == hip_attn.WIDE_ITEM_TILES
+  assert list(tl.schedule_for(jobs, 1).split_host[:, 0]) == [0]  # block 0 is the one split block
+  # The workspace is sized for the schedule the call launches, not for the 64-tile one.
+  for batch, st in ((jobs, wide), (jobs - 1, tl.struct)):
+    desc = nat.AttnDesc(batch, n, 1, 128, nat.BF16, 0.1, n * 128, 128, 128, n * 128, 128, 128)  # [batch, n, 1, 128]
     size = ctypes.c_uint64(0)
     nat.check(nat.lib().fwn_attn_workspace_size(desc, st, ctypes.byref(size)))
-    sizes.append(int(size.value))
-  assert tl.workspace_bytes(desc) == max(sizes) > 0
+    assert tl.workspace_bytes(desc) == int(size.value) == st.n_parts * batch * 128 * (2 * 128 + 2) * 4
+  # Nothing split: no workspace at all.
+  diag = hip_attn.TileList(np.arange(nb + 1, dtype=np.int32), np.arange(nb, dtype=np.int32), bits[:nb], n,
+                           device="cpu")
+  assert diag.workspace_bytes(nat.AttnDesc(1, n, 1, 128, nat.BF16, 0.1, n * 128, 128, 128, 0, 0, 0)) == 0
+  assert hip_attn.workspace(nat.AttnDesc(1, n, 1, 128, nat.BF16, 0.1, n * 128, 128, 128, 0, 0, 0), "cpu", diag) is None
+
+
+def test_tile_lists_reject_foreign_formats_and_mismatched_calls():
+  """The reference's 64 x 32 tile bits (uint32[T, 64]) raise a typed error; a prepared list is
+  checked against the call's key count and device; array triples passed directly to the op are
+  prepared once and kept in a bounded cache."""
+  import torch
+  from faster_weathernext_amd import hip_attn
+  tp = np.array([0, 1, 2], np.int32)
+  kb = np.array([0, 1], np.int32)
+  with pytest.raises(ValueError, match="128 x 128"):
+    hip_attn.TileList(tp, kb, np.zeros((2, 64), np.uint32), 256, device="cpu")
+  bits = np.zeros((2, nat.BLOCK, nat.BLOCK // 32), np.uint32)
+  bits[:, :, 0] = 1
+  tl = hip_attn.TileList(tp, kb, bits, 256, device="cpu")
+  with pytest.raises(ValueError, match="columns"):
+    hip_attn._as_tiles(tl, 255, torch.device("cpu"))
+  with pytest.raises(ValueError, match="lives on"):
+    hip_attn._as_tiles(tl, 256, torch.device("cuda", 0))
+  assert hip_attn._as_tiles(tl, 256, torch.device("cpu")) is tl
+  triples = [(tp.copy(), kb.copy(), bits.copy()) for _ in range(hip_attn.CACHE_LISTS + 2)]
+  first = hip_attn._as_tiles(triples[0], 256, torch.device("cpu"))
+  assert hip_attn._as_tiles(triples[0], 256, torch.device("cpu")) is first  # prepared once
+  for t in triples[1:]:
+    hip_attn._as_tiles(t, 256, torch.device("cpu"))
+  assert len(hip_attn._cache) == hip_attn.CACHE_LISTS
+  assert hip_attn._as_tiles(triples[0], 256, torch.device("cpu")) is not first  # evicted, rebuilt

@@ -259,6 +259,38 @@ def test_sampled_attention_equals_dense():
   np.testing.assert_allclose(got["dv"], dv[:, keys], atol=1e-12)
 
 
+@pytest.mark.parametrize("symmetric", [True, False])
+def test_block_attention_equals_dense(symmetric):
+  """Whole 16-row/16-key blocks (block=16 keeps the dense check small) of a ragged n, with key blocks
+  given out of order, a key block that no query reaches except through itself, and a row with no
+  valid key (zero output and gradients, the kernels' convention)."""
+  rng = np.random.default_rng(17)
+  b, n, h, d, blk = 2, 90, 2, 8, 16
+  q, k, v, do = (rng.standard_normal((b, n, h, d)) for _ in range(4))
+  m = _random_mask(n, 0.05, 10, symmetric=symmetric).tolil()
+  m[33, :] = False  # row 33 attends to nothing
+  m = m.tocsr()
+  dense = m.toarray()
+  row_blocks, key_blocks = [5, 0, 2], [5, 1, 3]  # 5 is the ragged last block (rows 80-89)
+  got = A.block_attention(q, k, v, do, m, 0.3, row_blocks, key_blocks, block=blk)
+  rows = np.concatenate([np.arange(r * blk, min(n, (r + 1) * blk)) for r in row_blocks])
+  keys = np.concatenate([np.arange(c * blk, min(n, (c + 1) * blk)) for c in key_blocks])
+  np.testing.assert_array_equal(got["rows"], rows)
+  np.testing.assert_array_equal(got["keys"], keys)
+  live = dense.any(1)
+  safe = dense | ~live[:, None]  # dense_* need every row to hold a key
+  out = A.dense_attention(q, k, v, safe, 0.3) * live[None, :, None, None]
+  lse = A.dense_lse(q, k, safe, 0.3)
+  dq, dk, dv = A.dense_grads(q, k, v, do * live[None, :, None, None], safe, 0.3)
+  dq = dq * live[None, :, None, None]
+  np.testing.assert_allclose(got["out"], out[:, rows], atol=1e-12)
+  np.testing.assert_allclose(got["lse"][:, :, live[rows]], lse[:, :, rows[live[rows]]], atol=1e-12)
+  np.testing.assert_allclose(got["dq"], dq[:, rows], atol=1e-12)
+  np.testing.assert_allclose(got["dk"], dk[:, keys], atol=1e-12)
+  np.testing.assert_allclose(got["dv"], dv[:, keys], atol=1e-12)
+  assert np.abs(got["out"][:, list(rows).index(33)]).max() == 0.0
+
+
 # ---- oracle.rows: the gather/scatter either side of the layer loop and the layer norm ----
 
 def test_rows_scatter_inverts_gather():
