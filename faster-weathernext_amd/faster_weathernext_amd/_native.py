@@ -50,6 +50,7 @@ class Tiles(ctypes.Structure):
 
 
 ITEM_TILES = 64  # FWN_ITEM_TILES: default longest run of tiles per work item
+SCRATCH_BYTES = 64 << 20  # FWN_SCRATCH_BYTES: static scratch of fwn_attn_fwd_launch_noalloc
 
 
 class RowsDesc(ctypes.Structure):
@@ -79,6 +80,7 @@ SIGNATURES = {
     "fwn_tiles_schedule_fill": [_I32, _P, _I32, _P, _P],
     "fwn_attn_workspace_size": [_DESC, _TILES, _P],
     "fwn_attn_fwd_launch": [_DESC, _P, _P, _P, _TILES, _P, _P, _P, _U64, _P],
+    "fwn_attn_fwd_launch_noalloc": [_DESC, _P, _P, _P, _TILES, _P, _P, _P],
     "fwn_attn_bwd_delta_launch": [_DESC, _P, _P, _P, _P],
     "fwn_attn_bwd_dq_launch": [_DESC, _P, _P, _P, _P, _P, _P, _TILES, _P, _P, _U64, _P],
     "fwn_attn_bwd_dkv_launch": [_DESC, _P, _P, _P, _P, _P, _P, _TILES, _P, _P, _P, _U64, _P],

@@ -177,6 +177,20 @@ int fwn_attn_fwd_launch(const fwn_attn_desc* desc, const void* q, const void* k,
                         const fwn_tiles* tiles, void* o, float* lse, void* workspace,
                         uint64_t workspace_bytes, void* stream);
 
+/* The forward launcher without a workspace argument: split work items use the library's static
+ * scratch (a __device__ array of FWN_SCRATCH_BYTES that each GPU holds from the library's load
+ * until the process ends), so the call allocates nothing and takes no caller memory beyond the
+ * inputs and outputs. No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under graph capture, serving loops, harnesses that forbid hipMalloc).
+ * Returns FWN_ERR_INVALID_ARG when the list's split schedule needs more than FWN_SCRATCH_BYTES
+ * (fwn_attn_workspace_size); lists whose blocks are not split need none. The scratch's device
+ * address is looked up on the first call on each device, so make that call outside graph
+ * capture. Calls on one device share its scratch: calls whose kernels can overlap on one device
+ * (other streams, other threads) race, so order them on one stream. */
+#define FWN_SCRATCH_BYTES (64ull << 20)
+int fwn_attn_fwd_launch_noalloc(const fwn_attn_desc* desc, const void* q, const void* k, const void* v,
+                                const fwn_tiles* tiles, void* o, float* lse, void* stream);
+
 /* delta = rowsum(o * dout) in float32 [batch, heads, n] (pallas_attn.py:278). */
 int fwn_attn_bwd_delta_launch(const fwn_attn_desc* desc, const void* o, const void* dout,
                               float* delta, void* stream);

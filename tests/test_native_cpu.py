@@ -544,3 +544,24 @@ def test_tile_lists_reject_foreign_formats_and_mismatched_calls():
     hip_attn._as_tiles(t, 256, torch.device("cpu"))
   assert len(hip_attn._cache) == hip_attn.CACHE_LISTS
   assert hip_attn._as_tiles(triples[0], 256, torch.device("cpu")) is not first  # evicted, rebuilt
+
+
+def test_noalloc_forward_rejects_schedules_beyond_the_static_scratch():
+  """fwn_attn_fwd_launch_noalloc checks the split schedule's scratch need against FWN_SCRATCH_BYTES
+  before any HIP call, and names the limit in its error."""
+  from faster_weathernext_amd import hip_attn
+  nb = 130
+  tp = np.concatenate([[0], nb + np.arange(nb, dtype=np.int32)]).astype(np.int32)
+  kb = np.concatenate([np.arange(nb), np.arange(1, nb)]).astype(np.int32)
+  bits = np.full((len(kb), nat.BLOCK, nat.BLOCK // 32), 0xFFFFFFFF, np.uint32)
+  n = nb * nat.BLOCK
+  tl = hip_attn.TileList(tp, kb, bits, n, device="cpu", max_item_tiles=1)  # block 0: 130 partial slots
+  desc = nat.AttnDesc(4, n, 8, 128, nat.BF16, 0.1, n * 1024, 1024, 128, 0, 0, 0)
+  size = ctypes.c_uint64(0)
+  nat.check(nat.lib().fwn_attn_workspace_size(desc, tl.struct, ctypes.byref(size)))
+  assert size.value == 130 * 4 * 8 * 128 * (2 * 128 + 2) * 4 > nat.SCRATCH_BYTES
+  rc = nat.lib().fwn_attn_fwd_launch_noalloc(desc, 256, 256, 256, tl.struct, 256, None, None)
+  assert rc == nat.ERR_INVALID_ARG
+  assert b"static scratch holds 67108864" in nat.lib().fwn_last_error()
+  bad = nat.AttnDesc(4, n, 8, 96, nat.BF16, 0.1, n * 1024, 1024, 128, 0, 0, 0)  # head_dim 96 is not built
+  assert nat.lib().fwn_attn_fwd_launch_noalloc(bad, 256, 256, 256, tl.struct, 256, None, None) == nat.ERR_UNSUPPORTED
