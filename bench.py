@@ -1,7 +1,8 @@
 #!/usr/bin/env python3
 """Benchmark of the block-sparse masked mesh attention on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c3|c2|c4|c5|c5mha|c5stack|rows] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c3|c2|c4|c5|c5bwd|c5f32|c5mha|c5stack|rows]
+                    [--no-cpu]
 
 A step is one pass of the hot path over one batch of synthetic input: for the default workload
 (configuration 3 of BASELINE.json) the forward kernel plus the backward (delta pre-pass, then dQ
@@ -11,10 +12,16 @@ fp32 accumulation. Inputs are resident in HBM before the timed region. The metri
 TFLOP/s over live 128x128 tiles (14 * D * 128^2 per live tile, batch and head for fwd + bwd;
 4 * D * 128^2 for forward-only workloads). The mask build is timed separately.
 
-Prints one JSON line (rank 0). Also reports a roofline entry for the dominant kernel (its
-algorithmic FLOPs per launch over its mean HIP-event duration in the timed region) and a CPU
-baseline: the restated reference XLA chunked path (oracle/attention.py) on a bounded sample of
-query chunks of the same workload, on this host's cores.
+Prints one JSON line (rank 0). Also reports a roofline entry for the dominant kernel: its
+algorithmic FLOPs per launch over its mean HIP-event duration in a second timed pass of K steps
+in which every kernel runs alone on one stream (the first pass, which gives `value`, runs dQ and
+dK/dV side by side as the package does). And a CPU baseline: the restated reference XLA chunked
+path (oracle/attention.py) on a bounded sample of query chunks of the same workload, on the cores
+this process may use (os.sched_getaffinity), with the CPU model.
+
+c5bwd and c5f32 are the reference's own attention benchmark (scripts/attn_bench.py --grad: 32-hop,
+Hilbert order, 6 x 128 heads, one layer's forward + backward) in bf16 and in float32; the line
+carries the reference's published RTX 5090 times for the same shape beside it.
 """
 import argparse
 import json
@@ -36,8 +43,19 @@ WORKLOADS = {
     "c4": dict(k_hop=8, heads=4, head_dim=128, batch=8, dtype="bf16", backward=True, reorder=False, sigma=1.0,
                desc="config 4: r6 mesh, 8-hop, 8 members x 4x128, bf16, forward + backward"),
     "c5": dict(k_hop=32, heads=6, head_dim=128, batch=1, dtype="bf16", backward=False, reorder=True, sigma=1.0,
+               reference_ms={"fwd, TF32 dots (reference default)": 9.3, "source": "docs/validation.md:397, RTX 5090"},
                desc="WN2 mesh-transformer attention shape: r6 mesh, 32-hop, Hilbert order, 6x128, bf16, "
                     "forward (one of 24 layers)"),
+    "c5bwd": dict(k_hop=32, heads=6, head_dim=128, batch=1, dtype="bf16", backward=True, reorder=True, sigma=1.0,
+                  reference_ms={"fwd+bwd, TF32 dots (reference default)": 42.2, "fwd+bwd, 3xTF32 (highest)": 115.4,
+                                "source": "docs/validation.md:396-397, RTX 5090"},
+                  desc="the reference's attention benchmark (scripts/attn_bench.py --grad): r6 mesh, 32-hop, Hilbert "
+                       "order, 6x128, bf16 (fp32 accumulate), forward + backward of one WN2 attention layer"),
+    "c5f32": dict(k_hop=32, heads=6, head_dim=128, batch=1, dtype="f32", backward=True, reorder=True, sigma=1.0,
+                  reference_ms={"fwd+bwd, 3xTF32 (highest)": 115.4, "fwd+bwd, IEEE fp32 dots (strict_fp32)": 797.0,
+                                "source": "docs/validation.md:396-397, 405, RTX 5090"},
+                  desc="the reference's attention benchmark at full precision: r6 mesh, 32-hop, Hilbert order, "
+                       "6x128, float32 (fp32 MFMA), forward + backward of one WN2 attention layer"),
     "c5mha": dict(k_hop=32, heads=6, head_dim=128, batch=1, dtype="bf16", backward=True, reorder=True, sigma=1.0,
                   d_model=768,
                   desc="WN2 attention block at C5 shape: fused q/k/v projection (768 -> 3x6x128), HIP attention "
@@ -306,30 +324,47 @@ def mesh_stack(args):
   return 0
 
 
+def cpu_model():
+  """The host CPU's model name (/proc/cpuinfo), or the platform's processor string."""
+  try:
+    with open("/proc/cpuinfo") as f:
+      for line in f:
+        if line.startswith("model name"):
+          return line.split(":", 1)[1].strip()
+  except OSError:
+    pass
+  import platform
+  return platform.processor() or "unknown"
+
+
 def cpu_baseline(cfg, q, k, v, do, mask, tiles, scale, budget_s):
-  """Times the restated reference XLA chunked path on whole query chunks until `budget_s` elapses."""
+  """Times the restated reference XLA chunked path on whole query chunks until `budget_s` elapses,
+  with the BLAS thread pool set to the cores this process may run on."""
   import numpy as np
-  from threadpoolctl import threadpool_info
+  from threadpoolctl import threadpool_info, threadpool_limits
 
   from oracle import attention as A
+  cores = len(os.sched_getaffinity(0))
   chunk = 512
   starts, bits, window, n_kv = A.build_chunked_mask(mask, chunk)
   D, B, H = cfg["head_dim"], cfg["batch"], cfg["heads"]
-  done, t0 = 0, time.perf_counter()
-  while True:
-    A.chunked_attention(q, k, v, starts, bits, window, n_kv, chunk, scale, chunks=[done])
-    if cfg["backward"]:
-      A.chunked_attention_grads(q, k, v, do, starts, bits, window, n_kv, chunk, scale, chunks=[done])
-    done += 1
-    if time.perf_counter() - t0 >= budget_s or done == len(starts):
-      break
-  elapsed = time.perf_counter() - t0
+  with threadpool_limits(limits=cores):
+    threads = max([t.get("num_threads", 1) for t in threadpool_info()] or [1])
+    done, t0 = 0, time.perf_counter()
+    while True:
+      A.chunked_attention(q, k, v, starts, bits, window, n_kv, chunk, scale, chunks=[done])
+      if cfg["backward"]:
+        A.chunked_attention_grads(q, k, v, do, starts, bits, window, n_kv, chunk, scale, chunks=[done])
+      done += 1
+      if time.perf_counter() - t0 >= budget_s or done == len(starts):
+        break
+    elapsed = time.perf_counter() - t0
   qb_per_chunk = chunk // 128
   ptr = tiles.ptr.cpu().numpy()
   live = int(ptr[min(done * qb_per_chunk, len(ptr) - 1)] - ptr[0])
   flops = (14 if cfg["backward"] else 4) * D * 128 * 128 * live * B * H
-  threads = max([t.get("num_threads", 1) for t in threadpool_info()] or [1])
-  return {"value": flops / elapsed / 1e12, "unit": "TFLOP/s", "cores": int(threads), "kind": "port",
+  return {"value": flops / elapsed / 1e12, "unit": "TFLOP/s", "cores": cores, "blas_threads": int(threads),
+          "cpu_model": cpu_model(), "kind": "port",
           "sample": f"{done} of {len(starts)} query chunks of {chunk} (window {window} keys), "
                     f"{'fwd+bwd' if cfg['backward'] else 'fwd'} float32 numpy/BLAS, {elapsed:.1f} s",
           "seconds": round(elapsed, 2)}
@@ -400,71 +435,80 @@ def main():
   # dK/dV runs on a second stream beside dQ (as the package's backward does), with its own
   # workspace; the step joins the two streams at its end.
   side = torch.cuda.Stream(dev)
-  sidep = side.cuda_stream
   ws2 = fwn.hip_attn.workspace(desc, dev, tiles)
   ws2p, ws2n = (ws2.data_ptr(), ws2.numel()) if ws2 is not None else (None, 0)
 
-  def fwd():
+  def fwd(st):
     nat.check(L.fwn_attn_fwd_launch(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), ts, out.data_ptr(),
-                                    lse.data_ptr(), wsp, wsn, sp))
+                                    lse.data_ptr(), wsp, wsn, st.cuda_stream))
 
-  def bwd_delta():
-    nat.check(L.fwn_attn_bwd_delta_launch(desc, out.data_ptr(), do.data_ptr(), delta.data_ptr(), sp))
+  def bwd_delta(st):
+    nat.check(L.fwn_attn_bwd_delta_launch(desc, out.data_ptr(), do.data_ptr(), delta.data_ptr(), st.cuda_stream))
 
-  def bwd_dq():
+  def bwd_dq(st):
     nat.check(L.fwn_attn_bwd_dq_launch(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(),
-                                       lse.data_ptr(), delta.data_ptr(), ts, dq.data_ptr(), wsp, wsn, sp))
+                                       lse.data_ptr(), delta.data_ptr(), ts, dq.data_ptr(), wsp, wsn, st.cuda_stream))
 
-  def bwd_dkv():
+  def bwd_dkv(st):
+    own = st is side  # beside dQ: its own workspace
     nat.check(L.fwn_attn_bwd_dkv_launch(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(),
-                                        lse.data_ptr(), delta.data_ptr(), ts, dk.data_ptr(), dv.data_ptr(), ws2p,
-                                        ws2n, sidep))
+                                        lse.data_ptr(), delta.data_ptr(), ts, dk.data_ptr(), dv.data_ptr(),
+                                        ws2p if own else wsp, ws2n if own else wsn, st.cuda_stream))
 
-  # (name, launch, stream it runs on); dkv runs on the side stream after delta.
-  kernels = [("fwd", fwd, stream)]
+  # (name, launch, stream it runs on). The step: dK/dV on the side stream after delta, beside dQ
+  # (unless --serial-bwd). The solo pass: every kernel on one stream, so each has the GPU alone;
+  # the roofline entry takes the dominant kernel's duration from it.
+  solo = [("fwd", fwd, stream)]
   if cfg["backward"]:
-    if args.serial_bwd:
-      # One stream, dQ then dK/dV (fwn_attn_bwd_launch's order): each kernel has the GPU alone.
-      ws2p, ws2n, sidep = wsp, wsn, sp
-      kernels += [("delta", bwd_delta, stream), ("dq", bwd_dq, stream), ("dkv", bwd_dkv, stream)]
-    else:
-      kernels += [("delta", bwd_delta, stream), ("dkv", bwd_dkv, side), ("dq", bwd_dq, stream)]
+    solo += [("delta", bwd_delta, stream), ("dq", bwd_dq, stream), ("dkv", bwd_dkv, stream)]
+  paired = solo if args.serial_bwd or not cfg["backward"] else \
+      [("fwd", fwd, stream), ("delta", bwd_delta, stream), ("dkv", bwd_dkv, side), ("dq", bwd_dq, stream)]
 
-  def step(ev=None):
+  def step(kernels, ev=None):
     for i, (name, fn, st) in enumerate(kernels):
-      if name == "dkv" and st is side:
+      if st is side:
         side.wait_stream(stream)
       if ev is not None:
         ev[i][0].record(st)
-      fn()
+      fn(st)
       if ev is not None:
         ev[i][1].record(st)
-    if cfg["backward"]:
+    if any(st is side for _, _, st in kernels):
       stream.wait_stream(side)
 
-  for _ in range(args.warmup):
-    step()
-  torch.cuda.synchronize()
+  def timed_pass(kernels):
+    """K steps between two events on the main stream, an event pair on its own stream around every
+    launch: (ms per step, mean ms per kernel, events)."""
+    events = [[[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in kernels] for _ in range(args.steps)]
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for s_ in range(args.steps):
+      step(kernels, events[s_])
+    stop.record(stream)
+    torch.cuda.synchronize()
+    per = {name: float(np.mean([events[s_][i][0].elapsed_time(events[s_][i][1]) for s_ in range(args.steps)]))
+           for i, (name, _, _) in enumerate(kernels)}
+    return start.elapsed_time(stop) / args.steps, per, events
 
-  # Timed region: K steps. An event pair on the launch's own stream brackets every kernel; the
-  # step time runs from the first launch to the join of the two streams.
-  events = [[[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in kernels] for _ in range(args.steps)]
-  start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-  torch.cuda.synchronize()
-  start.record(stream)
-  for s in range(args.steps):
-    step(events[s])
-  stop.record(stream)
-  torch.cuda.synchronize()
-  ms_step = start.elapsed_time(stop) / args.steps
-  per_kernel = {name: float(np.mean([events[s][i][0].elapsed_time(events[s][i][1]) for s in range(args.steps)]))
-                for i, (name, _, _) in enumerate(kernels)}
-  # dQ and dK/dV side by side: from the end of delta (both streams start there) to the later end.
-  if cfg["backward"]:
-    names = [nm for nm, _, _ in kernels]
+  for _ in range(args.warmup):
+    step(paired)
+  # Timed region 1 (the metric): K steps as the package runs them.
+  ms_step, per_kernel, events = timed_pass(paired)
+  pair_ms = None
+  if cfg["backward"] and paired is not solo:
+    # dQ and dK/dV side by side: from the end of delta (both streams start there) to the later end.
+    names = [nm for nm, _, _ in paired]
     i_d, i_q, i_kv = names.index("delta"), names.index("dq"), names.index("dkv")
-    pair_ms = float(np.mean([max(events[s][i_d][1].elapsed_time(events[s][i_q][1]),
-                                 events[s][i_d][1].elapsed_time(events[s][i_kv][1])) for s in range(args.steps)]))
+    pair_ms = float(np.mean([max(events[s_][i_d][1].elapsed_time(events[s_][i_q][1]),
+                                 events[s_][i_d][1].elapsed_time(events[s_][i_kv][1])) for s_ in range(args.steps)]))
+  # Timed region 2 (the roofline entry): K more steps with every kernel alone on the GPU.
+  if paired is solo:
+    ms_solo, per_solo = ms_step, per_kernel
+  else:
+    for _ in range(args.warmup):
+      step(solo)
+    ms_solo, per_solo, _ = timed_pass(solo)
 
   unit_flops = D * 128 * 128 * T * B * H  # one live tile x D, all batch members and heads
   total_flops = (14 if cfg["backward"] else 4) * unit_flops
@@ -472,10 +516,11 @@ def main():
   # Algorithmic FLOPs per launch: forward 4*D per live entry; the backward's 10*D (FA2 count, S
   # recomputed once) split as dQ kernel 4*D (dQ + half of the S/dP recompute) and dK/dV kernel 6*D.
   algo = {"fwd": 4 * unit_flops, "dq": 4 * unit_flops, "dkv": 6 * unit_flops, "delta": 0}
-  dominant = max((k_ for k_ in per_kernel if algo.get(k_)), key=lambda k_: per_kernel[k_])
-  achieved = algo[dominant] / (per_kernel[dominant] * 1e-3) / 1e12
+  dominant = max((k_ for k_ in per_solo if algo.get(k_)), key=lambda k_: per_solo[k_])
+  achieved = algo[dominant] / (per_solo[dominant] * 1e-3) / 1e12
   peak = PEAK[cfg["dtype"]]
   traffic, traffic_src = measured_traffic(args.workload, dominant)
+  rate = lambda name, ms: round(algo[name] / (ms * 1e-3) / 1e12, 3)
 
   result = {
       "metric": METRIC, "value": round(value, 3), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
@@ -487,24 +532,29 @@ def main():
                  "heads": H, "head_dim": D, "order": "hilbert" if cfg["reorder"] else "subdivision",
                  "sigma": cfg["sigma"], "live_tiles": T, "tile_density": round(tiles.density, 4),
                  "live_group_fraction": round(tiles.group_fraction, 4),
-                 "valid_entries": int(mask.nnz)},
+                 "valid_entries": int(mask.nnz), "item_tiles": tiles.item_cap_for(B, H)},
       "roofline": {"bound": "mfma", "kernel": dominant, "achieved": round(achieved, 3), "peak": peak,
                    "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": traffic,
-                   "traffic_source": traffic_src,
-                   **({"note": "dkv's duration is measured while dq runs beside it on the other stream"}
-                      if dominant in ("dkv", "dq") and cfg["backward"] and not args.serial_bwd else {})},
-      **({"backward_pair": {
-          "ms": round(pair_ms, 4), "kernels": ["dq", "dkv"],
-          "achieved": round((algo["dq"] + algo["dkv"]) / (pair_ms * 1e-3) / 1e12, 3), "unit": "TFLOP/s",
-          "frac": round((algo["dq"] + algo["dkv"]) / (pair_ms * 1e-3) / 1e12 / peak, 4)}}
-         if cfg["backward"] else {}),
+                   "traffic_source": traffic_src, "ms": round(per_solo[dominant], 4),
+                   "timing": "solo pass: the same K steps again with every kernel on one stream (each alone on "
+                             "the GPU), HIP events on that stream around each launch, split-K combine included"},
       "kernels_ms": {k_: round(v_, 4) for k_, v_ in per_kernel.items()},
+      "kernels_ms_solo": {k_: round(v_, 4) for k_, v_ in per_solo.items()},
+      "kernels_tflops_solo": {k_: rate(k_, v_) for k_, v_ in per_solo.items() if algo.get(k_)},
+      "ms_per_step_solo": round(ms_solo, 4),
       "valid_entry_tflops": round(value * mask.nnz / (T * 128 * 128), 3),
       "mask_build_s": round(t_mask, 3), "tile_prepare_s": round(t_tiles, 3),
       "step_s": None,
       "step_note": "the full WN2 0.25-deg step needs jax, haiku and weathernext, which this image lacks; "
                    "run --workload c5 for the attention share of a step (24 layers x forward)",
   }
+  if pair_ms is not None:
+    result["backward_pair"] = {
+        "ms": round(pair_ms, 4), "kernels": ["dq", "dkv"], "note": "dq and dkv side by side on two streams",
+        "achieved": round((algo["dq"] + algo["dkv"]) / (pair_ms * 1e-3) / 1e12, 3), "unit": "TFLOP/s",
+        "frac": round((algo["dq"] + algo["dkv"]) / (pair_ms * 1e-3) / 1e12 / peak, 4)}
+  if "reference_ms" in cfg:
+    result["reference_rtx5090_ms"] = cfg["reference_ms"]
   if args.workload == "c5":
     result["attn_s_per_step"] = round(24 * ms_step * 1e-3, 4)
   if not args.no_cpu:
