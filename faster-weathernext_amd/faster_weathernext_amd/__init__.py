@@ -24,18 +24,27 @@ __version__ = "0.1.0"
 def enable(force: bool = False, **options):
   """Selects the HIP attention path; keyword options update ``patch.Options``.
 
-  Mirrors ``faster_weathernext.enable`` (``__init__.py:14-30``): unknown options raise TypeError.
-  Unless ``force``, the native library must load (RuntimeError otherwise). Returns the Options.
+  Mirrors ``faster_weathernext.enable`` (``__init__.py:14-30``): unknown options raise TypeError,
+  an unknown ``attention`` value ValueError. Unless ``force`` (the reference's switch past its
+  compatibility check), the native library must load and the default device must be a gfx950
+  (RuntimeError otherwise). Returns the Options.
   """
   for key in options:
     if not hasattr(patch.OPTIONS, key):
       raise TypeError(f"unknown option {key!r}; see faster_weathernext_amd.patch.Options")
+  if options.get("attention", patch.OPTIONS.attention) not in ("auto", "hip"):
+    raise ValueError(f"unknown attention implementation {options['attention']!r} (auto, hip)")
   if not force:
     from . import _native
     _native.lib()
   for key, value in options.items():
     setattr(patch.OPTIONS, key, value)
-  patch.attention_impl()
+  if not force:
+    try:
+      patch.attention_impl()
+    except RuntimeError:
+      patch.OPTIONS = patch.Options()
+      raise
   patch.install()
   return patch.OPTIONS
 

@@ -84,7 +84,8 @@ def adjacency(faces, n):
 
 def khop_mask(adj, k):
   """Boolean CSR of the nodes within k hops of each node, itself included: the set of the
-  reference's ``(adj + I) ** k`` (``patch.py:209``). ``adj`` must be symmetric."""
+  reference's ``(adj + I) ** k`` (``patch.py:209``). Row i holds the nodes reachable from i in at
+  most k steps along edges i -> j (adj[i, j] set), so a directed adjacency gives that power too."""
   adj = sparse.csr_matrix(adj)
   n = adj.shape[0]
   indptr = nat.as_c(adj.indptr, np.int64)

@@ -16,6 +16,7 @@ package does not load.
 """
 import torch
 
+from . import patch
 from .hip_attn import TileList, tiled_flash_attention, tiled_flash_attention_qkv
 
 # hipBLASLt's bf16 GEMMs on MI355X run much faster when the row count is a multiple of 512: for
@@ -55,10 +56,12 @@ class TiledMHA(torch.nn.Module):
 
   ``tiles`` is the mesh's TileList (or the array triple of ``build_tile_mask``), built once and
   shared by every layer; ``tiles_t`` is the transposed mask's list for non-symmetric masks.
+  ``dtype`` None takes the enable() option (bfloat16 when ``bf16``, else float32).
   """
 
   def __init__(self, d_model, num_heads, key_size, tiles, tiles_t=None, *, device=None, dtype=None):
     super().__init__()
+    dtype = patch.default_dtype(dtype)
     self.num_heads, self.key_size = num_heads, key_size
     self.tiles, self.tiles_t = tiles, tiles_t
     self.qkv = torch.nn.Linear(d_model, 3 * num_heads * key_size, bias=False, device=device, dtype=dtype)

@@ -30,9 +30,11 @@ the JAX model, which this package does not load.
 import numpy as np
 import torch
 import torch.nn.functional as F
+from scipy import sparse
 
+from . import patch
 from .hip_attn import TileList
-from .mesh import mesh_mask
+from .mesh import hilbert_order, khop_mask, mesh_mask
 from .mha import TiledMHA, linear_rows, needs_grad
 from .rows import add_layer_norm_affine, gather_layer_norm, layer_norm_affine, layer_norm_scatter
 
@@ -111,23 +113,44 @@ class MeshBlock(torch.nn.Module):
 
 class MeshTransformer(torch.nn.Module):
   """The 24-layer mesh transformer of WeatherNext 2's processor, node features [batch, n, d_model]
-  in mesh (subdivision) order in and out; the attention runs in Hilbert order when `reorder`."""
+  in mesh (subdivision) order in and out; the attention runs in Hilbert order when `reorder`.
+
+  The mask is the k-hop neighbourhood of the refined icosahedral mesh, or of ``adjacency`` (a
+  boolean [n, n] sparse matrix, with the nodes' ``latlon`` in degrees for the Hilbert order) when
+  one is given, as the reference builds it from the model's own adjacency (``patch.py:193-219``).
+  A non-symmetric adjacency gives a non-symmetric mask, whose transposed tile list the backward
+  walks. ``reorder`` and ``dtype`` None take the enable() options (``reorder``, ``bf16``).
+  """
 
   def __init__(self, refinement=6, k_hop=32, num_layers=24, d_model=768, num_heads=6, key_size=128,
-               ffw_hidden=3072, cond_size=32, reorder=True, *, device="cuda", dtype=torch.bfloat16, tiles=None,
-               eps=1e-5):
+               ffw_hidden=3072, cond_size=32, reorder=None, *, device="cuda", dtype=None, tiles=None,
+               tiles_t=None, adjacency=None, latlon=None, eps=1e-5):
     super().__init__()
-    mask, lat, lon, perm = mesh_mask(refinement, k_hop, reorder=reorder)
+    reorder = patch.default_reorder(reorder)
+    dtype = patch.default_dtype(dtype)
+    if adjacency is None:
+      mask, lat, lon, perm = mesh_mask(refinement, k_hop, reorder=reorder)
+      symmetric = True  # powers of the mesh's symmetric adjacency
+    else:
+      adjacency = sparse.csr_matrix(adjacency).astype(bool)
+      mask = khop_mask(adjacency, k_hop)
+      perm = hilbert_order(*latlon) if reorder and latlon is not None else None
+      symmetric = (adjacency != adjacency.T).nnz == 0
     self.n = mask.shape[0]
     self.eps = eps
-    # One tile list for every layer; the k-hop mask of the symmetric mesh adjacency is symmetric,
-    # so it also serves the backward (patch.py:214-218).
-    self.tiles = tiles if tiles is not None else TileList.from_mask(mask, perm, device=device)
+    # One tile list for every layer (patch.py:214); the backward walks the transposed mask's list,
+    # built only when the adjacency is not symmetric (patch.py:215-218).
+    if tiles is None:
+      tiles = TileList.from_mask(mask, perm, device=device)
+      if not symmetric and tiles_t is None:
+        permuted = mask if perm is None else mask[perm][:, perm]
+        tiles_t = TileList.from_mask(permuted.T.tocsr(), device=device)
+    self.tiles, self.tiles_t = tiles, tiles_t
     self.register_buffer("perm", None if perm is None else torch.from_numpy(np.asarray(perm, np.int64)).to(device),
                          persistent=False)
     self.blocks = torch.nn.ModuleList(
-        MeshBlock(d_model, num_heads, key_size, ffw_hidden, cond_size, self.tiles, device=device, dtype=dtype,
-                  eps=eps)
+        MeshBlock(d_model, num_heads, key_size, ffw_hidden, cond_size, self.tiles, self.tiles_t, device=device,
+                  dtype=dtype, eps=eps)
         for _ in range(num_layers))
     self.final_norm = NormConditioning(d_model, cond_size, device=device, dtype=dtype)
 

@@ -10,8 +10,10 @@
  *     lists are rejected on the host before anything is launched.
  *   - Launchers enqueue work on `stream` and return without synchronising. They allocate
  *     nothing (temporary results go to a caller-provided workspace, see
- *     fwn_attn_workspace_size), keep no pointer after returning and hold no mutable global
- *     state, so they are re-entrant and safe under stream capture.
+ *     fwn_attn_workspace_size, or for fwn_attn_fwd_launch_noalloc to the library's static
+ *     scratch), keep no pointer after returning and hold no mutable global state (beyond the
+ *     per-device scratch address fwn_attn_fwd_launch_noalloc looks up on its first call), so
+ *     they are re-entrant and safe under stream capture.
  *   - Tensors q, k, v, o, dout, dq, dk, dv are [batch, n, heads, head_dim] in the element strides
  *     of fwn_attn_desc (head_dim contiguous): node-major by default, read and written in place
  *     (the reference transposes to head-major and pads, pallas_attn.py:334-335; here no copy is
@@ -109,9 +111,11 @@ const char* fwn_last_error(void);
  * patch.py:208-219: the k-hop mask (adj ** k), the Hilbert order and build_tile_mask.
  * ------------------------------------------------------------------------------------------- */
 
-/* Number of nodes within k hops of each node (itself included) of a symmetric adjacency in CSR
- * (adj_ptr[n + 1], adj_idx; self edges optional). Writes row_ptr[n + 1] of the k-hop mask
- * (exclusive prefix sums). Replaces `adj ** k` (patch.py:209, scripts/attn_bench.py:32). */
+/* Number of nodes within k hops of each node (itself included) of an adjacency in CSR
+ * (adj_ptr[n + 1], adj_idx; self edges optional): row i counts the nodes reachable from i in at
+ * most k steps along edges i -> j, which is row i of (adj + I) ** k for directed adjacencies too.
+ * Writes row_ptr[n + 1] of the k-hop mask (exclusive prefix sums). Replaces `adj ** k`
+ * (patch.py:209, scripts/attn_bench.py:32). */
 int fwn_khop_count(int32_t n, const int64_t* adj_ptr, const int32_t* adj_idx, int32_t k,
                    int64_t* row_ptr);
 

@@ -340,15 +340,69 @@ def test_workspace_size_and_checks():
 
 def test_enable_disable_and_unknown_option():
   # tests/test_masks.py:91-102 of the reference: enable/disable round trip, unknown option raises.
-  opts = fwn.enable(reorder=False)
-  assert fwn.patch.is_enabled() and opts.reorder is False and fwn.patch.attention_impl() == "hip"
+  import torch
+  from faster_weathernext_amd import patch
+  # Without a gfx950 (this host has no GPU) enable() refuses, as attention_impl() does, and leaves
+  # the options unchanged; force skips the check, as the reference's force skips its compat check.
+  if patch.device_arch() != patch.ARCH:
+    with pytest.raises(RuntimeError, match="gfx950"):
+      fwn.enable(reorder=False)
+    with pytest.raises(RuntimeError, match="gfx950"):
+      patch.attention_impl()
+    assert not patch.is_enabled() and fwn.options().reorder is True
+  opts = fwn.enable(force=True, reorder=False, bf16=True)
+  assert patch.is_enabled() and opts.reorder is False and opts.bf16 is True
+  # The options are the defaults of the modules built afterwards.
+  assert patch.default_reorder() is False and patch.default_reorder(True) is True
+  assert patch.default_dtype() is torch.bfloat16 and patch.default_dtype(torch.float32) is torch.float32
+  mha = fwn.TiledMHA(16, 2, 8, None, device="cpu")
+  assert mha.qkv.weight.dtype is torch.bfloat16
   fwn.disable()
-  assert not fwn.patch.is_enabled() and fwn.options().reorder is True
+  assert not patch.is_enabled() and fwn.options().reorder is True and patch.default_dtype() is torch.float32
+  assert fwn.TiledMHA(16, 2, 8, None, device="cpu").qkv.weight.dtype is torch.float32
   with pytest.raises(TypeError):
     fwn.enable(not_an_option=1)
   with pytest.raises(ValueError):
-    fwn.enable(attention="pallas")
+    fwn.enable(force=True, attention="pallas")
+  assert not patch.is_enabled()
   fwn.disable()
+
+
+def test_khop_of_a_directed_adjacency_is_the_boolean_power():
+  """Row i of the k-hop mask is row i of (adj + I)^k also when adj is not symmetric."""
+  n, k = 300, 3
+  adj = sparse.random(n, n, density=0.01, random_state=7, format="csr").astype(bool)
+  assert (adj != adj.T).nnz
+  power = sparse.identity(n, dtype=np.int64, format="csr")
+  step = (adj + sparse.identity(n, dtype=bool, format="csr")).astype(np.int64)
+  for _ in range(k):
+    power = ((power @ step) > 0).astype(np.int64)
+  got = fwn.khop_mask(adj, k)
+  np.testing.assert_array_equal(got.toarray(), power.toarray() > 0)
+
+
+def test_mesh_transformer_builds_the_transposed_list_for_a_directed_adjacency():
+  """MeshTransformer on a caller's adjacency (patch.py:193-219): a non-symmetric adjacency gets the
+  transposed mask's tile list (of the Hilbert-permuted mask) for the backward, shared by every
+  block; a symmetric one gets none."""
+  v, f, lat, lon = fwn.icosahedral_mesh(2)
+  n = len(v)
+  sym = fwn.adjacency(f, n)
+  rng = np.random.default_rng(3)
+  keep = rng.random(sym.nnz) < 0.7  # drop 30% of the directed edges: no longer symmetric
+  coo = sym.tocoo()
+  directed = sparse.csr_matrix((np.ones(int(keep.sum()), bool), (coo.row[keep], coo.col[keep])), shape=(n, n))
+  kw = dict(k_hop=2, num_layers=2, d_model=16, num_heads=2, key_size=32, ffw_hidden=32, cond_size=4, device="cpu")
+  model = fwn.MeshTransformer(adjacency=directed, latlon=(lat, lon), reorder=True, **kw)
+  assert model.tiles_t is not None and all(b.mha.tiles_t is model.tiles_t for b in model.blocks)
+  perm = fwn.hilbert_order(lat, lon)
+  mask = fwn.khop_mask(directed, 2)[perm][:, perm]
+  want = fwn.build_tile_mask(mask.T.tocsr())
+  assert model.tiles_t.n_tiles == len(want[1])
+  np.testing.assert_array_equal(model.tiles_t.col.numpy(), want[1])
+  np.testing.assert_array_equal(model.perm.numpy(), perm)
+  assert fwn.MeshTransformer(adjacency=sym, latlon=(lat, lon), reorder=True, **kw).tiles_t is None
+  assert fwn.MeshTransformer(refinement=2, reorder=False, **kw).tiles_t is None
 
 
 def test_public_op_refuses_cpu_tensors():

@@ -42,19 +42,42 @@ def _rel_rms(a, b):
   return float((a - b).square().mean().sqrt() / b.std())
 
 
-@pytest.mark.parametrize("reorder", [True, False])
-def test_mesh_transformer_matches_plain_torch(reorder):
-  print(f"mesh transformer reorder={reorder}", flush=True)
+def _directed_adjacency(refinement, seed):
+  """The mesh adjacency with 30% of its directed edges dropped: not symmetric."""
+  from scipy import sparse
+  v, f, lat, lon = fwn.icosahedral_mesh(refinement)
+  coo = fwn.adjacency(f, len(v)).tocoo()
+  keep = np.random.default_rng(seed).random(coo.nnz) < 0.7
+  adj = sparse.csr_matrix((np.ones(int(keep.sum()), bool), (coo.row[keep], coo.col[keep])), shape=(len(v), len(v)))
+  return adj, lat, lon
+
+
+@pytest.mark.parametrize("case", ["hilbert", "subdivision", "directed"])
+def test_mesh_transformer_matches_plain_torch(case):
+  """"directed" builds the model from a non-symmetric adjacency: its mask is not symmetric, so the
+  backward walks the transposed tile list the model builds (patch.py:215-218)."""
+  print(f"mesh transformer {case}", flush=True)
+  reorder = case != "subdivision"
   torch.manual_seed(0)
-  model = fwn.MeshTransformer(refinement=3, k_hop=2, num_layers=3, d_model=64, num_heads=2, key_size=32,
-                              ffw_hidden=128, cond_size=8, reorder=reorder, device=DEV, dtype=torch.float32)
+  kw = dict(refinement=3, k_hop=2, num_layers=3, d_model=64, num_heads=2, key_size=32, ffw_hidden=128, cond_size=8,
+            reorder=reorder, device=DEV, dtype=torch.float32)
+  if case == "directed":
+    adj, lat, lon = _directed_adjacency(3, 1)
+    model = fwn.MeshTransformer(adjacency=adj, latlon=(lat, lon), **kw)
+    assert model.tiles_t is not None
+  else:
+    model = fwn.MeshTransformer(**kw)
   with torch.no_grad():  # the conditioning starts at zero; give it weights so it is exercised
     for mod in model.modules():
       if isinstance(mod, fwn.transformer.NormConditioning):
         mod.linear.weight.normal_(0, 0.1)
         mod.linear.bias.normal_(0, 0.1)
-  mask, lat, lon, perm = fwn.mesh_mask(3, 2, reorder=reorder)
+  if case == "directed":
+    mask, perm = fwn.khop_mask(adj, 2), fwn.hilbert_order(lat, lon)
+  else:
+    mask, lat, lon, perm = fwn.mesh_mask(3, 2, reorder=reorder)
   dense = (mask[perm][:, perm] if perm is not None else mask).toarray()
+  assert (case == "directed") == bool((dense != dense.T).any())
   n = mask.shape[0]
   x = torch.randn(2, n, 64, device=DEV, requires_grad=True)
   cond = torch.randn(2, 8, device=DEV)
