@@ -39,6 +39,27 @@ __device__ __forceinline__ int swz(int row) {
   }
 }
 
+// The swizzle of the 16-key dK/dV kernel's Q and dO tiles. Its reads are 16-row b128 reads (16
+// consecutive rows, one logical chunk) and transpose reads whose 32 lanes cover 8 consecutive rows
+// x 32 bytes (a chunk pair). The chunk XOR s(row) is a bijection of row bits 0-3 (conflict-free
+// row reads), and s >> 1 takes 8 distinct values, or 8 distinct (row-in-bank-line, s >> 1) pairs
+// when a 256-byte bank line holds 2 or 4 rows, over any 8 aligned rows (conflict-free transpose
+// reads). Depends on the row's low 4 bits only.
+template <int C>
+__device__ __forceinline__ int swz16(int row) {
+  constexpr int sh = C >= 16 ? 0 : (C == 8 ? 1 : 2);
+  return (((row & 7) >> sh) << 1) | ((row >> 3) & 1);
+}
+
+template <int C, bool K16>
+__device__ __forceinline__ int tile_swz(int row) {
+  if constexpr (K16) {
+    return swz16<C>(row);
+  } else {
+    return swz<C>(row);
+  }
+}
+
 template <int D>
 struct Tile {
   static constexpr int C = D / 8;                     // 16-byte chunks per row
@@ -51,7 +72,7 @@ struct Tile {
 // Instruction (op, w) fills physical chunks [(4*op + w) * 64, +64): lane l the chunk at row
 // (4*op + w) * ROWS_PER_OP + l / C, physical column l % C, which holds logical column
 // (l % C) ^ swz(row). The swizzle depends on row % 16, which is the same for every op.
-template <int D>
+template <int D, bool K16 = false>
 struct TileDma {
   static constexpr int C = Tile<D>::C;
   static constexpr int RPO = Tile<D>::ROWS_PER_OP;
@@ -59,7 +80,7 @@ struct TileDma {
 
   __device__ __forceinline__ void init(int w, int lane, uint32_t snb) {
     const int row = w * RPO + lane / C;
-    voff = (uint32_t)row * snb + (uint32_t)((((lane % C) ^ swz<C>(row))) << 4);
+    voff = (uint32_t)row * snb + (uint32_t)((((lane % C) ^ tile_swz<C, K16>(row))) << 4);
   }
 
   // Copies the rows of the tile's 32-row groups in `live` (bit c: rows 32c..32c+31, a
@@ -396,69 +417,103 @@ __global__ void __launch_bounds__(NT, 2) dq_kernel(KArgs a) {
   store_acc_bf16<D>(make_rsrc((uint16_t*)a.out0 + j.base, a.slice_bytes), qrow, snb, acc, a.scale, g);
 }
 
+constexpr int NT8 = 512;  // dK/dV workgroup: 8 waves
+
 // ------------------------------------------------------------------------------------------
-// dK/dV: per work item of the transposed tile list; each workgroup owns its dK/dV rows, so there
-// are no atomics (pallas_attn.py:187-215). The tile's 128 log-sum-exps and deltas are copied next
-// to its Q and dO tiles; the log-sum-exps are rescaled to the log2 domain once per tile in LDS.
+// dK/dV with 16 keys per wave: per work item of the transposed tile list, 8 waves each own 16 keys
+// of the block and compute, for every 32-query group of a tile in which those 16 keys have a
+// valid element, S = Q K^T, P = exp2(S c2 - lse log2 e) (masked), dP - delta = dO V^T - delta,
+// dS = P (dP - delta), dV^T += dO^T P and dK^T += Q^T dS (pallas_attn.py:187-215), on
+// V_MFMA_F32_16X16X32_BF16. Each workgroup owns its dK/dV rows: no atomics. The waves share only
+// the Q/dO tile copies (double-buffered) and meet once per tile; they hand nothing over, and each
+// skips the query groups its own 16 keys have no valid element in.
 //
-// The work is split by role over 8 waves. Waves w and w + 4 share one SIMD and own the same 32
-// keys. Wave w (the P wave) holds the K fragment and computes S^T = K Q^T and P, hands P over
-// to wave w + 4 through LDS and accumulates the first half of dV's columns. Wave w + 4 holds the
-// V fragment and computes dP^T = V dO^T, dS = P (dP - delta), dK += dS^T Q and the second half
-// of dV's columns (all of them at D = 32). Splitting dV moves MFMAs off the P wave, whose
-// exponentials otherwise keep the other wave waiting at every hand-over.
-constexpr int NT8 = 512;
-constexpr int PSLOT = 2048;  // one P slot: 32 keys x 32 queries bf16
+// Register layout. S and dP are computed query-major (M = 16 queries, N = the wave's 16 keys,
+// K = head_dim): lane l holds queries 4(l/16) + r (r < 4) of each 16-query half m and key
+// l % 16. The contraction over queries then takes the lane's 8 values (m = 0, 1) as the 8
+// consecutive K elements of its lane group, provided the other operand's K order is the same
+// (queries 4g..4g+3 then 16+4g..16+4g+3): the transpose reads (ds_read_b64_tr_b16) give exactly
+// that from two 4-row reads. P and dS therefore stay in registers. dV and dK accumulate
+// transposed (M = 16 columns d, N = the 16 keys), so each lane ends up holding 4 consecutive
+// columns of its own key per 16-column block, stored as one 8- or 16-byte write.
+//
+// The mask bits come from the tile list's per-lane words (fwn_tiles_prepare): the 32-row wave W
+// = wid / 2 word of lane 32(g / 2) + 16(wid % 2) + l % 16, shifted right by 4(g % 2), holds
+// element (query group c, half m, r) at bit 16c + 8m + r.
+__device__ __forceinline__ f32x4 mfma16(const u32x4& a, const u32x4& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                 0, 0, 0);
+}
+
+__device__ __forceinline__ u32x4 pack8_bf16(const float (&x)[8]) {
+  bf16x8 r;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) r[e] = (__bf16)x[e];
+  return __builtin_bit_cast(u32x4, r);
+}
 
 template <int D>
-__global__ void __launch_bounds__(NT8, 1) dkv_kernel(KArgs a) {
+__global__ void __launch_bounds__(NT8, 1) dkv16_kernel(KArgs a) {
   constexpr int TB = Tile<D>::BYTES;
-  constexpr int NB = D / 32;     // 32-column blocks of dK and dV
-  constexpr int NV0 = NB / 2;    // dV blocks of the P wave (none at D = 32)
-  constexpr int NV1 = NB - NV0;  // dV blocks of the dK wave
+  constexpr int C = Tile<D>::C;
+  constexpr int KS = D / 32;  // K steps of the S and dP contractions
+  constexpr int NB = D / 16;  // 16-column blocks of dK^T and dV^T
+  constexpr int RS = 2 * D;   // bytes per tile row
   __shared__ __attribute__((aligned(1024))) char lds0[2 * TB + 1536];  // Q | dO | lse[128] | gap | delta[128]
   __shared__ __attribute__((aligned(1024))) char lds1[2 * TB + 1536];
-  __shared__ __attribute__((aligned(1024))) char lp[4 * 2 * PSLOT];  // 2 P slots per key sub-block
-  lds_char* bufs[2] = {(lds_char*)lds0, (lds_char*)lds1};
   const int tid = threadIdx.x, lane = tid & 63;
-  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int w = wid & 3;        // key sub-block
-  const bool kw = wid >= 4;     // dK wave (else P wave)
-  const int i = lane & 31, g = lane >> 5;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // keys 16 wid .. 16 wid + 15 of the block
+  const int g = lane >> 4, t16 = lane & 15;
   const Job j = decode_job(a);
-  const uint32_t snb = (uint32_t)a.sn * 2;
+  const uint32_t snb = (uint32_t)a.sn * 2, osnb = (uint32_t)a.osn * 2;
   const rsrc_t rQ = make_rsrc((const uint16_t*)a.q + j.base, a.slice_bytes);
   const rsrc_t rO = make_rsrc((const uint16_t*)a.dout + j.obase, a.oslice_bytes);
-  const uint32_t osnb = (uint32_t)a.osn * 2;
   const rsrc_t rL = make_rsrc(a.lse + stat_index(a, j, 0), (uint32_t)a.n * 4);
   const rsrc_t rD = make_rsrc(a.delta + stat_index(a, j, 0), (uint32_t)a.n * 4);
 
-  const int krow = j.blk * BLK + 32 * w + i;  // this lane's key
-  u32x4 frag[D / 16];                          // K (P waves) or V (dK waves)
-  load_frag<D>(frag, make_rsrc((const uint16_t*)(kw ? a.v : a.k) + j.base, a.slice_bytes), krow, snb, g);
-  Off<D> off;
-  off.init(lane);
-  TileDma<D> dma, dmaO;  // Q and dO tiles (their row strides may differ)
-  dma.init(w, lane, snb);
-  dmaO.init(w, lane, osnb);
-  f32x16 acc[NB];    // dK (dK waves) or dV blocks 0 .. NV0 - 1 (P waves)
-  f32x16 accv[NV1];  // dV blocks NV0 .. NB - 1 (dK waves)
+  // K and V fragments (B operands of S and dP): key krow, columns 32 s + 8 g .. +7.
+  const int krow = j.blk * BLK + 16 * wid + t16;
+  u32x4 kf[KS], vf[KS];
+  {
+    const rsrc_t rK = make_rsrc((const uint16_t*)a.k + j.base, a.slice_bytes);
+    const rsrc_t rV = make_rsrc((const uint16_t*)a.v + j.base, a.slice_bytes);
 #pragma unroll
-  for (int db = 0; db < NB; ++db) acc[db] = zero16();
+    for (int s = 0; s < KS; ++s) {
+      kf[s] = bload16(rK, (uint32_t)krow * snb + (uint32_t)(64 * s + 16 * g));
+      vf[s] = bload16(rV, (uint32_t)krow * snb + (uint32_t)(64 * s + 16 * g));
+    }
+  }
+  // LDS byte offsets within a tile, for query group 0 (group c adds 32 c rows).
+  //   roff[s]: b128 row read of query row t16 (+16 m), columns 32 s + 8 g .. +7;
+  //   toff[n]: transpose read, lane 4e + q of group g: row 4g + e (+16 h), columns 16 n + 4 q ..
+  uint32_t roff[KS], toff[NB];
+  {
+    const int sr = swz16<C>(t16);
 #pragma unroll
-  for (int db = 0; db < NV1; ++db) accv[db] = zero16();
-  // A P slot holds the two 8-element halves of every lane, each half 64 lanes x 16 bytes
-  // contiguous, so the slot's b128 writes and reads are free of bank conflicts.
-  lds_char* pslot = (lds_char*)lp + w * 2 * PSLOT + lane * 16;
+    for (int s = 0; s < KS; ++s) roff[s] = (uint32_t)(t16 * RS + (((4 * s + g) ^ sr) << 4));
+    const int e = t16 >> 2, q = t16 & 3, trow = 4 * g + e, st = swz16<C>(trow);
+#pragma unroll
+    for (int n = 0; n < NB; ++n) toff[n] = (uint32_t)(trow * RS + (((2 * n + (q >> 1)) ^ st) << 4) + (q & 1) * 8);
+  }
+  f32x4 dk[NB], dv[NB];
+#pragma unroll
+  for (int n = 0; n < NB; ++n) {
+    dk[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+    dv[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
 
-  int t0, t1;
-  tile_range(a, j, t0, t1);
+  // Tile copies: waves 0-3 copy Q, waves 4-7 dO, wave 0 also the tile's 128 lse and delta (two
+  // branch-free full-wave copies; out-of-range halves read zeros into the gap).
+  TileDma<D, true> dma;
+  dma.init(wid & 3, lane, wid < 4 ? snb : osnb);
   constexpr uint32_t kPastEnd = 0x7FFFFFF0u;
-  // The P waves copy the tiles, their statistics and their mask bits.
   auto issue = [&](int t, lds_char* buf, uint32_t copy) {
     const int qb = ((ci32_ptr)a.col)[t];
-    dma.issue(rQ, buf, w, qb * BLK, snb, copy);
-    dmaO.issue(rO, buf + TB, w, qb * BLK, osnb, copy);
+    if (wid < 4) {
+      dma.issue(rQ, buf, wid, qb * BLK, snb, copy);
+    } else {
+      dma.issue(rO, buf + TB, wid - 4, qb * BLK, osnb, copy);
+    }
     if (wid == 0) {
       const uint32_t vo = (uint32_t)(qb * BLK + 4 * (lane & 31)) * 4;
       lds_char* stats = buf + 2 * TB;
@@ -468,231 +523,134 @@ __global__ void __launch_bounds__(NT8, 1) dkv_kernel(KArgs a) {
                                                (int)(lane < 32 ? kPastEnd : vo), 0, 0, 0);
     }
   };
-  auto stats4 = [&](const lds_char* cur, int off_bytes, int sb, f32x4 (&x)[4]) {
-    const __attribute__((address_space(3))) float* p =
-        (const __attribute__((address_space(3))) float*)(cur + 2 * TB + off_bytes);
+  // This lane's mask word of tile t (see above), loaded a tile ahead.
+  const uint64_t* mword = a.lanes + (int64_t)(wid >> 1) * 64 + 32 * (g >> 1) + 16 * (wid & 1) + t16;
+  const int mshift = 4 * (g & 1);
+
+  // One 16-key x 32-query unit: query group c of the tile in buffer `cur`.
+  auto unit = [&](const lds_char* cur, int c, uint64_t mw, bool full) {
+    const lds_char* Q = cur;
+    const lds_char* O = cur + TB;
+    const lds_char* st = cur + 2 * TB;
+    typedef const __attribute__((address_space(3))) f32x4* cf4;
+    // Accumulators start at -lse / scale and -delta of the element's query (the stats are
+    // rescaled in LDS once per tile), so S c2 = s c2 - lse log2 e and dP holds dP - delta.
+    f32x4 s0 = *(cf4)(st + 4 * (32 * c + 4 * g)), s1 = *(cf4)(st + 4 * (32 * c + 16 + 4 * g));
+    f32x4 d0 = *(cf4)(st + 1024 + 4 * (32 * c + 4 * g)), d1 = *(cf4)(st + 1024 + 4 * (32 * c + 16 + 4 * g));
+    const uint32_t cb = (uint32_t)(32 * c * RS);
 #pragma unroll
-    for (int c = 0; c < 2; ++c)
+    for (int s = 0; s < KS; ++s) {
+      s0 = mfma16(row_read(Q, roff[s] + cb), kf[s], s0);
+      s1 = mfma16(row_read(Q, roff[s] + cb + 16 * RS), kf[s], s1);
+    }
 #pragma unroll
-      for (int hh = 0; hh < 2; ++hh)
-        x[2 * c + hh] = *(const __attribute__((address_space(3))) f32x4*)(p + 32 * sb + 16 * c + 8 * g + 4 * hh);
+    for (int s = 0; s < KS; ++s) {
+      d0 = mfma16(row_read(O, roff[s] + cb), vf[s], d0);
+      d1 = mfma16(row_read(O, roff[s] + cb + 16 * RS), vf[s], d1);
+    }
+    float p[8], ds[8];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      p[r] = fast_exp2(s0[r] * a.c2);
+      p[4 + r] = fast_exp2(s1[r] * a.c2);
+    }
+    if (!full) {
+      const uint32_t w32 = (uint32_t)(mw >> (32 * (c >> 1)));
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        p[i] = keep_or_zero(p[i], __builtin_amdgcn_sbfe(w32, (uint32_t)(16 * (c & 1) + 8 * (i >> 2) + (i & 3)), 1u));
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      ds[r] = p[r] * d0[r];
+      ds[4 + r] = p[4 + r] * d1[r];
+    }
+    const u32x4 pb = pack8_bf16(p), db = pack8_bf16(ds);
+#pragma unroll
+    for (int n = 0; n < NB; ++n) {
+      const u32x2 o_lo = tr_read(O, toff[n] + cb), o_hi = tr_read(O, toff[n] + cb + 16 * RS);
+      dv[n] = mfma16(u32x4{o_lo[0], o_lo[1], o_hi[0], o_hi[1]}, pb, dv[n]);
+      const u32x2 q_lo = tr_read(Q, toff[n] + cb), q_hi = tr_read(Q, toff[n] + cb + 16 * RS);
+      dk[n] = mfma16(u32x4{q_lo[0], q_lo[1], q_hi[0], q_hi[1]}, db, dk[n]);
+    }
   };
-  // Query groups (32 queries) of a tile with no valid element for any of the 4 key groups are
-  // skipped by every wave and not copied (they would add p = 0); the others cost one barrier each,
-  // so per tile each wave passes 1 + (number of live query groups) barriers. A dK wave also skips
-  // the live groups in which its own 32 keys have no valid element (its P is zero there). The P
-  // waves compute every live group: the barriers pace all 8 waves, so a skip there would only
-  // move the wait to another wave. Group bits are loaded a tile ahead of their use (two tiles
-  // ahead of the copy for P waves).
-  u32x2 mbits = {0u, 0u};
-  uint32_t gcur = 0u, gnext = 0u;  // group bits of the current and (P waves) the next tile
-  if (t0 < t1) gcur = tile_groups(a, t0);
-  if (t0 < t1 && !kw) {
-    mbits = tile_bits(a, t0, w, lane);
-    if (t0 + 1 < t1) gnext = tile_groups(a, t0 + 1);
-    issue(t0, bufs[0], 15u);
-  }
-  auto pv_step = [&](int tt, lds_char* cur, lds_char* nxt) {
+
+  auto tile_step = [&](int tt, int t1, lds_char* cur, lds_char* nxt, uint64_t& mnext, uint32_t& gnext) {
     const int t = __builtin_amdgcn_readfirstlane(tt);
-    wait_vmem();
-    const u32x2 mb = mbits;
+    wait_vmem();  // this wave's part of tile t and its mask word
+    const uint64_t mw = mnext >> mshift;
     if (wid == 0) {
-      // lse -> -lse / scale and delta -> -delta, the initial values of the S^T and dP^T
-      // accumulators: (s - lse / scale) * c2 = s * c2 - lse * log2(e), and dP - delta.
+      // lse -> -lse / scale and delta -> -delta, the initial values of the S and dP accumulators.
       __attribute__((address_space(3))) f32x4* x =
           (__attribute__((address_space(3))) f32x4*)(cur + 2 * TB + (lane < 32 ? 0 : 512) + 16 * lane);
       float m = lane < 32 ? a.nlse_mul : -1.f;
-      asm volatile("" : "+v"(m));  // computed here: hoisted, the compiler keeps it as spilled vectors
+      asm volatile("" : "+v"(m));
       *x = *x * m;
     }
     __syncthreads();  // tile t is in LDS; every wave is done with tile t - 1 (buffer nxt)
-    const uint32_t any = any_rows(gcur);
     if (t + 1 < t1) {
-      mbits = tile_bits(a, t + 1, w, lane);
+      mnext = mword[(int64_t)(t + 1) * 256];
       issue(t + 1, nxt, any_rows(gnext));
     }
-    gcur = gnext;
     if (t + 2 < t1) gnext = tile_groups(a, t + 2);
-    const lds_char* Q = cur;
-    const lds_char* O = cur + TB;
-    // S^T of query group sb, started at -lse / scale of the element's query.
-    auto s_chain = [&](int sb) {
-      u32x4 qa[D / 16];
+    // Query groups in which this wave's 16 keys have a valid element (a wave-uniform set), and
+    // those in which every one of the 512 elements is valid (no mask needed).
+    uint32_t live = 0u, full = 0u;
 #pragma unroll
-      for (int k = 0; k < D / 16; ++k) qa[k] = row_read(Q, off.row[k] + sb * 32 * (2 * D));
-      f32x4 lr[4];
-      stats4(cur, 0, sb, lr);
-      f32x16 sv;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) sv[r] = lr[r >> 2][r & 3];
-#pragma unroll
-      for (int k = 0; k < D / 16; ++k) sv = mfma_bf16(qa[k], frag[k], sv);
-      return sv;
-    };
-    // P = exp2(S c2) (masked), packed to bf16 and written to LDS slot `slot` for the dK wave.
-    auto finish_p = [&](f32x16& sv, int sb, int slot, bf16x8& p0, bf16x8& p1) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) sv[r] = keep_or_zero(fast_exp2(sv[r] * a.c2), elem_keep(mb, sb, r));
-      p0 = pack_bf16(sv, 0);
-      p1 = pack_bf16(sv, 1);
-      lds_char* ps = pslot + slot * PSLOT;
-      *(__attribute__((address_space(3))) bf16x8*)ps = p0;
-      *(__attribute__((address_space(3))) bf16x8*)(ps + 1024) = p1;
-    };
-    // P runs one live query group ahead. Between two barriers this wave computes S(next), then
-    // issues its dV(sb) MFMAs one at a time between slices of next's exponentials, so that the
-    // VALU work runs while the MFMA pipe is busy; the dK wave meanwhile issues dK(sb), its dV(sb)
-    // and dP(next). P(sb) goes to slot (its rank in `any`) & 1.
-    bf16x8 pc0, pc1;
-    if (any != 0u) {
-      const int sb0 = __builtin_ctz(any);
-      f32x16 sv = s_chain(sb0);
-      finish_p(sv, sb0, 0, pc0, pc1);
+    for (int c = 0; c < 4; ++c) {
+      const uint32_t b8 = (uint32_t)(mw >> (16 * c)) & 0x0F0Fu;
+      if (__builtin_amdgcn_ballot_w64(b8 != 0u) != 0u) live |= 1u << c;
+      if (__builtin_amdgcn_ballot_w64(b8 != 0x0F0Fu) == 0u) full |= 1u << c;
     }
-    int rank = 0;
 #pragma unroll
-    for (int sb = 0; sb < 4; ++sb) {
-      if (!(any >> sb & 1u)) continue;
-      lds_barrier();  // P(sb) is in LDS for the dK wave
-      ++rank;
-      const uint32_t later = sb < 3 ? any & (0xeu << sb) : 0u;
-      u32x4 ot[NV0 > 0 ? NV0 : 1][2];
-      if (later != 0u) {
-        const int nsb = __builtin_ctz(later);
-        f32x16 sv = s_chain(nsb);
-#pragma unroll
-        for (int db = 0; db < NV0; ++db)
-#pragma unroll
-          for (int c = 0; c < 2; ++c) ot[db][c] = tr_operand<D>(O, off, db, sb, c);
-        // Order: the Q and stats reads; the S chain with the dO^T reads between its MFMAs
-        // (they take the registers the Q operands free); then the dV MFMAs with slices of the
-        // exponential work between them; the P slot writes.
-        __builtin_amdgcn_sched_group_barrier(0x100, D / 16 + 4, 0);
-#pragma unroll
-        for (int m = 0; m < D / 16; ++m) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          if (m < 4 * NV0) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        bf16x8 pn0, pn1;
-#pragma unroll
-        for (int db = 0; db < NV0; ++db) {
-          acc[db] = mfma_bf16(ot[db][0], pc0, acc[db]);
-          acc[db] = mfma_bf16(ot[db][1], pc1, acc[db]);
-        }
-        finish_p(sv, nsb, rank & 1, pn0, pn1);
-        if constexpr (NV0 > 0) {
-#pragma unroll
-          for (int m = 0; m < 2 * NV0; ++m) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
-            __builtin_amdgcn_sched_group_barrier(0x002, 80 / (2 * NV0), 1);
-          }
-          __builtin_amdgcn_sched_group_barrier(0x200, 2, 1);
-        }
-        pc0 = pn0;
-        pc1 = pn1;
-      } else {
-#pragma unroll
-        for (int db = 0; db < NV0; ++db)
-#pragma unroll
-          for (int c = 0; c < 2; ++c) ot[db][c] = tr_operand<D>(O, off, db, sb, c);
-#pragma unroll
-        for (int db = 0; db < NV0; ++db) {
-          acc[db] = mfma_bf16(ot[db][0], pc0, acc[db]);
-          acc[db] = mfma_bf16(ot[db][1], pc1, acc[db]);
-        }
-      }
-    }
+    for (int c = 0; c < 4; ++c)
+      if (live >> c & 1u) unit(cur, c, mw, full >> c & 1u);
   };
-  auto dk_step = [&](int tt, lds_char* cur) {
-    __syncthreads();
-    const uint32_t any = any_rows(gcur), own = gcur >> (4 * w) & 15u;
-    if (tt + 1 < t1) gcur = tile_groups(a, tt + 1);
-    const lds_char* Q = cur;
-    const lds_char* O = cur + TB;
-    int rank = 0;
-#pragma unroll
-    for (int sb = 0; sb < 4; ++sb) {
-      if (!(any >> sb & 1u)) continue;
-      const bool mine = own >> sb & 1u;
-      f32x16 dp;
-      u32x4 qt[NB][2];
-      if (mine) {
-        u32x4 oa[D / 16];
-#pragma unroll
-        for (int k = 0; k < D / 16; ++k) oa[k] = row_read(O, off.row[k] + sb * 32 * (2 * D));
-        f32x4 dr[4];
-        stats4(cur, 1024, sb, dr);
-#pragma unroll
-        for (int r = 0; r < 16; ++r) dp[r] = dr[r >> 2][r & 3];  // -delta of the element's query
-#pragma unroll
-        for (int k = 0; k < D / 16; ++k) dp = mfma_bf16(oa[k], frag[k], dp);
-#pragma unroll
-        for (int db = 0; db < NB; ++db)
-#pragma unroll
-          for (int c = 0; c < 2; ++c) qt[db][c] = tr_operand<D>(Q, off, db, sb, c);
-      }
-      lds_barrier();  // P(sb) written by the P wave
-      if (mine) {
-        const lds_char* ps = pslot + (rank & 1) * PSLOT;
-        const u32x4 pw0 = *(const __attribute__((address_space(3))) u32x4*)ps;
-        const u32x4 pw1 = *(const __attribute__((address_space(3))) u32x4*)(ps + 1024);
-        u32x4 ot[NV1][2];
-#pragma unroll
-        for (int db = 0; db < NV1; ++db)
-#pragma unroll
-          for (int c = 0; c < 2; ++c) ot[db][c] = tr_operand<D>(O, off, NV0 + db, sb, c);
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const uint32_t word = (r < 8 ? pw0 : pw1)[(r & 7) >> 1];
-          const float p = __builtin_bit_cast(float, (r & 1) ? (word & 0xffff0000u) : (word << 16));
-          dp[r] = p * dp[r];
-        }
-        const bf16x8 d0 = pack_bf16(dp, 0), d1 = pack_bf16(dp, 1);
-#pragma unroll
-        for (int db = 0; db < NB; ++db) {
-          acc[db] = mfma_bf16(qt[db][0], d0, acc[db]);
-          acc[db] = mfma_bf16(qt[db][1], d1, acc[db]);
-        }
-        const bf16x8 p0 = __builtin_bit_cast(bf16x8, pw0), p1 = __builtin_bit_cast(bf16x8, pw1);
-#pragma unroll
-        for (int db = 0; db < NV1; ++db) {
-          accv[db] = mfma_bf16(ot[db][0], p0, accv[db]);
-          accv[db] = mfma_bf16(ot[db][1], p1, accv[db]);
-        }
-      }
-      ++rank;
-    }
-  };
-  if (!kw) {
-    for (int tt = t0; tt < t1; tt += 2) {
-      pv_step(tt, bufs[0], bufs[1]);
-      if (tt + 1 < t1) pv_step(tt + 1, bufs[1], bufs[0]);
-    }
-  } else {
-    for (int tt = t0; tt < t1; tt += 2) {
-      dk_step(tt, bufs[0]);
-      if (tt + 1 < t1) dk_step(tt + 1, bufs[1]);
-    }
+
+  int t0, t1;
+  tile_range(a, j, t0, t1);
+  uint64_t mnext = 0;
+  uint32_t gnext = 0u;
+  lds_char* b0 = (lds_char*)lds0;
+  lds_char* b1 = (lds_char*)lds1;
+  if (t0 < t1) {
+    mnext = mword[(int64_t)t0 * 256];
+    if (t0 + 1 < t1) gnext = tile_groups(a, t0 + 1);
+    issue(t0, b0, any_rows(tile_groups(a, t0)));
   }
-  const rsrc_t rV = make_rsrc((uint16_t*)a.out1 + j.base, a.slice_bytes);
-  if (kw) {
-    if (j.part >= 0) {
-      store_bwd_partial<D>(a, j, 32 * w + i, acc, 0, g);
-      store_bwd_partial<D, NV1>(a, j, 32 * w + i, accv, 1, g, NV0);
-      return;
-    }
-    store_acc_bf16<D>(make_rsrc((uint16_t*)a.out0 + j.base, a.slice_bytes), krow, snb, acc, a.scale, g);
-    store_acc_bf16<D, NV1>(rV, krow, snb, accv, 1.f, g, NV0);
-  } else if constexpr (NV0 > 0) {
-    f32x16 dv[NV0];
+  for (int tt = t0; tt < t1; tt += 2) {
+    tile_step(tt, t1, b0, b1, mnext, gnext);
+    if (tt + 1 < t1) tile_step(tt + 1, t1, b1, b0, mnext, gnext);
+  }
+
+  // dK^T / dV^T block n: lane l holds columns 16 n + 4 g .. +3 of key krow.
+  if (j.part >= 0) {
+    const rsrc_t r = part_slot<D>(a, j);
+    const int row = 16 * wid + t16;
 #pragma unroll
-    for (int db = 0; db < NV0; ++db) dv[db] = acc[db];
-    if (j.part >= 0) {
-      store_bwd_partial<D, NV0>(a, j, 32 * w + i, dv, 1, g, 0);
-      return;
+    for (int n = 0; n < NB; ++n) {
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, dk[n]), r,
+                                             (int)((uint32_t)(row * D + 16 * n + 4 * g) * 4), 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, dv[n]), r,
+                                             (int)((uint32_t)((128 + row) * D + 16 * n + 4 * g) * 4), 0, 0);
     }
-    store_acc_bf16<D, NV0>(rV, krow, snb, dv, 1.f, g, 0);
+    return;
+  }
+  const rsrc_t rdk = make_rsrc((uint16_t*)a.out0 + j.base, a.slice_bytes);
+  const rsrc_t rdv = make_rsrc((uint16_t*)a.out1 + j.base, a.slice_bytes);
+#pragma unroll
+  for (int n = 0; n < NB; ++n) {
+    u32x2 wk, wv;
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2) {
+      const __bf16 k0 = (__bf16)(dk[n][2 * h2] * a.scale), k1 = (__bf16)(dk[n][2 * h2 + 1] * a.scale);
+      const __bf16 v0 = (__bf16)dv[n][2 * h2], v1 = (__bf16)dv[n][2 * h2 + 1];
+      wk[h2] = (uint32_t)__builtin_bit_cast(uint16_t, k0) | ((uint32_t)__builtin_bit_cast(uint16_t, k1) << 16);
+      wv[h2] = (uint32_t)__builtin_bit_cast(uint16_t, v0) | ((uint32_t)__builtin_bit_cast(uint16_t, v1) << 16);
+    }
+    const uint32_t off = (uint32_t)krow * snb + (uint32_t)(2 * (16 * n + 4 * g));
+    __builtin_amdgcn_raw_buffer_store_b64(wk, rdk, (int)off, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b64(wv, rdv, (int)off, 0, 0);
   }
 }
 
@@ -702,7 +660,7 @@ hipError_t launch_d(Kind kind, const KArgs& a, hipStream_t stream) {
   switch (kind) {
     case Kind::kFwd: hipLaunchKernelGGL(fwd_kernel<D>, grid, block, 0, stream, a); break;
     case Kind::kDq: hipLaunchKernelGGL(dq_kernel<D>, grid, block, 0, stream, a); break;
-    case Kind::kDkv: hipLaunchKernelGGL(dkv_kernel<D>, grid, dim3(NT8), 0, stream, a); break;
+    case Kind::kDkv: hipLaunchKernelGGL(dkv16_kernel<D>, grid, dim3(NT8), 0, stream, a); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

@@ -81,7 +81,7 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 // __syncthreads() waits for every outstanding global load as well; this one waits for the
 // wave's LDS operations, plus any global load that writes LDS (a tile copy still in flight)
 // where the compiler sees one outstanding. A barrier that never waits for copies (inline
-// s_waitcnt lgkmcnt(0); s_barrier) measured 2% slower in dkv_kernel.
+// s_waitcnt lgkmcnt(0); s_barrier) measured 2% slower in an earlier dK/dV kernel.
 __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
   __builtin_amdgcn_s_barrier();
