@@ -39,16 +39,18 @@ __device__ __forceinline__ int swz(int row) {
   }
 }
 
-// The swizzle of the 16-key dK/dV kernel's Q and dO tiles. Its reads are 16-row b128 reads (16
-// consecutive rows, one logical chunk) and transpose reads whose 32 lanes cover 8 consecutive rows
-// x 32 bytes (a chunk pair). The chunk XOR s(row) is a bijection of row bits 0-3 (conflict-free
-// row reads), and s >> 1 takes 8 distinct values, or 8 distinct (row-in-bank-line, s >> 1) pairs
-// when a 256-byte bank line holds 2 or 4 rows, over any 8 aligned rows (conflict-free transpose
-// reads). Depends on the row's low 4 bits only.
+// The swizzle of the 16-key dK/dV kernel's Q and dO tiles. gfx950 serves a ds_read_b128 in four
+// 16-lane groups {l, l + 32 : l in [8k, 8k + 8)} and a ds_read_b64_tr_b16 in two 32-lane halves
+// (measured with bank-conflict counters). In this kernel's row reads, each b128 group covers 8
+// aligned rows at two logical chunks x and x ^ 2; in its transpose reads, each half covers 8
+// aligned rows x one chunk pair (32 bytes). Over any 8 aligned rows, s(row) must therefore keep
+// bits {0, 2, 3} distinct (row reads) and bits {1, 2, 3} distinct (transpose reads), per row
+// position within a 256-byte bank line when a line holds 2 or 4 rows: s = (hi << 2) | 3 lo, with
+// lo one row bit and hi the row bits above it. Depends on the row's low 3 bits only.
 template <int C>
 __device__ __forceinline__ int swz16(int row) {
   constexpr int sh = C >= 16 ? 0 : (C == 8 ? 1 : 2);
-  return (((row & 7) >> sh) << 1) | ((row >> 3) & 1);
+  return (((row & 7) >> (sh + 1)) << 2) | (((row >> sh) & 1) * 3);
 }
 
 template <int C, bool K16>
@@ -527,32 +529,55 @@ __global__ void __launch_bounds__(NT8, 1) dkv16_kernel(KArgs a) {
   const uint64_t* mword = a.lanes + (int64_t)(wid >> 1) * 64 + 32 * (g >> 1) + 16 * (wid & 1) + t16;
   const int mshift = 4 * (g & 1);
 
-  // One 16-key x 32-query unit: query group c of the tile in buffer `cur`.
+  // One 16-key x 32-query unit: query group c of the tile in buffer `cur`. The reads of each
+  // phase are all issued before its MFMAs (the phases are fenced against the scheduler), so an
+  // MFMA waits for the LDS latency once per phase rather than once per operand: the row reads,
+  // then the S and dP MFMAs; the transpose reads, in flight while the exponentials and dS run;
+  // then the dV and dK MFMAs.
   auto unit = [&](const lds_char* cur, int c, uint64_t mw, bool full) {
     const lds_char* Q = cur;
     const lds_char* O = cur + TB;
     const lds_char* st = cur + 2 * TB;
     typedef const __attribute__((address_space(3))) f32x4* cf4;
+    const uint32_t cb = (uint32_t)(32 * c * RS);
+    u32x4 qa[2][KS], oa[2][KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        qa[m][s] = row_read(Q, roff[s] + cb + 16 * m * RS);
+        oa[m][s] = row_read(O, roff[s] + cb + 16 * m * RS);
+      }
     // Accumulators start at -lse / scale and -delta of the element's query (the stats are
     // rescaled in LDS once per tile), so S c2 = s c2 - lse log2 e and dP holds dP - delta.
-    f32x4 s0 = *(cf4)(st + 4 * (32 * c + 4 * g)), s1 = *(cf4)(st + 4 * (32 * c + 16 + 4 * g));
-    f32x4 d0 = *(cf4)(st + 1024 + 4 * (32 * c + 4 * g)), d1 = *(cf4)(st + 1024 + 4 * (32 * c + 16 + 4 * g));
-    const uint32_t cb = (uint32_t)(32 * c * RS);
+    f32x4 sa[2], da[2];
 #pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      s0 = mfma16(row_read(Q, roff[s] + cb), kf[s], s0);
-      s1 = mfma16(row_read(Q, roff[s] + cb + 16 * RS), kf[s], s1);
+    for (int m = 0; m < 2; ++m) {
+      sa[m] = *(cf4)(st + 4 * (32 * c + 16 * m + 4 * g));
+      da[m] = *(cf4)(st + 1024 + 4 * (32 * c + 16 * m + 4 * g));
     }
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      d0 = mfma16(row_read(O, roff[s] + cb), vf[s], d0);
-      d1 = mfma16(row_read(O, roff[s] + cb + 16 * RS), vf[s], d1);
-    }
+    for (int s = 0; s < KS; ++s)
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        sa[m] = mfma16(qa[m][s], kf[s], sa[m]);
+        da[m] = mfma16(oa[m][s], vf[s], da[m]);
+      }
+    u32x2 ot[NB][2], qt[NB][2];
+#pragma unroll
+    for (int n = 0; n < NB; ++n)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        ot[n][h] = tr_read(O, toff[n] + cb + 16 * h * RS);
+        qt[n][h] = tr_read(Q, toff[n] + cb + 16 * h * RS);
+      }
+    __builtin_amdgcn_sched_barrier(0);
     float p[8], ds[8];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      p[r] = fast_exp2(s0[r] * a.c2);
-      p[4 + r] = fast_exp2(s1[r] * a.c2);
+      p[r] = fast_exp2(sa[0][r] * a.c2);
+      p[4 + r] = fast_exp2(sa[1][r] * a.c2);
     }
     if (!full) {
       const uint32_t w32 = (uint32_t)(mw >> (32 * (c >> 1)));
@@ -562,16 +587,15 @@ __global__ void __launch_bounds__(NT8, 1) dkv16_kernel(KArgs a) {
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      ds[r] = p[r] * d0[r];
-      ds[4 + r] = p[4 + r] * d1[r];
+      ds[r] = p[r] * da[0][r];
+      ds[4 + r] = p[4 + r] * da[1][r];
     }
     const u32x4 pb = pack8_bf16(p), db = pack8_bf16(ds);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int n = 0; n < NB; ++n) {
-      const u32x2 o_lo = tr_read(O, toff[n] + cb), o_hi = tr_read(O, toff[n] + cb + 16 * RS);
-      dv[n] = mfma16(u32x4{o_lo[0], o_lo[1], o_hi[0], o_hi[1]}, pb, dv[n]);
-      const u32x2 q_lo = tr_read(Q, toff[n] + cb), q_hi = tr_read(Q, toff[n] + cb + 16 * RS);
-      dk[n] = mfma16(u32x4{q_lo[0], q_lo[1], q_hi[0], q_hi[1]}, db, dk[n]);
+      dv[n] = mfma16(u32x4{ot[n][0][0], ot[n][0][1], ot[n][1][0], ot[n][1][1]}, pb, dv[n]);
+      dk[n] = mfma16(u32x4{qt[n][0][0], qt[n][0][1], qt[n][1][0], qt[n][1][1]}, db, dk[n]);
     }
   };
 
