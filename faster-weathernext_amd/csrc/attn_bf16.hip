@@ -422,13 +422,13 @@ __global__ void __launch_bounds__(NT, 2) dq_kernel(KArgs a) {
 constexpr int NT8 = 512;  // dK/dV workgroup: 8 waves
 
 // ------------------------------------------------------------------------------------------
-// dK/dV with 16 keys per wave: per work item of the transposed tile list, 8 waves each own 16 keys
-// of the block and compute, for every 32-query group of a tile in which those 16 keys have a
+// dK/dV with 16 keys per wave: per work item of the transposed tile list, each wave owns 16 keys
+// of the block and computes, for every 32-query group of a tile in which those 16 keys have a
 // valid element, S = Q K^T, P = exp2(S c2 - lse log2 e) (masked), dP - delta = dO V^T - delta,
 // dS = P (dP - delta), dV^T += dO^T P and dK^T += Q^T dS (pallas_attn.py:187-215), on
 // V_MFMA_F32_16X16X32_BF16. Each workgroup owns its dK/dV rows: no atomics. The waves share only
-// the Q/dO tile copies (double-buffered) and meet once per tile; they hand nothing over, and each
-// skips the query groups its own 16 keys have no valid element in.
+// the Q/dO tile copies and meet at the tile barriers; they hand nothing over, and each skips the
+// query groups its own 16 keys have no valid element in.
 //
 // Register layout. S and dP are computed query-major (M = 16 queries, N = the wave's 16 keys,
 // K = head_dim): lane l holds queries 4(l/16) + r (r < 4) of each 16-query half m and key
@@ -439,9 +439,9 @@ constexpr int NT8 = 512;  // dK/dV workgroup: 8 waves
 // transposed (M = 16 columns d, N = the 16 keys), so each lane ends up holding 4 consecutive
 // columns of its own key per 16-column block, stored as one 8- or 16-byte write.
 //
-// The mask bits come from the tile list's per-lane words (fwn_tiles_prepare): the 32-row wave W
-// = wid / 2 word of lane 32(g / 2) + 16(wid % 2) + l % 16, shifted right by 4(g % 2), holds
-// element (query group c, half m, r) at bit 16c + 8m + r.
+// The mask bits come from the tile list's per-lane words (fwn_tiles_prepare): for 16-key group
+// kg of the block, the word of 32-row wave kg / 2, lane 32(g / 2) + 16(kg % 2) + l % 16, shifted
+// right by 4(g % 2), holds element (query group c, half m, r) at bit 16c + 8m + r.
 __device__ __forceinline__ f32x4 mfma16(const u32x4& a, const u32x4& b, const f32x4& c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
                                                  0, 0, 0);
@@ -454,90 +454,52 @@ __device__ __forceinline__ u32x4 pack8_bf16(const float (&x)[8]) {
   return __builtin_bit_cast(u32x4, r);
 }
 
+// One wave's 16 keys: its K and V fragments, LDS offsets and dK^T / dV^T accumulators.
 template <int D>
-__global__ void __launch_bounds__(NT8, 1) dkv16_kernel(KArgs a) {
-  constexpr int TB = Tile<D>::BYTES;
-  constexpr int C = Tile<D>::C;
-  constexpr int KS = D / 32;  // K steps of the S and dP contractions
-  constexpr int NB = D / 16;  // 16-column blocks of dK^T and dV^T
-  constexpr int RS = 2 * D;   // bytes per tile row
-  __shared__ __attribute__((aligned(1024))) char lds0[2 * TB + 1536];  // Q | dO | lse[128] | gap | delta[128]
-  __shared__ __attribute__((aligned(1024))) char lds1[2 * TB + 1536];
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // keys 16 wid .. 16 wid + 15 of the block
-  const int g = lane >> 4, t16 = lane & 15;
-  const Job j = decode_job(a);
-  const uint32_t snb = (uint32_t)a.sn * 2, osnb = (uint32_t)a.osn * 2;
-  const rsrc_t rQ = make_rsrc((const uint16_t*)a.q + j.base, a.slice_bytes);
-  const rsrc_t rO = make_rsrc((const uint16_t*)a.dout + j.obase, a.oslice_bytes);
-  const rsrc_t rL = make_rsrc(a.lse + stat_index(a, j, 0), (uint32_t)a.n * 4);
-  const rsrc_t rD = make_rsrc(a.delta + stat_index(a, j, 0), (uint32_t)a.n * 4);
+struct KeyWave {
+  static constexpr int C = Tile<D>::C;
+  static constexpr int KS = D / 32;  // K steps of the S and dP contractions
+  static constexpr int NB = D / 16;  // 16-column blocks of dK^T and dV^T
+  static constexpr int RS = 2 * D;   // bytes per tile row
+  u32x4 kf[KS], vf[KS];              // B operands of S and dP: key krow, columns 32 s + 8 g .. +7
+  uint32_t roff[KS], toff[NB];
+  f32x4 dk[NB], dv[NB];
 
-  // K and V fragments (B operands of S and dP): key krow, columns 32 s + 8 g .. +7.
-  const int krow = j.blk * BLK + 16 * wid + t16;
-  u32x4 kf[KS], vf[KS];
-  {
+  __device__ __forceinline__ void init(const KArgs& a, const Job& j, int krow, int g, int t16) {
     const rsrc_t rK = make_rsrc((const uint16_t*)a.k + j.base, a.slice_bytes);
     const rsrc_t rV = make_rsrc((const uint16_t*)a.v + j.base, a.slice_bytes);
+    const uint32_t snb = (uint32_t)a.sn * 2;
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       kf[s] = bload16(rK, (uint32_t)krow * snb + (uint32_t)(64 * s + 16 * g));
       vf[s] = bload16(rV, (uint32_t)krow * snb + (uint32_t)(64 * s + 16 * g));
     }
-  }
-  // LDS byte offsets within a tile, for query group 0 (group c adds 32 c rows).
-  //   roff[s]: b128 row read of query row t16 (+16 m), columns 32 s + 8 g .. +7;
-  //   toff[n]: transpose read, lane 4e + q of group g: row 4g + e (+16 h), columns 16 n + 4 q ..
-  uint32_t roff[KS], toff[NB];
-  {
+    // LDS byte offsets within a tile, for query group 0 (group c adds 32 c rows):
+    //   roff[s]: b128 row read of query row t16 (+16 m), columns 32 s + 8 g .. +7;
+    //   toff[n]: transpose read, lane 4e + q of group g: row 4g + e (+16 h), columns 16 n + 4 q ..
     const int sr = swz16<C>(t16);
 #pragma unroll
     for (int s = 0; s < KS; ++s) roff[s] = (uint32_t)(t16 * RS + (((4 * s + g) ^ sr) << 4));
     const int e = t16 >> 2, q = t16 & 3, trow = 4 * g + e, st = swz16<C>(trow);
 #pragma unroll
     for (int n = 0; n < NB; ++n) toff[n] = (uint32_t)(trow * RS + (((2 * n + (q >> 1)) ^ st) << 4) + (q & 1) * 8);
-  }
-  f32x4 dk[NB], dv[NB];
 #pragma unroll
-  for (int n = 0; n < NB; ++n) {
-    dk[n] = f32x4{0.f, 0.f, 0.f, 0.f};
-    dv[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int n = 0; n < NB; ++n) {
+      dk[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+      dv[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
   }
 
-  // Tile copies: waves 0-3 copy Q, waves 4-7 dO, wave 0 also the tile's 128 lse and delta (two
-  // branch-free full-wave copies; out-of-range halves read zeros into the gap).
-  TileDma<D, true> dma;
-  dma.init(wid & 3, lane, wid < 4 ? snb : osnb);
-  constexpr uint32_t kPastEnd = 0x7FFFFFF0u;
-  auto issue = [&](int t, lds_char* buf, uint32_t copy) {
-    const int qb = ((ci32_ptr)a.col)[t];
-    if (wid < 4) {
-      dma.issue(rQ, buf, wid, qb * BLK, snb, copy);
-    } else {
-      dma.issue(rO, buf + TB, wid - 4, qb * BLK, osnb, copy);
-    }
-    if (wid == 0) {
-      const uint32_t vo = (uint32_t)(qb * BLK + 4 * (lane & 31)) * 4;
-      lds_char* stats = buf + 2 * TB;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rL, (__attribute__((address_space(3))) void*)stats, 16,
-                                               (int)(lane < 32 ? vo : kPastEnd), 0, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rD, (__attribute__((address_space(3))) void*)(stats + 512), 16,
-                                               (int)(lane < 32 ? kPastEnd : vo), 0, 0, 0);
-    }
-  };
-  // This lane's mask word of tile t (see above), loaded a tile ahead.
-  const uint64_t* mword = a.lanes + (int64_t)(wid >> 1) * 64 + 32 * (g >> 1) + 16 * (wid & 1) + t16;
-  const int mshift = 4 * (g & 1);
-
-  // One 16-key x 32-query unit: query group c of the tile in buffer `cur`. The reads of each
-  // phase are all issued before its MFMAs (the phases are fenced against the scheduler), so an
-  // MFMA waits for the LDS latency once per phase rather than once per operand: the row reads,
-  // then the S and dP MFMAs; the transpose reads, in flight while the exponentials and dS run;
-  // then the dV and dK MFMAs.
-  auto unit = [&](const lds_char* cur, int c, uint64_t mw, bool full) {
-    const lds_char* Q = cur;
-    const lds_char* O = cur + TB;
-    const lds_char* st = cur + 2 * TB;
+  // One 16-key x 32-query unit: query group c of the Q and dO tiles. `lse` and `del` point at
+  // the rescaled statistics of the group's first query (-lse / scale and -delta, the initial
+  // values of the S and dP accumulators, so S c2 = s c2 - lse log2 e and dP holds dP - delta).
+  // Schedule (phases fenced against the compiler's scheduler): the row reads; the 16 S and dP
+  // MFMAs with the 32 transpose reads of the dV and dK operands issued between them; the
+  // exponentials, masks and the P pack; the 8 dV MFMAs with dS and its pack between them; the
+  // 8 dK MFMAs. Each MFMA then waits for LDS once per phase, and the wave's own LDS and VALU
+  // work runs while its MFMAs keep the matrix pipe busy.
+  __device__ __forceinline__ void unit(const lds_char* Q, const lds_char* O, const lds_char* lse, const lds_char* del,
+                                       int c, uint64_t mw, bool full, int g, float c2) {
     typedef const __attribute__((address_space(3))) f32x4* cf4;
     const uint32_t cb = (uint32_t)(32 * c * RS);
     u32x4 qa[2][KS], oa[2][KS];
@@ -548,13 +510,11 @@ __global__ void __launch_bounds__(NT8, 1) dkv16_kernel(KArgs a) {
         qa[m][s] = row_read(Q, roff[s] + cb + 16 * m * RS);
         oa[m][s] = row_read(O, roff[s] + cb + 16 * m * RS);
       }
-    // Accumulators start at -lse / scale and -delta of the element's query (the stats are
-    // rescaled in LDS once per tile), so S c2 = s c2 - lse log2 e and dP holds dP - delta.
     f32x4 sa[2], da[2];
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
-      sa[m] = *(cf4)(st + 4 * (32 * c + 16 * m + 4 * g));
-      da[m] = *(cf4)(st + 1024 + 4 * (32 * c + 16 * m + 4 * g));
+      sa[m] = *(cf4)(lse + 4 * (16 * m + 4 * g));
+      da[m] = *(cf4)(del + 4 * (16 * m + 4 * g));
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -572,34 +532,144 @@ __global__ void __launch_bounds__(NT8, 1) dkv16_kernel(KArgs a) {
         ot[n][h] = tr_read(O, toff[n] + cb + 16 * h * RS);
         qt[n][h] = tr_read(Q, toff[n] + cb + 16 * h * RS);
       }
+#pragma unroll
+    for (int i = 0; i < 4 * KS; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, NB / KS, 0);  // then transpose reads
+    }
     __builtin_amdgcn_sched_barrier(0);
     float p[8], ds[8];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      p[r] = fast_exp2(sa[0][r] * a.c2);
-      p[4 + r] = fast_exp2(sa[1][r] * a.c2);
+      p[r] = fast_exp2(sa[0][r] * c2);
+      p[4 + r] = fast_exp2(sa[1][r] * c2);
     }
-    if (!full) {
+    {
+      // Applied to every unit, fully valid ones included (their bits are all set): a branch here
+      // would split the phase and let the compiler sink the transpose reads past it.
       const uint32_t w32 = (uint32_t)(mw >> (32 * (c >> 1)));
 #pragma unroll
       for (int i = 0; i < 8; ++i)
         p[i] = keep_or_zero(p[i], __builtin_amdgcn_sbfe(w32, (uint32_t)(16 * (c & 1) + 8 * (i >> 2) + (i & 3)), 1u));
     }
+    const u32x4 pb = pack8_bf16(p);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int n = 0; n < NB; ++n) dv[n] = mfma16(u32x4{ot[n][0][0], ot[n][0][1], ot[n][1][0], ot[n][1][1]}, pb, dv[n]);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       ds[r] = p[r] * da[0][r];
       ds[4 + r] = p[4 + r] * da[1][r];
     }
-    const u32x4 pb = pack8_bf16(p), db = pack8_bf16(ds);
+    const u32x4 db = pack8_bf16(ds);
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);  // one dV MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, 2, 1);  // then dS / pack VALU work
+    }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
+    for (int n = 0; n < NB; ++n) dk[n] = mfma16(u32x4{qt[n][0][0], qt[n][0][1], qt[n][1][0], qt[n][1][1]}, db, dk[n]);
+  }
+
+  // Query groups of the tile in which these 16 keys have a valid element (a wave-uniform set,
+  // from this lane's mask word `mw`), and those in which all 512 elements are valid.
+  static __device__ __forceinline__ void live_units(uint64_t mw, uint32_t& live, uint32_t& full) {
+    live = 0u;
+    full = 0u;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint32_t b8 = (uint32_t)(mw >> (16 * c)) & 0x0F0Fu;
+      if (__builtin_amdgcn_ballot_w64(b8 != 0u) != 0u) live |= 1u << c;
+      if (__builtin_amdgcn_ballot_w64(b8 != 0x0F0Fu) == 0u) full |= 1u << c;
+    }
+  }
+
+  // dK^T / dV^T block n: lane l holds columns 16 n + 4 g .. +3 of key krow (row `prow` of the
+  // block in a partial slot).
+  __device__ __forceinline__ void store(const KArgs& a, const Job& j, int krow, int prow, int g) const {
+    if (j.part >= 0) {
+      const rsrc_t r = part_slot<D>(a, j);
+#pragma unroll
+      for (int n = 0; n < NB; ++n) {
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, dk[n]), r,
+                                               (int)((uint32_t)(prow * D + 16 * n + 4 * g) * 4), 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, dv[n]), r,
+                                               (int)((uint32_t)((128 + prow) * D + 16 * n + 4 * g) * 4), 0, 0);
+      }
+      return;
+    }
+    const rsrc_t rdk = make_rsrc((uint16_t*)a.out0 + j.base, a.slice_bytes);
+    const rsrc_t rdv = make_rsrc((uint16_t*)a.out1 + j.base, a.slice_bytes);
+    const uint32_t snb = (uint32_t)a.sn * 2;
+#pragma unroll
     for (int n = 0; n < NB; ++n) {
-      dv[n] = mfma16(u32x4{ot[n][0][0], ot[n][0][1], ot[n][1][0], ot[n][1][1]}, pb, dv[n]);
-      dk[n] = mfma16(u32x4{qt[n][0][0], qt[n][0][1], qt[n][1][0], qt[n][1][1]}, db, dk[n]);
+      u32x2 wk, wv;
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2) {
+        const __bf16 k0 = (__bf16)(dk[n][2 * h2] * a.scale), k1 = (__bf16)(dk[n][2 * h2 + 1] * a.scale);
+        const __bf16 v0 = (__bf16)dv[n][2 * h2], v1 = (__bf16)dv[n][2 * h2 + 1];
+        wk[h2] = (uint32_t)__builtin_bit_cast(uint16_t, k0) | ((uint32_t)__builtin_bit_cast(uint16_t, k1) << 16);
+        wv[h2] = (uint32_t)__builtin_bit_cast(uint16_t, v0) | ((uint32_t)__builtin_bit_cast(uint16_t, v1) << 16);
+      }
+      const uint32_t off = (uint32_t)krow * snb + (uint32_t)(2 * (16 * n + 4 * g));
+      __builtin_amdgcn_raw_buffer_store_b64(wk, rdk, (int)off, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b64(wv, rdv, (int)off, 0, 0);
+    }
+  }
+};
+
+// This lane's mask word of tile 0 for 16-key group kg (add 256 words per tile).
+__device__ __forceinline__ const uint64_t* key_mask_words(const KArgs& a, int kg, int g, int t16) {
+  return a.lanes + (int64_t)(kg >> 1) * 64 + 32 * (g >> 1) + 16 * (kg & 1) + t16;
+}
+
+// 8 waves, one workgroup per CU, the Q/dO tiles double-buffered: one barrier per tile.
+template <int D>
+__global__ void __launch_bounds__(NT8, 1) dkv16_kernel(KArgs a) {
+  constexpr int TB = Tile<D>::BYTES;
+  __shared__ __attribute__((aligned(1024))) char lds0[2 * TB + 1536];  // Q | dO | lse[128] | gap | delta[128]
+  __shared__ __attribute__((aligned(1024))) char lds1[2 * TB + 1536];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // keys 16 wid .. 16 wid + 15 of the block
+  const int g = lane >> 4, t16 = lane & 15;
+  const Job j = decode_job(a);
+  const uint32_t snb = (uint32_t)a.sn * 2, osnb = (uint32_t)a.osn * 2;
+  const rsrc_t rQ = make_rsrc((const uint16_t*)a.q + j.base, a.slice_bytes);
+  const rsrc_t rO = make_rsrc((const uint16_t*)a.dout + j.obase, a.oslice_bytes);
+  const rsrc_t rL = make_rsrc(a.lse + stat_index(a, j, 0), (uint32_t)a.n * 4);
+  const rsrc_t rD = make_rsrc(a.delta + stat_index(a, j, 0), (uint32_t)a.n * 4);
+  const int krow = j.blk * BLK + 16 * wid + t16;
+  KeyWave<D> kw;
+  kw.init(a, j, krow, g, t16);
+
+  // Tile copies: waves 0-3 copy Q, waves 4-7 dO, wave 0 also the tile's 128 lse and delta (two
+  // branch-free full-wave copies; out-of-range halves read zeros into the gap).
+  TileDma<D, true> dma;
+  dma.init(wid & 3, lane, wid < 4 ? snb : osnb);
+  constexpr uint32_t kPastEnd = 0x7FFFFFF0u;
+  auto issue = [&](int qb, lds_char* buf, uint32_t copy) {
+    if (wid < 4) {
+      dma.issue(rQ, buf, wid, qb * BLK, snb, copy);
+    } else {
+      dma.issue(rO, buf + TB, wid - 4, qb * BLK, osnb, copy);
+    }
+    if (wid == 0) {
+      const uint32_t vo = (uint32_t)(qb * BLK + 4 * (lane & 31)) * 4;
+      lds_char* stats = buf + 2 * TB;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rL, (__attribute__((address_space(3))) void*)stats, 16,
+                                               (int)(lane < 32 ? vo : kPastEnd), 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rD, (__attribute__((address_space(3))) void*)(stats + 512), 16,
+                                               (int)(lane < 32 ? kPastEnd : vo), 0, 0, 0);
     }
   };
+  const uint64_t* mword = key_mask_words(a, wid, g, t16);
+  const int mshift = 4 * (g & 1);
 
-  auto tile_step = [&](int tt, int t1, lds_char* cur, lds_char* nxt, uint64_t& mnext, uint32_t& gnext) {
+  // The next tile's group bits and column block are read a tile ahead (scalar loads), so issuing
+  // its copy right after the barrier waits for neither.
+  auto tile_step = [&](int tt, int t1, lds_char* cur, lds_char* nxt, uint64_t& mnext, uint32_t& gnext,
+                       int& cnext) {
     const int t = __builtin_amdgcn_readfirstlane(tt);
     wait_vmem();  // this wave's part of tile t and its mask word
     const uint64_t mw = mnext >> mshift;
@@ -614,68 +684,40 @@ __global__ void __launch_bounds__(NT8, 1) dkv16_kernel(KArgs a) {
     __syncthreads();  // tile t is in LDS; every wave is done with tile t - 1 (buffer nxt)
     if (t + 1 < t1) {
       mnext = mword[(int64_t)(t + 1) * 256];
-      issue(t + 1, nxt, any_rows(gnext));
+      issue(cnext, nxt, any_rows(gnext));
     }
-    if (t + 2 < t1) gnext = tile_groups(a, t + 2);
-    // Query groups in which this wave's 16 keys have a valid element (a wave-uniform set), and
-    // those in which every one of the 512 elements is valid (no mask needed).
-    uint32_t live = 0u, full = 0u;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const uint32_t b8 = (uint32_t)(mw >> (16 * c)) & 0x0F0Fu;
-      if (__builtin_amdgcn_ballot_w64(b8 != 0u) != 0u) live |= 1u << c;
-      if (__builtin_amdgcn_ballot_w64(b8 != 0x0F0Fu) == 0u) full |= 1u << c;
+    if (t + 2 < t1) {
+      gnext = tile_groups(a, t + 2);
+      cnext = ((ci32_ptr)a.col)[t + 2];
     }
+    uint32_t live, full;
+    KeyWave<D>::live_units(mw, live, full);
+    const lds_char* st = cur + 2 * TB;
 #pragma unroll
     for (int c = 0; c < 4; ++c)
-      if (live >> c & 1u) unit(cur, c, mw, full >> c & 1u);
+      if (live >> c & 1u) kw.unit(cur, cur + TB, st + 128 * c, st + 1024 + 128 * c, c, mw, full >> c & 1u, g, a.c2);
   };
 
   int t0, t1;
   tile_range(a, j, t0, t1);
   uint64_t mnext = 0;
   uint32_t gnext = 0u;
+  int cnext = 0;
   lds_char* b0 = (lds_char*)lds0;
   lds_char* b1 = (lds_char*)lds1;
   if (t0 < t1) {
     mnext = mword[(int64_t)t0 * 256];
-    if (t0 + 1 < t1) gnext = tile_groups(a, t0 + 1);
-    issue(t0, b0, any_rows(tile_groups(a, t0)));
+    if (t0 + 1 < t1) {
+      gnext = tile_groups(a, t0 + 1);
+      cnext = ((ci32_ptr)a.col)[t0 + 1];
+    }
+    issue(((ci32_ptr)a.col)[t0], b0, any_rows(tile_groups(a, t0)));
   }
   for (int tt = t0; tt < t1; tt += 2) {
-    tile_step(tt, t1, b0, b1, mnext, gnext);
-    if (tt + 1 < t1) tile_step(tt + 1, t1, b1, b0, mnext, gnext);
+    tile_step(tt, t1, b0, b1, mnext, gnext, cnext);
+    if (tt + 1 < t1) tile_step(tt + 1, t1, b1, b0, mnext, gnext, cnext);
   }
-
-  // dK^T / dV^T block n: lane l holds columns 16 n + 4 g .. +3 of key krow.
-  if (j.part >= 0) {
-    const rsrc_t r = part_slot<D>(a, j);
-    const int row = 16 * wid + t16;
-#pragma unroll
-    for (int n = 0; n < NB; ++n) {
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, dk[n]), r,
-                                             (int)((uint32_t)(row * D + 16 * n + 4 * g) * 4), 0, 0);
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, dv[n]), r,
-                                             (int)((uint32_t)((128 + row) * D + 16 * n + 4 * g) * 4), 0, 0);
-    }
-    return;
-  }
-  const rsrc_t rdk = make_rsrc((uint16_t*)a.out0 + j.base, a.slice_bytes);
-  const rsrc_t rdv = make_rsrc((uint16_t*)a.out1 + j.base, a.slice_bytes);
-#pragma unroll
-  for (int n = 0; n < NB; ++n) {
-    u32x2 wk, wv;
-#pragma unroll
-    for (int h2 = 0; h2 < 2; ++h2) {
-      const __bf16 k0 = (__bf16)(dk[n][2 * h2] * a.scale), k1 = (__bf16)(dk[n][2 * h2 + 1] * a.scale);
-      const __bf16 v0 = (__bf16)dv[n][2 * h2], v1 = (__bf16)dv[n][2 * h2 + 1];
-      wk[h2] = (uint32_t)__builtin_bit_cast(uint16_t, k0) | ((uint32_t)__builtin_bit_cast(uint16_t, k1) << 16);
-      wv[h2] = (uint32_t)__builtin_bit_cast(uint16_t, v0) | ((uint32_t)__builtin_bit_cast(uint16_t, v1) << 16);
-    }
-    const uint32_t off = (uint32_t)krow * snb + (uint32_t)(2 * (16 * n + 4 * g));
-    __builtin_amdgcn_raw_buffer_store_b64(wk, rdk, (int)off, 0, 0);
-    __builtin_amdgcn_raw_buffer_store_b64(wv, rdv, (int)off, 0, 0);
-  }
+  kw.store(a, j, krow, 16 * wid + t16, g);
 }
 
 template <int D>
