@@ -225,6 +225,9 @@ __global__ void __launch_bounds__(NT, 2) fwd_kernel(KArgs a) {
       u32x4 ka[D / 16];
 #pragma unroll
       for (int k = 0; k < D / 16; ++k) ka[k] = row_read(K, off.row[k] + sb * 32 * (2 * D));
+      // All of the group's K reads are issued before its MFMA chain: the chain then waits for
+      // the LDS latency once, not once per pair of MFMAs.
+      __builtin_amdgcn_sched_barrier(0);
       s[sb] = zero16();
 #pragma unroll
       for (int k = 0; k < D / 16; ++k) s[sb] = mfma_bf16(ka[k], qf[k], s[sb]);
@@ -256,6 +259,8 @@ __global__ void __launch_bounds__(NT, 2) fwd_kernel(KArgs a) {
       for (int db = 0; db < D / 32; ++db)
 #pragma unroll
         for (int c = 0; c < 2; ++c) va[db][c] = tr_operand<D>(V, off, db, sb, c);
+      // The V transpose reads are all in flight while the exponentials run.
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const float p = fast_exp2(fmaf(s[sb][r], a.c2, -base));
