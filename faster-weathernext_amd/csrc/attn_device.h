@@ -292,12 +292,13 @@ __device__ __forceinline__ float softmax_base(const SoftmaxState& st) {
 
 // softmax_tile over the sub-blocks in `live` only (a nonzero wave-uniform set); the others are
 // neither read nor written.
-__device__ __forceinline__ bool softmax_live(f32x16 (&s)[4], uint32_t live, SoftmaxState& st, float c2,
+template <int N>
+__device__ __forceinline__ bool softmax_live(f32x16 (&s)[N], uint32_t live, SoftmaxState& st, float c2,
                                              float& corr) {
   const float ninf = -__builtin_inff();
   float mx = ninf;
 #pragma unroll
-  for (int sb = 0; sb < 4; ++sb)
+  for (int sb = 0; sb < N; ++sb)
     if (live >> sb & 1u) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[sb][r]);
@@ -306,7 +307,7 @@ __device__ __forceinline__ bool softmax_live(f32x16 (&s)[4], uint32_t live, Soft
   const float base = st.m == ninf ? 0.f : st.m;
   float sum = 0.f;
 #pragma unroll
-  for (int sb = 0; sb < 4; ++sb)
+  for (int sb = 0; sb < N; ++sb)
     if (live >> sb & 1u) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {

@@ -20,18 +20,23 @@ __device__ __forceinline__ int swz_row3(int row) { return (row & 3) | (((row >> 
 // fp32 staging: linear chunk mapping (coalesced), row-major tiles in LDS, optionally swizzled.
 
 // Only the rows of the 32-row groups in `live` (a uniform set) are copied; the others keep stale
-// data and must not be read.
-template <int D>
+// data and must not be read. NTH threads take part.
+template <int D, int NTH = NT>
 __device__ __forceinline__ void stage_rows_f32(char* lds, rsrc_t r, int row0, uint32_t snb, int tid, bool swizzle,
                                                uint32_t live) {
   constexpr int C = D / 4;
-  constexpr int PER = BLK * C / NT;
-  static_assert(NT % C == 0 && 32 % (NT / C) == 0, "an iteration's rows lie in one group");
+  constexpr int PER = BLK * C / NTH;
+  constexpr int ROWS = NTH / C;  // rows per iteration
+  static_assert(NTH % C == 0, "an iteration covers whole rows");
 #pragma unroll
   for (int it = 0; it < PER; ++it) {
-    if (!(live >> (it * (NT / C) / 32) & 1u)) continue;
-    const int id = tid + it * NT;
+    const int id = tid + it * NTH;
     const int row = id / C, ch = id % C;
+    if constexpr (32 % ROWS == 0) {
+      if (!(live >> (it * ROWS / 32) & 1u)) continue;  // the iteration's rows lie in one group: uniform
+    } else {
+      if (!(live >> (row >> 5) & 1u)) continue;
+    }
     const u32x4 x = bload16(r, (uint32_t)(row0 + row) * snb + (uint32_t)(16 * ch));
     const int pc = swizzle ? (ch ^ swz_row3(row)) : ch;
     *(u32x4*)(lds + row * (D * 4) + (pc << 4)) = x;
@@ -74,15 +79,20 @@ __device__ __forceinline__ void load_frag_f32(f32x4 (&f)[D / 8], rsrc_t r, int r
 }
 
 // ------------------------------------------------------------------------------------------
-// Forward, fp32. 128 KB of LDS: one workgroup per CU.
+// Forward, fp32. 128 KB of LDS: one workgroup per CU, 8 waves. Waves w and w + 4 share one SIMD
+// and the query rows 32 (w % 4) ..; each takes two of the tile's four key groups (w / 4 selects
+// which) with its own online-softmax state, and the pair merges (m, l, O) through LDS at the end.
+// Two waves per SIMD overlap one's softmax and LDS reads with the other's MFMA chains.
+constexpr int NT_F32 = 512;
 
 template <int D>
-__global__ void __launch_bounds__(NT, 1) fwd_f32_kernel(KArgs a) {
+__global__ void __launch_bounds__(NT_F32, 1) fwd_f32_kernel(KArgs a) {
   __shared__ __attribute__((aligned(16))) char smem[2 * BLK * D * 4];
   char* ldsK = smem;                // [128][D] swizzled
   char* ldsV = smem + BLK * D * 4;  // [128][D] plain
   const int tid = threadIdx.x, lane = tid & 63;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int w = wid & 3, kh = wid >> 2;  // query rows 32 w .., key groups 2 kh, 2 kh + 1
   const int i = lane & 31, g = lane >> 5;
   const Job j = decode_job(a);
   const uint32_t snb = (uint32_t)a.sn * 4;
@@ -111,23 +121,24 @@ __global__ void __launch_bounds__(NT, 1) fwd_f32_kernel(KArgs a) {
     const uint32_t gt = gnext;
     if (t + 1 < t1) gnext = tile_groups(a, t + 1);
     __syncthreads();
-    stage_rows_f32<D>(ldsK, rK, kb * BLK, snb, tid, true, any_rows(gt));
-    stage_rows_f32<D>(ldsV, rV, kb * BLK, snb, tid, false, any_rows(gt));
+    stage_rows_f32<D, NT_F32>(ldsK, rK, kb * BLK, snb, tid, true, any_rows(gt));
+    stage_rows_f32<D, NT_F32>(ldsV, rV, kb * BLK, snb, tid, false, any_rows(gt));
     __syncthreads();
-    const uint32_t live = gt >> (4 * w) & 15u;  // key groups with p = 0 throughout are skipped
-    f32x16 s[4];
+    const uint32_t live = gt >> (4 * w + 2 * kh) & 3u;  // this wave's key groups with p = 0 throughout are skipped
+    f32x16 s[2];
 #pragma unroll
-    for (int sb = 0; sb < 4; ++sb) {
-      if (!(live >> sb & 1u)) continue;
-      s[sb] = zero16();
+    for (int k2 = 0; k2 < 2; ++k2) {
+      if (!(live >> k2 & 1u)) continue;
+      const int sb = 2 * kh + k2;
+      s[k2] = zero16();
 #pragma unroll
       for (int u = 0; u < D / 8; ++u) {
         const f32x4 kx = *(const f32x4*)(ldsK + off.row[u & 3] + off.row_imm(sb, u));
 #pragma unroll
-        for (int e = 0; e < 4; ++e) s[sb] = mfma_f32(kx[e], qf[u][e], s[sb]);
+        for (int e = 0; e < 4; ++e) s[k2] = mfma_f32(kx[e], qf[u][e], s[k2]);
       }
 #pragma unroll
-      for (int r = 0; r < 16; ++r) s[sb][r] = keep_or_ninf(s[sb][r], elem_keep(mb, sb, r));
+      for (int r = 0; r < 16; ++r) s[k2][r] = keep_or_ninf(s[k2][r], elem_keep(mb, sb, r));
     }
     float corr;
     if (live != 0u && softmax_live(s, live, st, a.c2, corr)) {
@@ -135,15 +146,44 @@ __global__ void __launch_bounds__(NT, 1) fwd_f32_kernel(KArgs a) {
       for (int db = 0; db < D / 32; ++db) o[db] *= corr;
     }
 #pragma unroll
-    for (int sb = 0; sb < 4; ++sb) {
-      if (!(live >> sb & 1u)) continue;
+    for (int k2 = 0; k2 < 2; ++k2) {
+      if (!(live >> k2 & 1u)) continue;
+      const int sb = 2 * kh + k2;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
 #pragma unroll
         for (int db = 0; db < D / 32; ++db)
-          o[db] = mfma_f32(*(const float*)(ldsV + off.el_plain + off.el_imm(sb, r, db)), s[sb][r], o[db]);
+          o[db] = mfma_f32(*(const float*)(ldsV + off.el_plain + off.el_imm(sb, r, db)), s[k2][r], o[db]);
       }
     }
+  }
+  // Merge the pair: the second wave of each SIMD hands its O, m and l over through LDS (the tiles
+  // are dead after the barrier). m is the log2-domain reference max shared by lanes i, i + 32.
+  float* xo = (float*)smem + (size_t)w * (D / 32) * 16 * 64;  // [D / 32][16][64 lanes]
+  float* xm = (float*)smem + 4 * (D / 32) * 16 * 64 + w * 128;  // [64 lanes] m, then [64 lanes] l
+  __syncthreads();
+  if (kh == 1) {
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) xo[(db * 16 + r) * 64 + lane] = o[db][r];
+    xm[lane] = st.m;
+    xm[64 + lane] = st.l;
+  }
+  __syncthreads();
+  if (kh == 1) return;
+  {
+    const float m1 = xm[lane], l1 = xm[64 + lane];
+    const float ninf = -__builtin_inff();
+    const float mm = fmaxf(st.m, m1);
+    const float c0 = st.m == ninf ? 0.f : fast_exp2(st.m - mm);
+    const float c1 = m1 == ninf ? 0.f : fast_exp2(m1 - mm);
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[db][r] = o[db][r] * c0 + xo[(db * 16 + r) * 64 + lane] * c1;
+    st.l = st.l * c0 + l1 * c1;
+    st.m = mm;
   }
   const float ltot = st.l + __shfl_xor(st.l, 32);
   if (j.part >= 0) {
@@ -378,7 +418,7 @@ hipError_t launch_d(Kind kind, const KArgs& a, hipStream_t stream) {
   }
   const dim3 grid((unsigned)a.n_items * (unsigned)(a.batch * a.heads));
   switch (kind) {
-    case Kind::kFwd: hipLaunchKernelGGL(fwd_f32_kernel<D>, grid, block, 0, stream, a); break;
+    case Kind::kFwd: hipLaunchKernelGGL(fwd_f32_kernel<D>, grid, dim3(NT_F32), 0, stream, a); break;
     case Kind::kDq: hipLaunchKernelGGL(dq_f32_kernel<D>, grid, block, 0, stream, a); break;
     case Kind::kDkv: hipLaunchKernelGGL(dkv_f32_kernel<D>, grid, block, 0, stream, a); break;
     default: break;

@@ -153,16 +153,19 @@ def test_c5_attention_shape_bf16_forward_backward(r6):
   _same_to_combine_rounding(res, run(q, k, v, do, pinned, SCALE, BF16), "c5 128- vs 64-tile items")
 
 
-def test_c5_attention_shape_fp32_forward(r6):
-  """The same shape at full precision (the reference's "highest" mode, pallas_attn.py:336-347):
-  float32 MFMA forward within rel RMS 1e-5, lse within 1e-5, at rows of blocks 119, 200 and 320."""
+def test_c5_attention_shape_fp32_forward_backward(r6):
+  """The same shape at full precision (fp32 MFMA; the reference's strict_fp32, and tighter than its
+  "highest" 3xTF32 mode, pallas_attn.py:336-347): forward and backward within rel RMS 1e-5 and the
+  reference's max-relative bar, lse within 1e-5, at rows of blocks 119, 200 and 320 and every key of
+  blocks 119, 200 and 320 (bench.py --workload c5f32 times this call)."""
   mask = r6(32, hilbert=True)
   n = mask.shape[0]
-  q, k, v, _ = _inputs([0], n, 6, F32, grads=False)
+  q, k, v, do = _inputs([0], n, 6, F32)
   tiles = fwn.TileList.from_mask(mask)
-  out, lse = fwn.attention_forward(*(dev(x, F32) for x in (q, k, v)), tiles, SCALE)
-  ref = A.block_attention(q, k, v, np.zeros_like(q), mask, SCALE, row_blocks=[119, 200, LAST])
-  check(host(out)[:, ref["rows"]], ref["out"], F32, "out")
+  res = run(q, k, v, do, tiles, SCALE, F32)
+  ref = A.block_attention(q, k, v, do, mask, SCALE, row_blocks=[119, 200, LAST], key_blocks=[119, 200, LAST])
+  check_blocks(res, ref, F32, "c5 fp32")
+  _, lse = fwn.attention_forward(*(dev(x, F32) for x in (q, k, v)), tiles, SCALE)
   np.testing.assert_allclose(host(lse)[:, :, ref["rows"]], ref["lse"], rtol=0, atol=1e-5)
 
 
