@@ -78,6 +78,22 @@ __device__ __forceinline__ void load_frag_f32(f32x4 (&f)[D / 8], rsrc_t r, int r
     f[u] = __builtin_bit_cast(f32x4, bload16(r, (uint32_t)row * snb + (uint32_t)(32 * u + 16 * g)));
 }
 
+// Schedules a loop of N steps, each with R LDS reads followed by the M MFMAs that consume them,
+// so that the reads run two steps ahead of their MFMAs: with one wave per SIMD nothing else fills
+// the MFMA pipe while a wave waits for a read it issued just before use. (The compiler, left to
+// itself, issues each step's reads right before its MFMAs.) Place after the reads and MFMAs it
+// orders, in the same basic block.
+template <int N, int R, int M>
+__device__ __forceinline__ void sched_reads_ahead() {
+  __builtin_amdgcn_sched_group_barrier(0x100, 2 * R, 0);  // the reads of steps 0 and 1
+#pragma unroll
+  for (int k = 0; k < N - 2; ++k) {
+    __builtin_amdgcn_sched_group_barrier(0x008, M, 0);  // step k's MFMAs
+    __builtin_amdgcn_sched_group_barrier(0x100, R, 0);  // step k + 2's reads
+  }
+  __builtin_amdgcn_sched_group_barrier(0x008, 2 * M, 0);  // the last two steps' MFMAs
+}
+
 // ------------------------------------------------------------------------------------------
 // Forward, fp32. 128 KB of LDS: one workgroup per CU, 8 waves. Waves w and w + 4 share one SIMD
 // and the query rows 32 (w % 4) ..; each takes two of the tile's four key groups (w / 4 selects
@@ -244,28 +260,37 @@ __global__ void __launch_bounds__(NT, 1) dq_f32_kernel(KArgs a) {
     for (int sb = 0; sb < 4; ++sb) {
       if (!(live >> sb & 1u)) continue;
       f32x16 s = zero16(), dp = zero16();
+      f32x4 kx[D / 8], vx[D / 8];
 #pragma unroll
       for (int u = 0; u < D / 8; ++u) {
-        const f32x4 kx = *(const f32x4*)(ldsK + off.row[u & 3] + off.row_imm(sb, u));
-        const f32x4 vx = *(const f32x4*)(ldsV + off.row[u & 3] + off.row_imm(sb, u));
+        kx[u] = *(const f32x4*)(ldsK + off.row[u & 3] + off.row_imm(sb, u));
+        vx[u] = *(const f32x4*)(ldsV + off.row[u & 3] + off.row_imm(sb, u));
+      }
+#pragma unroll
+      for (int u = 0; u < D / 8; ++u)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          s = mfma_f32(kx[e], qf[u][e], s);
-          dp = mfma_f32(vx[e], df[u][e], dp);
+          s = mfma_f32(kx[u][e], qf[u][e], s);
+          dp = mfma_f32(vx[u][e], df[u][e], dp);
         }
-      }
+      sched_reads_ahead<D / 8, 2, 8>();
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         float p = fast_exp2(fmaf(s[r], a.c2, -lse_t));
         p = keep_or_zero(p, elem_keep(mb, sb, r));
         dp[r] = p * (dp[r] - delta);
       }
+      float kt[16][D / 32];
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+#pragma unroll
+        for (int db = 0; db < D / 32; ++db) kt[r][db] = *(const float*)(ldsK + off.el[r & 3] + off.el_imm(sb, r, db));
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
 #pragma unroll
-        for (int db = 0; db < D / 32; ++db)
-          acc[db] = mfma_f32(*(const float*)(ldsK + off.el[r & 3] + off.el_imm(sb, r, db)), dp[r], acc[db]);
+        for (int db = 0; db < D / 32; ++db) acc[db] = mfma_f32(kt[r][db], dp[r], acc[db]);
       }
+      sched_reads_ahead<16, D / 32, D / 32>();
     }
   }
   if (j.part >= 0) {
@@ -335,16 +360,20 @@ __global__ void __launch_bounds__(NT, 1) dkv_f32_kernel(KArgs a) {
       f32x16 s = zero16(), dp;
 #pragma unroll
       for (int r = 0; r < 16; ++r) dp[r] = -ldsDl[element_col(sb, r, g)];  // dP^T - delta accumulates directly
+      f32x4 qx[D / 8], ox[D / 8];
 #pragma unroll
       for (int u = 0; u < D / 8; ++u) {
-        const f32x4 qx = *(const f32x4*)(ldsQ + off.row[u & 3] + off.row_imm(sb, u));
-        const f32x4 ox = *(const f32x4*)(ldsO + off.row[u & 3] + off.row_imm(sb, u));
+        qx[u] = *(const f32x4*)(ldsQ + off.row[u & 3] + off.row_imm(sb, u));
+        ox[u] = *(const f32x4*)(ldsO + off.row[u & 3] + off.row_imm(sb, u));
+      }
+#pragma unroll
+      for (int u = 0; u < D / 8; ++u)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          s = mfma_f32(qx[e], kf[u][e], s);
-          dp = mfma_f32(ox[e], vf[u][e], dp);
+          s = mfma_f32(qx[u][e], kf[u][e], s);
+          dp = mfma_f32(ox[u][e], vf[u][e], dp);
         }
-      }
+      sched_reads_ahead<D / 8, 2, 8>();
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int qq = element_col(sb, r, g);
@@ -353,14 +382,23 @@ __global__ void __launch_bounds__(NT, 1) dkv_f32_kernel(KArgs a) {
         s[r] = p;
         dp[r] = p * dp[r];
       }
+      float ot[16][D / 32], qt[16][D / 32];
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+#pragma unroll
+        for (int db = 0; db < D / 32; ++db) {
+          ot[r][db] = *(const float*)(ldsO + off.el[r & 3] + off.el_imm(sb, r, db));
+          qt[r][db] = *(const float*)(ldsQ + off.el[r & 3] + off.el_imm(sb, r, db));
+        }
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
 #pragma unroll
         for (int db = 0; db < D / 32; ++db) {
-          dv[db] = mfma_f32(*(const float*)(ldsO + off.el[r & 3] + off.el_imm(sb, r, db)), s[r], dv[db]);
-          dk[db] = mfma_f32(*(const float*)(ldsQ + off.el[r & 3] + off.el_imm(sb, r, db)), dp[r], dk[db]);
+          dv[db] = mfma_f32(ot[r][db], s[r], dv[db]);
+          dk[db] = mfma_f32(qt[r][db], dp[r], dk[db]);
         }
       }
+      sched_reads_ahead<16, 2 * (D / 32), 2 * (D / 32)>();
     }
   }
   if (j.part >= 0) {
