@@ -94,6 +94,32 @@ __device__ __forceinline__ void sched_reads_ahead() {
   __builtin_amdgcn_sched_group_barrier(0x008, 2 * M, 0);  // the last two steps' MFMAs
 }
 
+// Copies rows 64h .. 64h + 63 of a 128-row fp32 tile (rows of 4D bytes, 16-byte chunks swizzled
+// by swz_row3) from global rows row0 + 64h .. into a 64-row half buffer with the buffer unit's LDS
+// DMA, so the copy needs no registers and runs while the other half is computed. Only the 32-row
+// groups in `live` (tile group bits 2h and 2h + 1) are copied. Wave w of 4 issues the 1 KB
+// instructions k = w, w + 4, ...; instruction k fills half rows kR .. kR + R - 1 (R = 1024 / 4D),
+// which lie in one group, and lane l the chunk that belongs at its position.
+template <int D>
+__device__ __forceinline__ void dma_half_f32(rsrc_t r, char* half, int row0, uint32_t snb, int w, int lane, int h,
+                                             uint32_t live) {
+  constexpr int R = 1024 / (D * 4);
+  constexpr int CPR = D / 4;
+  constexpr int NI = 64 / R;
+  uint32_t base = (uint32_t)(uintptr_t)half;
+  asm volatile("" : "+s"(base));
+  const int rl = lane / CPR, pc = lane % CPR;
+#pragma unroll
+  for (int m = 0; m < NI / 4; ++m) {
+    const int k = w + 4 * m;
+    if (!(live >> (2 * h + ((k * R) >> 5)) & 1u)) continue;
+    const int row = 64 * h + k * R + rl;  // row within the tile
+    const uint32_t src = (uint32_t)(row0 + row) * snb + (uint32_t)((pc ^ swz_row3(row)) << 4);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(uintptr_t)(base + 1024u * k),
+                                             16, (int)src, 0, 0, 0);
+  }
+}
+
 // ------------------------------------------------------------------------------------------
 // Forward, fp32. 128 KB of LDS: one workgroup per CU, 8 waves. Waves w and w + 4 share one SIMD
 // and the query rows 32 (w % 4) ..; each takes two of the tile's four key groups (w / 4 selects
@@ -211,13 +237,14 @@ __global__ void __launch_bounds__(NT_F32, 1) fwd_f32_kernel(KArgs a) {
   if (g == 0) write_lse(a, j, qrow, st, ltot);
 }
 
-// dQ, fp32.
+// dQ, fp32. The tile's K and V rows stream in halves (rows 0-63, 64-127) through two half
+// buffers: the copy of one half runs while the other is computed. Two barriers per tile.
 
 template <int D>
 __global__ void __launch_bounds__(NT, 1) dq_f32_kernel(KArgs a) {
-  __shared__ __attribute__((aligned(16))) char smem[2 * BLK * D * 4];
-  char* ldsK = smem;
-  char* ldsV = smem + BLK * D * 4;
+  constexpr int HB = 64 * D * 4;  // bytes of 64 rows of K or V
+  __shared__ __attribute__((aligned(1024))) char h0[2 * HB];  // rows 0-63: K | V
+  __shared__ __attribute__((aligned(1024))) char h1[2 * HB];  // rows 64-127: K | V
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int i = lane & 31, g = lane >> 5;
@@ -235,63 +262,86 @@ __global__ void __launch_bounds__(NT, 1) dq_f32_kernel(KArgs a) {
     lse_t = a.lse[stat_index(a, j, qrow)] * LOG2E;
     delta = a.delta[stat_index(a, j, qrow)];
   }
-  wait_vmem();
   F32Offsets<D> off;
   off.init(i, g);
   f32x16 acc[D / 32];
 #pragma unroll
   for (int db = 0; db < D / 32; ++db) acc[db] = zero16();
 
+  // Key group sb of the tile, from the half buffer holding it (local group sl = sb % 2).
+  auto group = [&](int sb, int sl, const char* ldsK, const char* ldsV, u32x2 mb) {
+    f32x16 s = zero16(), dp = zero16();
+    f32x4 kx[D / 8], vx[D / 8];
+#pragma unroll
+    for (int u = 0; u < D / 8; ++u) {
+      kx[u] = *(const f32x4*)(ldsK + off.row[u & 3] + off.row_imm(sl, u));
+      vx[u] = *(const f32x4*)(ldsV + off.row[u & 3] + off.row_imm(sl, u));
+    }
+#pragma unroll
+    for (int u = 0; u < D / 8; ++u)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        s = mfma_f32(kx[u][e], qf[u][e], s);
+        dp = mfma_f32(vx[u][e], df[u][e], dp);
+      }
+    sched_reads_ahead<D / 8, 2, 8>();
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      float p = fast_exp2(fmaf(s[r], a.c2, -lse_t));
+      p = keep_or_zero(p, elem_keep(mb, sb, r));
+      dp[r] = p * (dp[r] - delta);
+    }
+    float kt[16][D / 32];
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+#pragma unroll
+      for (int db = 0; db < D / 32; ++db) kt[r][db] = *(const float*)(ldsK + off.el[r & 3] + off.el_imm(sl, r, db));
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+#pragma unroll
+      for (int db = 0; db < D / 32; ++db) acc[db] = mfma_f32(kt[r][db], dp[r], acc[db]);
+    }
+    sched_reads_ahead<16, D / 32, D / 32>();
+  };
+
   int t0, t1;
   tile_range(a, j, t0, t1);
-  uint32_t gnext = t0 < t1 ? tile_groups(a, t0) : 0u;  // group bits, loaded a tile ahead
+  uint32_t gcur = 0u;
+  if (t0 < t1) {
+    gcur = tile_groups(a, t0);
+    const int kb = ((ci32_ptr)a.col)[t0];
+    dma_half_f32<D>(rK, h0, kb * BLK, snb, w, lane, 0, any_rows(gcur));
+    dma_half_f32<D>(rV, h0 + HB, kb * BLK, snb, w, lane, 0, any_rows(gcur));
+  }
   for (int tt = t0; tt < t1; ++tt) {
     const int t = __builtin_amdgcn_readfirstlane(tt);
     const int kb = ((ci32_ptr)a.col)[t];
-    const u32x2 mb = tile_bits(a, t, w, lane);  // lands while the tile is staged
-    const uint32_t gt = gnext;
-    if (t + 1 < t1) gnext = tile_groups(a, t + 1);
-    __syncthreads();
-    stage_rows_f32<D>(ldsK, rK, kb * BLK, snb, tid, true, any_rows(gt));
-    stage_rows_f32<D>(ldsV, rV, kb * BLK, snb, tid, true, any_rows(gt));
-    __syncthreads();
+    const u32x2 mb = tile_bits(a, t, w, lane);
+    const uint32_t gt = gcur;
     const uint32_t live = gt >> (4 * w) & 15u;  // key groups with p = 0 throughout are skipped
-#pragma unroll
-    for (int sb = 0; sb < 4; ++sb) {
-      if (!(live >> sb & 1u)) continue;
-      f32x16 s = zero16(), dp = zero16();
-      f32x4 kx[D / 8], vx[D / 8];
-#pragma unroll
-      for (int u = 0; u < D / 8; ++u) {
-        kx[u] = *(const f32x4*)(ldsK + off.row[u & 3] + off.row_imm(sb, u));
-        vx[u] = *(const f32x4*)(ldsV + off.row[u & 3] + off.row_imm(sb, u));
-      }
-#pragma unroll
-      for (int u = 0; u < D / 8; ++u)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          s = mfma_f32(kx[u][e], qf[u][e], s);
-          dp = mfma_f32(vx[u][e], df[u][e], dp);
-        }
-      sched_reads_ahead<D / 8, 2, 8>();
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float p = fast_exp2(fmaf(s[r], a.c2, -lse_t));
-        p = keep_or_zero(p, elem_keep(mb, sb, r));
-        dp[r] = p * (dp[r] - delta);
-      }
-      float kt[16][D / 32];
-#pragma unroll
-      for (int r = 0; r < 16; ++r)
-#pragma unroll
-        for (int db = 0; db < D / 32; ++db) kt[r][db] = *(const float*)(ldsK + off.el[r & 3] + off.el_imm(sb, r, db));
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-#pragma unroll
-        for (int db = 0; db < D / 32; ++db) acc[db] = mfma_f32(kt[r][db], dp[r], acc[db]);
-      }
-      sched_reads_ahead<16, D / 32, D / 32>();
+    wait_vmem();      // this wave's part of half 0 of tile t, and the mask bits
+    __syncthreads();  // half 0 landed; every wave is done with half 1 of tile t - 1
+    dma_half_f32<D>(rK, h1, kb * BLK, snb, w, lane, 1, any_rows(gt));
+    dma_half_f32<D>(rV, h1 + HB, kb * BLK, snb, w, lane, 1, any_rows(gt));
+    if (t + 1 < t1) gcur = tile_groups(a, t + 1);
+    // Fenced, so that one group's reads and MFMAs do not overlap the next group's registers.
+    __builtin_amdgcn_sched_barrier(0);
+    if (live & 1u) group(0, 0, h0, h0 + HB, mb);
+    __builtin_amdgcn_sched_barrier(0);
+    if (live & 2u) group(1, 1, h0, h0 + HB, mb);
+    __builtin_amdgcn_sched_barrier(0);
+    wait_vmem();      // this wave's part of half 1
+    __syncthreads();  // half 1 landed; every wave is done with half 0
+    if (t + 1 < t1) {
+      const int kbn = ((ci32_ptr)a.col)[t + 1];
+      dma_half_f32<D>(rK, h0, kbn * BLK, snb, w, lane, 0, any_rows(gcur));
+      dma_half_f32<D>(rV, h0 + HB, kbn * BLK, snb, w, lane, 0, any_rows(gcur));
     }
+    __builtin_amdgcn_sched_barrier(0);
+    if (live & 4u) group(2, 0, h1, h1 + HB, mb);
+    __builtin_amdgcn_sched_barrier(0);
+    if (live & 8u) group(3, 1, h1, h1 + HB, mb);
+    __builtin_amdgcn_sched_barrier(0);
   }
   if (j.part >= 0) {
     store_bwd_partial<D>(a, j, 32 * w + i, acc, 0, g);
@@ -300,15 +350,15 @@ __global__ void __launch_bounds__(NT, 1) dq_f32_kernel(KArgs a) {
   store_acc_f32<D>(make_rsrc((float*)a.out0 + j.base, a.slice_bytes), qrow, snb, acc, a.scale, g);
 }
 
-// dK/dV, fp32.
+// dK/dV, fp32. The tile's Q and dO rows, and their lse and delta, stream in halves through two
+// half buffers as in dQ.
 
 template <int D>
 __global__ void __launch_bounds__(NT, 1) dkv_f32_kernel(KArgs a) {
-  __shared__ __attribute__((aligned(16))) char smem[2 * BLK * D * 4 + 2 * BLK * 4];
-  char* ldsQ = smem;                // [128][D] swizzled
-  char* ldsO = smem + BLK * D * 4;  // dO [128][D] swizzled
-  float* ldsL = (float*)(smem + 2 * BLK * D * 4);
-  float* ldsDl = ldsL + BLK;
+  constexpr int HB = 64 * D * 4;  // bytes of 64 rows of Q or dO
+  // rows 0-63 (h0) and 64-127 (h1): Q | dO | lse * log2(e) [64] | delta [64]
+  __shared__ __attribute__((aligned(1024))) char h0[2 * HB + 512];
+  __shared__ __attribute__((aligned(1024))) char h1[2 * HB + 512];
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int i = lane & 31, g = lane >> 5;
@@ -317,14 +367,13 @@ __global__ void __launch_bounds__(NT, 1) dkv_f32_kernel(KArgs a) {
   const rsrc_t rQ = make_rsrc((const float*)a.q + j.base, a.slice_bytes);
   const rsrc_t rO = make_rsrc((const float*)a.dout + j.obase, a.oslice_bytes);
   const uint32_t osnb = (uint32_t)a.osn * 4;
-  const float* lse = a.lse + stat_index(a, j, 0);
-  const float* dl = a.delta + stat_index(a, j, 0);
+  const rsrc_t rL = make_rsrc(a.lse + stat_index(a, j, 0), (uint32_t)a.n * 4);
+  const rsrc_t rD = make_rsrc(a.delta + stat_index(a, j, 0), (uint32_t)a.n * 4);
 
   const int krow = j.blk * BLK + 32 * w + i;
   f32x4 kf[D / 8], vf[D / 8];
   load_frag_f32<D>(kf, make_rsrc((const float*)a.k + j.base, a.slice_bytes), krow, snb, g);
   load_frag_f32<D>(vf, make_rsrc((const float*)a.v + j.base, a.slice_bytes), krow, snb, g);
-  wait_vmem();
   F32Offsets<D> off;
   off.init(i, g);
   f32x16 dk[D / 32], dv[D / 32];
@@ -334,72 +383,106 @@ __global__ void __launch_bounds__(NT, 1) dkv_f32_kernel(KArgs a) {
     dv[db] = zero16();
   }
 
+  // Half h of query block qb: the Q and dO rows (live groups only) and, by wave 0, the 64 rows'
+  // lse and delta (4 bytes per lane; rows past n read zeros).
+  auto copy_half = [&](char* hb, int qb, int h, uint32_t live) {
+    dma_half_f32<D>(rQ, hb, qb * BLK, snb, w, lane, h, live);
+    dma_half_f32<D>(rO, hb + HB, qb * BLK, osnb, w, lane, h, live);
+    if (w == 0) {
+      const int so = (qb * BLK + 64 * h + lane) * 4;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rL, (__attribute__((address_space(3))) void*)(hb + 2 * HB), 4, so, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rD, (__attribute__((address_space(3))) void*)(hb + 2 * HB + 256), 4, so, 0, 0, 0);
+    }
+  };
+  // After the copy of a half landed: lse -> lse * log2(e), the form the exponent takes.
+  auto scale_lse = [&](char* hb) {
+    if (w == 0 && lane < 16) {
+      f32x4* x = (f32x4*)(hb + 2 * HB + 16 * lane);
+      *x = *x * LOG2E;
+    }
+  };
+  // Query group sb of the tile, from the half buffer holding it (local group sl = sb % 2).
+  auto group = [&](int sb, int sl, const char* hb, u32x2 mb) {
+    const char* ldsQ = hb;
+    const char* ldsO = hb + HB;
+    const float* ldsL = (const float*)(hb + 2 * HB);
+    const float* ldsDl = ldsL + 64;
+    f32x16 s = zero16(), dp;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dp[r] = -ldsDl[element_col(sl, r, g)];  // dP^T - delta accumulates directly
+    f32x4 qx[D / 8], ox[D / 8];
+#pragma unroll
+    for (int u = 0; u < D / 8; ++u) {
+      qx[u] = *(const f32x4*)(ldsQ + off.row[u & 3] + off.row_imm(sl, u));
+      ox[u] = *(const f32x4*)(ldsO + off.row[u & 3] + off.row_imm(sl, u));
+    }
+#pragma unroll
+    for (int u = 0; u < D / 8; ++u)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        s = mfma_f32(qx[u][e], kf[u][e], s);
+        dp = mfma_f32(ox[u][e], vf[u][e], dp);
+      }
+    sched_reads_ahead<D / 8, 2, 8>();
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      float p = fast_exp2(fmaf(s[r], a.c2, -ldsL[element_col(sl, r, g)]));
+      p = keep_or_zero(p, elem_keep(mb, sb, r));
+      s[r] = p;
+      dp[r] = p * dp[r];
+    }
+    float ot[16][D / 32], qt[16][D / 32];
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+#pragma unroll
+      for (int db = 0; db < D / 32; ++db) {
+        ot[r][db] = *(const float*)(ldsO + off.el[r & 3] + off.el_imm(sl, r, db));
+        qt[r][db] = *(const float*)(ldsQ + off.el[r & 3] + off.el_imm(sl, r, db));
+      }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+#pragma unroll
+      for (int db = 0; db < D / 32; ++db) {
+        dv[db] = mfma_f32(ot[r][db], s[r], dv[db]);
+        dk[db] = mfma_f32(qt[r][db], dp[r], dk[db]);
+      }
+    }
+    sched_reads_ahead<16, 2 * (D / 32), 2 * (D / 32)>();
+  };
+
   int t0, t1;
   tile_range(a, j, t0, t1);
-  uint32_t gnext = t0 < t1 ? tile_groups(a, t0) : 0u;  // group bits, loaded a tile ahead
+  uint32_t gcur = 0u;
+  if (t0 < t1) {
+    gcur = tile_groups(a, t0);
+    copy_half(h0, ((ci32_ptr)a.col)[t0], 0, any_rows(gcur));
+  }
   for (int tt = t0; tt < t1; ++tt) {
     const int t = __builtin_amdgcn_readfirstlane(tt);
     const int qb = ((ci32_ptr)a.col)[t];
-    const u32x2 mb = tile_bits(a, t, w, lane);  // lands while the tile is staged
-    const uint32_t gt = gnext;
-    if (t + 1 < t1) gnext = tile_groups(a, t + 1);
-    __syncthreads();
-    stage_rows_f32<D>(ldsQ, rQ, qb * BLK, snb, tid, true, any_rows(gt));
-    stage_rows_f32<D>(ldsO, rO, qb * BLK, osnb, tid, true, any_rows(gt));
-    {
-      const int row = qb * BLK + (tid & (BLK - 1));
-      float stat = 0.f;
-      if (row < a.n) stat = tid < BLK ? lse[row] * LOG2E : dl[row];
-      (tid < BLK ? ldsL : ldsDl)[tid & (BLK - 1)] = stat;
-    }
-    __syncthreads();
+    const u32x2 mb = tile_bits(a, t, w, lane);
+    const uint32_t gt = gcur;
     const uint32_t live = gt >> (4 * w) & 15u;  // query groups with p = 0 throughout are skipped
-#pragma unroll
-    for (int sb = 0; sb < 4; ++sb) {
-      if (!(live >> sb & 1u)) continue;
-      f32x16 s = zero16(), dp;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) dp[r] = -ldsDl[element_col(sb, r, g)];  // dP^T - delta accumulates directly
-      f32x4 qx[D / 8], ox[D / 8];
-#pragma unroll
-      for (int u = 0; u < D / 8; ++u) {
-        qx[u] = *(const f32x4*)(ldsQ + off.row[u & 3] + off.row_imm(sb, u));
-        ox[u] = *(const f32x4*)(ldsO + off.row[u & 3] + off.row_imm(sb, u));
-      }
-#pragma unroll
-      for (int u = 0; u < D / 8; ++u)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          s = mfma_f32(qx[u][e], kf[u][e], s);
-          dp = mfma_f32(ox[u][e], vf[u][e], dp);
-        }
-      sched_reads_ahead<D / 8, 2, 8>();
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int qq = element_col(sb, r, g);
-        float p = fast_exp2(fmaf(s[r], a.c2, -ldsL[qq]));
-        p = keep_or_zero(p, elem_keep(mb, sb, r));
-        s[r] = p;
-        dp[r] = p * dp[r];
-      }
-      float ot[16][D / 32], qt[16][D / 32];
-#pragma unroll
-      for (int r = 0; r < 16; ++r)
-#pragma unroll
-        for (int db = 0; db < D / 32; ++db) {
-          ot[r][db] = *(const float*)(ldsO + off.el[r & 3] + off.el_imm(sb, r, db));
-          qt[r][db] = *(const float*)(ldsQ + off.el[r & 3] + off.el_imm(sb, r, db));
-        }
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-#pragma unroll
-        for (int db = 0; db < D / 32; ++db) {
-          dv[db] = mfma_f32(ot[r][db], s[r], dv[db]);
-          dk[db] = mfma_f32(qt[r][db], dp[r], dk[db]);
-        }
-      }
-      sched_reads_ahead<16, 2 * (D / 32), 2 * (D / 32)>();
-    }
+    wait_vmem();  // this wave's part of half 0 of tile t, and the mask bits
+    scale_lse(h0);
+    __syncthreads();  // half 0 landed; every wave is done with half 1 of tile t - 1
+    copy_half(h1, qb, 1, any_rows(gt));
+    if (t + 1 < t1) gcur = tile_groups(a, t + 1);
+    // Fenced, so that one group's reads and MFMAs do not overlap the next group's registers.
+    __builtin_amdgcn_sched_barrier(0);
+    if (live & 1u) group(0, 0, h0, mb);
+    __builtin_amdgcn_sched_barrier(0);
+    if (live & 2u) group(1, 1, h0, mb);
+    __builtin_amdgcn_sched_barrier(0);
+    wait_vmem();  // this wave's part of half 1
+    scale_lse(h1);
+    __syncthreads();  // half 1 landed; every wave is done with half 0
+    if (t + 1 < t1) copy_half(h0, ((ci32_ptr)a.col)[t + 1], 0, any_rows(gcur));
+    __builtin_amdgcn_sched_barrier(0);
+    if (live & 4u) group(2, 0, h1, mb);
+    __builtin_amdgcn_sched_barrier(0);
+    if (live & 8u) group(3, 1, h1, mb);
+    __builtin_amdgcn_sched_barrier(0);
   }
   if (j.part >= 0) {
     store_bwd_partial<D>(a, j, 32 * w + i, dk, 0, g);
