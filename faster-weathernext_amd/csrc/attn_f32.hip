@@ -3,7 +3,8 @@
 //
 // fp32 MFMA operands are one element per lane, so the second contraction's A operand (V^T, K^T,
 // Q^T, dO^T) is read element-wise straight from the row-major LDS tile; no transposed copy is
-// needed. Tiles are staged through registers (256 threads, coalesced 16-byte loads).
+// needed. The forward stages its tiles through registers (coalesced 16-byte loads); dQ and dK/dV
+// stream theirs in 64-row halves by LDS DMA, double-buffered.
 //
 // Reference: pallas_attn.py:112-141 (forward), 161-215 (dQ, dK/dV), 274-311 (VJP driver).
 #include "attn_device.h"
