@@ -96,30 +96,46 @@ __device__ __forceinline__ void sched_reads_ahead() {
 }
 
 // Copies rows 64h .. 64h + 63 of a 128-row fp32 tile (rows of 4D bytes, 16-byte chunks swizzled
-// by swz_row3) from global rows row0 + 64h .. into a 64-row half buffer with the buffer unit's LDS
-// DMA, so the copy needs no registers and runs while the other half is computed. Only the 32-row
-// groups in `live` (tile group bits 2h and 2h + 1) are copied. Wave w of 4 issues the 1 KB
-// instructions k = w, w + 4, ...; instruction k fills half rows kR .. kR + R - 1 (R = 1024 / 4D),
-// which lie in one group, and lane l the chunk that belongs at its position.
+// by swz_row3, or plain) from global rows row0 + 64h .. into a 64-row half buffer with the buffer
+// unit's LDS DMA, so the copy needs no registers and runs while the other half is computed. Only
+// the 32-row groups in `live` (tile group bits 2h and 2h + 1) are copied. Wave w of 4 issues the
+// 1 KB instructions k = w + 4m; instruction k fills half rows kR .. kR + R - 1 (R = 1024 / 4D),
+// which lie in one group, and lane l the chunk that belongs at its position. The lane's part of
+// the global offset depends only on the parity of m (the swizzle's row bit 3 at D = 128), so two
+// registers hold it; the per-instruction offsets are formed at the copy and not hoisted out of
+// the tile loop, where they would hold 2 registers per instruction.
 template <int D>
-__device__ __forceinline__ void dma_half_f32(rsrc_t r, char* half, int row0, uint32_t snb, int w, int lane, int h,
-                                             uint32_t live) {
-  constexpr int R = 1024 / (D * 4);
-  constexpr int CPR = D / 4;
-  constexpr int NI = 64 / R;
-  uint32_t base = (uint32_t)(uintptr_t)half;
-  asm volatile("" : "+s"(base));
-  const int rl = lane / CPR, pc = lane % CPR;
+struct HalfDma {
+  static constexpr int R = 1024 / (D * 4);
+  static constexpr int CPR = D / 4;
+  static constexpr int NI = 64 / R;
+  uint32_t lo[2];
+
+  __device__ __forceinline__ void init(int w, int lane, uint32_t snb, bool swizzle) {
+    const int rl = lane / CPR, pc = lane % CPR;
 #pragma unroll
-  for (int m = 0; m < NI / 4; ++m) {
-    const int k = w + 4 * m;
-    if (!(live >> (2 * h + ((k * R) >> 5)) & 1u)) continue;
-    const int row = 64 * h + k * R + rl;  // row within the tile
-    const uint32_t src = (uint32_t)(row0 + row) * snb + (uint32_t)((pc ^ swz_row3(row)) << 4);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(uintptr_t)(base + 1024u * k),
-                                             16, (int)src, 0, 0, 0);
+    for (int m = 0; m < 2; ++m) {
+      const int row = (w + 4 * m) * R + rl;  // same low bits for every h and every m of this parity
+      lo[m] = (uint32_t)rl * snb + (uint32_t)((swizzle ? pc ^ swz_row3(row) : pc) << 4);
+    }
   }
-}
+
+  __device__ __forceinline__ void issue(rsrc_t r, char* half, int row0, uint32_t snb, int w, int h,
+                                        uint32_t live) const {
+    uint32_t base = (uint32_t)(uintptr_t)half;
+    asm volatile("" : "+s"(base));
+    uint32_t l0 = lo[0], l1 = lo[1];
+    asm volatile("" : "+v"(l0), "+v"(l1));
+#pragma unroll
+    for (int m = 0; m < NI / 4; ++m) {
+      const int k = w + 4 * m;
+      if (!(live >> (2 * h + ((k * R) >> 5)) & 1u)) continue;
+      const uint32_t src = (uint32_t)(row0 + 64 * h + k * R) * snb + ((m & 1) ? l1 : l0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(uintptr_t)(base + 1024u * k),
+                                               16, (int)src, 0, 0, 0);
+    }
+  }
+};
 
 // ------------------------------------------------------------------------------------------
 // Forward, fp32. 128 KB of LDS: one workgroup per CU, 8 waves. Waves w and w + 4 share one SIMD
@@ -265,6 +281,8 @@ __global__ void __launch_bounds__(NT, 1) dq_f32_kernel(KArgs a) {
   }
   F32Offsets<D> off;
   off.init(i, g);
+  HalfDma<D> dma;
+  dma.init(w, lane, snb, true);
   f32x16 acc[D / 32];
 #pragma unroll
   for (int db = 0; db < D / 32; ++db) acc[db] = zero16();
@@ -311,8 +329,8 @@ __global__ void __launch_bounds__(NT, 1) dq_f32_kernel(KArgs a) {
   if (t0 < t1) {
     gcur = tile_groups(a, t0);
     const int kb = ((ci32_ptr)a.col)[t0];
-    dma_half_f32<D>(rK, h0, kb * BLK, snb, w, lane, 0, any_rows(gcur));
-    dma_half_f32<D>(rV, h0 + HB, kb * BLK, snb, w, lane, 0, any_rows(gcur));
+    dma.issue(rK, h0, kb * BLK, snb, w, 0, any_rows(gcur));
+    dma.issue(rV, h0 + HB, kb * BLK, snb, w, 0, any_rows(gcur));
   }
   for (int tt = t0; tt < t1; ++tt) {
     const int t = __builtin_amdgcn_readfirstlane(tt);
@@ -322,8 +340,8 @@ __global__ void __launch_bounds__(NT, 1) dq_f32_kernel(KArgs a) {
     const uint32_t live = gt >> (4 * w) & 15u;  // key groups with p = 0 throughout are skipped
     wait_vmem();      // this wave's part of half 0 of tile t, and the mask bits
     __syncthreads();  // half 0 landed; every wave is done with half 1 of tile t - 1
-    dma_half_f32<D>(rK, h1, kb * BLK, snb, w, lane, 1, any_rows(gt));
-    dma_half_f32<D>(rV, h1 + HB, kb * BLK, snb, w, lane, 1, any_rows(gt));
+    dma.issue(rK, h1, kb * BLK, snb, w, 1, any_rows(gt));
+    dma.issue(rV, h1 + HB, kb * BLK, snb, w, 1, any_rows(gt));
     if (t + 1 < t1) gcur = tile_groups(a, t + 1);
     // Fenced, so that one group's reads and MFMAs do not overlap the next group's registers.
     __builtin_amdgcn_sched_barrier(0);
@@ -335,8 +353,8 @@ __global__ void __launch_bounds__(NT, 1) dq_f32_kernel(KArgs a) {
     __syncthreads();  // half 1 landed; every wave is done with half 0
     if (t + 1 < t1) {
       const int kbn = ((ci32_ptr)a.col)[t + 1];
-      dma_half_f32<D>(rK, h0, kbn * BLK, snb, w, lane, 0, any_rows(gcur));
-      dma_half_f32<D>(rV, h0 + HB, kbn * BLK, snb, w, lane, 0, any_rows(gcur));
+      dma.issue(rK, h0, kbn * BLK, snb, w, 0, any_rows(gcur));
+      dma.issue(rV, h0 + HB, kbn * BLK, snb, w, 0, any_rows(gcur));
     }
     __builtin_amdgcn_sched_barrier(0);
     if (live & 4u) group(2, 0, h1, h1 + HB, mb);
@@ -377,6 +395,9 @@ __global__ void __launch_bounds__(NT, 1) dkv_f32_kernel(KArgs a) {
   load_frag_f32<D>(vf, make_rsrc((const float*)a.v + j.base, a.slice_bytes), krow, snb, g);
   F32Offsets<D> off;
   off.init(i, g);
+  HalfDma<D> dmaQ, dmaO;
+  dmaQ.init(w, lane, snb, true);
+  dmaO.init(w, lane, osnb, true);
   f32x16 dk[D / 32], dv[D / 32];
 #pragma unroll
   for (int db = 0; db < D / 32; ++db) {
@@ -387,8 +408,8 @@ __global__ void __launch_bounds__(NT, 1) dkv_f32_kernel(KArgs a) {
   // Half h of query block qb: the Q and dO rows (live groups only) and, by wave 0, the 64 rows'
   // lse and delta (4 bytes per lane; rows past n read zeros).
   auto copy_half = [&](char* hb, int qb, int h, uint32_t live) {
-    dma_half_f32<D>(rQ, hb, qb * BLK, snb, w, lane, h, live);
-    dma_half_f32<D>(rO, hb + HB, qb * BLK, osnb, w, lane, h, live);
+    dmaQ.issue(rQ, hb, qb * BLK, snb, w, h, live);
+    dmaO.issue(rO, hb + HB, qb * BLK, osnb, w, h, live);
     if (w == 0) {
       const int so = (qb * BLK + 64 * h + lane) * 4;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rL, (__attribute__((address_space(3))) void*)(hb + 2 * HB), 4, so, 0, 0, 0);
