@@ -3,8 +3,7 @@
 //
 // fp32 MFMA operands are one element per lane, so the second contraction's A operand (V^T, K^T,
 // Q^T, dO^T) is read element-wise straight from the row-major LDS tile; no transposed copy is
-// needed. The forward stages its tiles through registers (coalesced 16-byte loads); dQ and dK/dV
-// stream theirs in 64-row halves by LDS DMA, double-buffered.
+// needed. Tiles stream into LDS in 64-row halves by LDS DMA, double-buffered (HalfDma).
 //
 // Reference: pallas_attn.py:112-141 (forward), 161-215 (dQ, dK/dV), 274-311 (VJP driver).
 #include "attn_device.h"
@@ -18,32 +17,6 @@ using namespace dev;
 __device__ __forceinline__ int swz_row3(int row) { return (row & 3) | (((row >> 3) & 1) << 2); }
 
 // ------------------------------------------------------------------------------------------
-// fp32 staging: linear chunk mapping (coalesced), row-major tiles in LDS, optionally swizzled.
-
-// Only the rows of the 32-row groups in `live` (a uniform set) are copied; the others keep stale
-// data and must not be read. NTH threads take part.
-template <int D, int NTH = NT>
-__device__ __forceinline__ void stage_rows_f32(char* lds, rsrc_t r, int row0, uint32_t snb, int tid, bool swizzle,
-                                               uint32_t live) {
-  constexpr int C = D / 4;
-  constexpr int PER = BLK * C / NTH;
-  constexpr int ROWS = NTH / C;  // rows per iteration
-  static_assert(NTH % C == 0, "an iteration covers whole rows");
-#pragma unroll
-  for (int it = 0; it < PER; ++it) {
-    const int id = tid + it * NTH;
-    const int row = id / C, ch = id % C;
-    if constexpr (32 % ROWS == 0) {
-      if (!(live >> (it * ROWS / 32) & 1u)) continue;  // the iteration's rows lie in one group: uniform
-    } else {
-      if (!(live >> (row >> 5) & 1u)) continue;
-    }
-    const u32x4 x = bload16(r, (uint32_t)(row0 + row) * snb + (uint32_t)(16 * ch));
-    const int pc = swizzle ? (ch ^ swz_row3(row)) : ch;
-    *(u32x4*)(lds + row * (D * 4) + (pc << 4)) = x;
-  }
-}
-
 // Per-lane LDS offsets of the fp32 MFMA A operands.
 //   row[u & 3]: sigma row of this lane, chunk 2*u + g of a swizzled tile;
 //               + 128 * (u / 4) + sb * 32 * 4D.
@@ -139,87 +112,96 @@ struct HalfDma {
 
 // ------------------------------------------------------------------------------------------
 // Forward, fp32. 128 KB of LDS: one workgroup per CU, 8 waves. Waves w and w + 4 share one SIMD
-// and the query rows 32 (w % 4) ..; each takes two of the tile's four key groups (w / 4 selects
-// which) with its own online-softmax state, and the pair merges (m, l, O) through LDS at the end.
-// Two waves per SIMD overlap one's softmax and LDS reads with the other's MFMA chains.
+// and the query rows 32 (w % 4) ..; wave w + 4k takes key group 2h + k of each tile half h with
+// its own online-softmax state, and the pair merges (m, l, O) through LDS at the end. Two waves
+// per SIMD overlap one's softmax and LDS reads with the other's MFMA chains. The tile's K and V
+// rows stream in halves (rows 0-63, 64-127) through two half buffers, waves 0-3 copying K and
+// waves 4-7 V: the copy of one half runs while the other is computed.
 constexpr int NT_F32 = 512;
 
 template <int D>
 __global__ void __launch_bounds__(NT_F32, 1) fwd_f32_kernel(KArgs a) {
-  __shared__ __attribute__((aligned(16))) char smem[2 * BLK * D * 4];
-  char* ldsK = smem;                // [128][D] swizzled
-  char* ldsV = smem + BLK * D * 4;  // [128][D] plain
+  constexpr int HB = 64 * D * 4;  // bytes of 64 rows of K or V
+  __shared__ __attribute__((aligned(1024))) char h0[2 * HB];  // rows 0-63: K (swizzled) | V (plain)
+  __shared__ __attribute__((aligned(1024))) char h1[2 * HB];  // rows 64-127
   const int tid = threadIdx.x, lane = tid & 63;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int w = wid & 3, kh = wid >> 2;  // query rows 32 w .., key groups 2 kh, 2 kh + 1
+  const int w = wid & 3, kh = wid >> 2;  // query rows 32 w .., key group 2h + kh of half h
   const int i = lane & 31, g = lane >> 5;
   const Job j = decode_job(a);
   const uint32_t snb = (uint32_t)a.sn * 4;
   const rsrc_t rQ = make_rsrc((const float*)a.q + j.base, a.slice_bytes);
-  const rsrc_t rK = make_rsrc((const float*)a.k + j.base, a.slice_bytes);
-  const rsrc_t rV = make_rsrc((const float*)a.v + j.base, a.slice_bytes);
+  // Waves 0-3 copy K (swizzled), waves 4-7 V (plain).
+  const rsrc_t rKV = make_rsrc((const float*)(kh == 0 ? a.k : a.v) + j.base, a.slice_bytes);
+  const int kvo = kh == 0 ? 0 : HB;
 
   const int qrow = j.blk * BLK + 32 * w + i;
   f32x4 qf[D / 8];
   load_frag_f32<D>(qf, rQ, qrow, snb, g);
-  wait_vmem();
   F32Offsets<D> off;
   off.init(i, g);
+  HalfDma<D> dma;
+  dma.init(w, lane, snb, kh == 0);
   f32x16 o[D / 32];
 #pragma unroll
   for (int db = 0; db < D / 32; ++db) o[db] = zero16();
   SoftmaxState st{-__builtin_inff(), 0.f};
 
-  int t0, t1;
-  tile_range(a, j, t0, t1);
-  uint32_t gnext = t0 < t1 ? tile_groups(a, t0) : 0u;  // group bits, loaded a tile ahead
-  for (int tt = t0; tt < t1; ++tt) {
-    const int t = __builtin_amdgcn_readfirstlane(tt);
-    const int kb = ((ci32_ptr)a.col)[t];
-    const u32x2 mb = tile_bits(a, t, w, lane);  // lands while the tile is staged
-    const uint32_t gt = gnext;
-    if (t + 1 < t1) gnext = tile_groups(a, t + 1);
-    __syncthreads();
-    stage_rows_f32<D, NT_F32>(ldsK, rK, kb * BLK, snb, tid, true, any_rows(gt));
-    stage_rows_f32<D, NT_F32>(ldsV, rV, kb * BLK, snb, tid, false, any_rows(gt));
-    __syncthreads();
-    const uint32_t live = gt >> (4 * w + 2 * kh) & 3u;  // this wave's key groups with p = 0 throughout are skipped
-    f32x16 s[2];
+  // Key group sb of the tile from the half buffer holding it (local group sl = sb % 2).
+  auto group = [&](int sb, int sl, const char* hb, u32x2 mb) {
+    const char* ldsK = hb;
+    const char* ldsV = hb + HB;
+    f32x16 s[1];
+    s[0] = zero16();
 #pragma unroll
-    for (int k2 = 0; k2 < 2; ++k2) {
-      if (!(live >> k2 & 1u)) continue;
-      const int sb = 2 * kh + k2;
-      s[k2] = zero16();
+    for (int u = 0; u < D / 8; ++u) {
+      const f32x4 kx = *(const f32x4*)(ldsK + off.row[u & 3] + off.row_imm(sl, u));
 #pragma unroll
-      for (int u = 0; u < D / 8; ++u) {
-        const f32x4 kx = *(const f32x4*)(ldsK + off.row[u & 3] + off.row_imm(sb, u));
-#pragma unroll
-        for (int e = 0; e < 4; ++e) s[k2] = mfma_f32(kx[e], qf[u][e], s[k2]);
-      }
-#pragma unroll
-      for (int r = 0; r < 16; ++r) s[k2][r] = keep_or_ninf(s[k2][r], elem_keep(mb, sb, r));
+      for (int e = 0; e < 4; ++e) s[0] = mfma_f32(kx[e], qf[u][e], s[0]);
     }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[0][r] = keep_or_ninf(s[0][r], elem_keep(mb, sb, r));
     float corr;
-    if (live != 0u && softmax_live(s, live, st, a.c2, corr)) {
+    if (softmax_live<1>(s, 1u, st, a.c2, corr)) {
 #pragma unroll
       for (int db = 0; db < D / 32; ++db) o[db] *= corr;
     }
 #pragma unroll
-    for (int k2 = 0; k2 < 2; ++k2) {
-      if (!(live >> k2 & 1u)) continue;
-      const int sb = 2 * kh + k2;
+    for (int r = 0; r < 16; ++r) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-#pragma unroll
-        for (int db = 0; db < D / 32; ++db)
-          o[db] = mfma_f32(*(const float*)(ldsV + off.el_plain + off.el_imm(sb, r, db)), s[k2][r], o[db]);
-      }
+      for (int db = 0; db < D / 32; ++db)
+        o[db] = mfma_f32(*(const float*)(ldsV + off.el_plain + off.el_imm(sl, r, db)), s[0][r], o[db]);
     }
+  };
+
+  int t0, t1;
+  tile_range(a, j, t0, t1);
+  uint32_t gcur = 0u;
+  if (t0 < t1) {
+    gcur = tile_groups(a, t0);
+    dma.issue(rKV, h0 + kvo, ((ci32_ptr)a.col)[t0] * BLK, snb, w, 0, any_rows(gcur));
   }
-  // Merge the pair: the second wave of each SIMD hands its O, m and l over through LDS (the tiles
-  // are dead after the barrier). m is the log2-domain reference max shared by lanes i, i + 32.
-  float* xo = (float*)smem + (size_t)w * (D / 32) * 16 * 64;  // [D / 32][16][64 lanes]
-  float* xm = (float*)smem + 4 * (D / 32) * 16 * 64 + w * 128;  // [64 lanes] m, then [64 lanes] l
+  for (int tt = t0; tt < t1; ++tt) {
+    const int t = __builtin_amdgcn_readfirstlane(tt);
+    const int kb = ((ci32_ptr)a.col)[t];
+    const u32x2 mb = tile_bits(a, t, w, lane);
+    const uint32_t gt = gcur;
+    const uint32_t live = gt >> (4 * w) & 15u;  // key groups with p = 0 throughout are skipped
+    wait_vmem();      // this wave's part of half 0 of tile t, the mask bits (and Q)
+    __syncthreads();  // half 0 landed; every wave is done with half 1 of tile t - 1
+    dma.issue(rKV, h1 + kvo, kb * BLK, snb, w, 1, any_rows(gt));
+    if (t + 1 < t1) gcur = tile_groups(a, t + 1);
+    if (live >> kh & 1u) group(kh, kh, h0, mb);
+    wait_vmem();      // this wave's part of half 1
+    __syncthreads();  // half 1 landed; every wave is done with half 0
+    if (t + 1 < t1) dma.issue(rKV, h0 + kvo, ((ci32_ptr)a.col)[t + 1] * BLK, snb, w, 0, any_rows(gcur));
+    if (live >> (2 + kh) & 1u) group(2 + kh, kh, h1, mb);
+  }
+  // Merge the pair: the second wave of each SIMD hands its O, m and l over through LDS (the halves
+  // are dead after the barrier, and no copy is in flight). m is the log2-domain reference max
+  // shared by lanes i, i + 32.
+  float* xo = (float*)h0 + (size_t)w * (D / 32) * 16 * 64;  // [D / 32][16][64 lanes] per w: all of h0
+  float* xm = (float*)h1 + w * 128;                         // [64 lanes] m, then [64 lanes] l
   __syncthreads();
   if (kh == 1) {
 #pragma unroll
