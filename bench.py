@@ -536,6 +536,9 @@ def main():
       "roofline": {"bound": "mfma", "kernel": dominant, "achieved": round(achieved, 3), "peak": peak,
                    "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": traffic,
                    "traffic_source": traffic_src, "ms": round(per_solo[dominant], 4),
+                   "work": "algorithmic FLOPs over whole live 128x128 tiles; the kernels skip 32x32 groups "
+                           "without a valid element (config.live_group_fraction of them execute), so frac "
+                           "can exceed 1",
                    "timing": "solo pass: the same K steps again with every kernel on one stream (each alone on "
                              "the GPU), HIP events on that stream around each launch, split-K combine included"},
       "kernels_ms": {k_: round(v_, 4) for k_, v_ in per_kernel.items()},
