@@ -5,10 +5,11 @@
                     [--no-cpu]
 
 A step is one pass of the hot path over one batch of synthetic input: for the default workload
-(configuration 3 of BASELINE.json) the forward kernel plus the backward (delta pre-pass, then dQ
-on the main stream and dK/dV on a second stream side by side, as the package's backward runs
-them) on the refinement-6 mesh (40,962 nodes) with the 16-hop mask, 4 heads x 128, bf16 inputs,
-fp32 accumulation. Inputs are resident in HBM before the timed region. The metric is effective
+(configuration 3 of BASELINE.json) the forward kernel plus the backward as the package's backward
+runs it, on the refinement-6 mesh (40,962 nodes) with the 16-hop mask, 4 heads x 128, bf16 inputs,
+fp32 accumulation. The bf16 backward is the dS exchange: delta pre-pass, dK/dV writing dS, then dQ
+from dS, on one stream. float32 (and --no-ds) recomputes S and dP in the dQ kernel, which runs on
+the main stream beside dK/dV on a second stream. Inputs are resident in HBM before the timed region. The metric is effective
 TFLOP/s over live 128x128 tiles (14 * D * 128^2 per live tile, batch and head for fwd + bwd;
 4 * D * 128^2 for forward-only workloads). The mask build is timed separately.
 
@@ -83,6 +84,8 @@ def parse():
                  help="longest run of tiles per work item (0: chosen per launch by the library)")
   p.add_argument("--serial-bwd", action="store_true",
                  help="run dQ and then dK/dV on one stream instead of side by side on two streams")
+  p.add_argument("--no-ds", action="store_true",
+                 help="bf16: the recomputing dQ kernel beside dK/dV instead of the dS exchange")
   p.add_argument("--layout", default="node", choices=["node", "head"],
                  help="storage of q, k, v, o, dO, dq, dk, dv: node-major [B, n, H, D] (the reference's "
                       "interface) or head-major [B, H, n, D] passed as strided views")
@@ -455,13 +458,33 @@ def main():
                                         lse.data_ptr(), delta.data_ptr(), ts, dk.data_ptr(), dv.data_ptr(),
                                         ws2p if own else wsp, ws2n if own else wsn, st.cuda_stream))
 
-  # (name, launch, stream it runs on). The step: dK/dV on the side stream after delta, beside dQ
-  # (unless --serial-bwd). The solo pass: every kernel on one stream, so each has the GPU alone;
-  # the roofline entry takes the dominant kernel's duration from it.
+  # The bf16 backward's dS exchange, as the package runs it (symmetric k-hop mask: the forward
+  # list is its own transpose, so one list serves both kernels).
+  dmap = None
+  if cfg["backward"] and dtype == torch.bfloat16 and not args.no_ds and fwn.hip_attn.DS_EXCHANGE:
+    dmap = tiles.ds_map(tiles)
+  if dmap is not None:
+    dsbuf = torch.empty(max(dmap.ds_bytes(desc), 256), dtype=torch.uint8, device=dev)
+
+  def bwd_dkv_ds(st):
+    nat.check(L.fwn_attn_bwd_dkv_ds_launch(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(),
+                                           lse.data_ptr(), delta.data_ptr(), ts, dmap.struct, dk.data_ptr(),
+                                           dv.data_ptr(), dsbuf.data_ptr(), dsbuf.numel(), wsp, wsn, st.cuda_stream))
+
+  def bwd_dq_ds(st):
+    nat.check(L.fwn_attn_bwd_dq_ds_launch(desc, k.data_ptr(), dsbuf.data_ptr(), dsbuf.numel(), ts, dmap.struct,
+                                          dq.data_ptr(), wsp, wsn, st.cuda_stream))
+
+  # (name, launch, stream it runs on). The step: with the dS exchange, every kernel in order on one
+  # stream; otherwise dK/dV on the side stream after delta, beside dQ (unless --serial-bwd). The
+  # solo pass: every kernel on one stream, so each has the GPU alone; the roofline entry takes the
+  # dominant kernel's duration from it.
   solo = [("fwd", fwd, stream)]
-  if cfg["backward"]:
+  if dmap is not None:
+    solo += [("delta", bwd_delta, stream), ("dkv_ds", bwd_dkv_ds, stream), ("dq_ds", bwd_dq_ds, stream)]
+  elif cfg["backward"]:
     solo += [("delta", bwd_delta, stream), ("dq", bwd_dq, stream), ("dkv", bwd_dkv, stream)]
-  paired = solo if args.serial_bwd or not cfg["backward"] else \
+  paired = solo if args.serial_bwd or not cfg["backward"] or dmap is not None else \
       [("fwd", fwd, stream), ("delta", bwd_delta, stream), ("dkv", bwd_dkv, side), ("dq", bwd_dq, stream)]
 
   def step(kernels, ev=None):
@@ -513,9 +536,12 @@ def main():
   unit_flops = D * 128 * 128 * T * B * H  # one live tile x D, all batch members and heads
   total_flops = (14 if cfg["backward"] else 4) * unit_flops
   value = total_flops / (ms_step * 1e-3) / 1e12
-  # Algorithmic FLOPs per launch: forward 4*D per live entry; the backward's 10*D (FA2 count, S
-  # recomputed once) split as dQ kernel 4*D (dQ + half of the S/dP recompute) and dK/dV kernel 6*D.
-  algo = {"fwd": 4 * unit_flops, "dq": 4 * unit_flops, "dkv": 6 * unit_flops, "delta": 0}
+  # Algorithmic FLOPs per launch: forward 4*D per live entry; the backward's 10*D (FA2 count: S,
+  # dP, dV, dK, dQ at 2*D each). The recomputing kernels split it as dQ 4*D (dQ + half of the S/dP
+  # recompute) and dK/dV 6*D; with the dS exchange dK/dV computes S, dP, dV, dK (8*D) and dQ only
+  # dQ (2*D).
+  algo = {"fwd": 4 * unit_flops, "dq": 4 * unit_flops, "dkv": 6 * unit_flops, "delta": 0,
+          "dkv_ds": 8 * unit_flops, "dq_ds": 2 * unit_flops}
   dominant = max((k_ for k_ in per_solo if algo.get(k_)), key=lambda k_: per_solo[k_])
   achieved = algo[dominant] / (per_solo[dominant] * 1e-3) / 1e12
   peak = PEAK[cfg["dtype"]]
@@ -539,8 +565,15 @@ def main():
                    "work": "algorithmic FLOPs over whole live 128x128 tiles; the kernels skip 32x32 groups "
                            "without a valid element (config.live_group_fraction of them execute), so frac "
                            "can exceed 1",
-                   "timing": "solo pass: the same K steps again with every kernel on one stream (each alone on "
-                             "the GPU), HIP events on that stream around each launch, split-K combine included"},
+                   "timing": ("the timed pass (every kernel in order on one stream, each alone on the GPU)"
+                              if paired is solo else
+                              "solo pass: the same K steps again with every kernel on one stream (each alone on "
+                              "the GPU)") + ", HIP events on that stream around each launch, split-K combine "
+                                            "included"},
+      "backward": None if not cfg["backward"] else (
+          "dS exchange: delta, dK/dV writing dS (bf16), dQ from dS, one stream" if dmap is not None else
+          "recomputing dQ kernel" + (" then dK/dV, one stream" if args.serial_bwd else
+                                     " beside dK/dV on a second stream")),
       "kernels_ms": {k_: round(v_, 4) for k_, v_ in per_kernel.items()},
       "kernels_ms_solo": {k_: round(v_, 4) for k_, v_ in per_solo.items()},
       "kernels_tflops_solo": {k_: rate(k_, v_) for k_, v_ in per_solo.items() if algo.get(k_)},
@@ -551,6 +584,9 @@ def main():
       "step_note": "the full WN2 0.25-deg step needs jax, haiku and weathernext, which this image lacks; "
                    "run --workload c5 for the attention share of a step (24 layers x forward)",
   }
+  if dmap is not None:
+    result["ds_exchange"] = {"units": dmap.n_units, "bytes": dmap.ds_bytes(desc),
+                             "note": "dS units (32 queries x 16 keys, bf16, 1 KB) written by dK/dV, read by dQ"}
   if pair_ms is not None:
     result["backward_pair"] = {
         "ms": round(pair_ms, 4), "kernels": ["dq", "dkv"], "note": "dq and dkv side by side on two streams",

@@ -168,6 +168,32 @@ int launch_with_combine(Kind kind, Kind combine, const fwn_attn_desc* d, const K
   return FWN_OK;
 }
 
+// The dS exchange needs bf16, the forward list's half bits, and a map and buffer that match the
+// call: n_units from fwn_tiles_ds_map, one (batch, head) slice of units addressable with 32-bit
+// offsets, and ds_bytes >= batch * heads * n_units * 1024.
+int check_ds(const fwn_attn_desc* d, const fwn_ds_map* m, const void* ds, uint64_t ds_bytes, bool need_ubase,
+             bool need_tmap) {
+  if (d->dtype != FWN_BF16) return fail(FWN_ERR_UNSUPPORTED, "the dS exchange is built for bf16 only");
+  if (!m) return fail(FWN_ERR_INVALID_ARG, "ds map is null");
+  if (m->n_units < 0 || m->n_units * 1024 >= ((int64_t)1 << 31))
+    return fail(FWN_ERR_INVALID_ARG, "ds map: %lld units (at most 2^21 per (batch, head))", (long long)m->n_units);
+  if ((need_ubase && !m->ubase) || (need_tmap && !m->tmap)) return fail(FWN_ERR_INVALID_ARG, "ds map: null arrays");
+  if (!ds) return fail(FWN_ERR_INVALID_ARG, "ds is null");
+  if (((uintptr_t)ds & 255u) != 0) return fail(FWN_ERR_INVALID_ARG, "ds is not 256-byte aligned");
+  const uint64_t need = (uint64_t)d->batch * (uint64_t)d->heads * (uint64_t)m->n_units * 1024u;
+  if (ds_bytes < need)
+    return fail(FWN_ERR_INVALID_ARG, "ds holds %llu bytes, %llu needed", (unsigned long long)ds_bytes,
+                (unsigned long long)need);
+  return FWN_OK;
+}
+
+void set_ds(KArgs& a, const fwn_ds_map* m, const void* ds) {
+  a.ds = (uint16_t*)ds;
+  a.ubase = m->ubase;
+  a.tmap = m->tmap;
+  a.ds_slice_bytes = (uint32_t)(m->n_units * 1024);
+}
+
 int hip_status(hipError_t e, const char* what) {
   if (e == hipSuccess) return FWN_OK;
   return fail(FWN_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
@@ -287,6 +313,76 @@ int fwn_attn_bwd_launch(const fwn_attn_desc* desc, const void* q, const void* k,
     return rc;
   return fwn_attn_bwd_dkv_launch(desc, q, k, v, dout, lse, delta, tiles_t ? tiles_t : tiles, dk, dv, workspace,
                                  workspace_bytes, stream);
+}
+
+int fwn_attn_ds_bytes(const fwn_attn_desc* desc, const fwn_ds_map* map, uint64_t* bytes) {
+  clear_error();
+  if (int rc = check_desc(desc)) return rc;
+  if (!map || !bytes) return fail(FWN_ERR_INVALID_ARG, "map and bytes are required");
+  if (map->n_units < 0) return fail(FWN_ERR_INVALID_ARG, "ds map: negative unit count");
+  *bytes = (uint64_t)desc->batch * (uint64_t)desc->heads * (uint64_t)map->n_units * 1024u;
+  return FWN_OK;
+}
+
+int fwn_attn_bwd_dkv_ds_launch(const fwn_attn_desc* desc, const void* q, const void* k, const void* v,
+                               const void* dout, const float* lse, const float* delta, const fwn_tiles* tiles_t,
+                               const fwn_ds_map* map, void* dk, void* dv, void* ds, uint64_t ds_bytes,
+                               void* workspace, uint64_t workspace_bytes, void* stream) {
+  clear_error();
+  if (int rc = check_desc(desc)) return rc;
+  if (int rc = check_ds(desc, map, ds, ds_bytes, false, true)) return rc;
+  if (int rc = check_tensor(q, "q")) return rc;
+  if (int rc = check_tensor(k, "k")) return rc;
+  if (int rc = check_tensor(v, "v")) return rc;
+  if (int rc = check_tensor(dout, "dout")) return rc;
+  if (int rc = check_tensor(dk, "dk")) return rc;
+  if (int rc = check_tensor(dv, "dv")) return rc;
+  if (!lse || !delta) return fail(FWN_ERR_INVALID_ARG, "lse and delta are required");
+  if (int rc = check_tiles(desc, tiles_t, "tiles_t")) return rc;
+  if (int rc = check_workspace(desc, tiles_t, workspace, workspace_bytes)) return rc;
+  KArgs a = base_args(desc);
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.dout = dout;
+  a.lse = lse;
+  a.delta = delta;
+  a.out0 = dk;
+  a.out1 = dv;
+  set_tiles(a, tiles_t, workspace);
+  set_ds(a, map, ds);
+  return launch_with_combine(Kind::kDkvDs, Kind::kDkvCombine, desc, a, (hipStream_t)stream, "dkv (dS exchange)");
+}
+
+int fwn_attn_bwd_dq_ds_launch(const fwn_attn_desc* desc, const void* k, const void* ds, uint64_t ds_bytes,
+                              const fwn_tiles* tiles, const fwn_ds_map* map, void* dq, void* workspace,
+                              uint64_t workspace_bytes, void* stream) {
+  clear_error();
+  if (int rc = check_desc(desc)) return rc;
+  if (int rc = check_ds(desc, map, ds, ds_bytes, true, false)) return rc;
+  if (int rc = check_tensor(k, "k")) return rc;
+  if (int rc = check_tensor(dq, "dq")) return rc;
+  if (int rc = check_tiles(desc, tiles, "tiles")) return rc;
+  if (tiles->n_tiles > 0 && !tiles->halves)
+    return fail(FWN_ERR_TILES, "tiles: the dS exchange needs the half bits (fwn_tiles_prepare with halves)");
+  if (int rc = check_workspace(desc, tiles, workspace, workspace_bytes)) return rc;
+  KArgs a = base_args(desc);
+  a.k = k;
+  a.out0 = dq;
+  set_tiles(a, tiles, workspace);
+  set_ds(a, map, ds);
+  return launch_with_combine(Kind::kDqDs, Kind::kDqCombine, desc, a, (hipStream_t)stream, "dq (dS exchange)");
+}
+
+int fwn_attn_bwd_ds_launch(const fwn_attn_desc* desc, const void* q, const void* k, const void* v, const void* o,
+                           const void* dout, const float* lse, float* delta, const fwn_tiles* tiles,
+                           const fwn_tiles* tiles_t, const fwn_ds_map* map, void* dq, void* dk, void* dv, void* ds,
+                           uint64_t ds_bytes, void* workspace, uint64_t workspace_bytes, void* stream) {
+  if (int rc = fwn_attn_bwd_delta_launch(desc, o, dout, delta, stream)) return rc;
+  if (int rc = fwn_attn_bwd_dkv_ds_launch(desc, q, k, v, dout, lse, delta, tiles_t ? tiles_t : tiles, map, dk, dv,
+                                          ds, ds_bytes, workspace, workspace_bytes, stream))
+    return rc;
+  return fwn_attn_bwd_dq_ds_launch(desc, k, ds, ds_bytes, tiles, map, dq, workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

@@ -424,6 +424,183 @@ __global__ void __launch_bounds__(NT, 2) dq_kernel(KArgs a) {
   store_acc_bf16<D>(make_rsrc((uint16_t*)a.out0 + j.base, a.slice_bytes), qrow, snb, acc, a.scale, g);
 }
 
+// ------------------------------------------------------------------------------------------
+// The dS exchange (bf16 backward): dkv16_kernel<D, true> writes every 32 x 16 unit of dS it
+// computes, dq_ds_kernel reads it instead of recomputing S and dP.
+//
+// A unit is one dK/dV wave's 16 keys x one 32-query group of a tile, which is exactly the 16-key
+// half (key group kg / 2, half kg % 2) of one dQ wave's 32 query rows. dK/dV stores it as its
+// registers hold it, 1 KB, 16 bytes per lane: lane L' = k + 16 g writes the bf16 dS of key k for
+// queries 4g..4g+3, then 16+4g..16+4g+3. The dQ contraction runs over keys, so its B operand
+// (V_MFMA_F32_32X32X16_BF16, lane L: query L % 32, keys 8 (L / 32) .. +7) is the transpose; the
+// dQ kernel does that transpose through LDS, where it has bandwidth to spare (dK/dV has none).
+// Lane L writes chunk L to 16-byte slot p(k, g) = 16 (k / 4) + 4 (k % 4) + (g ^ (k / 4)), then
+// two transpose reads (ds_read_b64_tr_b16: lane j of a 16-lane group gets column d0 + j of 4 rows)
+// give keys 8 (L / 32) .. +3 and +4 .. +7 of query L % 32. Over 32 lanes the reads hit 4 keys x 4
+// chunks x 2 halves, distinct banks. The writes hit 16 distinct slots of a 256-byte bank line
+// both over 16 consecutive lanes and over the lane groups {l, l + 32 : l in [8m, 8m + 8)} in which
+// gfx950 serves b128 reads (a first layout that was conflict-free only for the latter measured
+// 22% bank-conflict cycles).
+constexpr int kNonTemporal = 2;  // buffer store cache policy: non-temporal (gfx950 "nt")
+
+struct DsUnit {
+  uint32_t w;       // this lane's write: byte offset of slot p(L % 16, L / 16)
+  uint32_t r0, r1;  // this lane's transpose reads: keys 8 (L / 32) .. +3 and +4 .. +7
+
+  static __device__ __forceinline__ uint32_t slot(int k, int g) {
+    return (uint32_t)(16 * (16 * (k >> 2) + 4 * (k & 3) + (g ^ (k >> 2))));
+  }
+  __device__ __forceinline__ void init(int lane) {
+    w = slot(lane & 15, lane >> 4);
+    const int gg = lane >> 4, e = (lane >> 2) & 3, q = lane & 3, k0 = 8 * (gg >> 1);
+    r0 = slot(k0 + e, q) + 8u * (gg & 1);
+    r1 = slot(k0 + 4 + e, q) + 8u * (gg & 1);
+  }
+};
+
+// dQ from the dS units (pallas_attn.py:177-184, with dS taken from the dK/dV pass instead of
+// recomputed): per work item of the forward list, dQ^T += K^T dS^T over the live 16-key halves of
+// each wave's 32 query rows. Each live half is one unit, loaded with one 16-byte load per lane
+// and transposed through this wave's 2 KB of LDS (DsUnit): no S, no dP, no exponentials, one of
+// dq_kernel's three contractions.
+//
+// K tiles are double-buffered in LDS (64 KB at D = 128, one barrier per tile), two workgroups per
+// CU. After the barrier of tile t the K rows and the dS units of tile t + 1 are requested, so
+// both arrive while tile t is computed; the column block, group and half bits and first unit of
+// tile t + 2 are read with scalar loads at the same point.
+template <int D>
+__global__ void __launch_bounds__(NT, 2) dq_ds_kernel(KArgs a) {
+  constexpr int TB = Tile<D>::BYTES;
+  __shared__ __attribute__((aligned(1024))) char lk0[TB];
+  __shared__ __attribute__((aligned(1024))) char lk1[TB];
+  __shared__ __attribute__((aligned(1024))) char lstage[4 * 2048];  // per wave: two units (a key group)
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int i = lane & 31, g = lane >> 5;
+  const Job j = decode_job(a);
+  const uint32_t snb = (uint32_t)a.sn * 2;
+  const rsrc_t rK = make_rsrc((const uint16_t*)a.k + j.base, a.slice_bytes);
+  const rsrc_t rS = make_rsrc(a.ds + (int64_t)j.bh * (a.ds_slice_bytes >> 1), a.ds_slice_bytes);
+  lds_char* st = (lds_char*)lstage + 2048 * w;
+  DsUnit du;
+  du.init(lane);
+  const int qrow = j.blk * BLK + 32 * w + i;
+  Off<D> off;
+  off.init(lane);
+  TileDma<D> dma;
+  dma.init(w, lane, snb);
+  f32x16 acc[D / 32];
+#pragma unroll
+  for (int db = 0; db < D / 32; ++db) acc[db] = zero16();
+  typedef const __attribute__((address_space(4))) int32_t* cmap_ptr;
+
+  // This wave's units of a tile: half bits 8w .. 8w + 7 of the tile's word, numbered from the
+  // tile's first unit by their rank among all of the word's set bits. Each unit is read once:
+  // non-temporal loads.
+  auto load_units = [&](u32x4 (&dst)[8], uint32_t hf, uint32_t ub) {
+    const uint32_t hw = hf >> (8 * w) & 0xffu;
+    uint32_t u = ub + (uint32_t)__builtin_popcount(hf & ((1u << (8 * w)) - 1u));
+#pragma unroll
+    for (int x = 0; x < 8; ++x)
+      if (hw >> x & 1u) {
+        dst[x] = __builtin_amdgcn_raw_buffer_load_b128(rS, 16 * lane, (int)(u * 1024u), kNonTemporal);
+        ++u;
+      }
+  };
+  // Tile t's halves of key group sb for this wave (bit h of hv), from K buffer `K`: the units
+  // through this wave's stage (the previous group's reads of it come first in program order, and
+  // LDS runs one wave's accesses in order), then the K^T operands, then the MFMAs.
+  auto group = [&](const lds_char* K, int sb, uint32_t hv, const u32x4 (&ds)[8]) {
+    typedef __attribute__((address_space(3))) u32x4* l4p;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      if (hv >> h & 1u) *(l4p)(st + 1024 * h + du.w) = ds[2 * sb + h];
+    asm volatile("" ::: "memory");
+    u32x4 kt[2][D / 32], bs[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      if (hv >> h & 1u) {
+        const u32x2 x0 = tr_read(st + 1024 * h, du.r0), x1 = tr_read(st + 1024 * h, du.r1);
+        bs[h] = u32x4{x0[0], x0[1], x1[0], x1[1]};
+#pragma unroll
+        for (int db = 0; db < D / 32; ++db) kt[h][db] = tr_operand<D>(K, off, db, sb, h);
+      }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      if (hv >> h & 1u) {
+#pragma unroll
+        for (int db = 0; db < D / 32; ++db) acc[db] = mfma_bf16(kt[h][db], bs[h], acc[db]);
+      }
+    asm volatile("" ::: "memory");
+  };
+
+  int t0, t1;
+  tile_range(a, j, t0, t1);
+  // Scalars of tile t + 1 (n1: column block, group bits, half bits, first unit) and t + 2 (n2).
+  int c1 = 0, c2 = 0;
+  uint32_t g1 = 0u, g2 = 0u, h1 = 0u, h2 = 0u, u1 = 0u, u2 = 0u;
+  u32x4 dsA[8], dsB[8];
+  uint32_t gcur = 0u, hcur = 0u;
+  auto step = [&](int tt, const lds_char* cur, lds_char* nxt, const u32x4 (&dsc)[8], u32x4 (&dsn)[8]) {
+    const int t = __builtin_amdgcn_readfirstlane(tt);
+    wait_vmem();      // this wave's part of tile t's K rows and its dS units
+    __syncthreads();  // all of tile t's K rows landed; every wave is done with tile t - 1 (buffer nxt)
+    const uint32_t gt = gcur, ht = hcur;
+    if (t + 1 < t1) {
+      dma.issue(rK, nxt, w, c1 * BLK, snb, any_rows(g1));
+      load_units(dsn, h1, u1);
+    }
+    gcur = g1;
+    hcur = h1;
+    c1 = c2;
+    g1 = g2;
+    h1 = h2;
+    u1 = u2;
+    if (t + 3 < t1) {
+      c2 = ((ci32_ptr)a.col)[t + 3];
+      g2 = tile_groups(a, t + 3);
+      h2 = tile_halves(a, t + 3);
+      u2 = (uint32_t)((cmap_ptr)a.ubase)[t + 3];
+    }
+    const uint32_t live = gt >> (4 * w) & 15u;
+    const uint32_t hw = ht >> (8 * w) & 0xffu;
+#pragma unroll
+    for (int sb = 0; sb < 4; ++sb)
+      if (live >> sb & 1u) group(cur, sb, hw >> (2 * sb) & 3u, dsc);
+  };
+  lds_char* K0 = (lds_char*)lk0;
+  lds_char* K1 = (lds_char*)lk1;
+  if (t0 < t1) {
+    const uint32_t g0 = tile_groups(a, t0), hf0 = tile_halves(a, t0);
+    dma.issue(rK, K0, w, ((ci32_ptr)a.col)[t0] * BLK, snb, any_rows(g0));
+    load_units(dsA, hf0, (uint32_t)((cmap_ptr)a.ubase)[t0]);
+    gcur = g0;
+    hcur = hf0;
+    if (t0 + 1 < t1) {
+      c1 = ((ci32_ptr)a.col)[t0 + 1];
+      g1 = tile_groups(a, t0 + 1);
+      h1 = tile_halves(a, t0 + 1);
+      u1 = (uint32_t)((cmap_ptr)a.ubase)[t0 + 1];
+    }
+    if (t0 + 2 < t1) {
+      c2 = ((ci32_ptr)a.col)[t0 + 2];
+      g2 = tile_groups(a, t0 + 2);
+      h2 = tile_halves(a, t0 + 2);
+      u2 = (uint32_t)((cmap_ptr)a.ubase)[t0 + 2];
+    }
+  }
+  for (int tt = t0; tt < t1; tt += 2) {
+    step(tt, K0, K1, dsA, dsB);
+    if (tt + 1 < t1) step(tt + 1, K1, K0, dsB, dsA);
+  }
+  if (j.part >= 0) {
+    store_bwd_partial<D>(a, j, 32 * w + i, acc, 0, g);
+    return;
+  }
+  store_acc_bf16<D>(make_rsrc((uint16_t*)a.out0 + j.base, a.slice_bytes), qrow, snb, acc, a.scale, g);
+}
+
 constexpr int NT8 = 512;  // dK/dV workgroup: 8 waves
 
 // ------------------------------------------------------------------------------------------
@@ -502,9 +679,10 @@ struct KeyWave {
   // MFMAs with the 32 transpose reads of the dV and dK operands issued between them; the
   // exponentials, masks and the P pack; the 8 dV MFMAs with dS and its pack between them; the
   // 8 dK MFMAs. Each MFMA then waits for LDS once per phase, and the wave's own LDS and VALU
-  // work runs while its MFMAs keep the matrix pipe busy.
+  // work runs while its MFMAs keep the matrix pipe busy. With `dsv`, the unit's packed dS is also
+  // left there for the caller to store (the dS exchange's unit layout).
   __device__ __forceinline__ void unit(const lds_char* Q, const lds_char* O, const lds_char* lse, const lds_char* del,
-                                       int c, uint64_t mw, bool full, int g, float c2) {
+                                       int c, uint64_t mw, bool full, int g, float c2, u32x4* dsv = nullptr) {
     typedef const __attribute__((address_space(3))) f32x4* cf4;
     const uint32_t cb = (uint32_t)(32 * c * RS);
     u32x4 qa[2][KS], oa[2][KS];
@@ -573,6 +751,7 @@ struct KeyWave {
       __builtin_amdgcn_sched_group_barrier(0x002, 2, 1);  // then dS / pack VALU work
     }
     __builtin_amdgcn_sched_barrier(0);
+    if (dsv) *dsv = db;
 #pragma unroll
     for (int n = 0; n < NB; ++n) dk[n] = mfma16(u32x4{qt[n][0][0], qt[n][0][1], qt[n][1][0], qt[n][1][1]}, db, dk[n]);
   }
@@ -630,7 +809,17 @@ __device__ __forceinline__ const uint64_t* key_mask_words(const KArgs& a, int kg
 }
 
 // 8 waves, one workgroup per CU, the Q/dO tiles double-buffered: one barrier per tile.
-template <int D>
+//
+// With DS (the bf16 backward with the dS exchange), every unit's dS also goes to HBM as one 1 KB
+// unit, 16 bytes per lane in the order the registers hold it (DsUnit). Units are numbered over
+// the forward tile list: tile tf's live halves (bit 8c + kg for query group c and 16-key group kg)
+// hold units ubase[tf] + (rank of the bit among the set bits); tmap gives (ubase, halves) of the
+// forward tile for each tile of this transposed list. The host checks that this list is the exact
+// transpose of the forward one, so the units this wave computes are exactly that tile's set bits.
+// A unit's store is issued at the start of the wave's next unit (or after its final tile), so the
+// vmcnt(0) before each tile barrier never waits for a store issued just before it; the stores are
+// non-temporal (nothing in this kernel reads them; allocating them in L2 would evict Q/dO tiles).
+template <int D, bool DS = false>
 __global__ void __launch_bounds__(NT8, 1) dkv16_kernel(KArgs a) {
   constexpr int TB = Tile<D>::BYTES;
   __shared__ __attribute__((aligned(1024))) char lds0[2 * TB + 1536];  // Q | dO | lse[128] | gap | delta[128]
@@ -671,6 +860,22 @@ __global__ void __launch_bounds__(NT8, 1) dkv16_kernel(KArgs a) {
   const uint64_t* mword = key_mask_words(a, wid, g, t16);
   const int mshift = 4 * (g & 1);
 
+  // dS exchange state: the unit computed last (its dS in dsv, its byte offset in pend; an offset
+  // of ds_slice_bytes is past the slice, so that store is dropped) and the forward tile's
+  // (ubase, halves) for the current tile, read at the end of the previous tile's step (a scalar
+  // load pending when the units start would make their first LDS wait wait for it too).
+  rsrc_t rS;
+  u32x4 dsv = {0u, 0u, 0u, 0u};
+  uint32_t pend = 0u, ubc = 0u, hfc = 0u;
+  typedef const __attribute__((address_space(4))) uint32_t* cmap_ptr;
+  if constexpr (DS) {
+    rS = make_rsrc(a.ds + (int64_t)j.bh * (a.ds_slice_bytes >> 1), a.ds_slice_bytes);
+    pend = a.ds_slice_bytes;
+  }
+  auto store_ds = [&]() {
+    if constexpr (DS) __builtin_amdgcn_raw_buffer_store_b128(dsv, rS, 16 * lane, (int)pend, kNonTemporal);
+  };
+
   // The next tile's group bits and column block are read a tile ahead (scalar loads), so issuing
   // its copy right after the barrier waits for neither.
   auto tile_step = [&](int tt, int t1, lds_char* cur, lds_char* nxt, uint64_t& mnext, uint32_t& gnext,
@@ -697,10 +902,25 @@ __global__ void __launch_bounds__(NT8, 1) dkv16_kernel(KArgs a) {
     }
     uint32_t live, full;
     KeyWave<D>::live_units(mw, live, full);
-    const lds_char* st = cur + 2 * TB;
+    const lds_char* stats = cur + 2 * TB;
 #pragma unroll
     for (int c = 0; c < 4; ++c)
-      if (live >> c & 1u) kw.unit(cur, cur + TB, st + 128 * c, st + 1024 + 128 * c, c, mw, full >> c & 1u, g, a.c2);
+      if (live >> c & 1u) {
+        if constexpr (DS) {
+          store_ds();
+          kw.unit(cur, cur + TB, stats + 128 * c, stats + 1024 + 128 * c, c, mw, full >> c & 1u, g, a.c2, &dsv);
+          const uint32_t bit = 8u * c + (uint32_t)wid;
+          pend = (ubc + (uint32_t)__builtin_popcount(hfc & ((1u << bit) - 1u))) * 1024u;
+        } else {
+          kw.unit(cur, cur + TB, stats + 128 * c, stats + 1024 + 128 * c, c, mw, full >> c & 1u, g, a.c2);
+        }
+      }
+    if constexpr (DS) {
+      if (t + 1 < t1) {
+        ubc = ((cmap_ptr)a.tmap)[2 * (t + 1)];
+        hfc = ((cmap_ptr)a.tmap)[2 * (t + 1) + 1];
+      }
+    }
   };
 
   int t0, t1;
@@ -716,12 +936,17 @@ __global__ void __launch_bounds__(NT8, 1) dkv16_kernel(KArgs a) {
       gnext = tile_groups(a, t0 + 1);
       cnext = ((ci32_ptr)a.col)[t0 + 1];
     }
+    if constexpr (DS) {
+      ubc = ((cmap_ptr)a.tmap)[2 * t0];
+      hfc = ((cmap_ptr)a.tmap)[2 * t0 + 1];
+    }
     issue(((ci32_ptr)a.col)[t0], b0, any_rows(tile_groups(a, t0)));
   }
   for (int tt = t0; tt < t1; tt += 2) {
     tile_step(tt, t1, b0, b1, mnext, gnext, cnext);
     if (tt + 1 < t1) tile_step(tt + 1, t1, b1, b0, mnext, gnext, cnext);
   }
+  store_ds();  // the last unit's dS (dropped when the wave computed none)
   kw.store(a, j, krow, 16 * wid + t16, g);
 }
 
@@ -731,7 +956,9 @@ hipError_t launch_d(Kind kind, const KArgs& a, hipStream_t stream) {
   switch (kind) {
     case Kind::kFwd: hipLaunchKernelGGL(fwd_kernel<D>, grid, block, 0, stream, a); break;
     case Kind::kDq: hipLaunchKernelGGL(dq_kernel<D>, grid, block, 0, stream, a); break;
-    case Kind::kDkv: hipLaunchKernelGGL(dkv16_kernel<D>, grid, dim3(NT8), 0, stream, a); break;
+    case Kind::kDkv: hipLaunchKernelGGL((dkv16_kernel<D, false>), grid, dim3(NT8), 0, stream, a); break;
+    case Kind::kDkvDs: hipLaunchKernelGGL((dkv16_kernel<D, true>), grid, dim3(NT8), 0, stream, a); break;
+    case Kind::kDqDs: hipLaunchKernelGGL(dq_ds_kernel<D>, grid, block, 0, stream, a); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

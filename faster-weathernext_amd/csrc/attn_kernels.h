@@ -25,6 +25,10 @@ struct KArgs {
   const int32_t* items;   // fwn_item[n_items] as int32 quadruples (block, t0, t1, part)
   const int32_t* split;   // [n_split * 3] block, first partial slot, slot count (combine pass)
   float* work;            // partial slots: [n_parts][batch * heads][128][2 * head_dim + 2] float32
+  uint16_t* ds;           // dS units (bf16 backward with the dS exchange): [batch * heads][n_units][512]
+  const int32_t* ubase;   // dq from dS: first unit of each tile of the forward list
+  const int32_t* tmap;    // dK/dV writing dS: per transposed tile, (ubase, halves) of the forward tile
+  uint32_t ds_slice_bytes;  // bytes of one (batch, head) slice of ds: n_units * 1024
   int32_t n, heads, batch, n_blocks, n_tiles, n_items, n_parts, n_split;
   int64_t sb, sn, sh;     // strides of q, k, v, dq, dk, dv
   int64_t osb, osn, osh;  // strides of o, dout
@@ -35,7 +39,9 @@ struct KArgs {
   float nlse_mul;         // -1 / scale: turns a saved lse into the initial value of an S accumulator
 };
 
-enum class Kind { kFwd, kDq, kDkv, kDelta, kFwdCombine, kDqCombine, kDkvCombine };
+// kDqDs and kDkvDs: the bf16 backward with the dS exchange (dK/dV writes each 32 x 16 dS unit,
+// the dQ kernel reads it instead of recomputing S and dP).
+enum class Kind { kFwd, kDq, kDkv, kDelta, kFwdCombine, kDqCombine, kDkvCombine, kDqDs, kDkvDs };
 
 // Kernel launchers (each enqueues one kernel and returns hipSuccess or the launch error).
 hipError_t launch_bf16(Kind kind, int head_dim, const KArgs& a, hipStream_t stream);  // attn_bf16.hip

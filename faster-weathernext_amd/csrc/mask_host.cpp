@@ -359,6 +359,86 @@ int fwn_tiles_prepare(int32_t n_blocks, int32_t n_tiles, int32_t n_cols, const i
   return FWN_OK;
 }
 
+int fwn_tiles_ds_map(int32_t n_blocks, const int32_t* tile_ptr, const int32_t* tile_col,
+                     const uint32_t* tile_bits, const int32_t* tile_ptr_t, const int32_t* tile_col_t,
+                     const uint32_t* tile_bits_t, int32_t* ubase, int32_t* tmap, int64_t* n_units) {
+  fwn::clear_error();
+  if (n_blocks <= 0 || !tile_ptr || !tile_ptr_t || !n_units)
+    return fwn::fail(FWN_ERR_INVALID_ARG, "fwn_tiles_ds_map: null or empty argument");
+  const int32_t n_tiles = tile_ptr[n_blocks], n_tiles_t = tile_ptr_t[n_blocks];
+  if (n_tiles > 0 && (!tile_col || !tile_bits || !ubase))
+    return fwn::fail(FWN_ERR_INVALID_ARG, "fwn_tiles_ds_map: null forward arrays");
+  if (n_tiles_t > 0 && (!tile_col_t || !tile_bits_t || !tmap))
+    return fwn::fail(FWN_ERR_INVALID_ARG, "fwn_tiles_ds_map: null transposed arrays");
+  const int32_t n_cols = n_blocks * FWN_BLOCK;
+  if (int rc = fwn::check_tile_list(n_blocks, n_tiles, n_cols, tile_ptr, tile_col)) return rc;
+  if (int rc = fwn::check_tile_list(n_blocks, n_tiles_t, n_cols, tile_ptr_t, tile_col_t)) return rc;
+  if (n_tiles != n_tiles_t)
+    return fwn::fail(FWN_ERR_TILES, "fwn_tiles_ds_map: %d forward tiles but %d transposed ones", n_tiles, n_tiles_t);
+  constexpr int32_t words = FWN_BLOCK / 32;
+  constexpr int64_t tile_words = (int64_t)FWN_BLOCK * words;
+  // Half bits of each forward tile (bit 8r + 2c + h: rows 32r.., columns 32c + 16h ..), as
+  // fwn_tiles_prepare computes them, and the exclusive prefix of their counts.
+  std::vector<uint32_t> halves(n_tiles);
+  parallel_for(n_tiles, 256, [&](int64_t b, int64_t e) {
+    for (int64_t t = b; t < e; ++t) {
+      const uint32_t* bits = tile_bits + t * tile_words;
+      uint32_t hv = 0;
+      for (int32_t r = 0; r < FWN_BLOCK; ++r)
+        for (int32_t x = 0; x < words; ++x) {
+          const uint32_t wd = bits[r * words + x];
+          if (wd & 0xffffu) hv |= 1u << (8 * (r / 32) + 2 * x);
+          if (wd >> 16) hv |= 1u << (8 * (r / 32) + 2 * x + 1);
+        }
+      halves[t] = hv;
+    }
+  });
+  int64_t total = 0;
+  for (int32_t t = 0; t < n_tiles; ++t) {
+    ubase[t] = (int32_t)total;
+    total += __builtin_popcount(halves[t]);
+    if (total > INT32_MAX) return fwn::fail(FWN_ERR_INVALID_ARG, "fwn_tiles_ds_map: more than 2^31 units");
+  }
+  // Each transposed tile (row block kb, column block qb) must be forward tile (qb, kb) with its
+  // bits transposed.
+  std::atomic<int64_t> bad(-1);
+  parallel_for(n_tiles_t, 64, [&](int64_t b, int64_t e) {
+    std::vector<uint32_t> tr(tile_words);
+    int32_t kb = (int32_t)(std::upper_bound(tile_ptr_t, tile_ptr_t + n_blocks + 1, (int32_t)b) - tile_ptr_t) - 1;
+    for (int64_t t = b; t < e; ++t) {
+      while (tile_ptr_t[kb + 1] <= t) ++kb;
+      const int32_t qb = tile_col_t[t];
+      const int32_t* lo = tile_col + tile_ptr[qb];
+      const int32_t* hi = tile_col + tile_ptr[qb + 1];
+      const int32_t* it = std::lower_bound(lo, hi, kb);
+      if (it == hi || *it != kb) {
+        bad = t;
+        return;
+      }
+      const int64_t tf = it - tile_col;
+      std::fill(tr.begin(), tr.end(), 0u);
+      const uint32_t* fb = tile_bits + tf * tile_words;
+      for (int32_t r = 0; r < FWN_BLOCK; ++r)
+        for (int32_t x = 0; x < words; ++x)
+          for (uint32_t wd = fb[r * words + x]; wd; wd &= wd - 1) {
+            const int32_t c = 32 * x + __builtin_ctz(wd);
+            tr[c * words + r / 32] |= 1u << (r % 32);
+          }
+      if (std::memcmp(tr.data(), tile_bits_t + t * tile_words, tile_words * sizeof(uint32_t)) != 0) {
+        bad = t;
+        return;
+      }
+      tmap[2 * t] = ubase[tf];
+      tmap[2 * t + 1] = (int32_t)halves[tf];
+    }
+  });
+  if (bad.load() >= 0)
+    return fwn::fail(FWN_ERR_TILES, "fwn_tiles_ds_map: the second list is not the transpose of the first (tile %lld)",
+                     (long long)bad.load());
+  *n_units = total;
+  return FWN_OK;
+}
+
 int fwn_tiles_schedule_count(int32_t n_blocks, const int32_t* tile_ptr, int32_t max_item_tiles,
                              int32_t* n_items, int32_t* n_parts, int32_t* n_split) {
   fwn::clear_error();

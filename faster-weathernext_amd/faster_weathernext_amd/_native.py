@@ -49,6 +49,10 @@ class Tiles(ctypes.Structure):
               ("halves", ctypes.c_void_p)]
 
 
+class DsMap(ctypes.Structure):
+  _fields_ = [("n_units", ctypes.c_int64), ("ubase", ctypes.c_void_p), ("tmap", ctypes.c_void_p)]
+
+
 ITEM_TILES = 64  # FWN_ITEM_TILES: default longest run of tiles per work item
 SCRATCH_BYTES = 64 << 20  # FWN_SCRATCH_BYTES: static scratch of fwn_attn_fwd_launch_noalloc
 
@@ -66,6 +70,7 @@ _I32, _I64, _U64, _F = ctypes.c_int32, ctypes.c_int64, ctypes.c_uint64, ctypes.c
 _DESC = ctypes.POINTER(AttnDesc)
 _TILES = ctypes.POINTER(Tiles)
 _ROWS = ctypes.POINTER(RowsDesc)
+_DS = ctypes.POINTER(DsMap)
 
 # name -> argtypes, every entry point of include/fwn_attn.h and include/fwn_rows.h
 SIGNATURES = {
@@ -85,6 +90,12 @@ SIGNATURES = {
     "fwn_attn_bwd_dq_launch": [_DESC, _P, _P, _P, _P, _P, _P, _TILES, _P, _P, _U64, _P],
     "fwn_attn_bwd_dkv_launch": [_DESC, _P, _P, _P, _P, _P, _P, _TILES, _P, _P, _P, _U64, _P],
     "fwn_attn_bwd_launch": [_DESC, _P, _P, _P, _P, _P, _P, _P, _TILES, _TILES, _P, _P, _P, _P, _U64, _P],
+    "fwn_tiles_ds_map": [_I32, _P, _P, _P, _P, _P, _P, _P, _P, _P],
+    "fwn_attn_ds_bytes": [_DESC, _DS, _P],
+    "fwn_attn_bwd_dkv_ds_launch": [_DESC, _P, _P, _P, _P, _P, _P, _TILES, _DS, _P, _P, _P, _U64, _P, _U64, _P],
+    "fwn_attn_bwd_dq_ds_launch": [_DESC, _P, _P, _U64, _TILES, _DS, _P, _P, _U64, _P],
+    "fwn_attn_bwd_ds_launch": [_DESC, _P, _P, _P, _P, _P, _P, _P, _TILES, _TILES, _DS, _P, _P, _P, _P, _U64, _P, _U64,
+                               _P],
     "fwn_rows_gather_norm_launch": [_ROWS, _P, _P, _P, _P, _P],
     "fwn_rows_norm_scatter_launch": [_ROWS, _P, _P, _P, _P, _P, _P],
     "fwn_rows_norm_affine_launch": [_ROWS, _P, _P, _P, _P, _P],

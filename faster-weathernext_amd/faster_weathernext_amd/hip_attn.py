@@ -108,6 +108,9 @@ class TileList:
     self.counts = np.diff(tile_ptr)
     self.nnz = int(np.unpackbits(tile_bits.view(np.uint8)).sum()) if self.n_tiles else 0
     self._tile_ptr = tile_ptr
+    self._tile_col = tile_kb
+    self._tile_bits = tile_bits
+    self._ds_maps = {}
     self._fixed_cap = None if max_item_tiles is None else int(max_item_tiles)
     self._schedules = {}
     base = self._schedule(nat.ITEM_TILES if self._fixed_cap is None else self._fixed_cap)
@@ -144,6 +147,17 @@ class TileList:
     nat.check(nat.lib().fwn_attn_workspace_size(desc, self.struct_for(desc.batch, desc.heads), ctypes.byref(n)))
     return int(n.value)
 
+  def ds_map(self, tiles_t):
+    """The dS exchange's unit numbering of this (forward) list and `tiles_t` (this list itself
+    for a symmetric mask), or None when `tiles_t` is not this list's exact transpose; built on
+    first use and kept with this list."""
+    key = id(tiles_t)
+    hit = self._ds_maps.get(key)
+    if hit is None or hit[0] is not tiles_t:
+      hit = (tiles_t, DsMap.build(self, tiles_t))
+      self._ds_maps[key] = hit
+    return hit[1]
+
   @classmethod
   def from_mask(cls, mask, perm=None, device="cuda", max_item_tiles=None):
     """Tile list of a boolean scipy/numpy [n, n] mask (optionally permuted as mask[perm][:, perm])."""
@@ -164,6 +178,46 @@ class TileList:
     bits = np.unpackbits((self.groups_host & 0xFFFF).astype('<u4').view(np.uint8)).sum()
     return float(bits) / (16 * self.n_tiles)
 
+
+class DsMap:
+  """Unit numbering of the bf16 backward's dS exchange (``fwn_tiles_ds_map``): the dK/dV kernel
+  writes each 32-query x 16-key unit of dS = P (dP - delta) once, and the dQ kernel reads it
+  instead of recomputing S and dP (5 contractions per live tile instead of 7). Units are the set
+  bits of the forward list's half words, numbered tile by tile; ``struct`` is the C view."""
+
+  def __init__(self, n_units, ubase, tmap, device):
+    self.n_units = int(n_units)
+    self.ubase = torch.from_numpy(ubase).to(device)
+    self.tmap = torch.from_numpy(tmap).to(device)
+    addr = lambda t: t.data_ptr() if t.numel() else None
+    self.struct = nat.DsMap(self.n_units, addr(self.ubase), addr(self.tmap))
+
+  @classmethod
+  def build(cls, tl, tlt):
+    """The map of forward list `tl` and transposed list `tlt`, or None if `tlt` is not the
+    transpose of `tl` bit for bit (the recomputing backward applies then)."""
+    if tl.n_blocks != tlt.n_blocks or tl.n_cols != tlt.n_cols or tl.device != tlt.device:
+      return None
+    ubase = np.zeros(max(tl.n_tiles, 1), np.int32)
+    tmap = np.zeros((max(tlt.n_tiles, 1), 2), np.int32)
+    n_units = np.zeros(1, np.int64)
+    status = nat.lib().fwn_tiles_ds_map(tl.n_blocks, nat.ptr(tl._tile_ptr), nat.ptr(tl._tile_col),
+                                        nat.ptr(tl._tile_bits), nat.ptr(tlt._tile_ptr), nat.ptr(tlt._tile_col),
+                                        nat.ptr(tlt._tile_bits), nat.ptr(ubase), nat.ptr(tmap), nat.ptr(n_units))
+    if status == nat.ERR_TILES:
+      return None
+    nat.check(status)
+    return cls(n_units[0], ubase[:tl.n_tiles], tmap[:tlt.n_tiles], tl.device)
+
+  def ds_bytes(self, desc):
+    n = ctypes.c_uint64(0)
+    nat.check(nat.lib().fwn_attn_ds_bytes(desc, self.struct, ctypes.byref(n)))
+    return int(n.value)
+
+
+# The bf16 backward uses the dS exchange (DsMap) when the lists allow it; False keeps the
+# recomputing dQ kernel beside dK/dV for every call.
+DS_EXCHANGE = True
 
 _cache_lock = threading.Lock()
 _cache = collections.OrderedDict()
@@ -284,19 +338,38 @@ def _side_stream(device):
 
 
 def _backward_into(q, k, v, out, lse, dout, tiles, tiles_t, scale, dq, dk, dv):
-  """Backward kernels writing dq, dk, dv (q's strides): the delta pre-pass, then dQ on the current
-  stream and dK/dV on a side stream at the same time (each with its own workspace), joined
-  before returning. The two kernels are independent; run side by side, each fills the CUs the
-  other's last workgroups leave idle (C3: 1.89 -> 1.79 ms per fwd+bwd step). The sequence is
-  what fwn_attn_bwd_launch enqueues on one stream, with the dQ and dK/dV launches overlapped."""
+  """Backward kernels writing dq, dk, dv (q's strides).
+
+  bfloat16, with `tiles_t` the exact transpose of `tiles` (a symmetric mask with tiles_t None
+  included): the dS exchange, in stream order on the current stream (fwn_attn_bwd_ds_launch):
+  delta, dK/dV writing every 32 x 16 unit of dS, then dQ from dS. The reference computes S and dP
+  in both of its backward kernels (pallas_attn.py:172-180, 199-207); here once (C3: 1.71 -> 1.58
+  ms per fwd+bwd step, C4 7.87 -> 6.97 ms).
+
+  Otherwise (float32, lists that are not transposes, DS_EXCHANGE False): the delta pre-pass, then
+  the recomputing dQ kernel on the current stream and dK/dV on a side stream at the same time
+  (each with its own workspace), joined before returning. Run side by side, each fills the CUs the
+  other's last workgroups leave idle. The sequence is what fwn_attn_bwd_launch enqueues on one
+  stream, with the dQ and dK/dV launches overlapped."""
   desc = _desc(q, scale, out)
   n = q.shape[1]
   tl = _as_tiles(tiles, n, q.device)
   tlt = tl if tiles_t is None else _as_tiles(tiles_t, n, q.device)
   delta = torch.empty_like(lse)
-  ws_q, ws_kv = workspace(desc, q.device, tl), workspace(desc, q.device, tlt)
   L = nat.lib()
   main = torch.cuda.current_stream(q.device)
+  dmap = tl.ds_map(tlt) if DS_EXCHANGE and q.dtype == torch.bfloat16 else None
+  if dmap is not None:
+    # delta, dK/dV writing dS, then dQ from dS, in stream order (fwn_attn_bwd_ds_launch).
+    ws = workspace(desc, q.device, tl, tlt)
+    ds = torch.empty(max(dmap.ds_bytes(desc), 256), dtype=torch.uint8, device=q.device)
+    ts, tst = tl.struct_for(desc.batch, desc.heads), tlt.struct_for(desc.batch, desc.heads)
+    nat.check(L.fwn_attn_bwd_ds_launch(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                                       dout.data_ptr(), lse.data_ptr(), delta.data_ptr(), ts, tst, dmap.struct,
+                                       dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ds.data_ptr(), ds.numel(),
+                                       *_ws_args(ws), main.cuda_stream))
+    return
+  ws_q, ws_kv = workspace(desc, q.device, tl), workspace(desc, q.device, tlt)
   nat.check(L.fwn_attn_bwd_delta_launch(desc, out.data_ptr(), dout.data_ptr(), delta.data_ptr(), main.cuda_stream))
   side = _side_stream(q.device)
   side.wait_stream(main)

@@ -226,6 +226,60 @@ int fwn_attn_bwd_launch(const fwn_attn_desc* desc, const void* q, const void* k,
                         const fwn_tiles* tiles, const fwn_tiles* tiles_t, void* dq, void* dk,
                         void* dv, void* workspace, uint64_t workspace_bytes, void* stream);
 
+/* ---------------------------------------------------------------------------------------------
+ * bfloat16 backward with the dS exchange. The reference computes S and dP twice per live tile,
+ * once for dQ and once for dK/dV (pallas_attn.py:172-180, 199-207). Here the dK/dV kernel also
+ * writes dS = P (dP - delta) as bf16, and the dQ kernel computes dQ = scale * dS K from it:
+ * 5 contractions per tile instead of 7. dS is written and read in units of 32 query rows x 16
+ * keys (1 KB), one per 16-key half of a 32 x 32 group with a valid element (the forward list's
+ * halves bits), numbered over the forward list. The two lists must be exact transposes of each
+ * other, bit for bit (fwn_tiles_ds_map checks this); dQ then equals the recomputing dq kernel's
+ * up to the rounding order of S.
+ * ------------------------------------------------------------------------------------------- */
+
+/* Unit numbering of a forward tile list and its transposed list (device arrays). */
+typedef struct fwn_ds_map {
+  int64_t n_units;       /* units of the forward list: the set bits of all its halves words */
+  const int32_t* ubase;  /* [tiles->n_tiles] first unit of each forward tile */
+  const int32_t* tmap;   /* [tiles_t->n_tiles][2]: for each transposed tile, ubase and the halves
+                            word (as int32) of the same tile of the forward list */
+} fwn_ds_map;
+
+/* Builds the unit numbering (host arrays) from the canonical arrays of both lists (tile_ptr,
+ * tile_col, tile_bits as fwn_tiles_fill writes them, n_blocks row blocks each, n = n_blocks * 128
+ * or fewer nodes): ubase[n_tiles], tmap[n_tiles_t * 2], *n_units. Returns FWN_ERR_TILES when the
+ * second list is not the transpose of the first (a tile or a bit differs); the recomputing
+ * backward (fwn_attn_bwd_launch) is then the one that applies. No reference counterpart. */
+int fwn_tiles_ds_map(int32_t n_blocks, const int32_t* tile_ptr, const int32_t* tile_col,
+                     const uint32_t* tile_bits, const int32_t* tile_ptr_t, const int32_t* tile_col_t,
+                     const uint32_t* tile_bits_t, int32_t* ubase, int32_t* tmap, int64_t* n_units);
+
+/* Bytes of the dS buffer: batch * heads * n_units * 1024 (256-byte aligned device memory). */
+int fwn_attn_ds_bytes(const fwn_attn_desc* desc, const fwn_ds_map* map, uint64_t* bytes);
+
+/* dk, dv as fwn_attn_bwd_dkv_launch (bf16 only), and every dS unit into `ds`
+ * (pallas_attn.py:187-215). */
+int fwn_attn_bwd_dkv_ds_launch(const fwn_attn_desc* desc, const void* q, const void* k,
+                               const void* v, const void* dout, const float* lse,
+                               const float* delta, const fwn_tiles* tiles_t, const fwn_ds_map* map,
+                               void* dk, void* dv, void* ds, uint64_t ds_bytes, void* workspace,
+                               uint64_t workspace_bytes, void* stream);
+
+/* dq = scale * dS K over the forward list from the units fwn_attn_bwd_dkv_ds_launch wrote
+ * (bf16 only; replaces pallas_attn._bwd_dq_kernel, pallas_attn.py:161-184, in this mode). */
+int fwn_attn_bwd_dq_ds_launch(const fwn_attn_desc* desc, const void* k, const void* ds,
+                              uint64_t ds_bytes, const fwn_tiles* tiles, const fwn_ds_map* map,
+                              void* dq, void* workspace, uint64_t workspace_bytes, void* stream);
+
+/* Whole backward in this mode: delta, dk/dv (+ dS), then dq, in stream order
+ * (pallas_attn._attention_bwd, pallas_attn.py:274-311). `ds` holds fwn_attn_ds_bytes; the
+ * workspace holds the larger of the two lists' sizes. */
+int fwn_attn_bwd_ds_launch(const fwn_attn_desc* desc, const void* q, const void* k, const void* v,
+                           const void* o, const void* dout, const float* lse, float* delta,
+                           const fwn_tiles* tiles, const fwn_tiles* tiles_t, const fwn_ds_map* map,
+                           void* dq, void* dk, void* dv, void* ds, uint64_t ds_bytes,
+                           void* workspace, uint64_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -287,12 +287,13 @@ def _without_halves(tiles):
 
 
 @pytest.mark.parametrize("d", [32, 64, 128])
-def test_half_skipping_is_exact(d):
+def test_half_skipping_is_exact(d, monkeypatch):
   """Skipping the 16-column halves of live 32 x 32 groups that hold no valid element (the bf16
-  dQ kernel) only drops terms that are exact zeros: outputs and gradients are bitwise those of
-  the same list without half bits, and both match the dense oracle. The designed pattern has
-  live groups with one dead half; the random sparse mask has many."""
+  recomputing dQ kernel) only drops terms that are exact zeros: outputs and gradients are bitwise
+  those of the same list without half bits, and both match the dense oracle. The designed pattern
+  has live groups with one dead half; the random sparse mask has many."""
   print(f"half skipping d={d}", flush=True)
+  monkeypatch.setattr(fwn.hip_attn, "DS_EXCHANGE", False)
   dtype = torch.bfloat16
   rng = np.random.default_rng(70 + d)
   for m in (_group_pattern_mask(21), _random_mask(640, 0.004, 71, symmetric=True)):
@@ -311,6 +312,87 @@ def test_half_skipping_is_exact(d):
     _check(got["out"], A.dense_attention(q, k, v, dense, d ** -0.5), dtype, "out")
     for name, r in zip(("dq", "dk", "dv"), A.dense_grads(q, k, v, do, dense, d ** -0.5)):
       _check(got[name], r, dtype, name)
+
+
+def _run_modes(q, k, v, do, tiles, scale, dtype, tiles_t, monkeypatch):
+  """The backward with the dS exchange (the default for bf16) and with the recomputing dQ kernel."""
+  got = _run(q, k, v, do, tiles, scale, dtype, tiles_t)
+  monkeypatch.setattr(fwn.hip_attn, "DS_EXCHANGE", False)
+  ref = _run(q, k, v, do, tiles, scale, dtype, tiles_t)
+  monkeypatch.setattr(fwn.hip_attn, "DS_EXCHANGE", True)
+  return got, ref
+
+
+@pytest.mark.parametrize("d", [32, 64, 128])
+@pytest.mark.parametrize("case", ["symmetric", "transposed", "split", "groups"])
+def test_ds_exchange_matches_recompute_and_oracle(case, d, monkeypatch):
+  """bf16 backward with the dS exchange: the dK/dV kernel writes every 32 x 16 unit of dS and the
+  dQ kernel reads it (5 contractions per tile instead of 7). dK and dV come from the same kernel
+  arithmetic as without the exchange, bit for bit; dQ differs from the recomputing kernel's only
+  in the rounding order of S (the two kernels contract it in different MFMA shapes) and both meet
+  the bars against the dense float64 oracle. Cases: a symmetric mask (one list) with rows and
+  columns without a valid element, a non-symmetric mask with its transposed list, split
+  schedules (items of 1 and 3 tiles, so partial dQ and dK/dV slots are combined) and the
+  designed group/half patterns (non-symmetric)."""
+  print(f"ds exchange {case} d={d}", flush=True)
+  dtype = torch.bfloat16
+  rng = np.random.default_rng(80 + d)
+  n, b, h = 700, 2, 2
+  tiles_t = None
+  if case == "groups":
+    m = _group_pattern_mask(22)
+    n = m.shape[0]
+  else:
+    m = _random_mask(n, 0.02, 81, symmetric=case != "transposed")
+  if case == "symmetric":
+    m = m.tolil()
+    for r in (5, 300):
+      m[r, :] = False
+      m[:, r] = False
+    m = m.tocsr()
+    m.eliminate_zeros()
+  cap = 1 if case == "split" else None
+  tiles = fwn.TileList.from_mask(m, max_item_tiles=cap)
+  if case in ("transposed", "groups"):
+    tiles_t = fwn.TileList.from_mask(m.T.tocsr())
+  if case == "split":
+    tiles_t = fwn.TileList.from_mask(m, max_item_tiles=3)
+    assert tiles.n_split > 0 and tiles_t.n_split > 0
+  assert tiles.ds_map(tiles if tiles_t is None else tiles_t) is not None
+  q, k, v, do = (_rounded(rng.standard_normal((b, n, h, d)), dtype) for _ in range(4))
+  got, ref = _run_modes(q, k, v, do, tiles, d ** -0.5, dtype, tiles_t, monkeypatch)
+  for name in ("out", "dk", "dv"):
+    np.testing.assert_array_equal(got[name], ref[name], err_msg=name)
+  assert A.rel_rms(got["dq"], ref["dq"]) < 1e-3, A.rel_rms(got["dq"], ref["dq"])
+  # Rows and columns cleared in the symmetric case get zero gradients; the oracle runs on the rest.
+  keep = np.flatnonzero(m.getnnz(1) > 0)
+  empty = np.setdiff1d(np.arange(n), keep)
+  for name in ("dq", "dk", "dv"):
+    np.testing.assert_array_equal(got[name][:, empty], 0.0)
+  sub = m.toarray()[np.ix_(keep, keep)]
+  xs = (x[:, keep] for x in (q, k, v, do))
+  for name, r in zip(("dq", "dk", "dv"), A.dense_grads(*xs, sub, d ** -0.5)):
+    for res in (got, ref):
+      _check(res[name][:, keep], r, dtype, name)
+
+
+def test_ds_exchange_falls_back_for_a_list_that_is_not_the_transpose(monkeypatch):
+  """A non-symmetric mask run without its transposed list (the reference's tiles_t=None) is not
+  a transpose pair, so the dS exchange does not apply and the bf16 backward recomputes dQ: dQ
+  is right, dK is what the forward list gives (wrong for this mask, as in the reference)."""
+  rng = np.random.default_rng(90)
+  n, h, d = 300, 1, 64
+  dtype = torch.bfloat16
+  q, k, v, do = (_rounded(rng.standard_normal((1, n, h, d)), dtype) for _ in range(4))
+  m = _random_mask(n, 0.05, 91)
+  tiles = fwn.TileList.from_mask(m)
+  assert tiles.ds_map(tiles) is None
+  got, ref = _run_modes(q, k, v, do, tiles, d ** -0.5, dtype, None, monkeypatch)
+  for name in got:
+    np.testing.assert_array_equal(got[name], ref[name], err_msg=name)
+  dense = A.dense_grads(q, k, v, do, m.toarray(), d ** -0.5)
+  _check(got["dq"], dense[0], dtype, "dq")
+  assert A.max_rel_err(got["dk"], dense[1]) > 1e-1
 
 
 def test_packed_qkv_strides_through_c_abi():

@@ -28,12 +28,13 @@ def _ws_size(desc, *lists):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("split", [False, True])
-def test_bwd_launch_one_stream(split, dtype):
+def test_bwd_launch_one_stream(split, dtype, monkeypatch):
   """fwn_attn_bwd_launch (delta, dq, then dk/dv on one stream, one workspace sized for the larger
   of the two lists) on a non-symmetric mask with its transposed list. Split schedules cut every
   block into items of at most 2 (forward list) and 3 (transposed list) tiles. The results equal
-  the package's backward (the same kernels on two streams, each with its own workspace) bit for
-  bit and the dense float64 oracle within the bars."""
+  the package's recomputing backward (the same kernels on two streams, each with its own
+  workspace) bit for bit and the dense float64 oracle within the bars."""
+  monkeypatch.setattr(fwn.hip_attn, "DS_EXCHANGE", False)
   rng = np.random.default_rng(60)
   b, n, h, d = 2, 700, 2, 64
   q, k, v, do = (rounded(rng.standard_normal((b, n, h, d)), dtype) for _ in range(4))
@@ -66,8 +67,9 @@ def test_bwd_launch_one_stream(split, dtype):
     check(host(got), want, dtype, name)
 
 
-def test_bwd_launch_without_transposed_list_uses_the_forward_list():
+def test_bwd_launch_without_transposed_list_uses_the_forward_list(monkeypatch):
   """tiles_t = NULL means the forward list (a symmetric mask), as the reference's tiles_t=None."""
+  monkeypatch.setattr(fwn.hip_attn, "DS_EXCHANGE", False)
   rng = np.random.default_rng(62)
   b, n, h, d = 1, 400, 2, 32
   q, k, v, do = (rounded(rng.standard_normal((b, n, h, d)), torch.bfloat16) for _ in range(4))
@@ -88,6 +90,63 @@ def test_bwd_launch_without_transposed_list_uses_the_forward_list():
   torch.cuda.synchronize()
   for name, got, want in zip(("dq", "dk", "dv"), (dq, dk, dv), ref):
     np.testing.assert_array_equal(host(got), host(want), err_msg=name)
+
+
+@pytest.mark.parametrize("split", [False, True])
+def test_bwd_ds_launch_one_stream(split):
+  """fwn_attn_bwd_ds_launch (delta, dk/dv writing dS, then dq from dS, on one stream) on a
+  non-symmetric bf16 mask with its transposed list, through the C ABI with the map from
+  fwn_tiles_ds_map: equal bit for bit to the package's backward (which takes the same path),
+  dK and dV equal to fwn_attn_bwd_launch's, all within the bars of the dense float64 oracle.
+  The dS buffer starts as NaN bytes: every unit the dQ kernel reads was written."""
+  rng = np.random.default_rng(66)
+  dtype = torch.bfloat16
+  b, n, h, d = 2, 700, 2, 128
+  q, k, v, do = (rounded(rng.standard_normal((b, n, h, d)), dtype) for _ in range(4))
+  m = random_mask(n, 0.05, 67, symmetric=False)
+  cap, cap_t = (2, 3) if split else (1 << 20, 1 << 20)
+  tiles = fwn.TileList.from_mask(m, max_item_tiles=cap)
+  tiles_t = fwn.TileList.from_mask(m.T.tocsr(), max_item_tiles=cap_t)
+  dmap = tiles.ds_map(tiles_t)
+  assert dmap is not None and dmap.n_units > 0
+  qd, kd, vd, dod = (dev(x, dtype) for x in (q, k, v, do))
+  scale = d ** -0.5
+  out, lse = fwn.attention_forward(qd, kd, vd, tiles, scale)
+  desc = nat.AttnDesc(b, n, h, d, nat.BF16, scale, *qd.stride()[:3])
+  size = _ws_size(desc, tiles, tiles_t)
+  ws = torch.full((max(size, 1),), 255, dtype=torch.uint8, device="cuda")
+  nbytes = dmap.ds_bytes(desc)
+  assert nbytes == b * h * dmap.n_units * 1024
+  ds = torch.full((nbytes,), 0xFF, dtype=torch.uint8, device="cuda")
+  stream = torch.cuda.current_stream().cuda_stream
+  L = nat.lib()
+
+  def grads(ds_mode):
+    delta = torch.full((b, h, n), float("nan"), device="cuda")
+    dq, dk, dv = (torch.full_like(qd, float("nan")) for _ in range(3))
+    if ds_mode:
+      nat.check(L.fwn_attn_bwd_ds_launch(desc, qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), out.data_ptr(),
+                                         dod.data_ptr(), lse.data_ptr(), delta.data_ptr(), tiles.struct,
+                                         tiles_t.struct, dmap.struct, dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                                         ds.data_ptr(), nbytes, ws.data_ptr() if size else None, size, stream))
+    else:
+      nat.check(L.fwn_attn_bwd_launch(desc, qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), out.data_ptr(),
+                                      dod.data_ptr(), lse.data_ptr(), delta.data_ptr(), tiles.struct, tiles_t.struct,
+                                      dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr() if size else None,
+                                      size, stream))
+    return dq, dk, dv
+
+  got = grads(True)
+  recompute = grads(False)
+  ref = fwn.attention_backward(qd, kd, vd, out, lse, dod, tiles, tiles_t, scale)
+  torch.cuda.synchronize()
+  for name, x, want in zip(("dq", "dk", "dv"), got, ref):
+    np.testing.assert_array_equal(host(x), host(want), err_msg=name)
+  for name, x, want in zip(("dk", "dv"), got[1:], recompute[1:]):
+    np.testing.assert_array_equal(host(x), host(want), err_msg=name)
+  dense = A.dense_grads(q, k, v, do, m.toarray(), scale)
+  for name, x, want in zip(("dq", "dk", "dv"), got, dense):
+    check(host(x), want, dtype, name)
 
 
 def test_graph_capture_replays_match_eager():
