@@ -7,9 +7,9 @@
 A step is one pass of the hot path over one batch of synthetic input: for the default workload
 (configuration 3 of BASELINE.json) the forward kernel plus the backward as the package's backward
 runs it, on the refinement-6 mesh (40,962 nodes) with the 16-hop mask, 4 heads x 128, bf16 inputs,
-fp32 accumulation. The bf16 backward is the dS exchange: delta pre-pass, dK/dV writing dS, then dQ
-from dS, on one stream. float32 (and --no-ds) recomputes S and dP in the dQ kernel, which runs on
-the main stream beside dK/dV on a second stream. Inputs are resident in HBM before the timed region. The metric is effective
+fp32 accumulation. The backward is the dS exchange: delta pre-pass, dK/dV writing dS, then dQ
+from dS, on one stream. With --no-ds the dQ kernel recomputes S and dP and runs on the main stream
+beside dK/dV on a second stream. Inputs are resident in HBM before the timed region. The metric is effective
 TFLOP/s over live 128x128 tiles (14 * D * 128^2 per live tile, batch and head for fwd + bwd;
 4 * D * 128^2 for forward-only workloads). The mask build is timed separately.
 
@@ -85,7 +85,7 @@ def parse():
   p.add_argument("--serial-bwd", action="store_true",
                  help="run dQ and then dK/dV on one stream instead of side by side on two streams")
   p.add_argument("--no-ds", action="store_true",
-                 help="bf16: the recomputing dQ kernel beside dK/dV instead of the dS exchange")
+                 help="the recomputing dQ kernel beside dK/dV instead of the dS exchange")
   p.add_argument("--layout", default="node", choices=["node", "head"],
                  help="storage of q, k, v, o, dO, dq, dk, dv: node-major [B, n, H, D] (the reference's "
                       "interface) or head-major [B, H, n, D] passed as strided views")
@@ -461,8 +461,8 @@ def main():
   # The bf16 backward's dS exchange, as the package runs it (symmetric k-hop mask: the forward
   # list is its own transpose, so one list serves both kernels).
   dmap = None
-  if cfg["backward"] and dtype == torch.bfloat16 and not args.no_ds and fwn.hip_attn.DS_EXCHANGE:
-    dmap = tiles.ds_map(tiles)
+  if cfg["backward"] and not args.no_ds and fwn.hip_attn.DS_EXCHANGE:
+    dmap = tiles.ds_map(tiles, fwn.hip_attn.unit_keys_for(dtype))
   if dmap is not None:
     dsbuf = torch.empty(max(dmap.ds_bytes(desc), 256), dtype=torch.uint8, device=dev)
 
@@ -571,7 +571,7 @@ def main():
                               "the GPU)") + ", HIP events on that stream around each launch, split-K combine "
                                             "included"},
       "backward": None if not cfg["backward"] else (
-          "dS exchange: delta, dK/dV writing dS (bf16), dQ from dS, one stream" if dmap is not None else
+          "dS exchange: delta, dK/dV writing dS, dQ from dS, one stream" if dmap is not None else
           "recomputing dQ kernel" + (" then dK/dV, one stream" if args.serial_bwd else
                                      " beside dK/dV on a second stream")),
       "kernels_ms": {k_: round(v_, 4) for k_, v_ in per_kernel.items()},
@@ -586,7 +586,9 @@ def main():
   }
   if dmap is not None:
     result["ds_exchange"] = {"units": dmap.n_units, "bytes": dmap.ds_bytes(desc),
-                             "note": "dS units (32 queries x 16 keys, bf16, 1 KB) written by dK/dV, read by dQ"}
+                             "note": "dS units written by dK/dV, read by dQ: " +
+                                     ("32 queries x 16 keys, bf16, 1 KB" if dmap.unit_keys == 16 else
+                                      "32 queries x 32 keys, float32, 4 KB")}
   if pair_ms is not None:
     result["backward_pair"] = {
         "ms": round(pair_ms, 4), "kernels": ["dq", "dkv"], "note": "dq and dkv side by side on two streams",

@@ -168,19 +168,26 @@ int launch_with_combine(Kind kind, Kind combine, const fwn_attn_desc* d, const K
   return FWN_OK;
 }
 
-// The dS exchange needs bf16, the forward list's half bits, and a map and buffer that match the
-// call: n_units from fwn_tiles_ds_map, one (batch, head) slice of units addressable with 32-bit
-// offsets, and ds_bytes >= batch * heads * n_units * 1024.
+// Bytes of one dS unit: 32 queries x 16 keys of bf16, or 32 x 32 of float32.
+int64_t ds_unit_bytes(const fwn_ds_map* m) { return m->unit_keys == 16 ? 1024 : 4096; }
+
+// The dS exchange needs a map and buffer that match the call: the unit size of the dtype (16
+// keys for bf16, 32 for float32), n_units from fwn_tiles_ds_map, one (batch, head) slice of
+// units addressable with 32-bit offsets, and ds_bytes >= batch * heads * n_units * unit bytes.
 int check_ds(const fwn_attn_desc* d, const fwn_ds_map* m, const void* ds, uint64_t ds_bytes, bool need_ubase,
              bool need_tmap) {
-  if (d->dtype != FWN_BF16) return fail(FWN_ERR_UNSUPPORTED, "the dS exchange is built for bf16 only");
   if (!m) return fail(FWN_ERR_INVALID_ARG, "ds map is null");
-  if (m->n_units < 0 || m->n_units * 1024 >= ((int64_t)1 << 31))
-    return fail(FWN_ERR_INVALID_ARG, "ds map: %lld units (at most 2^21 per (batch, head))", (long long)m->n_units);
+  const int32_t want = d->dtype == FWN_BF16 ? 16 : 32;
+  if (m->unit_keys != want)
+    return fail(FWN_ERR_INVALID_ARG, "ds map: unit_keys %d, the %s exchange uses %d", m->unit_keys,
+                d->dtype == FWN_BF16 ? "bf16" : "float32", want);
+  if (m->n_units < 0 || m->n_units * ds_unit_bytes(m) >= ((int64_t)1 << 31))
+    return fail(FWN_ERR_INVALID_ARG, "ds map: %lld units of %lld bytes (a (batch, head) slice must stay below 2 GiB)",
+                (long long)m->n_units, (long long)ds_unit_bytes(m));
   if ((need_ubase && !m->ubase) || (need_tmap && !m->tmap)) return fail(FWN_ERR_INVALID_ARG, "ds map: null arrays");
   if (!ds) return fail(FWN_ERR_INVALID_ARG, "ds is null");
   if (((uintptr_t)ds & 255u) != 0) return fail(FWN_ERR_INVALID_ARG, "ds is not 256-byte aligned");
-  const uint64_t need = (uint64_t)d->batch * (uint64_t)d->heads * (uint64_t)m->n_units * 1024u;
+  const uint64_t need = (uint64_t)d->batch * (uint64_t)d->heads * (uint64_t)(m->n_units * ds_unit_bytes(m));
   if (ds_bytes < need)
     return fail(FWN_ERR_INVALID_ARG, "ds holds %llu bytes, %llu needed", (unsigned long long)ds_bytes,
                 (unsigned long long)need);
@@ -191,7 +198,7 @@ void set_ds(KArgs& a, const fwn_ds_map* m, const void* ds) {
   a.ds = (uint16_t*)ds;
   a.ubase = m->ubase;
   a.tmap = m->tmap;
-  a.ds_slice_bytes = (uint32_t)(m->n_units * 1024);
+  a.ds_slice_bytes = (uint32_t)(m->n_units * ds_unit_bytes(m));
 }
 
 int hip_status(hipError_t e, const char* what) {
@@ -320,7 +327,9 @@ int fwn_attn_ds_bytes(const fwn_attn_desc* desc, const fwn_ds_map* map, uint64_t
   if (int rc = check_desc(desc)) return rc;
   if (!map || !bytes) return fail(FWN_ERR_INVALID_ARG, "map and bytes are required");
   if (map->n_units < 0) return fail(FWN_ERR_INVALID_ARG, "ds map: negative unit count");
-  *bytes = (uint64_t)desc->batch * (uint64_t)desc->heads * (uint64_t)map->n_units * 1024u;
+  if (map->unit_keys != 16 && map->unit_keys != 32)
+    return fail(FWN_ERR_INVALID_ARG, "ds map: unit_keys %d (16 or 32)", map->unit_keys);
+  *bytes = (uint64_t)desc->batch * (uint64_t)desc->heads * (uint64_t)(map->n_units * ds_unit_bytes(map));
   return FWN_OK;
 }
 
@@ -363,8 +372,8 @@ int fwn_attn_bwd_dq_ds_launch(const fwn_attn_desc* desc, const void* k, const vo
   if (int rc = check_tensor(k, "k")) return rc;
   if (int rc = check_tensor(dq, "dq")) return rc;
   if (int rc = check_tiles(desc, tiles, "tiles")) return rc;
-  if (tiles->n_tiles > 0 && !tiles->halves)
-    return fail(FWN_ERR_TILES, "tiles: the dS exchange needs the half bits (fwn_tiles_prepare with halves)");
+  if (desc->dtype == FWN_BF16 && tiles->n_tiles > 0 && !tiles->halves)
+    return fail(FWN_ERR_TILES, "tiles: the bf16 dS exchange needs the half bits (fwn_tiles_prepare with halves)");
   if (int rc = check_workspace(desc, tiles, workspace, workspace_bytes)) return rc;
   KArgs a = base_args(desc);
   a.k = k;

@@ -351,10 +351,128 @@ __global__ void __launch_bounds__(NT, 1) dq_f32_kernel(KArgs a) {
   store_acc_f32<D>(make_rsrc((float*)a.out0 + j.base, a.slice_bytes), qrow, snb, acc, a.scale, g);
 }
 
+// dQ, fp32, from the dS units of dkv_f32_kernel<D, true> (the float32 dS exchange): per work
+// item of the forward list, dQ^T += K^T dS^T over each wave's live 32 x 32 groups
+// (pallas_attn.py:177-184 with dS from the dK/dV pass instead of recomputed). A unit is one
+// group's dS, 4 KB, laid out so that lane L's B operands (query L % 32, key
+// element_col(sb, r, L / 32) in register r) are its 16-byte chunks 64 k + L, k = 0..3: four
+// 16-byte loads per lane and group, straight into the MFMA operands. No V, Q, dO or statistics
+// are read and no S, dP or exponentials computed: a third of dq_f32_kernel's MFMAs.
+//
+// K rows stream in halves through two half buffers (32 KB each at D = 128), two workgroups per
+// CU. A half's units are loaded together with its K rows, so the barrier that publishes the rows
+// also covers the units.
+template <int D>
+__global__ void __launch_bounds__(NT, 2) dq_f32_ds_kernel(KArgs a) {
+  constexpr int HB = 64 * D * 4;  // bytes of 64 rows of K
+  __shared__ __attribute__((aligned(1024))) char h0[HB];  // rows 0-63
+  __shared__ __attribute__((aligned(1024))) char h1[HB];  // rows 64-127
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int i = lane & 31, g = lane >> 5;
+  const Job j = decode_job(a);
+  const uint32_t snb = (uint32_t)a.sn * 4;
+  const rsrc_t rK = make_rsrc((const float*)a.k + j.base, a.slice_bytes);
+  const rsrc_t rS = make_rsrc((const float*)a.ds + (int64_t)j.bh * (a.ds_slice_bytes >> 2), a.ds_slice_bytes);
+  const int qrow = j.blk * BLK + 32 * w + i;
+  F32Offsets<D> off;
+  off.init(i, g);
+  HalfDma<D> dma;
+  dma.init(w, lane, snb, true);
+  f32x16 acc[D / 32];
+#pragma unroll
+  for (int db = 0; db < D / 32; ++db) acc[db] = zero16();
+  typedef const __attribute__((address_space(4))) int32_t* cmap_ptr;
+
+  // This wave's units of tile half h (key groups 2h and 2h + 1: group bits 4w + 2h + x), numbered
+  // from the tile's first unit by their rank among its 16 group bits. Each is read once:
+  // non-temporal loads.
+  auto load_units = [&](f32x4 (&dst)[2][4], uint32_t gw, uint32_t ub, int h) {
+    const uint32_t b0 = 4u * (uint32_t)w + 2u * (uint32_t)h;
+    uint32_t u = ub + (uint32_t)__builtin_popcount(gw & 0xffffu & ((1u << b0) - 1u));
+#pragma unroll
+    for (int x = 0; x < 2; ++x)
+      if (gw >> (b0 + x) & 1u) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          dst[x][k] = __builtin_bit_cast(
+              f32x4, __builtin_amdgcn_raw_buffer_load_b128(rS, 16 * (64 * k + lane), (int)(u * 4096u), 2));
+        ++u;
+      }
+  };
+  // Key group sl of the half buffer ldsK, with its unit d.
+  auto group = [&](int sl, const char* ldsK, const f32x4 (&d)[4]) {
+    float kt[16][D / 32];
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+#pragma unroll
+      for (int db = 0; db < D / 32; ++db) kt[r][db] = *(const float*)(ldsK + off.el[r & 3] + off.el_imm(sl, r, db));
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+#pragma unroll
+      for (int db = 0; db < D / 32; ++db) acc[db] = mfma_f32(kt[r][db], d[r >> 2][r & 3], acc[db]);
+    }
+    sched_reads_ahead<16, D / 32, D / 32>();
+  };
+
+  int t0, t1;
+  tile_range(a, j, t0, t1);
+  f32x4 dsA[2][4], dsB[2][4];  // units of the current tile's half 0 and half 1
+  uint32_t gcur = 0u, ucur = 0u;
+  if (t0 < t1) {
+    gcur = tile_groups(a, t0);
+    ucur = (uint32_t)((cmap_ptr)a.ubase)[t0];
+    dma.issue(rK, h0, ((ci32_ptr)a.col)[t0] * BLK, snb, w, 0, any_rows(gcur));
+    load_units(dsA, gcur, ucur, 0);
+  }
+  for (int tt = t0; tt < t1; ++tt) {
+    const int t = __builtin_amdgcn_readfirstlane(tt);
+    const int kb = ((ci32_ptr)a.col)[t];
+    const uint32_t gt = gcur, ut = ucur;
+    const uint32_t live = gt >> (4 * w) & 15u;
+    wait_vmem();      // this wave's part of half 0 of tile t and its units
+    __syncthreads();  // half 0 landed; every wave is done with half 1 of tile t - 1
+    dma.issue(rK, h1, kb * BLK, snb, w, 1, any_rows(gt));
+    load_units(dsB, gt, ut, 1);
+    if (t + 1 < t1) {
+      gcur = tile_groups(a, t + 1);
+      ucur = (uint32_t)((cmap_ptr)a.ubase)[t + 1];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (live & 1u) group(0, h0, dsA[0]);
+    __builtin_amdgcn_sched_barrier(0);
+    if (live & 2u) group(1, h0, dsA[1]);
+    __builtin_amdgcn_sched_barrier(0);
+    wait_vmem();      // this wave's part of half 1 and its units
+    __syncthreads();  // half 1 landed; every wave is done with half 0
+    if (t + 1 < t1) {
+      dma.issue(rK, h0, ((ci32_ptr)a.col)[t + 1] * BLK, snb, w, 0, any_rows(gcur));
+      load_units(dsA, gcur, ucur, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (live & 4u) group(0, h1, dsB[0]);
+    __builtin_amdgcn_sched_barrier(0);
+    if (live & 8u) group(1, h1, dsB[1]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if (j.part >= 0) {
+    store_bwd_partial<D>(a, j, 32 * w + i, acc, 0, g);
+    return;
+  }
+  store_acc_f32<D>(make_rsrc((float*)a.out0 + j.base, a.slice_bytes), qrow, snb, acc, a.scale, g);
+}
+
 // dK/dV, fp32. The tile's Q and dO rows, and their lse and delta, stream in halves through two
 // half buffers as in dQ.
-
-template <int D>
+//
+// With DS (the float32 dS exchange), each group's dS also goes to HBM as one 4 KB unit in
+// dq_f32_ds_kernel's operand layout. This lane holds dS of key 32w + i and query
+// element_col(sb, r, g) in register r; in the unit that value belongs to dQ lane
+// (query, (key % 32 / 8) % 2), register 8 (key % 32 / 16) + key % 8, so each of the 16 stores
+// has a per-lane offset fixed at the start plus an immediate per register. Units are numbered
+// over the forward list by the rank of group bit 4 sb + w (query group sb, key group w) in the
+// forward tile's group word; tmap gives that word and the tile's first unit.
+template <int D, bool DS = false>
 __global__ void __launch_bounds__(NT, 1) dkv_f32_kernel(KArgs a) {
   constexpr int HB = 64 * D * 4;  // bytes of 64 rows of Q or dO
   // rows 0-63 (h0) and 64-127 (h1): Q | dO | lse * log2(e) [64] | delta [64]
@@ -385,6 +503,17 @@ __global__ void __launch_bounds__(NT, 1) dkv_f32_kernel(KArgs a) {
   for (int db = 0; db < D / 32; ++db) {
     dk[db] = zero16();
     dv[db] = zero16();
+  }
+  // dS exchange: this (batch, head)'s unit slice (a plain global pointer: a buffer resource's
+  // four SGPRs would push this kernel past its SGPR budget), this lane's offset in a unit, and
+  // the current tile's first unit and group word.
+  char* dsb = nullptr;
+  uint32_t dsl = 0u, ubc = 0u, gfc = 0u;
+  typedef const __attribute__((address_space(4))) uint32_t* cmap_ptr;
+  if constexpr (DS) {
+    dsb = (char*)a.ds + (int64_t)j.bh * a.ds_slice_bytes;
+    const int tk = (i >> 3) & 1, tr = 8 * (i >> 4) + (i & 7);
+    dsl = (uint32_t)((64 * (tr >> 2) + 32 * tk + 8 * g) * 16 + 4 * (tr & 3));
   }
 
   // Half h of query block qb: the Q and dO rows (live groups only) and, by wave 0, the 64 rows'
@@ -435,6 +564,13 @@ __global__ void __launch_bounds__(NT, 1) dkv_f32_kernel(KArgs a) {
       s[r] = p;
       dp[r] = p * dp[r];
     }
+    if constexpr (DS) {
+      const uint32_t bit = 4u * (uint32_t)sb + (uint32_t)w;
+      const uint32_t so = (ubc + (uint32_t)__builtin_popcount(gfc & 0xffffu & ((1u << bit) - 1u))) * 4096u;
+      float* u = (float*)(dsb + (so + dsl));
+#pragma unroll
+      for (int r = 0; r < 16; ++r) u[4 * (16 * (r >> 3) + (r & 7))] = dp[r];
+    }
     float ot[16][D / 32], qt[16][D / 32];
 #pragma unroll
     for (int r = 0; r < 16; ++r)
@@ -467,6 +603,10 @@ __global__ void __launch_bounds__(NT, 1) dkv_f32_kernel(KArgs a) {
     const u32x2 mb = tile_bits(a, t, w, lane);
     const uint32_t gt = gcur;
     const uint32_t live = gt >> (4 * w) & 15u;  // query groups with p = 0 throughout are skipped
+    if constexpr (DS) {
+      ubc = ((cmap_ptr)a.tmap)[2 * t];
+      gfc = ((cmap_ptr)a.tmap)[2 * t + 1];
+    }
     wait_vmem();  // this wave's part of half 0 of tile t, and the mask bits
     scale_lse(h0);
     __syncthreads();  // half 0 landed; every wave is done with half 1 of tile t - 1
@@ -545,7 +685,9 @@ hipError_t launch_d(Kind kind, const KArgs& a, hipStream_t stream) {
   switch (kind) {
     case Kind::kFwd: hipLaunchKernelGGL(fwd_f32_kernel<D>, grid, dim3(NT_F32), 0, stream, a); break;
     case Kind::kDq: hipLaunchKernelGGL(dq_f32_kernel<D>, grid, block, 0, stream, a); break;
-    case Kind::kDkv: hipLaunchKernelGGL(dkv_f32_kernel<D>, grid, block, 0, stream, a); break;
+    case Kind::kDkv: hipLaunchKernelGGL((dkv_f32_kernel<D, false>), grid, block, 0, stream, a); break;
+    case Kind::kDkvDs: hipLaunchKernelGGL((dkv_f32_kernel<D, true>), grid, block, 0, stream, a); break;
+    case Kind::kDqDs: hipLaunchKernelGGL(dq_f32_ds_kernel<D>, grid, block, 0, stream, a); break;
     default: break;
   }
   return hipGetLastError();

@@ -361,10 +361,13 @@ int fwn_tiles_prepare(int32_t n_blocks, int32_t n_tiles, int32_t n_cols, const i
 
 int fwn_tiles_ds_map(int32_t n_blocks, const int32_t* tile_ptr, const int32_t* tile_col,
                      const uint32_t* tile_bits, const int32_t* tile_ptr_t, const int32_t* tile_col_t,
-                     const uint32_t* tile_bits_t, int32_t* ubase, int32_t* tmap, int64_t* n_units) {
+                     const uint32_t* tile_bits_t, int32_t unit_keys, int32_t* ubase, int32_t* tmap,
+                     int64_t* n_units) {
   fwn::clear_error();
   if (n_blocks <= 0 || !tile_ptr || !tile_ptr_t || !n_units)
     return fwn::fail(FWN_ERR_INVALID_ARG, "fwn_tiles_ds_map: null or empty argument");
+  if (unit_keys != 16 && unit_keys != 32)
+    return fwn::fail(FWN_ERR_INVALID_ARG, "fwn_tiles_ds_map: unit_keys %d (16 or 32)", unit_keys);
   const int32_t n_tiles = tile_ptr[n_blocks], n_tiles_t = tile_ptr_t[n_blocks];
   if (n_tiles > 0 && (!tile_col || !tile_bits || !ubase))
     return fwn::fail(FWN_ERR_INVALID_ARG, "fwn_tiles_ds_map: null forward arrays");
@@ -377,8 +380,9 @@ int fwn_tiles_ds_map(int32_t n_blocks, const int32_t* tile_ptr, const int32_t* t
     return fwn::fail(FWN_ERR_TILES, "fwn_tiles_ds_map: %d forward tiles but %d transposed ones", n_tiles, n_tiles_t);
   constexpr int32_t words = FWN_BLOCK / 32;
   constexpr int64_t tile_words = (int64_t)FWN_BLOCK * words;
-  // Half bits of each forward tile (bit 8r + 2c + h: rows 32r.., columns 32c + 16h ..), as
-  // fwn_tiles_prepare computes them, and the exclusive prefix of their counts.
+  // Unit bits of each forward tile, as fwn_tiles_prepare computes them: the half bits (bit
+  // 8r + 2c + h: rows 32r.., columns 32c + 16h ..) for 16-key units, the group bits (bit 4r + c)
+  // for 32-key units; and the exclusive prefix of their counts.
   std::vector<uint32_t> halves(n_tiles);
   parallel_for(n_tiles, 256, [&](int64_t b, int64_t e) {
     for (int64_t t = b; t < e; ++t) {
@@ -387,6 +391,10 @@ int fwn_tiles_ds_map(int32_t n_blocks, const int32_t* tile_ptr, const int32_t* t
       for (int32_t r = 0; r < FWN_BLOCK; ++r)
         for (int32_t x = 0; x < words; ++x) {
           const uint32_t wd = bits[r * words + x];
+          if (unit_keys == 32) {
+            if (wd) hv |= 1u << (4 * (r / 32) + x);
+            continue;
+          }
           if (wd & 0xffffu) hv |= 1u << (8 * (r / 32) + 2 * x);
           if (wd >> 16) hv |= 1u << (8 * (r / 32) + 2 * x + 1);
         }

@@ -50,7 +50,8 @@ class Tiles(ctypes.Structure):
 
 
 class DsMap(ctypes.Structure):
-  _fields_ = [("n_units", ctypes.c_int64), ("ubase", ctypes.c_void_p), ("tmap", ctypes.c_void_p)]
+  _fields_ = [("n_units", ctypes.c_int64), ("ubase", ctypes.c_void_p), ("tmap", ctypes.c_void_p),
+              ("unit_keys", ctypes.c_int32), ("reserved", ctypes.c_int32)]
 
 
 ITEM_TILES = 64  # FWN_ITEM_TILES: default longest run of tiles per work item
@@ -90,7 +91,7 @@ SIGNATURES = {
     "fwn_attn_bwd_dq_launch": [_DESC, _P, _P, _P, _P, _P, _P, _TILES, _P, _P, _U64, _P],
     "fwn_attn_bwd_dkv_launch": [_DESC, _P, _P, _P, _P, _P, _P, _TILES, _P, _P, _P, _U64, _P],
     "fwn_attn_bwd_launch": [_DESC, _P, _P, _P, _P, _P, _P, _P, _TILES, _TILES, _P, _P, _P, _P, _U64, _P],
-    "fwn_tiles_ds_map": [_I32, _P, _P, _P, _P, _P, _P, _P, _P, _P],
+    "fwn_tiles_ds_map": [_I32, _P, _P, _P, _P, _P, _P, _I32, _P, _P, _P],
     "fwn_attn_ds_bytes": [_DESC, _DS, _P],
     "fwn_attn_bwd_dkv_ds_launch": [_DESC, _P, _P, _P, _P, _P, _P, _TILES, _DS, _P, _P, _P, _U64, _P, _U64, _P],
     "fwn_attn_bwd_dq_ds_launch": [_DESC, _P, _P, _U64, _TILES, _DS, _P, _P, _U64, _P],

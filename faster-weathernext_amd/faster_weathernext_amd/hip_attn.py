@@ -147,14 +147,15 @@ class TileList:
     nat.check(nat.lib().fwn_attn_workspace_size(desc, self.struct_for(desc.batch, desc.heads), ctypes.byref(n)))
     return int(n.value)
 
-  def ds_map(self, tiles_t):
+  def ds_map(self, tiles_t, unit_keys=16):
     """The dS exchange's unit numbering of this (forward) list and `tiles_t` (this list itself
-    for a symmetric mask), or None when `tiles_t` is not this list's exact transpose; built on
-    first use and kept with this list."""
-    key = id(tiles_t)
+    for a symmetric mask) for units of `unit_keys` keys (16 for bf16, 32 for float32), or None
+    when `tiles_t` is not this list's exact transpose; built on first use and kept with this
+    list."""
+    key = (id(tiles_t), int(unit_keys))
     hit = self._ds_maps.get(key)
     if hit is None or hit[0] is not tiles_t:
-      hit = (tiles_t, DsMap.build(self, tiles_t))
+      hit = (tiles_t, DsMap.build(self, tiles_t, unit_keys))
       self._ds_maps[key] = hit
     return hit[1]
 
@@ -180,20 +181,22 @@ class TileList:
 
 
 class DsMap:
-  """Unit numbering of the bf16 backward's dS exchange (``fwn_tiles_ds_map``): the dK/dV kernel
-  writes each 32-query x 16-key unit of dS = P (dP - delta) once, and the dQ kernel reads it
-  instead of recomputing S and dP (5 contractions per live tile instead of 7). Units are the set
-  bits of the forward list's half words, numbered tile by tile; ``struct`` is the C view."""
+  """Unit numbering of the backward's dS exchange (``fwn_tiles_ds_map``): the dK/dV kernel writes
+  each unit of dS = P (dP - delta) once, and the dQ kernel reads it instead of recomputing S and
+  dP (5 contractions per live tile instead of 7). A unit is 32 queries x `unit_keys` keys: 16
+  (bf16, the set bits of the forward list's half words) or 32 (float32, its group bits),
+  numbered tile by tile; ``struct`` is the C view."""
 
-  def __init__(self, n_units, ubase, tmap, device):
+  def __init__(self, n_units, ubase, tmap, unit_keys, device):
     self.n_units = int(n_units)
+    self.unit_keys = int(unit_keys)
     self.ubase = torch.from_numpy(ubase).to(device)
     self.tmap = torch.from_numpy(tmap).to(device)
     addr = lambda t: t.data_ptr() if t.numel() else None
-    self.struct = nat.DsMap(self.n_units, addr(self.ubase), addr(self.tmap))
+    self.struct = nat.DsMap(self.n_units, addr(self.ubase), addr(self.tmap), self.unit_keys, 0)
 
   @classmethod
-  def build(cls, tl, tlt):
+  def build(cls, tl, tlt, unit_keys=16):
     """The map of forward list `tl` and transposed list `tlt`, or None if `tlt` is not the
     transpose of `tl` bit for bit (the recomputing backward applies then)."""
     if tl.n_blocks != tlt.n_blocks or tl.n_cols != tlt.n_cols or tl.device != tlt.device:
@@ -203,11 +206,12 @@ class DsMap:
     n_units = np.zeros(1, np.int64)
     status = nat.lib().fwn_tiles_ds_map(tl.n_blocks, nat.ptr(tl._tile_ptr), nat.ptr(tl._tile_col),
                                         nat.ptr(tl._tile_bits), nat.ptr(tlt._tile_ptr), nat.ptr(tlt._tile_col),
-                                        nat.ptr(tlt._tile_bits), nat.ptr(ubase), nat.ptr(tmap), nat.ptr(n_units))
+                                        nat.ptr(tlt._tile_bits), int(unit_keys), nat.ptr(ubase), nat.ptr(tmap),
+                                        nat.ptr(n_units))
     if status == nat.ERR_TILES:
       return None
     nat.check(status)
-    return cls(n_units[0], ubase[:tl.n_tiles], tmap[:tlt.n_tiles], tl.device)
+    return cls(n_units[0], ubase[:tl.n_tiles], tmap[:tlt.n_tiles], unit_keys, tl.device)
 
   def ds_bytes(self, desc):
     n = ctypes.c_uint64(0)
@@ -215,9 +219,14 @@ class DsMap:
     return int(n.value)
 
 
-# The bf16 backward uses the dS exchange (DsMap) when the lists allow it; False keeps the
+# The backward uses the dS exchange (DsMap) when the lists allow it; False keeps the
 # recomputing dQ kernel beside dK/dV for every call.
 DS_EXCHANGE = True
+
+
+def unit_keys_for(dtype):
+  """Keys per dS unit of the exchange for a dtype: 16 for bf16, 32 for float32."""
+  return 16 if dtype == torch.bfloat16 else 32
 
 _cache_lock = threading.Lock()
 _cache = collections.OrderedDict()
@@ -340,15 +349,15 @@ def _side_stream(device):
 def _backward_into(q, k, v, out, lse, dout, tiles, tiles_t, scale, dq, dk, dv):
   """Backward kernels writing dq, dk, dv (q's strides).
 
-  bfloat16, with `tiles_t` the exact transpose of `tiles` (a symmetric mask with tiles_t None
-  included): the dS exchange, in stream order on the current stream (fwn_attn_bwd_ds_launch):
-  delta, dK/dV writing every 32 x 16 unit of dS, then dQ from dS. The reference computes S and dP
-  in both of its backward kernels (pallas_attn.py:172-180, 199-207); here once (C3: 1.71 -> 1.58
-  ms per fwd+bwd step, C4 7.87 -> 6.97 ms).
+  With `tiles_t` the exact transpose of `tiles` (a symmetric mask with tiles_t None included):
+  the dS exchange, in stream order on the current stream (fwn_attn_bwd_ds_launch): delta, dK/dV
+  writing every unit of dS (32 x 16 in bf16, 32 x 32 in float32), then dQ from dS. The
+  reference computes S and dP in both of its backward kernels (pallas_attn.py:172-180,
+  199-207); here once (bf16 C3: 1.71 -> 1.58 ms per fwd+bwd step, C4 7.87 -> 6.97 ms).
 
-  Otherwise (float32, lists that are not transposes, DS_EXCHANGE False): the delta pre-pass, then
-  the recomputing dQ kernel on the current stream and dK/dV on a side stream at the same time
-  (each with its own workspace), joined before returning. Run side by side, each fills the CUs the
+  Otherwise (lists that are not transposes, DS_EXCHANGE False): the delta pre-pass, then the
+  recomputing dQ kernel on the current stream and dK/dV on a side stream at the same time (each
+  with its own workspace), joined before returning. Run side by side, each fills the CUs the
   other's last workgroups leave idle. The sequence is what fwn_attn_bwd_launch enqueues on one
   stream, with the dQ and dK/dV launches overlapped."""
   desc = _desc(q, scale, out)
@@ -358,7 +367,7 @@ def _backward_into(q, k, v, out, lse, dout, tiles, tiles_t, scale, dq, dk, dv):
   delta = torch.empty_like(lse)
   L = nat.lib()
   main = torch.cuda.current_stream(q.device)
-  dmap = tl.ds_map(tlt) if DS_EXCHANGE and q.dtype == torch.bfloat16 else None
+  dmap = tl.ds_map(tlt, unit_keys_for(q.dtype)) if DS_EXCHANGE else None
   if dmap is not None:
     # delta, dK/dV writing dS, then dQ from dS, in stream order (fwn_attn_bwd_ds_launch).
     ws = workspace(desc, q.device, tl, tlt)

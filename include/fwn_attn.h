@@ -227,38 +227,45 @@ int fwn_attn_bwd_launch(const fwn_attn_desc* desc, const void* q, const void* k,
                         void* dv, void* workspace, uint64_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
- * bfloat16 backward with the dS exchange. The reference computes S and dP twice per live tile,
- * once for dQ and once for dK/dV (pallas_attn.py:172-180, 199-207). Here the dK/dV kernel also
- * writes dS = P (dP - delta) as bf16, and the dQ kernel computes dQ = scale * dS K from it:
- * 5 contractions per tile instead of 7. dS is written and read in units of 32 query rows x 16
- * keys (1 KB), one per 16-key half of a 32 x 32 group with a valid element (the forward list's
- * halves bits), numbered over the forward list. The two lists must be exact transposes of each
- * other, bit for bit (fwn_tiles_ds_map checks this); dQ then equals the recomputing dq kernel's
- * up to the rounding order of S.
+ * Backward with the dS exchange. The reference computes S and dP twice per live tile, once for
+ * dQ and once for dK/dV (pallas_attn.py:172-180, 199-207). Here the dK/dV kernel also writes
+ * dS = P (dP - delta) and the dQ kernel computes dQ = scale * dS K from it: 5 contractions per
+ * tile instead of 7. dS is written and read in units of 32 query rows x `unit_keys` keys, one
+ * per such block of a live tile with a valid element, numbered over the forward list:
+ *   - bf16: unit_keys 16 (the forward list's halves bits), bf16 dS, 1 KB per unit;
+ *   - float32: unit_keys 32 (its group bits 0-15), float32 dS, 4 KB per unit.
+ * The two lists must be exact transposes of each other, bit for bit (fwn_tiles_ds_map checks
+ * this). dQ then equals the recomputing dq kernel's up to the rounding order of S.
  * ------------------------------------------------------------------------------------------- */
 
 /* Unit numbering of a forward tile list and its transposed list (device arrays). */
 typedef struct fwn_ds_map {
-  int64_t n_units;       /* units of the forward list: the set bits of all its halves words */
+  int64_t n_units;       /* units of the forward list */
   const int32_t* ubase;  /* [tiles->n_tiles] first unit of each forward tile */
-  const int32_t* tmap;   /* [tiles_t->n_tiles][2]: for each transposed tile, ubase and the halves
-                            word (as int32) of the same tile of the forward list */
+  const int32_t* tmap;   /* [tiles_t->n_tiles][2]: for each transposed tile, ubase and the unit
+                            bits word (as int32: halves for 16, groups for 32) of the same tile of
+                            the forward list */
+  int32_t unit_keys;     /* 16 (bf16 calls) or 32 (float32 calls) */
+  int32_t reserved;      /* 0 */
 } fwn_ds_map;
 
 /* Builds the unit numbering (host arrays) from the canonical arrays of both lists (tile_ptr,
- * tile_col, tile_bits as fwn_tiles_fill writes them, n_blocks row blocks each, n = n_blocks * 128
- * or fewer nodes): ubase[n_tiles], tmap[n_tiles_t * 2], *n_units. Returns FWN_ERR_TILES when the
- * second list is not the transpose of the first (a tile or a bit differs); the recomputing
- * backward (fwn_attn_bwd_launch) is then the one that applies. No reference counterpart. */
+ * tile_col, tile_bits as fwn_tiles_fill writes them, n_blocks row blocks each) for units of
+ * unit_keys (16 or 32) keys: ubase[n_tiles], tmap[n_tiles_t * 2], *n_units. Returns
+ * FWN_ERR_TILES when the second list is not the transpose of the first (a tile or a bit
+ * differs); the recomputing backward (fwn_attn_bwd_launch) is then the one that applies. No
+ * reference counterpart. */
 int fwn_tiles_ds_map(int32_t n_blocks, const int32_t* tile_ptr, const int32_t* tile_col,
                      const uint32_t* tile_bits, const int32_t* tile_ptr_t, const int32_t* tile_col_t,
-                     const uint32_t* tile_bits_t, int32_t* ubase, int32_t* tmap, int64_t* n_units);
+                     const uint32_t* tile_bits_t, int32_t unit_keys, int32_t* ubase, int32_t* tmap,
+                     int64_t* n_units);
 
-/* Bytes of the dS buffer: batch * heads * n_units * 1024 (256-byte aligned device memory). */
+/* Bytes of the dS buffer: batch * heads * n_units * (1024 for unit_keys 16, 4096 for 32);
+ * 256-byte aligned device memory. */
 int fwn_attn_ds_bytes(const fwn_attn_desc* desc, const fwn_ds_map* map, uint64_t* bytes);
 
-/* dk, dv as fwn_attn_bwd_dkv_launch (bf16 only), and every dS unit into `ds`
- * (pallas_attn.py:187-215). */
+/* dk, dv as fwn_attn_bwd_dkv_launch, and every dS unit into `ds` (pallas_attn.py:187-215).
+ * The map's unit_keys must be 16 for bf16 and 32 for float32. */
 int fwn_attn_bwd_dkv_ds_launch(const fwn_attn_desc* desc, const void* q, const void* k,
                                const void* v, const void* dout, const float* lse,
                                const float* delta, const fwn_tiles* tiles_t, const fwn_ds_map* map,
@@ -266,7 +273,7 @@ int fwn_attn_bwd_dkv_ds_launch(const fwn_attn_desc* desc, const void* q, const v
                                uint64_t workspace_bytes, void* stream);
 
 /* dq = scale * dS K over the forward list from the units fwn_attn_bwd_dkv_ds_launch wrote
- * (bf16 only; replaces pallas_attn._bwd_dq_kernel, pallas_attn.py:161-184, in this mode). */
+ * (replaces pallas_attn._bwd_dq_kernel, pallas_attn.py:161-184, in this mode). */
 int fwn_attn_bwd_dq_ds_launch(const fwn_attn_desc* desc, const void* k, const void* ds,
                               uint64_t ds_bytes, const fwn_tiles* tiles, const fwn_ds_map* map,
                               void* dq, void* workspace, uint64_t workspace_bytes, void* stream);

@@ -323,19 +323,20 @@ def _run_modes(q, k, v, do, tiles, scale, dtype, tiles_t, monkeypatch):
   return got, ref
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("d", [32, 64, 128])
 @pytest.mark.parametrize("case", ["symmetric", "transposed", "split", "groups"])
-def test_ds_exchange_matches_recompute_and_oracle(case, d, monkeypatch):
-  """bf16 backward with the dS exchange: the dK/dV kernel writes every 32 x 16 unit of dS and the
-  dQ kernel reads it (5 contractions per tile instead of 7). dK and dV come from the same kernel
-  arithmetic as without the exchange, bit for bit; dQ differs from the recomputing kernel's only
-  in the rounding order of S (the two kernels contract it in different MFMA shapes) and both meet
-  the bars against the dense float64 oracle. Cases: a symmetric mask (one list) with rows and
-  columns without a valid element, a non-symmetric mask with its transposed list, split
-  schedules (items of 1 and 3 tiles, so partial dQ and dK/dV slots are combined) and the
-  designed group/half patterns (non-symmetric)."""
-  print(f"ds exchange {case} d={d}", flush=True)
-  dtype = torch.bfloat16
+def test_ds_exchange_matches_recompute_and_oracle(case, d, dtype, monkeypatch):
+  """Backward with the dS exchange: the dK/dV kernel writes every unit of dS (32 x 16 in bf16,
+  32 x 32 in float32) and the dQ kernel reads it (5 contractions per tile instead of 7). dK and
+  dV come from the same kernel arithmetic as without the exchange, bit for bit; dQ differs from
+  the recomputing kernel's only in rounding (S contracted in other MFMA shapes in bf16, delta
+  subtracted at another point in float32) and both meet the bars against the dense float64
+  oracle. Cases: a symmetric mask (one list) with rows and columns without a valid element, a
+  non-symmetric mask with its transposed list, split schedules (items of 1 and 3 tiles, so
+  partial dQ and dK/dV slots are combined) and the designed group/half patterns
+  (non-symmetric)."""
+  print(f"ds exchange {case} d={d} {dtype}", flush=True)
   rng = np.random.default_rng(80 + d)
   n, b, h = 700, 2, 2
   tiles_t = None
@@ -358,12 +359,13 @@ def test_ds_exchange_matches_recompute_and_oracle(case, d, monkeypatch):
   if case == "split":
     tiles_t = fwn.TileList.from_mask(m, max_item_tiles=3)
     assert tiles.n_split > 0 and tiles_t.n_split > 0
-  assert tiles.ds_map(tiles if tiles_t is None else tiles_t) is not None
+  assert tiles.ds_map(tiles if tiles_t is None else tiles_t, fwn.hip_attn.unit_keys_for(dtype)) is not None
   q, k, v, do = (_rounded(rng.standard_normal((b, n, h, d)), dtype) for _ in range(4))
   got, ref = _run_modes(q, k, v, do, tiles, d ** -0.5, dtype, tiles_t, monkeypatch)
   for name in ("out", "dk", "dv"):
     np.testing.assert_array_equal(got[name], ref[name], err_msg=name)
-  assert A.rel_rms(got["dq"], ref["dq"]) < 1e-3, A.rel_rms(got["dq"], ref["dq"])
+  close = 1e-3 if dtype == torch.bfloat16 else 1e-6
+  assert A.rel_rms(got["dq"], ref["dq"]) < close, A.rel_rms(got["dq"], ref["dq"])
   # Rows and columns cleared in the symmetric case get zero gradients; the oracle runs on the rest.
   keep = np.flatnonzero(m.getnnz(1) > 0)
   empty = np.setdiff1d(np.arange(n), keep)

@@ -92,31 +92,31 @@ def test_bwd_launch_without_transposed_list_uses_the_forward_list(monkeypatch):
     np.testing.assert_array_equal(host(got), host(want), err_msg=name)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("split", [False, True])
-def test_bwd_ds_launch_one_stream(split):
+def test_bwd_ds_launch_one_stream(split, dtype):
   """fwn_attn_bwd_ds_launch (delta, dk/dv writing dS, then dq from dS, on one stream) on a
-  non-symmetric bf16 mask with its transposed list, through the C ABI with the map from
+  non-symmetric mask with its transposed list, through the C ABI with the map from
   fwn_tiles_ds_map: equal bit for bit to the package's backward (which takes the same path),
   dK and dV equal to fwn_attn_bwd_launch's, all within the bars of the dense float64 oracle.
   The dS buffer starts as NaN bytes: every unit the dQ kernel reads was written."""
   rng = np.random.default_rng(66)
-  dtype = torch.bfloat16
   b, n, h, d = 2, 700, 2, 128
   q, k, v, do = (rounded(rng.standard_normal((b, n, h, d)), dtype) for _ in range(4))
   m = random_mask(n, 0.05, 67, symmetric=False)
   cap, cap_t = (2, 3) if split else (1 << 20, 1 << 20)
   tiles = fwn.TileList.from_mask(m, max_item_tiles=cap)
   tiles_t = fwn.TileList.from_mask(m.T.tocsr(), max_item_tiles=cap_t)
-  dmap = tiles.ds_map(tiles_t)
+  dmap = tiles.ds_map(tiles_t, fwn.hip_attn.unit_keys_for(dtype))
   assert dmap is not None and dmap.n_units > 0
   qd, kd, vd, dod = (dev(x, dtype) for x in (q, k, v, do))
   scale = d ** -0.5
   out, lse = fwn.attention_forward(qd, kd, vd, tiles, scale)
-  desc = nat.AttnDesc(b, n, h, d, nat.BF16, scale, *qd.stride()[:3])
+  desc = nat.AttnDesc(b, n, h, d, DT[dtype], scale, *qd.stride()[:3])
   size = _ws_size(desc, tiles, tiles_t)
   ws = torch.full((max(size, 1),), 255, dtype=torch.uint8, device="cuda")
   nbytes = dmap.ds_bytes(desc)
-  assert nbytes == b * h * dmap.n_units * 1024
+  assert nbytes == b * h * dmap.n_units * (1024 if dtype == torch.bfloat16 else 4096)
   ds = torch.full((nbytes,), 0xFF, dtype=torch.uint8, device="cuda")
   stream = torch.cuda.current_stream().cuda_stream
   L = nat.lib()

@@ -621,29 +621,33 @@ def test_noalloc_forward_rejects_schedules_beyond_the_static_scratch():
   assert nat.lib().fwn_attn_fwd_launch_noalloc(bad, 256, 256, 256, tl.struct, 256, None, None) == nat.ERR_UNSUPPORTED
 
 
-def _ds_map(fwd, tr):
+def _ds_map(fwd, tr, unit_keys=16):
   tp, kb, bits = fwd
   tpt, kbt, bitst = tr
   ubase = np.zeros(max(len(kb), 1), np.int32)
   tmap = np.zeros((max(len(kbt), 1), 2), np.int32)
   n_units = np.zeros(1, np.int64)
   status = nat.lib().fwn_tiles_ds_map(len(tp) - 1, nat.ptr(tp), nat.ptr(kb), nat.ptr(bits), nat.ptr(tpt),
-                                      nat.ptr(kbt), nat.ptr(bitst), nat.ptr(ubase), nat.ptr(tmap), nat.ptr(n_units))
+                                      nat.ptr(kbt), nat.ptr(bitst), unit_keys, nat.ptr(ubase), nat.ptr(tmap),
+                                      nat.ptr(n_units))
   return status, ubase[:len(kb)], tmap[:len(kbt)], int(n_units[0])
 
 
+@pytest.mark.parametrize("unit_keys", [16, 32])
 @pytest.mark.parametrize("symmetric", [True, False])
-def test_ds_map_numbers_units_from_the_dense_mask(symmetric):
-  # The dS exchange: unit (query group r, 16-key half u = 2c + h) of forward tile (qb, kb) exists
-  # when the dense mask has a valid element in rows 32r.. x columns 16u.. of the tile; units are
-  # numbered tile by tile in list order, by bit 8r + u. The dK/dV kernel's unit for key group kg
-  # and query group c of transposed tile (kb, qb) must be that same unit (bit 8c + kg).
+def test_ds_map_numbers_units_from_the_dense_mask(symmetric, unit_keys):
+  # The dS exchange: unit (query group r, key block u of unit_keys keys) of forward tile (qb, kb)
+  # exists when the dense mask has a valid element in rows 32r.. x columns unit_keys * u.. of the
+  # tile; units are numbered tile by tile in list order, by bit (128 / unit_keys) r + u. The
+  # dK/dV kernel's unit for query group c and key block kg of transposed tile (kb, qb) must be
+  # that same unit (bit (128 / unit_keys) c + kg).
   n = 700
   m = _random_mask(n, 0.02, 5, symmetric=symmetric)
   fwd = fwn.build_tile_mask(m)
   tr = fwd if symmetric else fwn.build_tile_mask(m.T.tocsr())
-  status, ubase, tmap, n_units = _ds_map(fwd, tr)
+  status, ubase, tmap, n_units = _ds_map(fwd, tr, unit_keys)
   assert status == nat.OK
+  per = 128 // unit_keys  # units per 32-row group
   dense = np.zeros((6 * 128, 6 * 128), bool)
   dense[:n, :n] = m.toarray()
   tp, kb, _ = fwd
@@ -653,9 +657,9 @@ def test_ds_map_numbers_units_from_the_dense_mask(symmetric):
     blk = dense[128 * qb_of[t]:128 * qb_of[t] + 128, 128 * kb[t]:128 * kb[t] + 128]
     word = 0
     for r in range(4):
-      for u in range(8):
-        if blk[32 * r:32 * r + 32, 16 * u:16 * u + 16].any():
-          word |= 1 << (8 * r + u)
+      for u in range(per):
+        if blk[32 * r:32 * r + 32, unit_keys * u:unit_keys * (u + 1)].any():
+          word |= 1 << (per * r + u)
     words[(qb_of[t], kb[t])] = (total, word)
     want_base.append(total)
     total += bin(word).count("1")
@@ -667,9 +671,10 @@ def test_ds_map_numbers_units_from_the_dense_mask(symmetric):
     base, word = words[(kbt[t], kb_of[t])]
     assert tmap[t, 0] == base and int(tmap[t, 1].view(np.uint32)) == word
     keys = dense.T[128 * kb_of[t]:128 * kb_of[t] + 128, 128 * kbt[t]:128 * kbt[t] + 128]
-    for kg in range(8):
+    for kg in range(per):
       for c in range(4):
-        assert keys[16 * kg:16 * kg + 16, 32 * c:32 * c + 32].any() == bool(word >> (8 * c + kg) & 1)
+        live = keys[unit_keys * kg:unit_keys * (kg + 1), 32 * c:32 * c + 32].any()
+        assert live == bool(word >> (per * c + kg) & 1)
 
 
 def test_ds_map_rejects_lists_that_are_not_transposes():
@@ -677,6 +682,7 @@ def test_ds_map_rejects_lists_that_are_not_transposes():
   fwd = fwn.build_tile_mask(m)
   tr = fwn.build_tile_mask(m.T.tocsr())
   assert _ds_map(fwd, tr)[0] == nat.OK
+  assert _ds_map(fwd, tr, 24)[0] == nat.ERR_INVALID_ARG  # 16 or 32 keys per unit
   assert _ds_map(fwd, fwd)[0] == nat.ERR_TILES  # not symmetric
   assert "transpose" in nat.lib().fwn_last_error().decode()
   tp, kb, bits = tr
@@ -691,25 +697,30 @@ def test_ds_launchers_validate_before_launching():
   L = nat.lib()
   F = FAKE
   tiles = _tiles()
-  dmap = nat.DsMap(10, F, F)
-  bf = _desc(dtype=nat.BF16, stride_b=300 * 128, stride_n=128, stride_h=64)
-  need = 1 * 2 * 10 * 1024
+  dmap, dmap32 = nat.DsMap(10, F, F, 16, 0), nat.DsMap(10, F, F, 32, 0)
+  bf, f32 = _desc(dtype=nat.BF16, stride_b=300 * 128, stride_n=128, stride_h=64), _desc()
+  need, need32 = 1 * 2 * 10 * 1024, 1 * 2 * 10 * 4096
   n = ctypes.c_uint64(0)
   assert L.fwn_attn_ds_bytes(bf, dmap, ctypes.byref(n)) == nat.OK and n.value == need
-  # float32 is not built for the exchange
-  assert L.fwn_attn_bwd_dq_ds_launch(_desc(), F, F, need, tiles, dmap, F, None, 0, None) == nat.ERR_UNSUPPORTED
-  assert L.fwn_attn_bwd_dkv_ds_launch(_desc(), F, F, F, F, F, F, tiles, dmap, F, F, F, need, None, 0,
-                                      None) == nat.ERR_UNSUPPORTED
-  # a dS buffer too small, misaligned or missing; a map past 2^21 units per (batch, head)
+  assert L.fwn_attn_ds_bytes(f32, dmap32, ctypes.byref(n)) == nat.OK and n.value == need32
+  assert L.fwn_attn_ds_bytes(f32, nat.DsMap(10, F, F, 8, 0), ctypes.byref(n)) == nat.ERR_INVALID_ARG
+  # a map of the other dtype's unit size
+  assert L.fwn_attn_bwd_dq_ds_launch(f32, F, F, need32, tiles, dmap, F, None, 0, None) == nat.ERR_INVALID_ARG
+  assert L.fwn_attn_bwd_dkv_ds_launch(bf, F, F, F, F, F, F, tiles, dmap32, F, F, F, need32, None, 0,
+                                      None) == nat.ERR_INVALID_ARG
+  # a dS buffer too small, misaligned or missing; a (batch, head) slice of units past 2 GiB
   assert L.fwn_attn_bwd_dq_ds_launch(bf, F, F, need - 1, tiles, dmap, F, None, 0, None) == nat.ERR_INVALID_ARG
+  assert L.fwn_attn_bwd_dq_ds_launch(f32, F, F, need32 - 1, tiles, dmap32, F, None, 0, None) == nat.ERR_INVALID_ARG
   assert L.fwn_attn_bwd_dq_ds_launch(bf, F, F + 16, need, tiles, dmap, F, None, 0, None) == nat.ERR_INVALID_ARG
   assert L.fwn_attn_bwd_dq_ds_launch(bf, F, None, need, tiles, dmap, F, None, 0, None) == nat.ERR_INVALID_ARG
-  assert L.fwn_attn_bwd_dq_ds_launch(bf, F, F, 1 << 40, tiles, nat.DsMap(1 << 21, F, F), F, None, 0,
+  assert L.fwn_attn_bwd_dq_ds_launch(bf, F, F, 1 << 40, tiles, nat.DsMap(1 << 21, F, F, 16, 0), F, None, 0,
                                      None) == nat.ERR_INVALID_ARG
-  assert L.fwn_attn_bwd_dq_ds_launch(bf, F, F, need, tiles, nat.DsMap(10, None, F), F, None, 0,
+  assert L.fwn_attn_bwd_dq_ds_launch(f32, F, F, 1 << 40, tiles, nat.DsMap(1 << 19, F, F, 32, 0), F, None, 0,
                                      None) == nat.ERR_INVALID_ARG
-  assert L.fwn_attn_bwd_dkv_ds_launch(bf, F, F, F, F, F, F, tiles, nat.DsMap(10, F, None), F, F, F, need, None, 0,
-                                      None) == nat.ERR_INVALID_ARG
-  # the dq kernel needs the forward list's half bits
+  assert L.fwn_attn_bwd_dq_ds_launch(bf, F, F, need, tiles, nat.DsMap(10, None, F, 16, 0), F, None, 0,
+                                     None) == nat.ERR_INVALID_ARG
+  assert L.fwn_attn_bwd_dkv_ds_launch(bf, F, F, F, F, F, F, tiles, nat.DsMap(10, F, None, 16, 0), F, F, F, need, None,
+                                      0, None) == nat.ERR_INVALID_ARG
+  # the bf16 dq kernel needs the forward list's half bits (the float32 one does not)
   t1 = nat.Tiles(3, 1, F, F, F, F, 3, 0, 0, 0, F, None, None)
   assert L.fwn_attn_bwd_dq_ds_launch(bf, F, F, need, t1, dmap, F, None, 0, None) == nat.ERR_TILES
