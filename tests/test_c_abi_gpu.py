@@ -149,12 +149,14 @@ def test_bwd_ds_launch_one_stream(split, dtype):
     check(host(x), want, dtype, name)
 
 
-def test_graph_capture_replays_match_eager():
+@pytest.mark.parametrize("ds", [False, True])
+def test_graph_capture_replays_match_eager(ds):
   """The launchers allocate nothing and never synchronise, so a caller may capture them. The
-  forward and the one-stream backward (split schedules, so the combine passes are captured too)
-  are captured into one graph, which is replayed four times with new inputs written in place
-  between replays (eager copies and fills, with synchronisations in between); every replay
-  equals the eager launches on the same inputs bit for bit."""
+  forward and the one-stream backward (split schedules, so the combine passes are captured too;
+  with `ds`, the backward with the dS exchange and its dS buffer) are captured into one graph,
+  which is replayed four times with new inputs written in place between replays (eager copies
+  and fills, with synchronisations in between); every replay equals the eager launches on the
+  same inputs bit for bit."""
   rng = np.random.default_rng(64)
   b, n, h, d = 1, 600, 2, 64
   dtype = torch.bfloat16
@@ -165,16 +167,25 @@ def test_graph_capture_replays_match_eager():
   scale = d ** -0.5
   desc = nat.AttnDesc(b, n, h, d, nat.BF16, scale, *q.stride()[:3])
   size = _ws_size(desc, tiles)
+  dmap = tiles.ds_map(tiles, 16)
+  ds_bytes = dmap.ds_bytes(desc)
   L = nat.lib()
 
   def buffers():
     return dict(out=torch.empty_like(q), lse=torch.empty((b, h, n), device="cuda"),
                 delta=torch.empty((b, h, n), device="cuda"), dq=torch.empty_like(q), dk=torch.empty_like(q),
-                dv=torch.empty_like(q), ws=torch.empty(size, dtype=torch.uint8, device="cuda"))
+                dv=torch.empty_like(q), ws=torch.empty(size, dtype=torch.uint8, device="cuda"),
+                ds=torch.empty(ds_bytes, dtype=torch.uint8, device="cuda"))
 
   def launch(o, stream):
     nat.check(L.fwn_attn_fwd_launch(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), tiles.struct, o["out"].data_ptr(),
                                     o["lse"].data_ptr(), o["ws"].data_ptr(), size, stream))
+    if ds:
+      nat.check(L.fwn_attn_bwd_ds_launch(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), o["out"].data_ptr(),
+                                         do.data_ptr(), o["lse"].data_ptr(), o["delta"].data_ptr(), tiles.struct,
+                                         None, dmap.struct, o["dq"].data_ptr(), o["dk"].data_ptr(), o["dv"].data_ptr(),
+                                         o["ds"].data_ptr(), ds_bytes, o["ws"].data_ptr(), size, stream))
+      return
     nat.check(L.fwn_attn_bwd_launch(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), o["out"].data_ptr(),
                                     do.data_ptr(), o["lse"].data_ptr(), o["delta"].data_ptr(), tiles.struct, None,
                                     o["dq"].data_ptr(), o["dk"].data_ptr(), o["dv"].data_ptr(), o["ws"].data_ptr(),
