@@ -567,9 +567,13 @@ __global__ void __launch_bounds__(NT, 1) dkv_f32_kernel(KArgs a) {
     if constexpr (DS) {
       const uint32_t bit = 4u * (uint32_t)sb + (uint32_t)w;
       const uint32_t so = (ubc + (uint32_t)__builtin_popcount(gfc & 0xffffu & ((1u << bit) - 1u))) * 4096u;
-      float* u = (float*)(dsb + (so + dsl));
+      // A plain pointer has no range check: store only a unit the map has, inside the slice (a
+      // map of other lists cannot write outside the buffer).
+      if ((gfc >> bit & 1u) && so + 4096u <= a.ds_slice_bytes) {
+        float* u = (float*)(dsb + (so + dsl));
 #pragma unroll
-      for (int r = 0; r < 16; ++r) u[4 * (16 * (r >> 3) + (r & 7))] = dp[r];
+        for (int r = 0; r < 16; ++r) u[4 * (16 * (r >> 3) + (r & 7))] = dp[r];
+      }
     }
     float ot[16][D / 32], qt[16][D / 32];
 #pragma unroll
