@@ -3,7 +3,8 @@
 //
 // fp32 MFMA operands are one element per lane, so the second contraction's A operand (V^T, K^T,
 // Q^T, dO^T) is read element-wise straight from the row-major LDS tile; no transposed copy is
-// needed. Tiles stream into LDS in 64-row halves by LDS DMA, double-buffered (HalfDma).
+// needed. Tiles stream into LDS by LDS DMA, double-buffered: in 64-row halves for the backward
+// kernels (HalfDma), in 32-row key groups for the forward (GroupDma).
 //
 // Reference: pallas_attn.py:112-141 (forward), 161-215 (dQ, dK/dV), 274-311 (VJP driver).
 #include "attn_device.h"
@@ -111,51 +112,79 @@ struct HalfDma {
 };
 
 // ------------------------------------------------------------------------------------------
-// Forward, fp32. 128 KB of LDS: one workgroup per CU, 8 waves. Waves w and w + 4 share one SIMD
-// and the query rows 32 (w % 4) ..; wave w + 4k takes key group 2h + k of each tile half h with
-// its own online-softmax state, and the pair merges (m, l, O) through LDS at the end. Two waves
-// per SIMD overlap one's softmax and LDS reads with the other's MFMA chains. The tile's K and V
-// rows stream in halves (rows 0-63, 64-127) through two half buffers, waves 0-3 copying K and
-// waves 4-7 V: the copy of one half runs while the other is computed.
-constexpr int NT_F32 = 512;
-
+// Copies one 32-row key group of a 128-row fp32 tile (global rows row0 ..) into a 32-row group
+// buffer with the buffer unit's LDS DMA, in the layout of HalfDma's rows 0-31 (the swizzle
+// depends on the row modulo 16). Wave w of 4 issues instructions k = w + 4m, each filling rows
+// kR .. kR + R - 1; the lane's part of the source offset depends on the parity of m only.
 template <int D>
-__global__ void __launch_bounds__(NT_F32, 1) fwd_f32_kernel(KArgs a) {
-  constexpr int HB = 64 * D * 4;  // bytes of 64 rows of K or V
-  __shared__ __attribute__((aligned(1024))) char h0[2 * HB];  // rows 0-63: K (swizzled) | V (plain)
-  __shared__ __attribute__((aligned(1024))) char h1[2 * HB];  // rows 64-127
+struct GroupDma {
+  static constexpr int R = 1024 / (D * 4);
+  static constexpr int CPR = D / 4;
+  static constexpr int NI = 32 / R;
+  uint32_t lo[2];
+
+  __device__ __forceinline__ void init(int w, int lane, uint32_t snb, bool swizzle) {
+    const int rl = lane / CPR, pc = lane % CPR;
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      const int row = (w + 4 * m) * R + rl;
+      lo[m] = (uint32_t)rl * snb + (uint32_t)((swizzle ? pc ^ swz_row3(row) : pc) << 4);
+    }
+  }
+
+  __device__ __forceinline__ void issue(rsrc_t r, char* buf, int row0, uint32_t snb, int w) const {
+    uint32_t base = (uint32_t)(uintptr_t)buf;
+    asm volatile("" : "+s"(base));
+    uint32_t l0 = lo[0], l1 = lo[1];
+    asm volatile("" : "+v"(l0), "+v"(l1));
+#pragma unroll
+    for (int m = 0; m < NI / 4; ++m) {
+      const int k = w + 4 * m;
+      const uint32_t src = (uint32_t)(row0 + k * R) * snb + ((m & 1) ? l1 : l0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(uintptr_t)(base + 1024u * k),
+                                               16, (int)src, 0, 0, 0);
+    }
+  }
+};
+
+// Forward, fp32, two workgroups per CU, streamed by 32-key group: the work item's steps are its
+// (tile, key group) pairs in which some wave has a valid element; each step's K and V rows (32 KB
+// at D = 128) go into one of two group buffers, the copy of step s + 1 running while step s is
+// computed, one barrier per step. Groups no wave needs cost neither a copy nor a barrier.
+template <int D>
+__global__ void __launch_bounds__(NT, 2) fwd_f32g_kernel(KArgs a) {
+  constexpr int GB = 32 * D * 4;  // bytes of 32 rows of K or V
+  __shared__ __attribute__((aligned(1024))) char gb0[2 * GB];  // K group (swizzled) | V group (plain)
+  __shared__ __attribute__((aligned(1024))) char gb1[2 * GB];
   const int tid = threadIdx.x, lane = tid & 63;
-  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int w = wid & 3, kh = wid >> 2;  // query rows 32 w .., key group 2h + kh of half h
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int i = lane & 31, g = lane >> 5;
   const Job j = decode_job(a);
   const uint32_t snb = (uint32_t)a.sn * 4;
-  const rsrc_t rQ = make_rsrc((const float*)a.q + j.base, a.slice_bytes);
-  // Waves 0-3 copy K (swizzled), waves 4-7 V (plain).
-  const rsrc_t rKV = make_rsrc((const float*)(kh == 0 ? a.k : a.v) + j.base, a.slice_bytes);
-  const int kvo = kh == 0 ? 0 : HB;
-
+  const rsrc_t rK = make_rsrc((const float*)a.k + j.base, a.slice_bytes);
+  const rsrc_t rV = make_rsrc((const float*)a.v + j.base, a.slice_bytes);
   const int qrow = j.blk * BLK + 32 * w + i;
   f32x4 qf[D / 8];
-  load_frag_f32<D>(qf, rQ, qrow, snb, g);
+  load_frag_f32<D>(qf, make_rsrc((const float*)a.q + j.base, a.slice_bytes), qrow, snb, g);
   F32Offsets<D> off;
   off.init(i, g);
-  HalfDma<D> dma;
-  dma.init(w, lane, snb, kh == 0);
+  GroupDma<D> dmaK, dmaV;
+  dmaK.init(w, lane, snb, true);
+  dmaV.init(w, lane, snb, false);
   f32x16 o[D / 32];
 #pragma unroll
   for (int db = 0; db < D / 32; ++db) o[db] = zero16();
   SoftmaxState st{-__builtin_inff(), 0.f};
 
-  // Key group sb of the tile from the half buffer holding it (local group sl = sb % 2).
-  auto group = [&](int sb, int sl, const char* hb, u32x2 mb) {
-    const char* ldsK = hb;
-    const char* ldsV = hb + HB;
+  // Key group sb of a tile from group buffer gb.
+  auto group = [&](int sb, const char* gb, u32x2 mb) {
+    const char* ldsK = gb;
+    const char* ldsV = gb + GB;
     f32x16 s[1];
     s[0] = zero16();
 #pragma unroll
     for (int u = 0; u < D / 8; ++u) {
-      const f32x4 kx = *(const f32x4*)(ldsK + off.row[u & 3] + off.row_imm(sl, u));
+      const f32x4 kx = *(const f32x4*)(ldsK + off.row[u & 3] + off.row_imm(0, u));
 #pragma unroll
       for (int e = 0; e < 4; ++e) s[0] = mfma_f32(kx[e], qf[u][e], s[0]);
     }
@@ -170,61 +199,58 @@ __global__ void __launch_bounds__(NT_F32, 1) fwd_f32_kernel(KArgs a) {
     for (int r = 0; r < 16; ++r) {
 #pragma unroll
       for (int db = 0; db < D / 32; ++db)
-        o[db] = mfma_f32(*(const float*)(ldsV + off.el_plain + off.el_imm(sl, r, db)), s[0][r], o[db]);
+        o[db] = mfma_f32(*(const float*)(ldsV + off.el_plain + off.el_imm(0, r, db)), s[0][r], o[db]);
     }
   };
 
   int t0, t1;
   tile_range(a, j, t0, t1);
-  uint32_t gcur = 0u;
-  if (t0 < t1) {
-    gcur = tile_groups(a, t0);
-    dma.issue(rKV, h0 + kvo, ((ci32_ptr)a.col)[t0] * BLK, snb, w, 0, any_rows(gcur));
+  // Step iterator: tile ti, its key groups not taken yet in rem (wave-uniform scalars).
+  int ti = t0 - 1;
+  uint32_t rem = 0u;
+  auto take = [&](int& t, int& c) -> bool {
+    while (rem == 0u) {
+      if (++ti >= t1) return false;
+      rem = any_rows(tile_groups(a, ti));
+    }
+    t = ti;
+    c = __builtin_ctz(rem);
+    rem &= rem - 1u;
+    return true;
+  };
+  auto copy = [&](char* gb, int t, int c) {
+    const int row0 = ((ci32_ptr)a.col)[t] * BLK + 32 * c;
+    dmaK.issue(rK, gb, row0, snb, w);
+    dmaV.issue(rV, gb + GB, row0, snb, w);
+  };
+  int tc = 0, cc = 0, tn = 0, cn = 0;
+  bool vc = take(tc, cc), vn = false;
+  u32x2 mbc = {0u, 0u}, mbn = {0u, 0u};
+  if (vc) {
+    copy(gb0, tc, cc);
+    mbc = tile_bits(a, tc, w, lane);
+    vn = take(tn, cn);
   }
-  for (int tt = t0; tt < t1; ++tt) {
-    const int t = __builtin_amdgcn_readfirstlane(tt);
-    const int kb = ((ci32_ptr)a.col)[t];
-    const u32x2 mb = tile_bits(a, t, w, lane);
-    const uint32_t gt = gcur;
-    const uint32_t live = gt >> (4 * w) & 15u;  // key groups with p = 0 throughout are skipped
-    wait_vmem();      // this wave's part of half 0 of tile t, the mask bits (and Q)
-    __syncthreads();  // half 0 landed; every wave is done with half 1 of tile t - 1
-    dma.issue(rKV, h1 + kvo, kb * BLK, snb, w, 1, any_rows(gt));
-    if (t + 1 < t1) gcur = tile_groups(a, t + 1);
-    if (live >> kh & 1u) group(kh, kh, h0, mb);
-    wait_vmem();      // this wave's part of half 1
-    __syncthreads();  // half 1 landed; every wave is done with half 0
-    if (t + 1 < t1) dma.issue(rKV, h0 + kvo, ((ci32_ptr)a.col)[t + 1] * BLK, snb, w, 0, any_rows(gcur));
-    if (live >> (2 + kh) & 1u) group(2 + kh, kh, h1, mb);
-  }
-  // Merge the pair: the second wave of each SIMD hands its O, m and l over through LDS (the halves
-  // are dead after the barrier, and no copy is in flight). m is the log2-domain reference max
-  // shared by lanes i, i + 32.
-  float* xo = (float*)h0 + (size_t)w * (D / 32) * 16 * 64;  // [D / 32][16][64 lanes] per w: all of h0
-  float* xm = (float*)h1 + w * 128;                         // [64 lanes] m, then [64 lanes] l
-  __syncthreads();
-  if (kh == 1) {
-#pragma unroll
-    for (int db = 0; db < D / 32; ++db)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) xo[(db * 16 + r) * 64 + lane] = o[db][r];
-    xm[lane] = st.m;
-    xm[64 + lane] = st.l;
-  }
-  __syncthreads();
-  if (kh == 1) return;
-  {
-    const float m1 = xm[lane], l1 = xm[64 + lane];
-    const float ninf = -__builtin_inff();
-    const float mm = fmaxf(st.m, m1);
-    const float c0 = st.m == ninf ? 0.f : fast_exp2(st.m - mm);
-    const float c1 = m1 == ninf ? 0.f : fast_exp2(m1 - mm);
-#pragma unroll
-    for (int db = 0; db < D / 32; ++db)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[db][r] = o[db][r] * c0 + xo[(db * 16 + r) * 64 + lane] * c1;
-    st.l = st.l * c0 + l1 * c1;
-    st.m = mm;
+  // One step: step (tc, cc) is in `cur`; the copy of step (tn, cn) goes into `nxt`.
+  auto step = [&](char* cur, char* nxt) {
+    wait_vmem();      // this wave's part of the current step (and its mask bits)
+    __syncthreads();  // the step landed; every wave is done with the previous step's buffer
+    if (vn) {
+      copy(nxt, tn, cn);
+      mbn = tn != tc ? tile_bits(a, tn, w, lane) : mbc;
+    }
+    const uint32_t live = tile_groups(a, tc) >> (4 * w) & 15u;
+    if (live >> cc & 1u) group(cc, cur, mbc);
+    tc = tn;
+    cc = cn;
+    mbc = mbn;
+    vc = vn;
+    vn = vc && take(tn, cn);
+  };
+  while (vc) {
+    step(gb0, gb1);
+    if (!vc) break;
+    step(gb1, gb0);
   }
   const float ltot = st.l + __shfl_xor(st.l, 32);
   if (j.part >= 0) {
@@ -687,7 +713,7 @@ hipError_t launch_d(Kind kind, const KArgs& a, hipStream_t stream) {
   }
   const dim3 grid((unsigned)a.n_items * (unsigned)(a.batch * a.heads));
   switch (kind) {
-    case Kind::kFwd: hipLaunchKernelGGL(fwd_f32_kernel<D>, grid, dim3(NT_F32), 0, stream, a); break;
+    case Kind::kFwd: hipLaunchKernelGGL(fwd_f32g_kernel<D>, grid, block, 0, stream, a); break;
     case Kind::kDq: hipLaunchKernelGGL(dq_f32_kernel<D>, grid, block, 0, stream, a); break;
     case Kind::kDkv: hipLaunchKernelGGL((dkv_f32_kernel<D, false>), grid, block, 0, stream, a); break;
     case Kind::kDkvDs: hipLaunchKernelGGL((dkv_f32_kernel<D, true>), grid, block, 0, stream, a); break;
