@@ -803,11 +803,6 @@ struct KeyWave {
   }
 };
 
-// This lane's mask word of tile 0 for 16-key group kg (add 256 words per tile).
-__device__ __forceinline__ const uint64_t* key_mask_words(const KArgs& a, int kg, int g, int t16) {
-  return a.lanes + (int64_t)(kg >> 1) * 64 + 32 * (g >> 1) + 16 * (kg & 1) + t16;
-}
-
 // 8 waves, one workgroup per CU, the Q/dO tiles double-buffered: one barrier per tile.
 //
 // With DS (the bf16 backward with the dS exchange), every unit's dS also goes to HBM as one 1 KB

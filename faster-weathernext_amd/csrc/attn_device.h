@@ -197,6 +197,15 @@ __device__ __forceinline__ uint32_t tile_halves(const KArgs& a, int t) {
   return a.halves ? ((const __attribute__((address_space(4))) uint32_t*)a.halves)[t] : ~0u;
 }
 
+// Masks of the 16-key dK/dV kernel, whose lane l holds key l % 16 of its wave's 16 and queries
+// 4g + r, 16 + 4g + r (g = l / 16, r < 4) of a 32-query group. This lane's mask word of tile 0 for
+// 16-key group kg (add 256 words per tile): the word of 32-row wave kg / 2, lane
+// 32 (g / 2) + 16 (kg % 2) + l % 16, which, shifted right by 4 (g % 2), holds element (query
+// group c, half m, r) at bit 16c + 8m + r.
+__device__ __forceinline__ const uint64_t* key_mask_words(const KArgs& a, int kg, int g, int t16) {
+  return a.lanes + (int64_t)(kg >> 1) * 64 + 32 * (g >> 1) + 16 * (kg & 1) + t16;
+}
+
 // Column groups with a valid element in any row group.
 __device__ __forceinline__ uint32_t any_rows(uint32_t g) { return (g | g >> 4 | g >> 8 | g >> 12) & 15u; }
 
