@@ -86,6 +86,9 @@ def parse():
                  help="run dQ and then dK/dV on one stream instead of side by side on two streams")
   p.add_argument("--no-ds", action="store_true",
                  help="the recomputing dQ kernel beside dK/dV instead of the dS exchange")
+  p.add_argument("--precision", default="native", choices=["native", "bf16x3"],
+                 help="float32 workloads: the forward's products (bf16x3: three bf16 products per fp32 "
+                      "product, the backward in IEEE fp32)")
   p.add_argument("--layout", default="node", choices=["node", "head"],
                  help="storage of q, k, v, o, dO, dq, dk, dv: node-major [B, n, H, D] (the reference's "
                       "interface) or head-major [B, H, n, D] passed as strided views")
@@ -397,6 +400,10 @@ def main():
   cfg = WORKLOADS[args.workload]
   D, H, B = cfg["head_dim"], cfg["heads"], cfg["batch"]
   dtype = torch.bfloat16 if cfg["dtype"] == "bf16" else torch.float32
+  x3 = args.precision == "bf16x3"
+  if x3 and dtype != torch.float32:
+    print("--precision bf16x3 applies to float32 workloads (c2, c5f32)", file=sys.stderr)
+    return 2
   dev = torch.device("cuda:0")
   torch.cuda.set_device(dev)
 
@@ -425,6 +432,8 @@ def main():
     q, k, v, do = (x.permute(0, 2, 1, 3).contiguous().permute(0, 2, 1, 3) for x in (q, k, v, do))
   scale = D ** -0.5
   desc = nat.AttnDesc(B, n, H, D, nat.BF16 if dtype == torch.bfloat16 else nat.F32, scale, *q.stride()[:3])
+  # The forward's descriptor (bf16x3: k and v split into its workspace first); the backward's is native.
+  fdesc = nat.AttnDesc(B, n, H, D, nat.F32, scale, *q.stride()[:3], 0, 0, 0, nat.PREC_BF16X3, 0) if x3 else desc
   out = torch.empty_like(q)
   lse = torch.empty((B, H, n), device=dev, dtype=torch.float32)
   delta = torch.empty_like(lse)
@@ -433,7 +442,7 @@ def main():
   stream = torch.cuda.current_stream(dev)
   sp = stream.cuda_stream
   ts = tiles.struct_for(B, H)
-  ws = fwn.hip_attn.workspace(desc, dev, tiles)
+  ws = fwn.hip_attn.workspace(fdesc, dev, tiles)
   wsp, wsn = (ws.data_ptr(), ws.numel()) if ws is not None else (None, 0)
   # dK/dV runs on a second stream beside dQ (as the package's backward does), with its own
   # workspace; the step joins the two streams at its end.
@@ -442,7 +451,7 @@ def main():
   ws2p, ws2n = (ws2.data_ptr(), ws2.numel()) if ws2 is not None else (None, 0)
 
   def fwd(st):
-    nat.check(L.fwn_attn_fwd_launch(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), ts, out.data_ptr(),
+    nat.check(L.fwn_attn_fwd_launch(fdesc, q.data_ptr(), k.data_ptr(), v.data_ptr(), ts, out.data_ptr(),
                                     lse.data_ptr(), wsp, wsn, st.cuda_stream))
 
   def bwd_delta(st):
@@ -545,26 +554,31 @@ def main():
   dominant = max((k_ for k_ in per_solo if algo.get(k_)), key=lambda k_: per_solo[k_])
   achieved = algo[dominant] / (per_solo[dominant] * 1e-3) / 1e12
   peak = PEAK[cfg["dtype"]]
+  if x3 and dominant == "fwd":
+    peak = round(PEAK["bf16"] / 3, 1)  # three bf16 MFMA products per counted fp32 product
   traffic, traffic_src = measured_traffic(args.workload, dominant)
   rate = lambda name, ms: round(algo[name] / (ms * 1e-3) / 1e12, 3)
 
   result = {
       "metric": METRIC, "value": round(value, 3), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
       "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak",
-      "vs_baseline": None, "dtype": cfg["dtype"],
+      "vs_baseline": None,
+      "dtype": cfg["dtype"] if not x3 else ("bf16x3" if not cfg["backward"] else "bf16x3 fwd, f32 bwd"),
       "data": "synthetic: N(0, sigma) q/k/v and N(0,1) dO, member m from numpy PCG64 seed m, on a generated "
               "icosahedral mesh; no weights or datasets",
       "config": {"workload": cfg["desc"], "mesh_refinement": 6, "n": n, "k_hop": cfg["k_hop"], "batch": B,
                  "heads": H, "head_dim": D, "order": "hilbert" if cfg["reorder"] else "subdivision",
                  "sigma": cfg["sigma"], "live_tiles": T, "tile_density": round(tiles.density, 4),
                  "live_group_fraction": round(tiles.group_fraction, 4),
-                 "valid_entries": int(mask.nnz), "item_tiles": tiles.item_cap_for(B, H)},
+                 "valid_entries": int(mask.nnz), "item_tiles": tiles.item_cap_for(B, H),
+                 "precision": args.precision},
       "roofline": {"bound": "mfma", "kernel": dominant, "achieved": round(achieved, 3), "peak": peak,
                    "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": traffic,
                    "traffic_source": traffic_src, "ms": round(per_solo[dominant], 4),
                    "work": "algorithmic FLOPs over whole live 128x128 tiles; the kernels skip 32x32 groups "
                            "without a valid element (config.live_group_fraction of them execute), so frac "
-                           "can exceed 1",
+                           "can exceed 1" + ("; bf16x3: fp32-equivalent products against the bf16 MFMA "
+                                             "peak / 3" if x3 and dominant == "fwd" else ""),
                    "timing": ("the timed pass (every kernel in order on one stream, each alone on the GPU)"
                               if paired is solo else
                               "solo pass: the same K steps again with every kernel on one stream (each alone on "

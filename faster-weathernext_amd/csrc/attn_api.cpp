@@ -57,6 +57,16 @@ int check_desc(const fwn_attn_desc* d) {
     return fail(FWN_ERR_UNSUPPORTED, "dtype %d not supported (0 = f32, 1 = bf16)", d->dtype);
   if (!(d->scale > 0.f) || !std::isfinite(d->scale))
     return fail(FWN_ERR_INVALID_ARG, "scale must be positive and finite");
+  if (d->precision != FWN_PREC_NATIVE && d->precision != FWN_PREC_BF16X3)
+    return fail(FWN_ERR_UNSUPPORTED, "precision %d not supported (0 = native, 1 = bf16x3)", d->precision);
+  if (d->precision == FWN_PREC_BF16X3) {
+    if (d->dtype != FWN_F32) return fail(FWN_ERR_UNSUPPORTED, "bf16x3 precision needs float32 tensors");
+    // The split k and v slices are n rows of 4 * head_dim bytes, addressed with 32-bit offsets,
+    // and the split pass indexes 8-element chunks with 32-bit integers.
+    if ((int64_t)d->n * 4 * d->head_dim >= ((int64_t)1 << 31) ||
+        (int64_t)d->batch * d->heads * d->n * (d->head_dim / 8) >= ((int64_t)1 << 31))
+      return fail(FWN_ERR_INVALID_ARG, "bf16x3: batch * heads * n too large for the split pass");
+  }
   const int64_t vec = d->dtype == FWN_BF16 ? 8 : 4;  // elements per 16 bytes
   const int64_t n_blocks = (d->n + FWN_BLOCK - 1) / FWN_BLOCK;
   if (n_blocks * d->batch * d->heads > INT32_MAX)
@@ -104,8 +114,27 @@ int check_tiles(const fwn_attn_desc* d, const fwn_tiles* t, const char* name) {
   return FWN_OK;
 }
 
-uint64_t workspace_bytes_for(const fwn_attn_desc* d, const fwn_tiles* t) {
+uint64_t partial_bytes(const fwn_attn_desc* d, const fwn_tiles* t) {
   return (uint64_t)t->n_parts * (uint64_t)d->batch * (uint64_t)d->heads * (uint64_t)slot_words(d->head_dim) * 4u;
+}
+
+// Bytes of one split tensor (bf16x3 forward): batch * heads * n rows of hi and lo bf16.
+uint64_t split_bytes(const fwn_attn_desc* d) {
+  return (uint64_t)d->batch * (uint64_t)d->heads * (uint64_t)d->n * (uint64_t)d->head_dim * 4u;
+}
+
+// Partial slots, then (bf16x3) the split k and v, each from a 256-byte boundary.
+uint64_t workspace_bytes_for(const fwn_attn_desc* d, const fwn_tiles* t) {
+  const uint64_t parts = partial_bytes(d, t);
+  if (d->precision != FWN_PREC_BF16X3) return parts;
+  return ((parts + 255u) & ~(uint64_t)255u) + 2u * ((split_bytes(d) + 255u) & ~(uint64_t)255u);
+}
+
+// The backward kernels compute in the tensors' dtype only.
+int check_native(const fwn_attn_desc* d, const char* what) {
+  if (d->precision != FWN_PREC_NATIVE)
+    return fail(FWN_ERR_UNSUPPORTED, "%s: only FWN_PREC_NATIVE is built (got precision %d)", what, d->precision);
+  return FWN_OK;
 }
 
 int check_workspace(const fwn_attn_desc* d, const fwn_tiles* t, const void* ws, uint64_t ws_bytes) {
@@ -159,7 +188,9 @@ void set_tiles(KArgs& a, const fwn_tiles* t, void* ws) {
 // The main kernel, then (when the list has split blocks) the combine pass, in stream order.
 int launch_with_combine(Kind kind, Kind combine, const fwn_attn_desc* d, const KArgs& a, hipStream_t stream,
                         const char* what) {
-  if (hipError_t e = launch(kind, d->dtype, d->head_dim, a, stream); e != hipSuccess)
+  const hipError_t err = d->precision == FWN_PREC_BF16X3 ? launch_x3(kind, d->head_dim, a, stream)
+                                                          : launch(kind, d->dtype, d->head_dim, a, stream);
+  if (hipError_t e = err; e != hipSuccess)
     return fail(FWN_ERR_HIP, "%s launch: %s", what, hipGetErrorString(e));
   if (a.n_split > 0) {
     if (hipError_t e = launch(combine, d->dtype, d->head_dim, a, stream); e != hipSuccess)
@@ -242,6 +273,23 @@ int fwn_attn_fwd_launch(const fwn_attn_desc* desc, const void* q, const void* k,
   a.out0 = o;
   a.lse_out = lse;
   set_tiles(a, tiles, workspace);
+  if (desc->precision == FWN_PREC_BF16X3) {
+    // k and v split into the workspace after the partial slots, in stream order before the forward.
+    const uint64_t x0 = (partial_bytes(desc, tiles) + 255u) & ~(uint64_t)255u;
+    const uint64_t xs = (split_bytes(desc) + 255u) & ~(uint64_t)255u;
+    uint16_t* kx = (uint16_t*)((char*)workspace + x0);
+    uint16_t* vx = (uint16_t*)((char*)workspace + x0 + xs);
+    const hipStream_t st = (hipStream_t)stream;
+    for (int m = 0; m < 2; ++m) {
+      if (hipError_t e = launch_split_x3((const float*)(m ? v : k), desc->stride_b, desc->stride_n, desc->stride_h,
+                                         desc->batch, desc->n, desc->heads, desc->head_dim, m ? vx : kx, st);
+          e != hipSuccess)
+        return fail(FWN_ERR_HIP, "bf16x3 split launch: %s", hipGetErrorString(e));
+    }
+    a.kx = kx;
+    a.vx = vx;
+    a.xslice_bytes = (uint32_t)((int64_t)desc->n * 4 * desc->head_dim);
+  }
   return launch_with_combine(Kind::kFwd, Kind::kFwdCombine, desc, a, (hipStream_t)stream, "forward");
 }
 
@@ -264,6 +312,7 @@ int fwn_attn_bwd_dq_launch(const fwn_attn_desc* desc, const void* q, const void*
                            void* dq, void* workspace, uint64_t workspace_bytes, void* stream) {
   clear_error();
   if (int rc = check_desc(desc)) return rc;
+  if (int rc = check_native(desc, "bwd_dq")) return rc;
   if (int rc = check_tensor(q, "q")) return rc;
   if (int rc = check_tensor(k, "k")) return rc;
   if (int rc = check_tensor(v, "v")) return rc;
@@ -289,6 +338,7 @@ int fwn_attn_bwd_dkv_launch(const fwn_attn_desc* desc, const void* q, const void
                             void* dk, void* dv, void* workspace, uint64_t workspace_bytes, void* stream) {
   clear_error();
   if (int rc = check_desc(desc)) return rc;
+  if (int rc = check_native(desc, "bwd_dkv")) return rc;
   if (int rc = check_tensor(q, "q")) return rc;
   if (int rc = check_tensor(k, "k")) return rc;
   if (int rc = check_tensor(v, "v")) return rc;
@@ -339,6 +389,7 @@ int fwn_attn_bwd_dkv_ds_launch(const fwn_attn_desc* desc, const void* q, const v
                                void* workspace, uint64_t workspace_bytes, void* stream) {
   clear_error();
   if (int rc = check_desc(desc)) return rc;
+  if (int rc = check_native(desc, "bwd_dkv_ds")) return rc;
   if (int rc = check_ds(desc, map, ds, ds_bytes, false, true)) return rc;
   if (int rc = check_tensor(q, "q")) return rc;
   if (int rc = check_tensor(k, "k")) return rc;
@@ -368,6 +419,7 @@ int fwn_attn_bwd_dq_ds_launch(const fwn_attn_desc* desc, const void* k, const vo
                               uint64_t workspace_bytes, void* stream) {
   clear_error();
   if (int rc = check_desc(desc)) return rc;
+  if (int rc = check_native(desc, "bwd_dq_ds")) return rc;
   if (int rc = check_ds(desc, map, ds, ds_bytes, true, false)) return rc;
   if (int rc = check_tensor(k, "k")) return rc;
   if (int rc = check_tensor(dq, "dq")) return rc;

@@ -53,6 +53,9 @@ extern "C" int fwn_attn_fwd_launch_noalloc(const fwn_attn_desc* desc, const void
                                            const fwn_tiles* tiles, void* o, float* lse, void* stream) {
   uint64_t need = 0;
   if (int rc = fwn_attn_workspace_size(desc, tiles, &need)) return rc;  // validates desc and tiles
+  if (desc->precision != FWN_PREC_NATIVE)
+    return fwn::fail(FWN_ERR_UNSUPPORTED, "the scratch forward takes FWN_PREC_NATIVE only (bf16x3 splits k and v "
+                                          "into a workspace: use fwn_attn_fwd_launch)");
   if (need > FWN_SCRATCH_BYTES)
     return fwn::fail(FWN_ERR_INVALID_ARG,
                      "the split schedule needs %llu bytes of scratch; the static scratch holds %llu "

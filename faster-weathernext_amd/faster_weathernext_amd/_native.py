@@ -38,7 +38,12 @@ class AttnDesc(ctypes.Structure):
   _fields_ = [("batch", ctypes.c_int32), ("n", ctypes.c_int32), ("heads", ctypes.c_int32),
               ("head_dim", ctypes.c_int32), ("dtype", ctypes.c_int32), ("scale", ctypes.c_float),
               ("stride_b", ctypes.c_int64), ("stride_n", ctypes.c_int64), ("stride_h", ctypes.c_int64),
-              ("ostride_b", ctypes.c_int64), ("ostride_n", ctypes.c_int64), ("ostride_h", ctypes.c_int64)]
+              ("ostride_b", ctypes.c_int64), ("ostride_n", ctypes.c_int64), ("ostride_h", ctypes.c_int64),
+              ("precision", ctypes.c_int32), ("reserved", ctypes.c_int32)]
+
+
+PREC_NATIVE = 0  # FWN_PREC_NATIVE: products in the tensors' dtype
+PREC_BF16X3 = 1  # FWN_PREC_BF16X3: float32 tensors, products from three bf16 parts (forward only)
 
 
 class Tiles(ctypes.Structure):

@@ -269,14 +269,32 @@ def _check(q):
     raise ValueError("expected [batch, n, heads, head_dim]")
 
 
-def _desc(q, scale, o=None):
+# Product precision of the forward (the reference picks its dot algorithm from jax's default
+# matmul precision and strict_fp32, pallas_attn.py:336-341):
+#   "native": products in the tensors' dtype (IEEE float32 products for float32, the reference's
+#             strict_fp32; bf16 products for bf16);
+#   "bf16x3": float32 tensors, each product from bf16 parts, hi*hi + hi*lo + lo*hi (about 16
+#             significant bits per operand; the role of the reference's 3xTF32 "highest" dots).
+#             The backward of a bf16x3 forward computes in IEEE float32.
+PRECISIONS = {"native": nat.PREC_NATIVE, "bf16x3": nat.PREC_BF16X3}
+
+
+def _precision(precision, dtype):
+  if precision not in PRECISIONS:
+    raise ValueError(f"precision {precision!r}: one of {sorted(PRECISIONS)}")
+  if precision == "bf16x3" and dtype != torch.float32:
+    raise TypeError("precision 'bf16x3' needs float32 tensors")
+  return PRECISIONS[precision]
+
+
+def _desc(q, scale, o=None, precision=nat.PREC_NATIVE):
   """Call descriptor: q's strides for q, k, v, dq, dk, dv and o's for o, dout (0 = the same)."""
   b, n, h, d = q.shape
   sb, sn, sh, _ = q.stride()
   osb = osn = osh = 0
   if o is not None and o.stride() != q.stride():
     osb, osn, osh, _ = o.stride()
-  return nat.AttnDesc(b, n, h, d, _DTYPES[q.dtype], float(scale), sb, sn, sh, osb, osn, osh)
+  return nat.AttnDesc(b, n, h, d, _DTYPES[q.dtype], float(scale), sb, sn, sh, osb, osn, osh, precision, 0)
 
 
 def _in_place(x):
@@ -312,18 +330,20 @@ def _ws_args(ws):
   return (ws.data_ptr(), ws.numel()) if ws is not None else (None, 0)
 
 
-def attention_forward(q, k, v, tiles, scale, with_lse=True):
+def attention_forward(q, k, v, tiles, scale, with_lse=True, precision="native"):
   """Forward kernel: returns (out, lse) with lse float32 [batch, heads, n] (None if not requested).
 
   q, k, v are read where they lie when their strides allow it (e.g. views of one fused
-  projection); out is a new contiguous [batch, n, heads, head_dim] tensor.
+  projection); out is a new contiguous [batch, n, heads, head_dim] tensor. ``precision``: see
+  PRECISIONS.
   """
   _check(q)
+  prec = _precision(precision, q.dtype)
   q = _in_place(q)
   k = _same_layout(k, q, "k")
   v = _same_layout(v, q, "v")
   out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
-  desc = _desc(q, scale, out)
+  desc = _desc(q, scale, out, prec)
   tl = _as_tiles(tiles, q.shape[1], q.device)
   lse = torch.empty((q.shape[0], q.shape[2], q.shape[1]), dtype=torch.float32, device=q.device) if with_lse else None
   ws = workspace(desc, q.device, tl)
@@ -412,9 +432,9 @@ class _TiledAttention(torch.autograd.Function):
   the per-row log-sum-exp; the backward recomputes P tile by tile."""
 
   @staticmethod
-  def forward(ctx, q, k, v, tiles, tiles_t, scale):
+  def forward(ctx, q, k, v, tiles, tiles_t, scale, precision):
     need = any(ctx.needs_input_grad[:3])
-    out, lse = attention_forward(q, k, v, tiles, scale, with_lse=need)
+    out, lse = attention_forward(q, k, v, tiles, scale, with_lse=need, precision=precision)
     if need:
       ctx.save_for_backward(q, k, v, out, lse)
       ctx.tiles, ctx.tiles_t, ctx.scale = tiles, tiles_t, scale
@@ -424,7 +444,7 @@ class _TiledAttention(torch.autograd.Function):
   def backward(ctx, dout):
     q, k, v, out, lse = ctx.saved_tensors
     dq, dk, dv = attention_backward(q, k, v, out, lse, dout, ctx.tiles, ctx.tiles_t, ctx.scale)
-    return dq, dk, dv, None, None, None
+    return dq, dk, dv, None, None, None, None
 
 
 class _TiledAttentionQKV(torch.autograd.Function):
@@ -432,10 +452,10 @@ class _TiledAttentionQKV(torch.autograd.Function):
   read q, k, v where the projection wrote them and write dq, dk, dv into one packed gradient."""
 
   @staticmethod
-  def forward(ctx, qkv, tiles, tiles_t, scale):
+  def forward(ctx, qkv, tiles, tiles_t, scale, precision):
     q, k, v = qkv.unbind(2)
     need = ctx.needs_input_grad[0]
-    out, lse = attention_forward(q, k, v, tiles, scale, with_lse=need)
+    out, lse = attention_forward(q, k, v, tiles, scale, with_lse=need, precision=precision)
     if need:
       ctx.save_for_backward(qkv, out, lse)
       ctx.tiles, ctx.tiles_t, ctx.scale = tiles, tiles_t, scale
@@ -449,28 +469,33 @@ class _TiledAttentionQKV(torch.autograd.Function):
     dq, dk, dv = dqkv.unbind(2)
     _backward_into(q, k, v, out, lse, _same_layout(dout, out, "dout"), ctx.tiles, ctx.tiles_t, ctx.scale,
                    dq, dk, dv)
-    return dqkv, None, None, None
+    return dqkv, None, None, None, None
 
 
-def tiled_flash_attention_qkv(qkv, tiles, *, scale, tiles_t=None):
+def tiled_flash_attention_qkv(qkv, tiles, *, scale, tiles_t=None, precision="native"):
   """Attention over a packed qkv [batch, n, 3, heads, head_dim] (one fused projection's output,
   contiguous) -> [batch, n, heads, head_dim], with no copy of q, k, v or of their gradients."""
   _check(qkv[:, :, 0])
+  _precision(precision, qkv.dtype)
   if qkv.dim() != 5 or qkv.shape[2] != 3 or not qkv.is_contiguous():
     raise ValueError("expected a contiguous [batch, n, 3, heads, head_dim] tensor")
   if tiles_t is not None and not isinstance(tiles_t, TileList):
     tiles_t = tuple(tiles_t)
-  return _TiledAttentionQKV.apply(qkv, tiles, tiles_t, float(scale))
+  return _TiledAttentionQKV.apply(qkv, tiles, tiles_t, float(scale), precision)
 
 
-def tiled_flash_attention(q, k, v, tile_ptr, tile_kb=None, tile_bits=None, *, scale, tiles_t=None):
+def tiled_flash_attention(q, k, v, tile_ptr, tile_kb=None, tile_bits=None, *, scale, tiles_t=None,
+                          precision="native"):
   """q, k, v: [batch, n, heads, head_dim] float32/bfloat16 on the GPU -> [batch, n, heads, head_dim].
 
   ``tile_ptr`` may be a prepared TileList (then tile_kb and tile_bits are omitted) or the first of
   the three arrays of ``build_tile_mask``. ``tiles_t`` (TileList or array triple) is the
   transposed mask's list for the dK/dV kernel; it defaults to the forward's (symmetric masks).
+  ``precision`` ("native" or "bf16x3", float32 only): the forward's products, see PRECISIONS.
   """
+  _check(q)
+  _precision(precision, q.dtype)
   tiles = tile_ptr if isinstance(tile_ptr, TileList) else (tile_ptr, tile_kb, tile_bits)
   if tiles_t is not None and not isinstance(tiles_t, TileList):
     tiles_t = tuple(tiles_t)
-  return _TiledAttention.apply(q, k, v, tiles, tiles_t, float(scale))
+  return _TiledAttention.apply(q, k, v, tiles, tiles_t, float(scale), precision)

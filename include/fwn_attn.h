@@ -45,6 +45,20 @@ typedef enum fwn_status {
 
 typedef enum fwn_dtype { FWN_F32 = 0, FWN_BF16 = 1 } fwn_dtype;
 
+/* How the forward forms its products (the reference's dot precision, chosen in
+ * pallas_attn.py:336-341 and passed to every dot):
+ *   FWN_PREC_NATIVE: in the tensors' dtype: IEEE float32 products on the float32 matrix
+ *     instructions (the reference's strict_fp32 F32_F32_F32) or bf16 products for bf16 tensors.
+ *   FWN_PREC_BF16X3: float32 tensors only. Each operand x is split into bf16 parts
+ *     hi = bf16(x), lo = bf16(x - hi) and each product is hi*hi + hi*lo + lo*hi with float32
+ *     accumulation: about 16 significant bits per operand (TF32 has 11) on the bf16 matrix
+ *     instructions, the role of the reference's TF32_TF32_F32_X3 under "highest". The
+ *     forward launcher splits k and v into the workspace first (fwn_attn_workspace_size counts
+ *     it); q and P are split in registers. The backward launchers take FWN_PREC_NATIVE only
+ *     (they return FWN_ERR_UNSUPPORTED for this mode; run them with a native descriptor).
+ * A zeroed descriptor field means FWN_PREC_NATIVE. */
+typedef enum fwn_precision { FWN_PREC_NATIVE = 0, FWN_PREC_BF16X3 = 1 } fwn_precision;
+
 /* Shape of one attention call. scale multiplies q.k (the reference passes key_size**-0.5,
  * patch.py:174). Strides are in elements. stride_* apply to q, k, v and to dq, dk, dv;
  * ostride_* to o and dout, or are all 0 to mean "the same as stride_*". Two layouts let a fused
@@ -63,6 +77,8 @@ typedef struct fwn_attn_desc {
   int64_t ostride_b;
   int64_t ostride_n;
   int64_t ostride_h;
+  int32_t precision;  /* fwn_precision */
+  int32_t reserved;   /* 0 */
 } fwn_attn_desc;
 
 /* One work item of a tile list: tiles [t0, t1) of row block `block`. With part < 0 the item
@@ -171,7 +187,8 @@ int fwn_tiles_schedule_fill(int32_t n_blocks, const int32_t* tile_ptr, int32_t m
 
 /* Workspace bytes the forward, dq and dk/dv launchers need for `tiles`:
  * tiles->n_parts * batch * heads * 128 * (2 * head_dim + 2) * 4 (float32 partial outputs plus
- * the forward's per-row max and sum). */
+ * the forward's per-row max and sum), rounded up to 256 bytes and, with FWN_PREC_BF16X3, plus
+ * 2 * batch * heads * n * head_dim * 4 for the split k and v. */
 int fwn_attn_workspace_size(const fwn_attn_desc* desc, const fwn_tiles* tiles, uint64_t* bytes);
 
 /* Forward: o = softmax(mask(q k^T * scale)) v, walking only live tiles with an online softmax.
@@ -190,7 +207,7 @@ int fwn_attn_fwd_launch(const fwn_attn_desc* desc, const void* q, const void* k,
  * (fwn_attn_workspace_size); lists whose blocks are not split need none. The scratch's device
  * address is looked up on the first call on each device, so make that call outside graph
  * capture. Calls on one device share its scratch: calls whose kernels can overlap on one device
- * (other streams, other threads) race, so order them on one stream. */
+ * (other streams, other threads) race, so order them on one stream. FWN_PREC_NATIVE only. */
 #define FWN_SCRATCH_BYTES (64ull << 20)
 int fwn_attn_fwd_launch_noalloc(const fwn_attn_desc* desc, const void* q, const void* k, const void* v,
                                 const fwn_tiles* tiles, void* o, float* lse, void* stream);

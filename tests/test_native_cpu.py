@@ -724,3 +724,48 @@ def test_ds_launchers_validate_before_launching():
   # the bf16 dq kernel needs the forward list's half bits (the float32 one does not)
   t1 = nat.Tiles(3, 1, F, F, F, F, 3, 0, 0, 0, F, None, None)
   assert L.fwn_attn_bwd_dq_ds_launch(bf, F, F, need, t1, dmap, F, None, 0, None) == nat.ERR_TILES
+
+
+def test_split_precision_is_validated():
+  """FWN_PREC_BF16X3 takes float32 tensors; the backward launchers and the scratch forward take
+  FWN_PREC_NATIVE only; unknown precisions are refused. All before any HIP call. The workspace
+  adds the split k and v (2 * batch * heads * n * head_dim * 4 bytes) after the partial slots."""
+  L = nat.lib()
+  F = FAKE
+  tiles = _tiles()
+  x3 = _desc(precision=nat.PREC_BF16X3)
+  n = ctypes.c_uint64(0)
+  assert L.fwn_attn_workspace_size(x3, tiles, ctypes.byref(n)) == nat.OK
+  assert n.value == 2 * (1 * 2 * 300 * 64 * 4)
+  split = _tiles(n_items=5, n_parts=3, n_split=1, split=F)
+  assert L.fwn_attn_workspace_size(x3, split, ctypes.byref(n)) == nat.OK
+  parts = 3 * 1 * 2 * 128 * (2 * 64 + 2) * 4
+  assert n.value == ((parts + 255) // 256) * 256 + 2 * (2 * 300 * 64 * 4)
+  # a workspace without room for the split k and v is refused
+  assert L.fwn_attn_fwd_launch(x3, F, F, F, split, F, None, F, n.value - 1, None) == nat.ERR_INVALID_ARG
+  assert L.fwn_attn_fwd_launch(x3, F, F, F, tiles, F, None, F, 2 * (2 * 300 * 64 * 4) - 1,
+                               None) == nat.ERR_INVALID_ARG
+  assert L.fwn_attn_fwd_launch(x3, F, F, F, tiles, F, None, None, 0, None) == nat.ERR_INVALID_ARG
+  for bad, code in ((_desc(dtype=nat.BF16, precision=nat.PREC_BF16X3), nat.ERR_UNSUPPORTED),
+                    (_desc(precision=2), nat.ERR_UNSUPPORTED), (_desc(precision=-1), nat.ERR_UNSUPPORTED)):
+    assert L.fwn_attn_fwd_launch(bad, F, F, F, tiles, F, None, None, 0, None) == code
+    assert L.fwn_attn_workspace_size(bad, tiles, ctypes.byref(n)) == code
+  assert L.fwn_attn_bwd_dq_launch(x3, F, F, F, F, F, F, tiles, F, None, 0, None) == nat.ERR_UNSUPPORTED
+  assert L.fwn_attn_bwd_dkv_launch(x3, F, F, F, F, F, F, tiles, F, F, None, 0, None) == nat.ERR_UNSUPPORTED
+  dmap = nat.DsMap(10, F, F, 32, 0)
+  assert L.fwn_attn_bwd_dkv_ds_launch(x3, F, F, F, F, F, F, tiles, dmap, F, F, F, 1 << 20, None, 0,
+                                      None) == nat.ERR_UNSUPPORTED
+  assert L.fwn_attn_bwd_dq_ds_launch(x3, F, F, 1 << 20, tiles, dmap, F, None, 0, None) == nat.ERR_UNSUPPORTED
+  assert "NATIVE" in L.fwn_last_error().decode()
+  assert L.fwn_attn_fwd_launch_noalloc(x3, F, F, F, tiles, F, None, None) == nat.ERR_UNSUPPORTED
+
+
+def test_split_precision_python_options():
+  import torch
+  from faster_weathernext_amd import hip_attn
+  assert hip_attn._precision("bf16x3", torch.float32) == nat.PREC_BF16X3
+  assert hip_attn._precision("native", torch.bfloat16) == nat.PREC_NATIVE
+  with pytest.raises(TypeError):
+    hip_attn._precision("bf16x3", torch.bfloat16)
+  with pytest.raises(ValueError):
+    hip_attn._precision("tf32", torch.float32)
