@@ -101,14 +101,15 @@ def parse():
 TRAFFIC_DIR = os.path.join(ROOT, "profiles")
 
 
-def measured_traffic(workload, kernel):
+def measured_traffic(workload, kernel, precision="native"):
   """HBM bytes per launch of `kernel` on `workload` from the committed PMC summary, if there is one.
 
-  The summary (profiles/hbm_traffic_<kernel>_<workload>.txt) holds a line
-  `traffic_bytes_per_launch <N>`: FETCH_SIZE + WRITE_SIZE per dispatch, each scaled by what the same
-  counter reads for a copy of known size.
+  The summary (profiles/hbm_traffic_<kernel>_<workload>.txt, with a _bf16x3 suffix for the
+  split-precision kernels) holds a line `traffic_bytes_per_launch <N>`: FETCH_SIZE + WRITE_SIZE per
+  dispatch, each scaled by what the same counter reads for a copy of known size.
   """
-  path = os.path.join(TRAFFIC_DIR, f"hbm_traffic_{kernel}_{workload}.txt")
+  suffix = "" if precision == "native" else "_" + precision
+  path = os.path.join(TRAFFIC_DIR, f"hbm_traffic_{kernel}_{workload}{suffix}.txt")
   if not os.path.exists(path):
     return None, None
   with open(path) as f:
@@ -432,7 +433,8 @@ def main():
     q, k, v, do = (x.permute(0, 2, 1, 3).contiguous().permute(0, 2, 1, 3) for x in (q, k, v, do))
   scale = D ** -0.5
   desc = nat.AttnDesc(B, n, H, D, nat.BF16 if dtype == torch.bfloat16 else nat.F32, scale, *q.stride()[:3])
-  # The forward's descriptor (bf16x3: k and v split into its workspace first); the backward's is native.
+  # bf16x3: the forward and the dS-exchange kernels take this descriptor (each splits its streamed
+  # operands into the workspace first); delta and the recomputing kernels take the native one.
   fdesc = nat.AttnDesc(B, n, H, D, nat.F32, scale, *q.stride()[:3], 0, 0, 0, nat.PREC_BF16X3, 0) if x3 else desc
   out = torch.empty_like(q)
   lse = torch.empty((B, H, n), device=dev, dtype=torch.float32)
@@ -476,12 +478,12 @@ def main():
     dsbuf = torch.empty(max(dmap.ds_bytes(desc), 256), dtype=torch.uint8, device=dev)
 
   def bwd_dkv_ds(st):
-    nat.check(L.fwn_attn_bwd_dkv_ds_launch(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(),
+    nat.check(L.fwn_attn_bwd_dkv_ds_launch(fdesc, q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(),
                                            lse.data_ptr(), delta.data_ptr(), ts, dmap.struct, dk.data_ptr(),
                                            dv.data_ptr(), dsbuf.data_ptr(), dsbuf.numel(), wsp, wsn, st.cuda_stream))
 
   def bwd_dq_ds(st):
-    nat.check(L.fwn_attn_bwd_dq_ds_launch(desc, k.data_ptr(), dsbuf.data_ptr(), dsbuf.numel(), ts, dmap.struct,
+    nat.check(L.fwn_attn_bwd_dq_ds_launch(fdesc, k.data_ptr(), dsbuf.data_ptr(), dsbuf.numel(), ts, dmap.struct,
                                           dq.data_ptr(), wsp, wsn, st.cuda_stream))
 
   # (name, launch, stream it runs on). The step: with the dS exchange, every kernel in order on one
@@ -554,16 +556,17 @@ def main():
   dominant = max((k_ for k_ in per_solo if algo.get(k_)), key=lambda k_: per_solo[k_])
   achieved = algo[dominant] / (per_solo[dominant] * 1e-3) / 1e12
   peak = PEAK[cfg["dtype"]]
-  if x3 and dominant == "fwd":
+  if x3 and (dominant == "fwd" or dmap is not None):
     peak = round(PEAK["bf16"] / 3, 1)  # three bf16 MFMA products per counted fp32 product
-  traffic, traffic_src = measured_traffic(args.workload, dominant)
+  traffic, traffic_src = measured_traffic(args.workload, dominant, args.precision)
   rate = lambda name, ms: round(algo[name] / (ms * 1e-3) / 1e12, 3)
 
   result = {
       "metric": METRIC, "value": round(value, 3), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
       "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak",
       "vs_baseline": None,
-      "dtype": cfg["dtype"] if not x3 else ("bf16x3" if not cfg["backward"] else "bf16x3 fwd, f32 bwd"),
+      "dtype": cfg["dtype"] if not x3 else ("bf16x3" if not cfg["backward"] or dmap is not None
+                                            else "bf16x3 fwd, f32 bwd"),
       "data": "synthetic: N(0, sigma) q/k/v and N(0,1) dO, member m from numpy PCG64 seed m, on a generated "
               "icosahedral mesh; no weights or datasets",
       "config": {"workload": cfg["desc"], "mesh_refinement": 6, "n": n, "k_hop": cfg["k_hop"], "batch": B,
@@ -578,7 +581,7 @@ def main():
                    "work": "algorithmic FLOPs over whole live 128x128 tiles; the kernels skip 32x32 groups "
                            "without a valid element (config.live_group_fraction of them execute), so frac "
                            "can exceed 1" + ("; bf16x3: fp32-equivalent products against the bf16 MFMA "
-                                             "peak / 3" if x3 and dominant == "fwd" else ""),
+                                             "peak / 3" if x3 and peak != PEAK["f32"] else ""),
                    "timing": ("the timed pass (every kernel in order on one stream, each alone on the GPU)"
                               if paired is solo else
                               "solo pass: the same K steps again with every kernel on one stream (each alone on "

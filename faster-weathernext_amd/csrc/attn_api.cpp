@@ -123,11 +123,26 @@ uint64_t split_bytes(const fwn_attn_desc* d) {
   return (uint64_t)d->batch * (uint64_t)d->heads * (uint64_t)d->n * (uint64_t)d->head_dim * 4u;
 }
 
-// Partial slots, then (bf16x3) the split k and v, each from a 256-byte boundary.
+uint64_t round256(uint64_t x) { return (x + 255u) & ~(uint64_t)255u; }
+
+// Partial slots, then (bf16x3) three split tensors, each from a 256-byte boundary: the forward
+// splits k and v into slots 0 and 1, dK/dV q and dout into 0 and 1, dQ k into 2.
 uint64_t workspace_bytes_for(const fwn_attn_desc* d, const fwn_tiles* t) {
   const uint64_t parts = partial_bytes(d, t);
   if (d->precision != FWN_PREC_BF16X3) return parts;
-  return ((parts + 255u) & ~(uint64_t)255u) + 2u * ((split_bytes(d) + 255u) & ~(uint64_t)255u);
+  return round256(parts) + 3u * round256(split_bytes(d));
+}
+
+// Splits the float32 tensor x (strides sb, sn, sh) into split slot `slot` of the workspace (stream
+// order); returns the slot's address in *out.
+int split_to_slot(const fwn_attn_desc* d, const fwn_tiles* t, void* ws, int slot, const void* x, int64_t sb,
+                  int64_t sn, int64_t sh, hipStream_t stream, const uint16_t** out) {
+  uint16_t* dst = (uint16_t*)((char*)ws + round256(partial_bytes(d, t)) + (uint64_t)slot * round256(split_bytes(d)));
+  if (hipError_t e = launch_split_x3((const float*)x, sb, sn, sh, d->batch, d->n, d->heads, d->head_dim, dst, stream);
+      e != hipSuccess)
+    return fail(FWN_ERR_HIP, "bf16x3 split launch: %s", hipGetErrorString(e));
+  *out = dst;
+  return FWN_OK;
 }
 
 // The backward kernels compute in the tensors' dtype only.
@@ -275,19 +290,9 @@ int fwn_attn_fwd_launch(const fwn_attn_desc* desc, const void* q, const void* k,
   set_tiles(a, tiles, workspace);
   if (desc->precision == FWN_PREC_BF16X3) {
     // k and v split into the workspace after the partial slots, in stream order before the forward.
-    const uint64_t x0 = (partial_bytes(desc, tiles) + 255u) & ~(uint64_t)255u;
-    const uint64_t xs = (split_bytes(desc) + 255u) & ~(uint64_t)255u;
-    uint16_t* kx = (uint16_t*)((char*)workspace + x0);
-    uint16_t* vx = (uint16_t*)((char*)workspace + x0 + xs);
     const hipStream_t st = (hipStream_t)stream;
-    for (int m = 0; m < 2; ++m) {
-      if (hipError_t e = launch_split_x3((const float*)(m ? v : k), desc->stride_b, desc->stride_n, desc->stride_h,
-                                         desc->batch, desc->n, desc->heads, desc->head_dim, m ? vx : kx, st);
-          e != hipSuccess)
-        return fail(FWN_ERR_HIP, "bf16x3 split launch: %s", hipGetErrorString(e));
-    }
-    a.kx = kx;
-    a.vx = vx;
+    if (int rc = split_to_slot(desc, tiles, workspace, 0, k, a.sb, a.sn, a.sh, st, &a.xa)) return rc;
+    if (int rc = split_to_slot(desc, tiles, workspace, 1, v, a.sb, a.sn, a.sh, st, &a.xb)) return rc;
     a.xslice_bytes = (uint32_t)((int64_t)desc->n * 4 * desc->head_dim);
   }
   return launch_with_combine(Kind::kFwd, Kind::kFwdCombine, desc, a, (hipStream_t)stream, "forward");
@@ -389,7 +394,6 @@ int fwn_attn_bwd_dkv_ds_launch(const fwn_attn_desc* desc, const void* q, const v
                                void* workspace, uint64_t workspace_bytes, void* stream) {
   clear_error();
   if (int rc = check_desc(desc)) return rc;
-  if (int rc = check_native(desc, "bwd_dkv_ds")) return rc;
   if (int rc = check_ds(desc, map, ds, ds_bytes, false, true)) return rc;
   if (int rc = check_tensor(q, "q")) return rc;
   if (int rc = check_tensor(k, "k")) return rc;
@@ -411,6 +415,12 @@ int fwn_attn_bwd_dkv_ds_launch(const fwn_attn_desc* desc, const void* q, const v
   a.out1 = dv;
   set_tiles(a, tiles_t, workspace);
   set_ds(a, map, ds);
+  if (desc->precision == FWN_PREC_BF16X3) {
+    const hipStream_t st = (hipStream_t)stream;
+    if (int rc = split_to_slot(desc, tiles_t, workspace, 0, q, a.sb, a.sn, a.sh, st, &a.xa)) return rc;
+    if (int rc = split_to_slot(desc, tiles_t, workspace, 1, dout, a.osb, a.osn, a.osh, st, &a.xb)) return rc;
+    a.xslice_bytes = (uint32_t)((int64_t)desc->n * 4 * desc->head_dim);
+  }
   return launch_with_combine(Kind::kDkvDs, Kind::kDkvCombine, desc, a, (hipStream_t)stream, "dkv (dS exchange)");
 }
 
@@ -419,7 +429,6 @@ int fwn_attn_bwd_dq_ds_launch(const fwn_attn_desc* desc, const void* k, const vo
                               uint64_t workspace_bytes, void* stream) {
   clear_error();
   if (int rc = check_desc(desc)) return rc;
-  if (int rc = check_native(desc, "bwd_dq_ds")) return rc;
   if (int rc = check_ds(desc, map, ds, ds_bytes, true, false)) return rc;
   if (int rc = check_tensor(k, "k")) return rc;
   if (int rc = check_tensor(dq, "dq")) return rc;
@@ -432,6 +441,10 @@ int fwn_attn_bwd_dq_ds_launch(const fwn_attn_desc* desc, const void* k, const vo
   a.out0 = dq;
   set_tiles(a, tiles, workspace);
   set_ds(a, map, ds);
+  if (desc->precision == FWN_PREC_BF16X3) {
+    if (int rc = split_to_slot(desc, tiles, workspace, 2, k, a.sb, a.sn, a.sh, (hipStream_t)stream, &a.xa)) return rc;
+    a.xslice_bytes = (uint32_t)((int64_t)desc->n * 4 * desc->head_dim);
+  }
   return launch_with_combine(Kind::kDqDs, Kind::kDqCombine, desc, a, (hipStream_t)stream, "dq (dS exchange)");
 }
 

@@ -29,9 +29,9 @@ struct KArgs {
   const int32_t* ubase;   // dq from dS: first unit of each tile of the forward list
   const int32_t* tmap;    // dK/dV writing dS: per transposed tile, (ubase, halves) of the forward tile
   uint32_t ds_slice_bytes;  // bytes of one (batch, head) slice of ds: n_units * 1024
-  const uint16_t* kx;     // split-precision forward: K and V as [batch * heads][n][2][head_dim] bf16
-  const uint16_t* vx;     //   (hi row, lo row; written by the split pass)
-  uint32_t xslice_bytes;  // bytes of one (batch, head) slice of kx / vx: n * 4 * head_dim
+  const uint16_t* xa;     // bf16x3 kernels: split operands, [batch * heads][n][2][head_dim] bf16 (hi row,
+  const uint16_t* xb;     //   lo row; written by the split pass): forward k, v; dK/dV q, dout; dQ k
+  uint32_t xslice_bytes;  // bytes of one (batch, head) slice of xa / xb: n * 4 * head_dim
   int32_t n, heads, batch, n_blocks, n_tiles, n_items, n_parts, n_split;
   int64_t sb, sn, sh;     // strides of q, k, v, dq, dk, dv
   int64_t osb, osn, osh;  // strides of o, dout
@@ -50,7 +50,7 @@ enum class Kind { kFwd, kDq, kDkv, kDelta, kFwdCombine, kDqCombine, kDkvCombine,
 hipError_t launch_bf16(Kind kind, int head_dim, const KArgs& a, hipStream_t stream);  // attn_bf16.hip
 hipError_t launch_f32(Kind kind, int head_dim, const KArgs& a, hipStream_t stream);   // attn_f32.hip
 hipError_t launch_delta_bf16(int head_dim, const KArgs& a, hipStream_t stream);      // attn_f32.hip
-hipError_t launch_x3(Kind kind, int head_dim, const KArgs& a, hipStream_t stream);    // attn_x3.hip (kFwd)
+hipError_t launch_x3(Kind kind, int head_dim, const KArgs& a, hipStream_t stream);    // attn_x3.hip: kFwd, kDkvDs, kDqDs
 // Splits a float32 [batch, n, heads, head_dim] tensor (element strides sb, sn, sh) into dst,
 // [batch * heads][n][2][head_dim] bf16: hi = bf16(x), lo = bf16(x - hi) (attn_x3.hip).
 hipError_t launch_split_x3(const float* src, int64_t sb, int64_t sn, int64_t sh, int batch, int n, int heads,

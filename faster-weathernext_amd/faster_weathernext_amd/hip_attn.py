@@ -275,7 +275,8 @@ def _check(q):
 #             strict_fp32; bf16 products for bf16);
 #   "bf16x3": float32 tensors, each product from bf16 parts, hi*hi + hi*lo + lo*hi (about 16
 #             significant bits per operand; the role of the reference's 3xTF32 "highest" dots).
-#             The backward of a bf16x3 forward computes in IEEE float32.
+#             The backward runs in bf16x3 as well with the dS exchange; with lists that are not
+#             exact transposes (or DS_EXCHANGE False) it is the recomputing IEEE float32 one.
 PRECISIONS = {"native": nat.PREC_NATIVE, "bf16x3": nat.PREC_BF16X3}
 
 
@@ -366,7 +367,7 @@ def _side_stream(device):
   return s
 
 
-def _backward_into(q, k, v, out, lse, dout, tiles, tiles_t, scale, dq, dk, dv):
+def _backward_into(q, k, v, out, lse, dout, tiles, tiles_t, scale, dq, dk, dv, precision="native"):
   """Backward kernels writing dq, dk, dv (q's strides).
 
   With `tiles_t` the exact transpose of `tiles` (a symmetric mask with tiles_t None included):
@@ -379,7 +380,8 @@ def _backward_into(q, k, v, out, lse, dout, tiles, tiles_t, scale, dq, dk, dv):
   recomputing dQ kernel on the current stream and dK/dV on a side stream at the same time (each
   with its own workspace), joined before returning. Run side by side, each fills the CUs the
   other's last workgroups leave idle. The sequence is what fwn_attn_bwd_launch enqueues on one
-  stream, with the dQ and dK/dV launches overlapped."""
+  stream, with the dQ and dK/dV launches overlapped. ``precision`` "bf16x3" applies to the dS
+  exchange only."""
   desc = _desc(q, scale, out)
   n = q.shape[1]
   tl = _as_tiles(tiles, n, q.device)
@@ -390,6 +392,7 @@ def _backward_into(q, k, v, out, lse, dout, tiles, tiles_t, scale, dq, dk, dv):
   dmap = tl.ds_map(tlt, unit_keys_for(q.dtype)) if DS_EXCHANGE else None
   if dmap is not None:
     # delta, dK/dV writing dS, then dQ from dS, in stream order (fwn_attn_bwd_ds_launch).
+    desc = _desc(q, scale, out, _precision(precision, q.dtype))
     ws = workspace(desc, q.device, tl, tlt)
     ds = torch.empty(max(dmap.ds_bytes(desc), 256), dtype=torch.uint8, device=q.device)
     ts, tst = tl.struct_for(desc.batch, desc.heads), tlt.struct_for(desc.batch, desc.heads)
@@ -414,7 +417,7 @@ def _backward_into(q, k, v, out, lse, dout, tiles, tiles_t, scale, dq, dk, dv):
   main.wait_stream(side)
 
 
-def attention_backward(q, k, v, out, lse, dout, tiles, tiles_t, scale):
+def attention_backward(q, k, v, out, lse, dout, tiles, tiles_t, scale, precision="native"):
   """Backward kernels (delta pre-pass, dQ, dK/dV): returns contiguous (dq, dk, dv)."""
   _check(q)
   q = q.contiguous()  # dq, dk, dv are written in q's strides: keep them dense
@@ -423,7 +426,7 @@ def attention_backward(q, k, v, out, lse, dout, tiles, tiles_t, scale):
   out = _in_place(out)
   dout = _same_layout(dout, out, "dout")
   dq, dk, dv = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
-  _backward_into(q, k, v, out, lse, dout, tiles, tiles_t, scale, dq, dk, dv)
+  _backward_into(q, k, v, out, lse, dout, tiles, tiles_t, scale, dq, dk, dv, precision)
   return dq, dk, dv
 
 
@@ -437,13 +440,13 @@ class _TiledAttention(torch.autograd.Function):
     out, lse = attention_forward(q, k, v, tiles, scale, with_lse=need, precision=precision)
     if need:
       ctx.save_for_backward(q, k, v, out, lse)
-      ctx.tiles, ctx.tiles_t, ctx.scale = tiles, tiles_t, scale
+      ctx.tiles, ctx.tiles_t, ctx.scale, ctx.precision = tiles, tiles_t, scale, precision
     return out
 
   @staticmethod
   def backward(ctx, dout):
     q, k, v, out, lse = ctx.saved_tensors
-    dq, dk, dv = attention_backward(q, k, v, out, lse, dout, ctx.tiles, ctx.tiles_t, ctx.scale)
+    dq, dk, dv = attention_backward(q, k, v, out, lse, dout, ctx.tiles, ctx.tiles_t, ctx.scale, ctx.precision)
     return dq, dk, dv, None, None, None, None
 
 
@@ -458,7 +461,7 @@ class _TiledAttentionQKV(torch.autograd.Function):
     out, lse = attention_forward(q, k, v, tiles, scale, with_lse=need, precision=precision)
     if need:
       ctx.save_for_backward(qkv, out, lse)
-      ctx.tiles, ctx.tiles_t, ctx.scale = tiles, tiles_t, scale
+      ctx.tiles, ctx.tiles_t, ctx.scale, ctx.precision = tiles, tiles_t, scale, precision
     return out
 
   @staticmethod
@@ -468,7 +471,7 @@ class _TiledAttentionQKV(torch.autograd.Function):
     dqkv = torch.empty_like(qkv)
     dq, dk, dv = dqkv.unbind(2)
     _backward_into(q, k, v, out, lse, _same_layout(dout, out, "dout"), ctx.tiles, ctx.tiles_t, ctx.scale,
-                   dq, dk, dv)
+                   dq, dk, dv, ctx.precision)
     return dqkv, None, None, None, None
 
 

@@ -52,10 +52,12 @@ typedef enum fwn_dtype { FWN_F32 = 0, FWN_BF16 = 1 } fwn_dtype;
  *   FWN_PREC_BF16X3: float32 tensors only. Each operand x is split into bf16 parts
  *     hi = bf16(x), lo = bf16(x - hi) and each product is hi*hi + hi*lo + lo*hi with float32
  *     accumulation: about 16 significant bits per operand (TF32 has 11) on the bf16 matrix
- *     instructions, the role of the reference's TF32_TF32_F32_X3 under "highest". The
- *     forward launcher splits k and v into the workspace first (fwn_attn_workspace_size counts
- *     it); q and P are split in registers. The backward launchers take FWN_PREC_NATIVE only
- *     (they return FWN_ERR_UNSUPPORTED for this mode; run them with a native descriptor).
+ *     instructions, the role of the reference's TF32_TF32_F32_X3 under "highest". Built for
+ *     the forward and the dS-exchange backward (fwn_attn_bwd_dkv_ds_launch,
+ *     fwn_attn_bwd_dq_ds_launch, fwn_attn_bwd_ds_launch, with float32-sized units); each
+ *     launcher first splits the tensors that stream through LDS into the workspace
+ *     (fwn_attn_workspace_size counts them). The recomputing dq and dk/dv launchers return
+ *     FWN_ERR_UNSUPPORTED for this mode (run them with a native descriptor).
  * A zeroed descriptor field means FWN_PREC_NATIVE. */
 typedef enum fwn_precision { FWN_PREC_NATIVE = 0, FWN_PREC_BF16X3 = 1 } fwn_precision;
 
@@ -188,7 +190,7 @@ int fwn_tiles_schedule_fill(int32_t n_blocks, const int32_t* tile_ptr, int32_t m
 /* Workspace bytes the forward, dq and dk/dv launchers need for `tiles`:
  * tiles->n_parts * batch * heads * 128 * (2 * head_dim + 2) * 4 (float32 partial outputs plus
  * the forward's per-row max and sum), rounded up to 256 bytes and, with FWN_PREC_BF16X3, plus
- * 2 * batch * heads * n * head_dim * 4 for the split k and v. */
+ * three split tensors of batch * heads * n * head_dim * 4 bytes (each rounded up to 256). */
 int fwn_attn_workspace_size(const fwn_attn_desc* desc, const fwn_tiles* tiles, uint64_t* bytes);
 
 /* Forward: o = softmax(mask(q k^T * scale)) v, walking only live tiles with an online softmax.

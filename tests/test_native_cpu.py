@@ -736,14 +736,14 @@ def test_split_precision_is_validated():
   x3 = _desc(precision=nat.PREC_BF16X3)
   n = ctypes.c_uint64(0)
   assert L.fwn_attn_workspace_size(x3, tiles, ctypes.byref(n)) == nat.OK
-  assert n.value == 2 * (1 * 2 * 300 * 64 * 4)
+  assert n.value == 3 * (1 * 2 * 300 * 64 * 4)
   split = _tiles(n_items=5, n_parts=3, n_split=1, split=F)
   assert L.fwn_attn_workspace_size(x3, split, ctypes.byref(n)) == nat.OK
   parts = 3 * 1 * 2 * 128 * (2 * 64 + 2) * 4
-  assert n.value == ((parts + 255) // 256) * 256 + 2 * (2 * 300 * 64 * 4)
-  # a workspace without room for the split k and v is refused
+  assert n.value == ((parts + 255) // 256) * 256 + 3 * (2 * 300 * 64 * 4)
+  # a workspace without room for the split tensors is refused
   assert L.fwn_attn_fwd_launch(x3, F, F, F, split, F, None, F, n.value - 1, None) == nat.ERR_INVALID_ARG
-  assert L.fwn_attn_fwd_launch(x3, F, F, F, tiles, F, None, F, 2 * (2 * 300 * 64 * 4) - 1,
+  assert L.fwn_attn_fwd_launch(x3, F, F, F, tiles, F, None, F, 3 * (2 * 300 * 64 * 4) - 1,
                                None) == nat.ERR_INVALID_ARG
   assert L.fwn_attn_fwd_launch(x3, F, F, F, tiles, F, None, None, 0, None) == nat.ERR_INVALID_ARG
   for bad, code in ((_desc(dtype=nat.BF16, precision=nat.PREC_BF16X3), nat.ERR_UNSUPPORTED),
@@ -752,11 +752,13 @@ def test_split_precision_is_validated():
     assert L.fwn_attn_workspace_size(bad, tiles, ctypes.byref(n)) == code
   assert L.fwn_attn_bwd_dq_launch(x3, F, F, F, F, F, F, tiles, F, None, 0, None) == nat.ERR_UNSUPPORTED
   assert L.fwn_attn_bwd_dkv_launch(x3, F, F, F, F, F, F, tiles, F, F, None, 0, None) == nat.ERR_UNSUPPORTED
-  dmap = nat.DsMap(10, F, F, 32, 0)
-  assert L.fwn_attn_bwd_dkv_ds_launch(x3, F, F, F, F, F, F, tiles, dmap, F, F, F, 1 << 20, None, 0,
-                                      None) == nat.ERR_UNSUPPORTED
-  assert L.fwn_attn_bwd_dq_ds_launch(x3, F, F, 1 << 20, tiles, dmap, F, None, 0, None) == nat.ERR_UNSUPPORTED
   assert "NATIVE" in L.fwn_last_error().decode()
+  # the dS-exchange launchers take bf16x3 with float32-sized (32-key) units and its workspace
+  dmap, dmap16 = nat.DsMap(10, F, F, 32, 0), nat.DsMap(10, F, F, 16, 0)
+  assert L.fwn_attn_bwd_dkv_ds_launch(x3, F, F, F, F, F, F, tiles, dmap16, F, F, F, 1 << 20, None, 0,
+                                      None) == nat.ERR_INVALID_ARG
+  assert L.fwn_attn_bwd_dq_ds_launch(x3, F, F, 1 << 20, tiles, dmap, F, None, 0, None) == nat.ERR_INVALID_ARG
+  assert "workspace" in L.fwn_last_error().decode()
   assert L.fwn_attn_fwd_launch_noalloc(x3, F, F, F, tiles, F, None, None) == nat.ERR_UNSUPPORTED
 
 

@@ -8,7 +8,8 @@ rel RMS <= 1e-5 per output tensor against the float64 oracle on the same float32
 max|got - ref| / max|ref| (the reference's unit-test metric, tests/test_pallas_kernel.py:54, 98)
 within 2e-5. With sigma = 4 (logits of standard deviation 16) the bar is rel RMS 3e-5 and
 max 1e-4; TF32 dots, the reference's default (pallas_attn.py:342-343), are about 30x coarser.
-The backward of a bf16x3 forward computes in IEEE float32 from the forward's log-sum-exp.
+The backward runs in bf16x3 too (the dS exchange: dK/dV writes dS as hi and lo parts, dQ reads
+them); lists that are not exact transposes take the recomputing IEEE float32 backward.
 """
 import numpy as np
 import pytest
@@ -16,6 +17,7 @@ import torch
 from scipy import sparse
 
 import faster_weathernext_amd as fwn
+from faster_weathernext_amd import hip_attn
 from gpu_helpers import dev, host, random_mask
 from oracle import attention as A
 
@@ -101,22 +103,76 @@ def test_c2_forward_model_scale():
     np.testing.assert_allclose(lse[:, :, ref["rows"]], ref["lse"], rtol=0, atol=1e-5)
 
 
-def test_autograd_after_split_forward():
-  """tiled_flash_attention(precision="bf16x3"): the forward in bf16x3, the backward in IEEE
-  float32 from its log-sum-exp; outputs and gradients within the float32 bar."""
-  rng = np.random.default_rng(0)
-  n, h, d = 300, 2, 64
-  q, k, v, do = (rng.standard_normal((1, n, h, d)).astype(np.float32) for _ in range(4))
-  mask = random_mask(n, 0.05, 1, symmetric=True)
-  tiles = fwn.TileList.from_mask(mask)
+def _grads(q, k, v, do, tiles, scale, tiles_t=None):
   qt, kt, vt = (dev(x, F32, True) for x in (q, k, v))
-  out = fwn.tiled_flash_attention(qt, kt, vt, tiles, scale=d ** -0.5, precision=X3)
+  out = fwn.tiled_flash_attention(qt, kt, vt, tiles, scale=scale, precision=X3, tiles_t=tiles_t)
   out.backward(dev(do, F32))
+  torch.cuda.synchronize()
+  return {"out": host(out), "dq": host(qt.grad), "dk": host(kt.grad), "dv": host(vt.grad)}
+
+
+def test_c1_golden_gradients():
+  g = np.load(__file__.replace("test_x3_gpu.py", "golden/c1_r3_2hop.npz"))
+  n = g["q"].shape[1]
+  mask = sparse.csr_matrix((np.ones(len(g["indices"]), bool), g["indices"], g["indptr"]), shape=(n, n))
+  res = _grads(g["q"], g["k"], g["v"], g["do"], fwn.TileList.from_mask(mask), float(g["scale"]))
+  for name in ("out", "dq", "dk", "dv"):
+    check(res[name], g[name], name)
+
+
+@pytest.mark.parametrize("d", [32, 64, 128])
+@pytest.mark.parametrize("cap", [None, 1, 3])
+def test_backward_matches_dense_oracle(d, cap):
+  """The bf16x3 backward (dS exchange) on a symmetric random mask, batch 2, whole and split work
+  items (split blocks go through the combine passes), against the float64 gradients."""
+  rng = np.random.default_rng(0)
+  n, h = 300, 2
+  q, k, v, do = (rng.standard_normal((2, n, h, d)).astype(np.float32) for _ in range(4))
+  mask = random_mask(n, 0.05, 1, symmetric=True)
+  tiles = fwn.TileList.from_mask(mask, max_item_tiles=cap)
+  res = _grads(q, k, v, do, tiles, d ** -0.5)
   dense = mask.toarray()
-  check(host(out), A.dense_attention(q, k, v, dense, d ** -0.5), "out")
-  for name, got, ref in zip(("dq", "dk", "dv"), (qt.grad, kt.grad, vt.grad),
-                            A.dense_grads(q, k, v, do, dense, d ** -0.5)):
-    check(host(got), ref, name)
+  check(res["out"], A.dense_attention(q, k, v, dense, d ** -0.5), "out")
+  for name, ref in zip(("dq", "dk", "dv"), A.dense_grads(q, k, v, do, dense, d ** -0.5)):
+    check(res[name], ref, name)
+
+
+@pytest.mark.parametrize("exchange", [True, False])
+def test_non_symmetric_mask_with_its_transposed_list(exchange, monkeypatch):
+  """A non-symmetric mask with its transposed list (the reference's tiles_t): the bf16x3 dS
+  exchange walks the transposed list in dK/dV and the forward list in dQ. With the exchange off
+  the backward is the recomputing IEEE float32 one. Both within the bar."""
+  monkeypatch.setattr(hip_attn, "DS_EXCHANGE", exchange)
+  rng = np.random.default_rng(3)
+  n, h, d = 280, 2, 64
+  q, k, v, do = (rng.standard_normal((1, n, h, d)).astype(np.float32) for _ in range(4))
+  mask = random_mask(n, 0.06, 5)
+  tiles, tiles_t = fwn.TileList.from_mask(mask), fwn.TileList.from_mask(mask.T.tocsr())
+  assert tiles.ds_map(tiles_t, 32) is not None
+  res = _grads(q, k, v, do, tiles, d ** -0.5, tiles_t=tiles_t)
+  dense = mask.toarray()
+  check(res["out"], A.dense_attention(q, k, v, dense, d ** -0.5), "out")
+  for name, ref in zip(("dq", "dk", "dv"), A.dense_grads(q, k, v, do, dense, d ** -0.5)):
+    check(res[name], ref, name)
+
+
+def test_c3_mask_float32_model_scale():
+  """The 16-hop refinement-6 mask (configuration 3's), float32 tensors in bf16x3, 2 heads x 128,
+  fwd + bwd: rows of blocks 0, 77 and 320 and every key of blocks 77, 200 and 320 against the
+  exact block oracle, plus sum_j dV_j = sum_i dO_i and sum_j dK_j = 0 over all nodes."""
+  mask, _, _, _ = fwn.mesh_mask(6, 16)
+  n = mask.shape[0]
+  rng = np.random.default_rng(0)
+  q, k, v, do = (rng.standard_normal((1, n, 2, 128)).astype(np.float32) for _ in range(4))
+  res = _grads(q, k, v, do, fwn.TileList.from_mask(mask), 128 ** -0.5)
+  ref = A.block_attention(q, k, v, do, mask, 128 ** -0.5, row_blocks=[0, 77, 320], key_blocks=[77, 200, 320])
+  check(res["out"][:, ref["rows"]], ref["out"], "out")
+  check(res["dq"][:, ref["rows"]], ref["dq"], "dq")
+  check(res["dk"][:, ref["keys"]], ref["dk"], "dk")
+  check(res["dv"][:, ref["keys"]], ref["dv"], "dv")
+  np.testing.assert_allclose(res["dv"].astype(np.float64).sum(1), do.astype(np.float64).sum(1), rtol=0,
+                             atol=float(1e-4 * np.abs(do).sum(1).max()))
+  assert np.abs(res["dk"].astype(np.float64).sum(1)).max() <= 1e-4 * np.abs(res["dk"]).sum(1).max()
 
 
 def test_packed_qkv_strided_views():
