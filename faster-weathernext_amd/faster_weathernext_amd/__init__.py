@@ -34,6 +34,8 @@ def enable(force: bool = False, **options):
       raise TypeError(f"unknown option {key!r}; see faster_weathernext_amd.patch.Options")
   if options.get("attention", patch.OPTIONS.attention) not in ("auto", "hip"):
     raise ValueError(f"unknown attention implementation {options['attention']!r} (auto, hip)")
+  if options.get("precision", patch.OPTIONS.precision) not in ("native", "bf16x3"):
+    raise ValueError(f"unknown precision {options['precision']!r} (native, bf16x3)")
   if not force:
     from . import _native
     _native.lib()

@@ -56,12 +56,14 @@ class TiledMHA(torch.nn.Module):
 
   ``tiles`` is the mesh's TileList (or the array triple of ``build_tile_mask``), built once and
   shared by every layer; ``tiles_t`` is the transposed mask's list for non-symmetric masks.
-  ``dtype`` None takes the enable() option (bfloat16 when ``bf16``, else float32).
+  ``dtype`` None takes the enable() option (bfloat16 when ``bf16``, else float32), ``precision``
+  None the enable() option ``precision`` (float32 only: "native" or "bf16x3").
   """
 
-  def __init__(self, d_model, num_heads, key_size, tiles, tiles_t=None, *, device=None, dtype=None):
+  def __init__(self, d_model, num_heads, key_size, tiles, tiles_t=None, *, device=None, dtype=None, precision=None):
     super().__init__()
     dtype = patch.default_dtype(dtype)
+    self.precision = patch.default_precision(precision, dtype)
     self.num_heads, self.key_size = num_heads, key_size
     self.tiles, self.tiles_t = tiles, tiles_t
     self.qkv = torch.nn.Linear(d_model, 3 * num_heads * key_size, bias=False, device=device, dtype=dtype)
@@ -72,11 +74,13 @@ class TiledMHA(torch.nn.Module):
     hd = self.num_heads * self.key_size
     if needs_grad(x, self):
       qkv = self.qkv(x).view(b, n, 3, self.num_heads, self.key_size)
-      out = tiled_flash_attention_qkv(qkv, self.tiles, scale=self.key_size ** -0.5, tiles_t=self.tiles_t)
+      out = tiled_flash_attention_qkv(qkv, self.tiles, scale=self.key_size ** -0.5, tiles_t=self.tiles_t,
+                                      precision=self.precision)
       return self.final(out.view(b, n, hd))
     # Without autograd the projections run through linear_rows (the faster GEMM row split).
     qkv = linear_rows(x.reshape(b * n, d), self.qkv.weight).view(b, n, 3, self.num_heads, self.key_size)
-    out = tiled_flash_attention_qkv(qkv, self.tiles, scale=self.key_size ** -0.5, tiles_t=self.tiles_t)
+    out = tiled_flash_attention_qkv(qkv, self.tiles, scale=self.key_size ** -0.5, tiles_t=self.tiles_t,
+                                      precision=self.precision)
     return linear_rows(out.reshape(b * n, hd), self.final.weight, self.final.bias).view(b, n, -1)
 
   def forward_unfused(self, x):
@@ -86,7 +90,9 @@ class TiledMHA(torch.nn.Module):
     q, k, v = (t.contiguous() for t in self.qkv(x).view(b, n, 3, self.num_heads, self.key_size).unbind(2))
     tiles = self.tiles if isinstance(self.tiles, TileList) else tuple(self.tiles)
     if isinstance(tiles, tuple):
-      out = tiled_flash_attention(q, k, v, *tiles, scale=self.key_size ** -0.5, tiles_t=self.tiles_t)
+      out = tiled_flash_attention(q, k, v, *tiles, scale=self.key_size ** -0.5, tiles_t=self.tiles_t,
+                                  precision=self.precision)
     else:
-      out = tiled_flash_attention(q, k, v, tiles, scale=self.key_size ** -0.5, tiles_t=self.tiles_t)
+      out = tiled_flash_attention(q, k, v, tiles, scale=self.key_size ** -0.5, tiles_t=self.tiles_t,
+                                  precision=self.precision)
     return self.final(out.reshape(b, n, self.num_heads * self.key_size))

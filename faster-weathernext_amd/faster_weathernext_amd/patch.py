@@ -32,6 +32,11 @@ class Options:
   # bfloat16 parameters and activations with float32 accumulation instead of float32 (fp32 MFMA).
   # MeshTransformer's and TiledMHA's default dtype.
   bf16: bool = False
+  # Products of the attention kernels on float32 tensors: "native" (IEEE float32 products, the
+  # reference's strict_fp32) or "bf16x3" (three bf16 products per float32 product, about 16
+  # significant bits per operand: the role of the reference's 3xTF32 "highest" dots, at 2.5-3.2x
+  # the speed). bfloat16 tensors always take bf16 products.
+  precision: str = "native"
 
 
 OPTIONS = Options()
@@ -69,6 +74,14 @@ def default_dtype(dtype=None):
   if dtype is not None:
     return dtype
   return torch.bfloat16 if OPTIONS.bf16 else torch.float32
+
+
+def default_precision(precision=None, dtype=None):
+  """`precision` if given, else ``OPTIONS.precision`` for float32 and "native" for bfloat16."""
+  import torch
+  if precision is not None:
+    return precision
+  return "native" if dtype == torch.bfloat16 else OPTIONS.precision
 
 
 def default_reorder(reorder=None):

@@ -72,12 +72,12 @@ class MeshBlock(torch.nn.Module):
   """One transformer block (``ChunkedBlock``, ``patch.py:229-253``)."""
 
   def __init__(self, d_model, num_heads, key_size, ffw_hidden, cond_size, tiles, tiles_t=None, *, device=None,
-               dtype=None, eps=1e-5):
+               dtype=None, eps=1e-5, precision=None):
     super().__init__()
     self.eps = eps
     kw = dict(device=device, dtype=dtype)
     self.norm_mha = NormConditioning(d_model, cond_size, **kw)
-    self.mha = TiledMHA(d_model, num_heads, key_size, tiles, tiles_t, **kw)
+    self.mha = TiledMHA(d_model, num_heads, key_size, tiles, tiles_t, precision=precision, **kw)
     self.norm_ffw = NormConditioning(d_model, cond_size, **kw)
     self.ffw = torch.nn.Sequential(torch.nn.Linear(d_model, ffw_hidden, **kw), torch.nn.GELU(approximate="tanh"),
                                    torch.nn.Linear(ffw_hidden, d_model, **kw))
@@ -119,12 +119,13 @@ class MeshTransformer(torch.nn.Module):
   boolean [n, n] sparse matrix, with the nodes' ``latlon`` in degrees for the Hilbert order) when
   one is given, as the reference builds it from the model's own adjacency (``patch.py:193-219``).
   A non-symmetric adjacency gives a non-symmetric mask, whose transposed tile list the backward
-  walks. ``reorder`` and ``dtype`` None take the enable() options (``reorder``, ``bf16``).
+  walks. ``reorder``, ``dtype`` and ``precision`` None take the enable() options (``reorder``,
+  ``bf16``, ``precision``).
   """
 
   def __init__(self, refinement=6, k_hop=32, num_layers=24, d_model=768, num_heads=6, key_size=128,
                ffw_hidden=3072, cond_size=32, reorder=None, *, device="cuda", dtype=None, tiles=None,
-               tiles_t=None, adjacency=None, latlon=None, eps=1e-5):
+               tiles_t=None, adjacency=None, latlon=None, eps=1e-5, precision=None):
     super().__init__()
     reorder = patch.default_reorder(reorder)
     dtype = patch.default_dtype(dtype)
@@ -150,7 +151,7 @@ class MeshTransformer(torch.nn.Module):
                          persistent=False)
     self.blocks = torch.nn.ModuleList(
         MeshBlock(d_model, num_heads, key_size, ffw_hidden, cond_size, self.tiles, self.tiles_t, device=device,
-                  dtype=dtype, eps=eps)
+                  dtype=dtype, eps=eps, precision=precision)
         for _ in range(num_layers))
     self.final_norm = NormConditioning(d_model, cond_size, device=device, dtype=dtype)
 

@@ -149,25 +149,75 @@ def test_bwd_ds_launch_one_stream(split, dtype):
     check(host(x), want, dtype, name)
 
 
-@pytest.mark.parametrize("ds", [False, True])
-def test_graph_capture_replays_match_eager(ds):
+@pytest.mark.parametrize("split", [False, True])
+def test_bwd_ds_launch_bf16x3_one_stream(split):
+  """The bf16x3 (split-precision) forward and dS-exchange backward through the C ABI on one
+  stream, float32 tensors of a non-symmetric mask with its transposed list: equal bit for bit to
+  the package's path (precision="bf16x3"), within rel RMS 1e-5 of the float64 oracle. The
+  workspace starts as 0xFF bytes and the dS buffer as NaNs: every split row and unit read was
+  written."""
+  rng = np.random.default_rng(68)
+  b, n, h, d = 2, 700, 2, 128
+  q, k, v, do = (rng.standard_normal((b, n, h, d)).astype(np.float32) for _ in range(4))
+  m = random_mask(n, 0.05, 69, symmetric=False)
+  cap, cap_t = (2, 3) if split else (1 << 20, 1 << 20)
+  tiles = fwn.TileList.from_mask(m, max_item_tiles=cap)
+  tiles_t = fwn.TileList.from_mask(m.T.tocsr(), max_item_tiles=cap_t)
+  dmap = tiles.ds_map(tiles_t, 32)
+  qd, kd, vd, dod = (dev(x, torch.float32) for x in (q, k, v, do))
+  scale = d ** -0.5
+  desc = nat.AttnDesc(b, n, h, d, nat.F32, scale, *qd.stride()[:3], 0, 0, 0, nat.PREC_BF16X3, 0)
+  size = _ws_size(desc, tiles, tiles_t)
+  ws = torch.full((size,), 255, dtype=torch.uint8, device="cuda")
+  nbytes = dmap.ds_bytes(desc)
+  ds = torch.full((nbytes,), 0xFF, dtype=torch.uint8, device="cuda")
+  stream = torch.cuda.current_stream().cuda_stream
+  L = nat.lib()
+  out, lse = torch.full_like(qd, float("nan")), torch.full((b, h, n), float("nan"), device="cuda")
+  nat.check(L.fwn_attn_fwd_launch(desc, qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), tiles.struct, out.data_ptr(),
+                                  lse.data_ptr(), ws.data_ptr(), size, stream))
+  delta = torch.full((b, h, n), float("nan"), device="cuda")
+  dq, dk, dv = (torch.full_like(qd, float("nan")) for _ in range(3))
+  nat.check(L.fwn_attn_bwd_ds_launch(desc, qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), out.data_ptr(),
+                                     dod.data_ptr(), lse.data_ptr(), delta.data_ptr(), tiles.struct, tiles_t.struct,
+                                     dmap.struct, dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ds.data_ptr(), nbytes,
+                                     ws.data_ptr(), size, stream))
+  pout, plse = fwn.attention_forward(qd, kd, vd, tiles, scale, precision="bf16x3")
+  ref = fwn.attention_backward(qd, kd, vd, pout, plse, dod, tiles, tiles_t, scale, precision="bf16x3")
+  torch.cuda.synchronize()
+  np.testing.assert_array_equal(host(out), host(pout))
+  for name, x, want in zip(("dq", "dk", "dv"), (dq, dk, dv), ref):
+    np.testing.assert_array_equal(host(x), host(want), err_msg=name)
+  dense = m.toarray()
+  for name, x, want in zip(("out", "dq", "dk", "dv"), (out, dq, dk, dv),
+                           (A.dense_attention(q, k, v, dense, scale),) + A.dense_grads(q, k, v, do, dense, scale)):
+    assert A.rel_rms(host(x), want) <= 1e-5 and A.max_rel_err(host(x), want) <= 2e-5, name
+
+
+@pytest.mark.parametrize("mode", ["recompute", "ds", "bf16x3"])
+def test_graph_capture_replays_match_eager(mode):
   """The launchers allocate nothing and never synchronise, so a caller may capture them. The
   forward and the one-stream backward (split schedules, so the combine passes are captured too;
-  with `ds`, the backward with the dS exchange and its dS buffer) are captured into one graph,
-  which is replayed four times with new inputs written in place between replays (eager copies
-  and fills, with synchronisations in between); every replay equals the eager launches on the
-  same inputs bit for bit."""
+  "ds": the backward with the dS exchange and its dS buffer; "bf16x3": float32 tensors in the
+  split precision, whose split passes are captured too) are captured into one graph, which is
+  replayed four times with new inputs written in place between replays (eager copies and fills,
+  with synchronisations in between); every replay equals the eager launches on the same inputs
+  bit for bit."""
+  ds = mode != "recompute"
   rng = np.random.default_rng(64)
   b, n, h, d = 1, 600, 2, 64
-  dtype = torch.bfloat16
+  dtype = torch.float32 if mode == "bf16x3" else torch.bfloat16
   m = random_mask(n, 0.04, 65, symmetric=True)
   tiles = fwn.TileList.from_mask(m, max_item_tiles=2)
   assert tiles.n_split > 0
   q, k, v, do = (torch.empty((b, n, h, d), dtype=dtype, device="cuda") for _ in range(4))
   scale = d ** -0.5
-  desc = nat.AttnDesc(b, n, h, d, nat.BF16, scale, *q.stride()[:3])
+  if mode == "bf16x3":
+    desc = nat.AttnDesc(b, n, h, d, nat.F32, scale, *q.stride()[:3], 0, 0, 0, nat.PREC_BF16X3, 0)
+  else:
+    desc = nat.AttnDesc(b, n, h, d, nat.BF16, scale, *q.stride()[:3])
   size = _ws_size(desc, tiles)
-  dmap = tiles.ds_map(tiles, 16)
+  dmap = tiles.ds_map(tiles, 32 if mode == "bf16x3" else 16)
   ds_bytes = dmap.ds_bytes(desc)
   L = nat.lib()
 
@@ -217,4 +267,4 @@ def test_graph_capture_replays_match_eager(ds):
     for name in ("out", "lse", "delta", "dq", "dk", "dv"):
       np.testing.assert_array_equal(host(captured[name]), host(eager[name]), err_msg=f"replay {replay} {name}")
     ref = A.dense_attention(*(host(t) for t in (q, k, v)), m.toarray(), scale)
-    check(host(captured["out"]), ref, dtype, ("replay", replay))
+    check(host(captured["out"]), ref, torch.bfloat16 if mode == "bf16x3" else dtype, ("replay", replay))

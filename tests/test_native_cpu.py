@@ -764,7 +764,17 @@ def test_split_precision_is_validated():
 
 def test_split_precision_python_options():
   import torch
-  from faster_weathernext_amd import hip_attn
+  from faster_weathernext_amd import hip_attn, patch
+  with pytest.raises(ValueError):
+    fwn.enable(force=True, precision="tf32")
+  fwn.enable(force=True, precision="bf16x3")
+  try:
+    assert fwn.TiledMHA(16, 2, 8, None, device="cpu").precision == "bf16x3"
+    assert fwn.TiledMHA(16, 2, 8, None, device="cpu", dtype=torch.bfloat16).precision == "native"
+    assert fwn.TiledMHA(16, 2, 8, None, device="cpu", precision="native").precision == "native"
+  finally:
+    fwn.disable()
+  assert patch.OPTIONS.precision == "native"
   assert hip_attn._precision("bf16x3", torch.float32) == nat.PREC_BF16X3
   assert hip_attn._precision("native", torch.bfloat16) == nat.PREC_NATIVE
   with pytest.raises(TypeError):
