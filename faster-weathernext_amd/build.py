@@ -22,7 +22,8 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
 ARCH = "gfx950"
 
-DEVICE_SOURCES = ["attn_bf16.hip", "attn_x3.hip", "attn_f32.hip", "attn_combine.hip", "attn_noalloc.hip", "rows.hip"]
+DEVICE_SOURCES = ["attn_bf16.hip", "attn_x3.hip", "attn_x3_dkv.hip", "attn_f32.hip", "attn_combine.hip",
+                  "attn_noalloc.hip", "rows.hip"]
 HOST_SOURCES = ["attn_api.cpp", "mask_host.cpp", "rows_api.cpp"]
 
 

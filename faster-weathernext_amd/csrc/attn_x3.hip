@@ -17,40 +17,12 @@
 //
 // Reference: pallas_attn.py:112-141 (forward kernel), 161-215 (backward kernels), 317-354
 // (precision selection).
-#include "attn_bf16_tiles.h"
+#include "attn_x3.h"
 
 namespace fwn {
 namespace {
 
 using namespace dev;
-
-// hi = bf16(x) (round to nearest even), lo = bf16(x - hi): x - hi is exact in fp32.
-__device__ __forceinline__ void split8(const float (&x)[8], u32x4& hi, u32x4& lo) {
-  bf16x8 h, l;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    h[e] = (__bf16)x[e];
-    l[e] = (__bf16)(x[e] - (float)h[e]);
-  }
-  hi = __builtin_bit_cast(u32x4, h);
-  lo = __builtin_bit_cast(u32x4, l);
-}
-
-// Elements 8 * half .. + 7 of an accumulator, split.
-__device__ __forceinline__ void split_acc(const f32x16& v, int half, u32x4& hi, u32x4& lo) {
-  float x[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) x[e] = v[8 * half + e];
-  split8(x, hi, lo);
-}
-
-// The three-part product into c: the two cross terms first, then hi * hi.
-__device__ __forceinline__ f32x16 mfma_x3(const u32x4& ah, const u32x4& al, const u32x4& bh, const u32x4& bl,
-                                          f32x16 c) {
-  c = mfma_bf16(al, bh, c);
-  c = mfma_bf16(ah, bl, c);
-  return mfma_bf16(ah, bh, c);
-}
 
 struct SplitArgs {
   const float* src;
@@ -78,67 +50,6 @@ __global__ void __launch_bounds__(256) split_x3_kernel(SplitArgs s) {
   *(u32x4*)q = hi;
   *(u32x4*)(q + s.d) = lo;
 }
-
-// This lane's row fragment of a float32 tensor (columns 16 s + 8 g .. + 7 of `row`), split: the B
-// operands of the first contractions.
-template <int D>
-__device__ __forceinline__ void load_frag_x3(u32x4 (&hi)[D / 16], u32x4 (&lo)[D / 16], rsrc_t r, int row,
-                                             uint32_t snb, int g) {
-  const uint32_t off = (uint32_t)row * snb + (uint32_t)(32 * g);
-#pragma unroll
-  for (int s = 0; s < D / 16; ++s) {
-    const f32x4 x0 = __builtin_bit_cast(f32x4, bload16(r, off + 64 * s));
-    const f32x4 x1 = __builtin_bit_cast(f32x4, bload16(r, off + 64 * s + 16));
-    const float x[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
-    split8(x, hi[s], lo[s]);
-  }
-}
-
-// Copy of one step's 32 split K rows and 32 split V rows into a group buffer of four 32-row planes
-// (K hi, K lo, V hi, V lo; each [32][D] bf16, chunks swizzled as the bf16 tiles). Each wave-wide
-// LDS DMA instruction fills 1 KB = RPO rows of one plane; the 4 waves share the 4 * NI
-// instructions of a step. Lane l of instruction (plane, sub) copies row RPO * sub + l / C,
-// physical chunk l % C, which holds logical chunk (l % C) ^ swz(row); the swizzle depends on
-// row % 16, which is the same for every instruction of one wave.
-template <int D>
-struct X3Dma {
-  static constexpr int C = D / 8;
-  static constexpr int RPO = 1024 / (2 * D);
-  static constexpr int NI = 32 / RPO;
-  static constexpr int GB = 32 * 2 * D;  // bytes of one plane
-  static constexpr int XROW = 4 * D;     // bytes of one split row (hi, lo)
-  uint32_t voff;
-
-  __device__ __forceinline__ void init(int w, int lane) {
-    const int row = RPO * (w % NI) + lane / C;
-    voff = (uint32_t)(lane / C) * XROW + (uint32_t)(((lane % C) ^ swz<C>(row)) << 4);
-  }
-
-  // Planes 0, 1 from rA (rows row0 .. row0 + 31, hi and lo), planes 2, 3 from rB; only the planes
-  // in `planes` (bit p: plane p, a wave-uniform set) are copied.
-  __device__ __forceinline__ void issue(rsrc_t rA, rsrc_t rB, lds_char* buf, int row0, int w,
-                                        uint32_t planes = 15u) const {
-    uint32_t base = (uint32_t)(uintptr_t)buf;
-    asm volatile("" : "+s"(base));
-#pragma unroll
-    for (int m = 0; m < D / 16; ++m) {
-      int plane, sub;
-      if constexpr (NI >= 4) {
-        plane = 4 * m / NI;
-        sub = w + (4 * m) % NI;
-      } else {
-        plane = 2 * m + (w >> 1);
-        sub = w & 1;
-      }
-      if (!(planes >> plane & 1u)) continue;
-      const uint32_t src = (uint32_t)(row0 + RPO * sub) * XROW + voff + (uint32_t)(plane & 1) * (2 * D);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          m < D / 32 ? rA : rB,
-          (__attribute__((address_space(3))) void*)(uintptr_t)(base + (uint32_t)(plane * GB + sub * 1024)), 16,
-          (int)src, 0, 0, 0);
-    }
-  }
-};
 
 // Forward, float32 tensors, bf16x3 products: two workgroups per CU, streamed by 32-key group
 // (the steps are the work item's (tile, key group) pairs in which some wave has a valid element).
@@ -267,226 +178,6 @@ __global__ void __launch_bounds__(NT, 2) fwd_x3_kernel(KArgs a) {
   if (g == 0) write_lse(a, j, qrow, st, ltot);
 }
 
-constexpr int kNonTemporal = 2;  // buffer load/store cache policy: non-temporal (gfx950 "nt")
-constexpr uint32_t kPastEnd = 0x7FFFFFF0u;  // a buffer offset past every slice: reads zeros
-
-// dK/dV, float32 tensors, bf16x3 products, the dS exchange (pallas_attn.py:187-215). Four waves,
-// one workgroup per CU; wave w owns keys 32 w .. + 31 of the key block and keeps their K and V
-// rows split in registers (the B operands of S = Q K^T and dP = dO V^T) and dK^T, dV^T in
-// accumulators. The transposed list's (tile, query group) steps stream through two group buffers
-// as in the forward: Q and dO as split planes plus the group's 32 lse (times log2 e) and delta.
-// Per live 32 x 32 group: S and dP (3 D/16 MFMAs each, dP's accumulator starting at -delta),
-// P = exp2(S c2 - lse log2 e) masked, dS = P (dP - delta), dV^T += dO^T P and dK^T += Q^T dS
-// (3 D/16 each, the transposed operands by ds_read_b64_tr_b16).
-//
-// With DS every group's dS goes to HBM as one 4 KB unit: chunk 64 k + L (16 bytes) holds, for dQ
-// lane L (query L % 32, g = L / 32), keys 16 c + 8 g .. + 7 of plane p (k = 2 p + c; p = 0 hi,
-// 1 lo). This lane holds one key and 16 queries, so the wave transposes through its own LDS stage
-// ([plane][query][key] bf16, 80-byte rows: conflict-free 16-byte row reads) before four 16-byte
-// non-temporal stores per lane. Units are numbered as in the float32 exchange (rank of group bit
-// 4 c + w of the forward tile, from tmap).
-template <int D, bool DS>
-__global__ void __launch_bounds__(NT, 1) dkv_x3_kernel(KArgs a) {
-  constexpr int GB = X3Dma<D>::GB;
-  constexpr int SB = 4 * GB;  // Q hi | Q lo | dO hi | dO lo | lse [32], 0 [32] | delta [32], 0 [32]
-  constexpr int SROW = 80, SPLANE = 32 * SROW;
-  __shared__ __attribute__((aligned(1024))) char gb0[SB + 512];
-  __shared__ __attribute__((aligned(1024))) char gb1[SB + 512];
-  __shared__ __attribute__((aligned(16))) char stage[DS ? 4 * 2 * SPLANE : 16];
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int i = lane & 31, g = lane >> 5;
-  const Job j = decode_job(a);
-  const int64_t xbase = (int64_t)j.bh * a.n * (2 * D);
-  const rsrc_t rQ = make_rsrc(a.xa + xbase, a.xslice_bytes);
-  const rsrc_t rO = make_rsrc(a.xb + xbase, a.xslice_bytes);
-  const rsrc_t rL = make_rsrc(a.lse + stat_index(a, j, 0), (uint32_t)a.n * 4);
-  const rsrc_t rD = make_rsrc(a.delta + stat_index(a, j, 0), (uint32_t)a.n * 4);
-  const uint32_t snb = (uint32_t)a.sn * 4;
-  const int krow = j.blk * BLK + 32 * w + i;
-  u32x4 kh[D / 16], kl[D / 16], vh[D / 16], vl[D / 16];
-  load_frag_x3<D>(kh, kl, make_rsrc((const float*)a.k + j.base, a.slice_bytes), krow, snb, g);
-  load_frag_x3<D>(vh, vl, make_rsrc((const float*)a.v + j.base, a.slice_bytes), krow, snb, g);
-  Off<D> off;
-  off.init(lane);
-  X3Dma<D> dma;
-  dma.init(w, lane);
-  f32x16 dk[D / 32], dv[D / 32];
-#pragma unroll
-  for (int db = 0; db < D / 32; ++db) {
-    dk[db] = zero16();
-    dv[db] = zero16();
-  }
-  rsrc_t rS;
-  if constexpr (DS) rS = make_rsrc(a.ds + (int64_t)j.bh * (a.ds_slice_bytes >> 1), a.ds_slice_bytes);
-  typedef const __attribute__((address_space(4))) uint32_t* cmap_ptr;
-
-  // Query group c of the tile from group buffer buf; `ub`, `gw`: the forward tile's first unit and
-  // group word (DS).
-  auto group = [&](int c, const lds_char* buf, u32x2 mb, uint32_t ub, uint32_t gw) {
-    const lds_char* lq = buf;
-    const lds_char* lo = buf + 2 * GB;
-    typedef const __attribute__((address_space(3))) float* cfp;
-    const cfp lse = (cfp)(buf + SB);
-    const cfp del = (cfp)(buf + SB + 256);
-    u32x4 qa[D / 16], qb[D / 16], oa[D / 16], ob[D / 16];
-#pragma unroll
-    for (int k = 0; k < D / 16; ++k) {
-      qa[k] = row_read(lq, off.row[k]);
-      qb[k] = row_read(lq + GB, off.row[k]);
-      oa[k] = row_read(lo, off.row[k]);
-      ob[k] = row_read(lo + GB, off.row[k]);
-    }
-    f32x16 s = zero16(), dp;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) dp[r] = -del[element_col(0, r, g)];
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int k = 0; k < D / 16; ++k) {
-      s = mfma_x3(qa[k], qb[k], kh[k], kl[k], s);
-      dp = mfma_x3(oa[k], ob[k], vh[k], vl[k], dp);
-    }
-    // The transposed reads of the second contractions are in flight during the exponentials.
-    u32x4 oth[D / 32][2], otl[D / 32][2], qth[D / 32][2], qtl[D / 32][2];
-#pragma unroll
-    for (int db = 0; db < D / 32; ++db)
-#pragma unroll
-      for (int c2 = 0; c2 < 2; ++c2) {
-        oth[db][c2] = tr_operand<D>(lo, off, db, 0, c2);
-        otl[db][c2] = tr_operand<D>(lo + GB, off, db, 0, c2);
-        qth[db][c2] = tr_operand<D>(lq, off, db, 0, c2);
-        qtl[db][c2] = tr_operand<D>(lq + GB, off, db, 0, c2);
-      }
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      float p = fast_exp2(fmaf(s[r], a.c2, -lse[element_col(0, r, g)]));
-      p = keep_or_zero(p, elem_keep(mb, c, r));
-      s[r] = p;
-      dp[r] = p * dp[r];
-    }
-    u32x4 ph[2], pl[2], dh[2], dl[2];
-#pragma unroll
-    for (int c2 = 0; c2 < 2; ++c2) {
-      split_acc(s, c2, ph[c2], pl[c2]);
-      split_acc(dp, c2, dh[c2], dl[c2]);
-    }
-#pragma unroll
-    for (int db = 0; db < D / 32; ++db)
-#pragma unroll
-      for (int c2 = 0; c2 < 2; ++c2) {
-        dv[db] = mfma_x3(oth[db][c2], otl[db][c2], ph[c2], pl[c2], dv[db]);
-        dk[db] = mfma_x3(qth[db][c2], qtl[db][c2], dh[c2], dl[c2], dk[db]);
-      }
-    if constexpr (DS) {
-      const uint32_t bit = 4u * (uint32_t)c + (uint32_t)w;
-      if (gw >> bit & 1u) {
-        const uint32_t u = ub + (uint32_t)__builtin_popcount(gw & 0xffffu & ((1u << bit) - 1u));
-        __attribute__((address_space(3))) char* st = (__attribute__((address_space(3))) char*)stage + w * 2 * SPLANE;
-        // The stage is written as 16-bit and read as 128-bit values: compiler barriers keep this
-        // unit's writes after the previous unit's reads and before this unit's reads (the LDS
-        // executes one wave's accesses in order).
-        asm volatile("" ::: "memory");
-        // This lane's key i, queries 16 c2 + 8 g + e, into column i of the stage.
-#pragma unroll
-        for (int pl2 = 0; pl2 < 2; ++pl2)
-#pragma unroll
-          for (int c2 = 0; c2 < 2; ++c2) {
-            const u32x4 x = pl2 ? dl[c2] : dh[c2];
-#pragma unroll
-            for (int e = 0; e < 8; ++e)
-              *(__attribute__((address_space(3))) uint16_t*)(st + pl2 * SPLANE + (16 * c2 + 8 * g + e) * SROW + 2 * i) =
-                  (uint16_t)(x[e >> 1] >> (16 * (e & 1)));
-          }
-        asm volatile("" ::: "memory");
-        // Lane (query i, g): keys 16 cc + 8 g .. + 7 of its row, per plane.
-#pragma unroll
-        for (int pl2 = 0; pl2 < 2; ++pl2)
-#pragma unroll
-          for (int cc = 0; cc < 2; ++cc) {
-            const u32x4 x = *(const __attribute__((address_space(3))) u32x4*)(st + pl2 * SPLANE + i * SROW +
-                                                                               2 * (16 * cc + 8 * g));
-            __builtin_amdgcn_raw_buffer_store_b128(x, rS, 16 * (64 * (2 * pl2 + cc) + lane), (int)(u * 4096u),
-                                                   kNonTemporal);
-          }
-      }
-    }
-  };
-
-  int t0, t1;
-  tile_range(a, j, t0, t1);
-  int ti = t0 - 1;
-  uint32_t rem = 0u;
-  auto take = [&](int& t, int& c) -> bool {
-    while (rem == 0u) {
-      if (++ti >= t1) return false;
-      rem = any_rows(tile_groups(a, ti));
-    }
-    t = ti;
-    c = __builtin_ctz(rem);
-    rem &= rem - 1u;
-    return true;
-  };
-  // Step (t, c): the group's Q and dO planes and, by wave 0, its lse and delta (lanes 32-63 read
-  // zeros into the gaps).
-  auto copy = [&](lds_char* buf, int t, int c) {
-    const int row0 = ((ci32_ptr)a.col)[t] * BLK + 32 * c;
-    dma.issue(rQ, rO, buf, row0, w);
-    if (w == 0) {
-      const int so = lane < 32 ? (row0 + lane) * 4 : (int)kPastEnd;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rL, (__attribute__((address_space(3))) void*)(buf + SB), 4, so, 0, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rD, (__attribute__((address_space(3))) void*)(buf + SB + 256), 4, so, 0,
-                                               0, 0);
-    }
-  };
-  lds_char* b0 = (lds_char*)gb0;
-  lds_char* b1 = (lds_char*)gb1;
-  int tc = 0, cc = 0, tn = 0, cn = 0;
-  bool vc = take(tc, cc), vn = false;
-  u32x2 mbc = {0u, 0u}, mbn = {0u, 0u};
-  if (vc) {
-    copy(b0, tc, cc);
-    mbc = tile_bits(a, tc, w, lane);
-    vn = take(tn, cn);
-  }
-  auto step = [&](lds_char* cur, lds_char* nxt) {
-    wait_vmem();  // this wave's part of the current step (wave 0: the statistics too) and its mask bits
-    if (w == 0 && lane < 8) {
-      // lse -> lse * log2(e), the form the exponent takes
-      __attribute__((address_space(3))) f32x4* x = (__attribute__((address_space(3))) f32x4*)(cur + SB + 16 * lane);
-      *x = *x * LOG2E;
-    }
-    __syncthreads();  // the step landed; every wave is done with the previous step's buffer
-    if (vn) {
-      copy(nxt, tn, cn);
-      mbn = tn != tc ? tile_bits(a, tn, w, lane) : mbc;
-    }
-    const uint32_t gt = tile_groups(a, tc);
-    uint32_t ub = 0u, gw = 0u;
-    if constexpr (DS) {
-      ub = ((cmap_ptr)a.tmap)[2 * tc];
-      gw = ((cmap_ptr)a.tmap)[2 * tc + 1];
-    }
-    if (gt >> (4 * w + cc) & 1u) group(cc, cur, mbc, ub, gw);
-    tc = tn;
-    cc = cn;
-    mbc = mbn;
-    vc = vn;
-    vn = vc && take(tn, cn);
-  };
-  while (vc) {
-    step(b0, b1);
-    if (!vc) break;
-    step(b1, b0);
-  }
-  if (j.part >= 0) {
-    store_bwd_partial<D>(a, j, 32 * w + i, dk, 0, g);
-    store_bwd_partial<D>(a, j, 32 * w + i, dv, 1, g);
-    return;
-  }
-  store_acc_f32<D>(make_rsrc((float*)a.out0 + j.base, a.slice_bytes), krow, snb, dk, a.scale, g);
-  store_acc_f32<D>(make_rsrc((float*)a.out1 + j.base, a.slice_bytes), krow, snb, dv, 1.f, g);
-}
-
 // dQ, float32 tensors, bf16x3 products, from the dS units of dkv_x3_kernel<D, true>: per work item
 // of the forward list, dQ^T += K^T dS^T over each wave's live 32 x 32 groups (pallas_attn.py:
 // 177-184 with dS from the dK/dV pass). Per tile half (key groups 2h, 2h + 1) the split K rows go
@@ -606,7 +297,6 @@ hipError_t launch_d(Kind kind, const KArgs& a, hipStream_t stream) {
   const dim3 grid((unsigned)a.n_items * (unsigned)(a.batch * a.heads)), block(NT);
   switch (kind) {
     case Kind::kFwd: hipLaunchKernelGGL(fwd_x3_kernel<D>, grid, block, 0, stream, a); break;
-    case Kind::kDkvDs: hipLaunchKernelGGL((dkv_x3_kernel<D, true>), grid, block, 0, stream, a); break;
     case Kind::kDqDs: hipLaunchKernelGGL(dq_x3_ds_kernel<D>, grid, block, 0, stream, a); break;
     default: return hipErrorInvalidValue;
   }
@@ -616,6 +306,7 @@ hipError_t launch_d(Kind kind, const KArgs& a, hipStream_t stream) {
 }  // namespace
 
 hipError_t launch_x3(Kind kind, int head_dim, const KArgs& a, hipStream_t stream) {
+  if (kind == Kind::kDkvDs) return launch_x3_dkv(head_dim, a, stream);
   switch (head_dim) {
     case 32: return launch_d<32>(kind, a, stream);
     case 64: return launch_d<64>(kind, a, stream);
