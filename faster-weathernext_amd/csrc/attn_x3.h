@@ -53,8 +53,9 @@ __device__ __forceinline__ void load_frag_x3(u32x4 (&hi)[D / 16], u32x4 (&lo)[D 
   }
 }
 
-// Copy of one step's 32 split K rows and 32 split V rows into a group buffer of four 32-row planes
-// (K hi, K lo, V hi, V lo; each [32][D] bf16, chunks swizzled as the bf16 tiles). Each wave-wide
+// Copy of 32 split rows of two operands (forward: K and V; dK/dV: Q and dO; dQ: two key groups of
+// K) into a group buffer of four 32-row planes (A hi, A lo, B hi, B lo; each [32][D] bf16, chunks
+// swizzled as the bf16 tiles). Each wave-wide
 // LDS DMA instruction fills 1 KB = RPO rows of one plane; the 4 waves share the 4 * NI
 // instructions of a step. Lane l of instruction (plane, sub) copies row RPO * sub + l / C,
 // physical chunk l % C, which holds logical chunk (l % C) ^ swz(row); the swizzle depends on

@@ -1,10 +1,11 @@
-// Split-precision forward for float32 tensors (FWN_PREC_BF16X3): every product of S = Q K^T and
-// O = P V is formed from bfloat16 parts on V_MFMA_F32_32X32X16_BF16, x = hi + lo with
-// hi = bf16(x) and lo = bf16(x - hi), as hi*hi + hi*lo + lo*hi in fp32 accumulation (the lo*lo
-// term is below fp32 rounding of the sum). Each operand then carries about 16 significant bits
-// instead of bf16's 8 (TF32 has 11), at three bf16 MFMAs per product: 5.3x the fp32-MFMA rate.
-// This is the role of the reference's TF32_TF32_F32_X3 dots under "highest" precision
-// (pallas_attn.py:336-341): an fp32-accurate forward on the matrix cores' fast type.
+// The bf16x3 (split-precision) kernels for float32 tensors (FWN_PREC_BF16X3): the split pass,
+// the forward and dQ from dS (dK/dV is in attn_x3_dkv.hip). Every product is formed from bf16
+// parts on V_MFMA_F32_32X32X16_BF16: x = hi + lo with hi = bf16(x) and lo = bf16(x - hi), and
+// a*b = ah*bh + ah*bl + al*bh in fp32 accumulation (al*bl, about 2^-18 of the product, is
+// dropped). Each operand then carries about 16-17 significant bits instead of bf16's 8 (TF32 has
+// 11), at three bf16 MFMAs per product: 5.3x the fp32-MFMA rate. This is the role of the
+// reference's TF32 and TF32_TF32_F32_X3 dots (pallas_attn.py:336-343) on a target without TF32
+// matrix instructions.
 //
 // The operands that stream through LDS (forward: K, V; dK/dV: Q, dO; dQ: K) are split once per
 // call by split_x3_kernel into [batch * heads][n][2][D] bf16 (hi row, then lo row) and copied by
