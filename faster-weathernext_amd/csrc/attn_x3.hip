@@ -179,7 +179,7 @@ __global__ void __launch_bounds__(NT, 2) fwd_x3_kernel(KArgs a) {
   if (g == 0) write_lse(a, j, qrow, st, ltot);
 }
 
-// dQ, float32 tensors, bf16x3 products, from the dS units of dkv_x3_kernel<D, true>: per work item
+// dQ, float32 tensors, bf16x3 products, from the dS units of dkv16_x3_kernel: per work item
 // of the forward list, dQ^T += K^T dS^T over each wave's live 32 x 32 groups (pallas_attn.py:
 // 177-184 with dS from the dK/dV pass). Per tile half (key groups 2h, 2h + 1) the split K rows go
 // into one of two half buffers (planes K hi, K lo of each group: 32 KB at D = 128), two workgroups
