@@ -487,15 +487,38 @@ def tiled_flash_attention_qkv(qkv, tiles, *, scale, tiles_t=None, precision="nat
   return _TiledAttentionQKV.apply(qkv, tiles, tiles_t, float(scale), precision)
 
 
-def tiled_flash_attention(q, k, v, tile_ptr, tile_kb=None, tile_bits=None, *, scale, tiles_t=None,
-                          precision="native"):
+def _reference_options(strict_fp32, precision, block_q, block_k, interpret):
+  """The reference's keyword arguments (pallas_attn.py:317-347) in this build's terms.
+
+  strict_fp32 asks for IEEE float32 products, which is "native"; block_q / block_k must be the
+  tile size the lists are built with (128); num_warps, num_stages, bwd_num_warps and bwd_split
+  tune the reference's Triton programs and have no counterpart (the kernels fix their own
+  launch shapes), so any value is accepted; interpret=True asks for the CPU interpreter, which
+  does not exist here."""
+  if strict_fp32 and precision != "native":
+    raise ValueError("strict_fp32 asks for IEEE float32 products: precision must be 'native'")
+  for name, val in (("block_q", block_q), ("block_k", block_k)):
+    if val is not None and val != nat.BLOCK:
+      raise ValueError(f"{name}={val}: the kernels use {nat.BLOCK} x {nat.BLOCK} tiles (build the lists with "
+                       f"build_tile_mask / TileList)")
+  if interpret:
+    raise ValueError("interpret=True: there is no CPU interpreter; the kernels run on the GPU only")
+
+
+def tiled_flash_attention(q, k, v, tile_ptr, tile_kb=None, tile_bits=None, *, scale, strict_fp32=False,
+                          tiles_t=None, block_q=None, block_k=None, num_warps=None, num_stages=None,
+                          bwd_num_warps=None, bwd_split=None, interpret=False, precision="native"):
   """q, k, v: [batch, n, heads, head_dim] float32/bfloat16 on the GPU -> [batch, n, heads, head_dim].
 
-  ``tile_ptr`` may be a prepared TileList (then tile_kb and tile_bits are omitted) or the first of
-  the three arrays of ``build_tile_mask``. ``tiles_t`` (TileList or array triple) is the
-  transposed mask's list for the dK/dV kernel; it defaults to the forward's (symmetric masks).
-  ``precision`` ("native" or "bf16x3", float32 only): the forward's products, see PRECISIONS.
+  The reference's signature (pallas_attn.py:317-320). ``tile_ptr`` may be a prepared TileList (then
+  tile_kb and tile_bits are omitted) or the first of the three arrays of ``build_tile_mask``.
+  ``tiles_t`` (TileList or array triple) is the transposed mask's list for the dK/dV kernel; it
+  defaults to the forward's (symmetric masks). ``precision`` ("native" or "bf16x3", float32
+  only): the products, see PRECISIONS; ``strict_fp32`` requires "native". The Triton tuning
+  arguments are accepted and have no effect (see _reference_options).
   """
+  del num_warps, num_stages, bwd_num_warps, bwd_split
+  _reference_options(strict_fp32, precision, block_q, block_k, interpret)
   _check(q)
   _precision(precision, q.dtype)
   tiles = tile_ptr if isinstance(tile_ptr, TileList) else (tile_ptr, tile_kb, tile_bits)

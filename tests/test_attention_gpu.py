@@ -570,3 +570,22 @@ def test_exp2_based_softmax_accuracy():
   np.testing.assert_allclose(_np(out), 1.0, rtol=0, atol=4e-6)
   ref = A.dense_lse(q, k, m.toarray(), d ** -0.5)
   np.testing.assert_allclose(_np(lse), ref, rtol=2e-6, atol=2e-6)
+
+
+def test_reference_keywords_give_the_same_result():
+  """A call written for the reference's signature (pallas_attn.py:317-320: strict_fp32, block
+  sizes, Triton tuning values) runs the same kernels: bit-identical outputs and gradients."""
+  rng = np.random.default_rng(12)
+  n, h, d = 300, 2, 64
+  q, k, v, do = (rng.standard_normal((1, n, h, d)).astype(np.float32) for _ in range(4))
+  tiles = fwn.TileList.from_mask(_random_mask(n, 0.05, 13, symmetric=True))
+  res = []
+  for kw in ({}, dict(strict_fp32=True, block_q=128, block_k=128, num_warps=4, num_stages=1, bwd_num_warps=4,
+                      bwd_split=2, interpret=False)):
+    qt, kt, vt = (_dev(x, torch.float32, True) for x in (q, k, v))
+    out = fwn.tiled_flash_attention(qt, kt, vt, tiles, scale=d ** -0.5, **kw)
+    out.backward(_dev(do, torch.float32))
+    res.append([_np(t) for t in (out, qt.grad, kt.grad, vt.grad)])
+  torch.cuda.synchronize()
+  for a, b in zip(*res):
+    np.testing.assert_array_equal(a, b)

@@ -781,3 +781,21 @@ def test_split_precision_python_options():
     hip_attn._precision("bf16x3", torch.bfloat16)
   with pytest.raises(ValueError):
     hip_attn._precision("tf32", torch.float32)
+
+
+def test_reference_keyword_arguments():
+  """tiled_flash_attention takes the reference's keywords (pallas_attn.py:317-320): Triton tuning
+  values are accepted, strict_fp32 requires IEEE products, other tile sizes and the CPU
+  interpreter are refused with ValueError before any GPU work."""
+  from faster_weathernext_amd import hip_attn
+  hip_attn._reference_options(True, "native", 128, 128, False)
+  hip_attn._reference_options(False, "bf16x3", None, None, False)
+  for args in ((True, "bf16x3", None, None, False), (False, "native", 64, None, False),
+               (False, "native", None, 32, False), (False, "native", None, None, True)):
+    with pytest.raises(ValueError):
+      hip_attn._reference_options(*args)
+  import inspect
+  params = inspect.signature(fwn.tiled_flash_attention).parameters
+  for name in ("scale", "strict_fp32", "tiles_t", "block_q", "block_k", "num_warps", "num_stages", "bwd_num_warps",
+               "bwd_split", "interpret"):
+    assert name in params, name
