@@ -162,7 +162,7 @@ class TileList:
   @classmethod
   def from_mask(cls, mask, perm=None, device="cuda", max_item_tiles=None):
     """Tile list of a boolean scipy/numpy [n, n] mask (optionally permuted as mask[perm][:, perm])."""
-    tp, kb, bits = build_tile_mask(mask, perm)
+    tp, kb, bits = build_tile_mask(mask, perm=perm)
     return cls(tp, kb, bits, mask.shape[1], device, max_item_tiles)
 
   @property

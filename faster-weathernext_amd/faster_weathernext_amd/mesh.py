@@ -110,8 +110,11 @@ def hilbert_order(lat_deg, lon_deg, bits=10):
   return perm
 
 
-def build_tile_mask(mask, perm=None):
+def build_tile_mask(mask, block_q=nat.BLOCK, block_k=nat.BLOCK, *, perm=None):
   """CSR live-tile list of a boolean [n_rows, n_cols] mask at 128 x 128 tiles.
+
+  The reference's signature (``pallas_attn.py:85``); its 64 x 32 tiles are not built here, so
+  ``block_q`` and ``block_k`` must be 128 (ValueError otherwise).
 
   Returns (tile_ptr int32[n_blocks + 1], tile_kb int32[T], tile_bits uint32[T, 128, 4]): block i owns
   tiles tile_ptr[i]:tile_ptr[i+1]; tile t covers columns tile_kb[t]*128 + [0, 128) and bit j of word
@@ -119,6 +122,8 @@ def build_tile_mask(mask, perm=None):
   With ``perm`` the list describes mask[perm][:, perm]. Same layout as the reference's
   ``build_tile_mask`` (``pallas_attn.py:85-109``) with 128-wide tiles (4 words per row).
   """
+  if block_q != nat.BLOCK or block_k != nat.BLOCK:
+    raise ValueError(f"tiles of {block_q} x {block_k}: the kernels use {nat.BLOCK} x {nat.BLOCK}")
   m = sparse.csr_matrix(mask)
   n_rows, n_cols = m.shape
   indptr = nat.as_c(m.indptr, np.int64)
@@ -140,8 +145,9 @@ def mesh_mask(refinement, k_hop, reorder=False):
   """The attention mask of one mesh transformer: (mask CSR, lat, lon, perm or None).
 
   The mask is the k-hop neighbourhood of the refined icosahedral mesh in subdivision order; with
-  ``reorder`` the Hilbert permutation is returned as well (apply it with ``build_tile_mask(mask,
-  perm)``), as the reference's patched transformer does (``patch.py:208-214``).
+  ``reorder`` the Hilbert permutation is returned as well (apply it with
+  ``build_tile_mask(mask, perm=perm)``), as the reference's patched transformer does
+  (``patch.py:208-214``).
   """
   v, f, lat, lon = icosahedral_mesh(refinement)
   mask = khop_mask(adjacency(f, len(v)), k_hop)

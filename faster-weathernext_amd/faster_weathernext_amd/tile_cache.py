@@ -102,7 +102,7 @@ def load(path, *, n_rows, n_cols, key):
 
 
 def cached_tile_mask(mask, perm=None, *, cache_dir, k_hop=-1):
-  """build_tile_mask(mask, perm) through a cache file in `cache_dir` keyed by the mask's content.
+  """build_tile_mask(mask, perm=perm) through a cache file in `cache_dir` keyed by the mask's content.
 
   Returns (tile_ptr, tile_kb, tile_bits, hit)."""
   n_rows, n_cols = mask.shape
@@ -112,7 +112,7 @@ def cached_tile_mask(mask, perm=None, *, cache_dir, k_hop=-1):
   got = load(path, n_rows=n_rows, n_cols=n_cols, key=key)
   if got is not None:
     return (*got, True)
-  tp, kb, bits = build_tile_mask(mask, perm)
+  tp, kb, bits = build_tile_mask(mask, perm=perm)
   save(path, tp, kb, bits, n_rows=n_rows, n_cols=n_cols, key=key, k_hop=k_hop, order=int(perm is not None))
   return tp, kb, bits, False
 
@@ -128,6 +128,6 @@ def cached_khop_tiles(adj, k_hop, perm=None, *, cache_dir):
   got = load(path, n_rows=n, n_cols=n, key=key)
   if got is not None:
     return (*got, True)
-  tp, kb, bits = build_tile_mask(khop_mask(adj, k_hop), perm)
+  tp, kb, bits = build_tile_mask(khop_mask(adj, k_hop), perm=perm)
   save(path, tp, kb, bits, n_rows=n, n_cols=n, key=key, k_hop=k_hop, order=int(perm is not None))
   return tp, kb, bits, False

@@ -88,7 +88,7 @@ def test_hilbert_matches_oracle():
 def test_tile_list_matches_oracle(n, density, permute):
   m = _random_mask(n, density, 7)
   perm = np.random.default_rng(1).permutation(n) if permute else None
-  got = fwn.build_tile_mask(m, perm)
+  got = fwn.build_tile_mask(m, perm=perm)
   ref = ot.build_tile_mask(m[perm][:, perm] if permute else m, 128, 128)
   for g, r in zip(got, ref):
     np.testing.assert_array_equal(g, r)
@@ -420,7 +420,7 @@ def test_tile_cache_round_trip_and_invalidation(tmp_path):
   v, f, lat, lon = fwn.icosahedral_mesh(3)
   adj = fwn.adjacency(f, len(v))
   perm = fwn.hilbert_order(lat, lon)
-  ref = fwn.build_tile_mask(fwn.khop_mask(adj, 2), perm)
+  ref = fwn.build_tile_mask(fwn.khop_mask(adj, 2), perm=perm)
   got = tile_cache.cached_khop_tiles(adj, 2, perm, cache_dir=str(tmp_path))
   assert not got[3]
   for a, b in zip(got[:3], ref):
@@ -799,3 +799,16 @@ def test_reference_keyword_arguments():
   for name in ("scale", "strict_fp32", "tiles_t", "block_q", "block_k", "num_warps", "num_stages", "bwd_num_warps",
                "bwd_split", "interpret"):
     assert name in params, name
+
+
+def test_build_tile_mask_takes_the_reference_signature():
+  """build_tile_mask(mask, block_q, block_k) as the reference's (pallas_attn.py:85): 128 x 128 is
+  what the kernels use; the reference's 64 x 32 default is refused rather than misread."""
+  from scipy import sparse
+  m = sparse.identity(300, dtype=bool, format="csr")
+  a = fwn.build_tile_mask(m)
+  b = fwn.build_tile_mask(m, 128, 128)
+  for x, y in zip(a, b):
+    np.testing.assert_array_equal(x, y)
+  with pytest.raises(ValueError):
+    fwn.build_tile_mask(m, 64, 32)
