@@ -89,6 +89,32 @@ int check_desc(const fwn_attn_desc* d) {
   return FWN_OK;
 }
 
+// Outputs are written through one of the two stride sets (o through the o set; dq, dk, dv through
+// the q set), so their (batch, row, head) rows of head_dim elements must not overlap, or two work
+// items would race on the same memory. Sufficient test: with the dimensions of size > 1 sorted by
+// stride, each stride reaches past the extent of the ones before it.
+int check_disjoint(const fwn_attn_desc* d, bool o_set, const char* what) {
+  const bool same = d->ostride_b == 0 && d->ostride_n == 0 && d->ostride_h == 0;
+  const bool use_o = o_set && !same;
+  int64_t st[3] = {use_o ? d->ostride_b : d->stride_b, use_o ? d->ostride_n : d->stride_n,
+                   use_o ? d->ostride_h : d->stride_h};
+  int64_t sz[3] = {d->batch, d->n, d->heads};
+  // insertion sort of the three (stride, size) pairs by stride
+  for (int a = 1; a < 3; ++a)
+    for (int b = a; b > 0 && st[b] < st[b - 1]; --b) {
+      const int64_t t = st[b]; st[b] = st[b - 1]; st[b - 1] = t;
+      const int64_t u = sz[b]; sz[b] = sz[b - 1]; sz[b - 1] = u;
+    }
+  int64_t extent = d->head_dim;
+  for (int a = 0; a < 3; ++a) {
+    if (sz[a] <= 1) continue;
+    if (st[a] < extent)
+      return fail(FWN_ERR_INVALID_ARG, "%s: the (batch, row, head) rows of the strides overlap", what);
+    extent = st[a] * (sz[a] - 1) + extent;
+  }
+  return FWN_OK;
+}
+
 int check_tensor(const void* p, const char* name) {
   if (!p) return fail(FWN_ERR_INVALID_ARG, "%s is null", name);
   if (!aligned16(p)) return fail(FWN_ERR_INVALID_ARG, "%s is not 16-byte aligned", name);
@@ -279,6 +305,7 @@ int fwn_attn_fwd_launch(const fwn_attn_desc* desc, const void* q, const void* k,
   if (int rc = check_tensor(k, "k")) return rc;
   if (int rc = check_tensor(v, "v")) return rc;
   if (int rc = check_tensor(o, "o")) return rc;
+  if (int rc = check_disjoint(desc, true, "o")) return rc;
   if (int rc = check_tiles(desc, tiles, "tiles")) return rc;
   if (int rc = check_workspace(desc, tiles, workspace, workspace_bytes)) return rc;
   KArgs a = base_args(desc);
@@ -323,6 +350,7 @@ int fwn_attn_bwd_dq_launch(const fwn_attn_desc* desc, const void* q, const void*
   if (int rc = check_tensor(v, "v")) return rc;
   if (int rc = check_tensor(dout, "dout")) return rc;
   if (int rc = check_tensor(dq, "dq")) return rc;
+  if (int rc = check_disjoint(desc, false, "dq")) return rc;
   if (!lse || !delta) return fail(FWN_ERR_INVALID_ARG, "lse and delta are required");
   if (int rc = check_tiles(desc, tiles, "tiles")) return rc;
   if (int rc = check_workspace(desc, tiles, workspace, workspace_bytes)) return rc;
@@ -350,6 +378,7 @@ int fwn_attn_bwd_dkv_launch(const fwn_attn_desc* desc, const void* q, const void
   if (int rc = check_tensor(dout, "dout")) return rc;
   if (int rc = check_tensor(dk, "dk")) return rc;
   if (int rc = check_tensor(dv, "dv")) return rc;
+  if (int rc = check_disjoint(desc, false, "dk/dv")) return rc;
   if (!lse || !delta) return fail(FWN_ERR_INVALID_ARG, "lse and delta are required");
   if (int rc = check_tiles(desc, tiles_t, "tiles_t")) return rc;
   if (int rc = check_workspace(desc, tiles_t, workspace, workspace_bytes)) return rc;
@@ -401,6 +430,7 @@ int fwn_attn_bwd_dkv_ds_launch(const fwn_attn_desc* desc, const void* q, const v
   if (int rc = check_tensor(dout, "dout")) return rc;
   if (int rc = check_tensor(dk, "dk")) return rc;
   if (int rc = check_tensor(dv, "dv")) return rc;
+  if (int rc = check_disjoint(desc, false, "dk/dv")) return rc;
   if (!lse || !delta) return fail(FWN_ERR_INVALID_ARG, "lse and delta are required");
   if (int rc = check_tiles(desc, tiles_t, "tiles_t")) return rc;
   if (int rc = check_workspace(desc, tiles_t, workspace, workspace_bytes)) return rc;
@@ -432,6 +462,7 @@ int fwn_attn_bwd_dq_ds_launch(const fwn_attn_desc* desc, const void* k, const vo
   if (int rc = check_ds(desc, map, ds, ds_bytes, true, false)) return rc;
   if (int rc = check_tensor(k, "k")) return rc;
   if (int rc = check_tensor(dq, "dq")) return rc;
+  if (int rc = check_disjoint(desc, false, "dq")) return rc;
   if (int rc = check_tiles(desc, tiles, "tiles")) return rc;
   if (desc->dtype == FWN_BF16 && tiles->n_tiles > 0 && !tiles->halves)
     return fail(FWN_ERR_TILES, "tiles: the bf16 dS exchange needs the half bits (fwn_tiles_prepare with halves)");

@@ -17,7 +17,9 @@
  *   - Tensors q, k, v, o, dout, dq, dk, dv are [batch, n, heads, head_dim] in the element strides
  *     of fwn_attn_desc (head_dim contiguous): node-major by default, read and written in place
  *     (the reference transposes to head-major and pads, pallas_attn.py:334-335; here no copy is
- *     made). q, k, v, dq, dk, dv share one set of strides, o and dout another.
+ *     made). q, k, v, dq, dk, dv share one set of strides, o and dout another. The stride set an
+ *     output is written through (o; dq, dk, dv) must map distinct (batch, row, head) rows to
+ *     disjoint memory, or the launcher returns FWN_ERR_INVALID_ARG.
  *   - lse and delta are float32 [batch, heads, n], contiguous.
  *   - Rows are processed in blocks of FWN_BLOCK = 128 and key tiles are 128 wide
  *     (the reference uses 64 x 32, pallas_attn.py:30-31).

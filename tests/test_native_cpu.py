@@ -812,3 +812,28 @@ def test_build_tile_mask_takes_the_reference_signature():
     np.testing.assert_array_equal(x, y)
   with pytest.raises(ValueError):
     fwn.build_tile_mask(m, 64, 32)
+
+
+def test_output_strides_must_not_overlap():
+  """Outputs written through strides whose (batch, row, head) rows overlap would race: the
+  forward checks the o strides, the dq/dk/dv launchers the q strides, before any HIP call.
+  Inputs may overlap (read only): a forward whose q, k, v broadcast over the batch (stride 0)
+  with a proper o passes validation."""
+  L = nat.lib()
+  F = FAKE
+  tiles = _tiles()
+  # head-major with stride_n == stride_h == head_dim: head 1 row 0 is head 0 row 1
+  bad = _desc(stride_b=300 * 128, stride_n=64, stride_h=64)
+  assert L.fwn_attn_fwd_launch(bad, F, F, F, tiles, F, None, None, 0, None) == nat.ERR_INVALID_ARG
+  assert "overlap" in L.fwn_last_error().decode()
+  assert L.fwn_attn_bwd_dq_launch(bad, F, F, F, F, F, F, tiles, F, None, 0, None) == nat.ERR_INVALID_ARG
+  assert L.fwn_attn_bwd_dkv_launch(bad, F, F, F, F, F, F, tiles, F, F, None, 0, None) == nat.ERR_INVALID_ARG
+  # batches overlapping (stride_b smaller than a batch's extent)
+  bad_b = _desc(batch=2, stride_b=128, stride_n=128, stride_h=64)
+  assert L.fwn_attn_bwd_dq_launch(bad_b, F, F, F, F, F, F, tiles, F, None, 0, None) == nat.ERR_INVALID_ARG
+  # broadcast inputs (stride_b 0), disjoint o strides: passes validation (fails later at the tiles)
+  bcast = _desc(batch=2, stride_b=0, stride_n=128, stride_h=64, ostride_b=300 * 128, ostride_n=128, ostride_h=64)
+  assert L.fwn_attn_fwd_launch(bcast, F, F, F, _tiles(n_blocks=5), F, None, None, 0, None) == nat.ERR_TILES
+  # the packed qkv views are disjoint
+  packed = _desc(stride_b=300 * 3 * 2 * 64, stride_n=3 * 2 * 64, stride_h=64)
+  assert L.fwn_attn_fwd_launch(packed, F, F, F, _tiles(n_blocks=5), F, None, None, 0, None) == nat.ERR_TILES
