@@ -204,3 +204,21 @@ def test_more_accurate_than_bf16_and_close_to_native():
   bf, _ = fwn.attention_forward(*(dev(x, torch.bfloat16) for x in (q, k, v)), tiles, d ** -0.5)
   e_x3, e_nat, e_bf = A.rel_rms(x3, ref), A.rel_rms(native, ref), A.rel_rms(host(bf), ref)
   assert e_x3 <= 1e-5 and e_x3 * 50 < e_bf and e_x3 < 30 * max(e_nat, 1e-7), (e_x3, e_nat, e_bf)
+
+
+def test_c5_attention_shape_forward_backward():
+  """The reference benchmark's attention shape (scripts/attn_bench.py:23, 115-119: 32-hop mask
+  in Hilbert order, 6 heads x 128, fwd + bwd) with float32 tensors in bf16x3 (bench.py
+  --workload c5f32 --precision bf16x3 times this call): rows of blocks 119, 200 and 320 and every
+  key of blocks 119, 200 and 320 against the exact block oracle, within the float32 bar."""
+  mask, _, _, perm = fwn.mesh_mask(6, 32, reorder=True)
+  mask = mask[perm][:, perm].tocsr()
+  n = mask.shape[0]
+  rng = np.random.default_rng(0)
+  q, k, v, do = (rng.standard_normal((1, n, 6, 128)).astype(np.float32) for _ in range(4))
+  res = _grads(q, k, v, do, fwn.TileList.from_mask(mask), 128 ** -0.5)
+  ref = A.block_attention(q, k, v, do, mask, 128 ** -0.5, row_blocks=[119, 200, 320], key_blocks=[119, 200, 320])
+  check(res["out"][:, ref["rows"]], ref["out"], "out")
+  check(res["dq"][:, ref["rows"]], ref["dq"], "dq")
+  check(res["dk"][:, ref["keys"]], ref["dk"], "dk")
+  check(res["dv"][:, ref["keys"]], ref["dv"], "dv")
