@@ -2,7 +2,7 @@
 """Benchmark of the block-sparse masked mesh attention on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c3|c2|c4|c5|c5bwd|c5f32|c5mha|c5stack|rows]
-                    [--no-cpu]
+                    [--precision native|bf16x3] [--no-cpu]
 
 A step is one pass of the hot path over one batch of synthetic input: for the default workload
 (configuration 3 of BASELINE.json) the forward kernel plus the backward as the package's backward
@@ -87,8 +87,9 @@ def parse():
   p.add_argument("--no-ds", action="store_true",
                  help="the recomputing dQ kernel beside dK/dV instead of the dS exchange")
   p.add_argument("--precision", default="native", choices=["native", "bf16x3"],
-                 help="float32 workloads: the forward's products (bf16x3: three bf16 products per fp32 "
-                      "product, the backward in IEEE fp32)")
+                 help="float32 workloads: bf16x3 forms each product from bf16 parts (three bf16 MFMA "
+                      "products) in the forward and the dS-exchange backward; with --no-ds the backward "
+                      "stays IEEE fp32")
   p.add_argument("--layout", default="node", choices=["node", "head"],
                  help="storage of q, k, v, o, dO, dq, dk, dv: node-major [B, n, H, D] (the reference's "
                       "interface) or head-major [B, H, n, D] passed as strided views")
