@@ -269,7 +269,7 @@ def _check(q):
     raise ValueError("expected [batch, n, heads, head_dim]")
 
 
-# Product precision of the forward (the reference picks its dot algorithm from jax's default
+# Product precision of the kernels (the reference picks its dot algorithm from jax's default
 # matmul precision and strict_fp32, pallas_attn.py:336-341):
 #   "native": products in the tensors' dtype (IEEE float32 products for float32, the reference's
 #             strict_fp32; bf16 products for bf16);
