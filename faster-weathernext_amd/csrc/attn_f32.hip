@@ -1,5 +1,6 @@
-// float32 attention kernels for gfx950: forward, dQ, dK/dV (V_MFMA_F32_32X32X2_F32, full fp32
-// products and accumulation), and the delta pre-pass for both dtypes.
+// float32 attention kernels for gfx950: forward, dQ, dK/dV (V_MFMA_F32_32X32X2_F32, and
+// V_MFMA_F32_16X16X4F32 for the 16-key dK/dV at head_dim 128; full fp32 products and
+// accumulation), and the delta pre-pass for both dtypes.
 //
 // fp32 MFMA operands are one element per lane, so the second contraction's A operand (V^T, K^T,
 // Q^T, dO^T) is read element-wise straight from the row-major LDS tile; no transposed copy is
@@ -377,7 +378,8 @@ __global__ void __launch_bounds__(NT, 1) dq_f32_kernel(KArgs a) {
   store_acc_f32<D>(make_rsrc((float*)a.out0 + j.base, a.slice_bytes), qrow, snb, acc, a.scale, g);
 }
 
-// dQ, fp32, from the dS units of dkv_f32_kernel<D, true> (the float32 dS exchange): per work
+// dQ, fp32, from the dS units of the float32 dK/dV kernels (the float32 dS exchange: written by
+// dkv16_f32_kernel<true> at head_dim 128, dkv_f32_kernel<D, true> below it): per work
 // item of the forward list, dQ^T += K^T dS^T over each wave's live 32 x 32 groups
 // (pallas_attn.py:177-184 with dS from the dK/dV pass instead of recomputed). A unit is one
 // group's dS, 4 KB, laid out so that lane L's B operands (query L % 32, key
@@ -488,8 +490,8 @@ __global__ void __launch_bounds__(NT, 2) dq_f32_ds_kernel(KArgs a) {
   store_acc_f32<D>(make_rsrc((float*)a.out0 + j.base, a.slice_bytes), qrow, snb, acc, a.scale, g);
 }
 
-// dK/dV, fp32. The tile's Q and dO rows, and their lse and delta, stream in halves through two
-// half buffers as in dQ.
+// dK/dV, fp32, head_dim 32 and 64 (head_dim 128 runs dkv16_f32_kernel). The tile's Q and dO
+// rows, and their lse and delta, stream in halves through two half buffers as in dQ.
 //
 // With DS (the float32 dS exchange), each group's dS also goes to HBM as one 4 KB unit in
 // dq_f32_ds_kernel's operand layout. This lane holds dS of key 32w + i and query
@@ -668,6 +670,297 @@ __global__ void __launch_bounds__(NT, 1) dkv_f32_kernel(KArgs a) {
 }
 
 // ------------------------------------------------------------------------------------------
+// dK/dV, fp32, head_dim 128, 16 keys per wave (V_MFMA_F32_16X16X4F32), 8 waves, one workgroup per
+// CU: a wave's K and V rows (64 registers) and dK^T, dV^T (64) leave room for a second wave per
+// SIMD, twice dkv_f32_kernel's waves per CU.
+//
+// The k order of the first contractions is permuted so that each lane's fragment is contiguous:
+// k-step s of lane group g (= lane / 16) contracts column 32 g + s, so lane (key l % 16, g) holds
+// K and V columns 32 g .. 32 g + 31 of its key, and one 16-byte row read of a Q or dO row gives
+// the A operands of four k-steps. The accumulator layout is the bf16 16-key kernel's: lane
+// (key l % 16, g) holds S and dP of queries 16 m + 4 g + r. P and dS are then the B operands of
+// dV^T += dO^T P and dK^T += Q^T dS with query 16 m + 4 g + r as step (m, r), and the A operands
+// are single dO / Q elements, read straight from the row-major tile.
+//
+// Tiles: the transposed list's (tile, query group) steps stream the group's Q and dO rows and its
+// statistics through two group buffers. Rows are padded to 528 bytes (16 bytes over a row), so
+// both read patterns are conflict-free without a swizzle and every LDS address is a per-lane base
+// plus an immediate: 16 lanes of a row read cover rows t .. t + 15 at one column (16 t bytes apart
+// modulo the 256-byte bank line), and the 64 lanes of an element read cover rows 4 g + r at 16
+// columns (64 g bytes apart). A padded row is one LDS DMA instruction of 32 lanes.
+//
+// dS (DS): the float32 exchange's 4 KB units, written by the two waves of a 32-key group: wave w
+// writes dQ registers 8 (w % 2) .. + 7 of every dQ lane (chunks 2 (w % 2) and 2 (w % 2) + 1)
+// through its own LDS stage ([query][16 keys] fp32, 80-byte rows: conflict-free both ways). A wave
+// whose 16 keys have no valid element in a unit the map has writes zeros for its chunks.
+constexpr int kRowPad = 4 * 128 + 16;  // padded LDS row of a head_dim 128 fp32 tile
+constexpr uint32_t kPastEndF = 0x7FFFFFF0u;  // a buffer offset past every slice: reads zeros
+
+__device__ __forceinline__ f32x4 mfma16f(float a, float b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+template <bool DS>
+__global__ void __launch_bounds__(512, 1) dkv16_f32_kernel(KArgs a) {
+  constexpr int D = 128;
+  constexpr int RB = kRowPad;
+  constexpr int PB = 32 * RB;  // one plane: 32 padded rows
+  constexpr int SB = 2 * PB;   // Q | dO | -lse/scale [32], 0 [32] | -delta [32], 0 [32]
+  constexpr int NB = D / 16;   // 16-column blocks of dK^T and dV^T
+  constexpr int SROW = 80;
+  __shared__ __attribute__((aligned(1024))) char gb0[SB + 512];
+  __shared__ __attribute__((aligned(1024))) char gb1[SB + 512];
+  __shared__ __attribute__((aligned(16))) char stage[DS ? 8 * 32 * SROW : 16];
+  typedef const __attribute__((address_space(3))) f32x4* cf4;
+  typedef const __attribute__((address_space(3))) float* cf1;
+  typedef const __attribute__((address_space(4))) uint32_t* cmap_ptr;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, t16 = lane & 15;
+  const Job j = decode_job(a);
+  const uint32_t snb = (uint32_t)a.sn * 4, osnb = (uint32_t)a.osn * 4;
+  const rsrc_t rQ = make_rsrc((const float*)a.q + j.base, a.slice_bytes);
+  const rsrc_t rO = make_rsrc((const float*)a.dout + j.obase, a.oslice_bytes);
+  const rsrc_t rL = make_rsrc(a.lse + stat_index(a, j, 0), (uint32_t)a.n * 4);
+  const rsrc_t rD = make_rsrc(a.delta + stat_index(a, j, 0), (uint32_t)a.n * 4);
+  const rsrc_t rS = make_rsrc(DS ? (const void*)(a.ds + (int64_t)j.bh * (a.ds_slice_bytes >> 1)) : (const void*)a.q,
+                              DS ? a.ds_slice_bytes : 0u);
+  const int krow = j.blk * BLK + 16 * wid + t16;
+  // K and V of this lane's key: kf[u][e] = column 32 g + 4 u + e (k-step 4 u + e).
+  f32x4 kf[8], vf[8];
+  {
+    const rsrc_t rK = make_rsrc((const float*)a.k + j.base, a.slice_bytes);
+    const rsrc_t rV = make_rsrc((const float*)a.v + j.base, a.slice_bytes);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const uint32_t off = (uint32_t)krow * snb + (uint32_t)(128 * g + 16 * u);
+      kf[u] = __builtin_bit_cast(f32x4, bload16(rK, off));
+      vf[u] = __builtin_bit_cast(f32x4, bload16(rV, off));
+    }
+  }
+  // Per-lane LDS bases: row reads (row t16, columns 32 g ..) and element reads (row 4 g, column
+  // t16); the loop indexes add immediates.
+  const uint32_t rbase = (uint32_t)(t16 * RB + 128 * g);
+  const uint32_t ebase = (uint32_t)(4 * g * RB + 4 * t16);
+  f32x4 dk[NB], dv[NB];
+#pragma unroll
+  for (int n = 0; n < NB; ++n) {
+    dk[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+    dv[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  const uint64_t* mword = key_mask_words(a, wid, g, t16);
+  const int mshift = 4 * (g & 1);
+  lds_char* stw = (lds_char*)stage + wid * 32 * SROW;
+
+  // The dS chunks of a unit: `have` false writes zeros.
+  auto store_chunks = [&](bool have, const float (&ds)[8], uint32_t u) {
+    const int i = lane & 31, gq = lane >> 5;
+    u32x4 y[2] = {u32x4{0u, 0u, 0u, 0u}, u32x4{0u, 0u, 0u, 0u}};
+    if (have) {
+      asm volatile("" ::: "memory");
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        *(__attribute__((address_space(3))) float*)(stw + (16 * (e >> 2) + 4 * g + (e & 3)) * SROW + 4 * t16) = ds[e];
+      asm volatile("" ::: "memory");
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        y[h] = *(const __attribute__((address_space(3))) u32x4*)(stw + i * SROW + 32 * gq + 16 * h);
+      asm volatile("" ::: "memory");
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      __builtin_amdgcn_raw_buffer_store_b128(y[h], rS, 16 * (64 * (2 * (wid & 1) + h) + lane), (int)(u * 4096u), 2);
+  };
+
+  // Unit: query group c of the group buffer buf (mask word mw of this lane).
+  auto unit = [&](int c, const lds_char* buf, uint64_t mw, bool have_unit, uint32_t u_idx) {
+    const lds_char* lq = buf;
+    const lds_char* lo = buf + PB;
+    f32x4 sa[2], da[2];
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      sa[m] = *(cf4)(buf + SB + 4 * (16 * m + 4 * g));
+      da[m] = *(cf4)(buf + SB + 256 + 4 * (16 * m + 4 * g));
+    }
+    // S and dP: the Q and dO row reads of the next (row read u, query half m) go out before this
+    // pair's eight MFMAs.
+    auto rows = [&](f32x4 (&x)[2], int it) {
+      const uint32_t o = rbase + (uint32_t)(16 * (it >> 1) + 16 * (it & 1) * RB);
+      x[0] = *(cf4)(lq + o);
+      x[1] = *(cf4)(lo + o);
+    };
+    f32x4 rd[2][2];
+    rows(rd[0], 0);
+#pragma unroll
+    for (int it = 0; it < 16; ++it) {
+      if (it + 1 < 16) rows(rd[(it + 1) & 1], it + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      const int u = it >> 1, m = it & 1;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        sa[m] = mfma16f(rd[it & 1][0][e], kf[u][e], sa[m]);
+        da[m] = mfma16f(rd[it & 1][1][e], vf[u][e], da[m]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    float p[8], ds[8];
+    const uint32_t w32 = (uint32_t)(mw >> (32 * (c >> 1)));
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float se = e < 4 ? sa[0][e & 3] : sa[1][e & 3];
+      const float de = e < 4 ? da[0][e & 3] : da[1][e & 3];
+      const float pe = keep_or_zero(fast_exp2(se * a.c2),
+                                    __builtin_amdgcn_sbfe(w32, (uint32_t)(16 * (c & 1) + 8 * (e >> 2) + (e & 3)), 1u));
+      p[e] = pe;
+      ds[e] = pe * de;
+    }
+    // dV^T and dK^T by 16-column block n; the block's 16 element reads go out before the previous
+    // block's 16 MFMAs.
+    auto els = [&](float (&x)[16], int n) {
+#pragma unroll
+      for (int m = 0; m < 2; ++m)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const uint32_t o = ebase + (uint32_t)((16 * m + r) * RB + 64 * n);
+          x[8 * m + 2 * r] = *(cf1)(lo + o);
+          x[8 * m + 2 * r + 1] = *(cf1)(lq + o);
+        }
+    };
+    float ex[2][16];
+    els(ex[0], 0);
+#pragma unroll
+    for (int n = 0; n < NB; ++n) {
+      if (n + 1 < NB) els(ex[(n + 1) & 1], n + 1);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int m = 0; m < 2; ++m)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          dv[n] = mfma16f(ex[n & 1][8 * m + 2 * r], p[4 * m + r], dv[n]);
+          dk[n] = mfma16f(ex[n & 1][8 * m + 2 * r + 1], ds[4 * m + r], dk[n]);
+        }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (DS) {
+      if (have_unit) store_chunks(true, ds, u_idx);
+    }
+  };
+
+  int t0, t1;
+  tile_range(a, j, t0, t1);
+  int ti = t0 - 1;
+  uint32_t rem = 0u;
+  auto take = [&](int& t, int& c) -> bool {
+    while (rem == 0u) {
+      if (++ti >= t1) return false;
+      rem = any_rows(tile_groups(a, ti));
+    }
+    t = ti;
+    c = __builtin_ctz(rem);
+    rem &= rem - 1u;
+    return true;
+  };
+  // Rows row0 .. row0 + 31 of Q (plane 0) and dO (plane 1), one padded row per instruction: wave w
+  // copies rows w + 8 m' of both planes with lanes 0-31 (16 bytes each); then, by wave 0, the
+  // group's lse and delta (rows past n read zeros).
+  auto copy = [&](lds_char* buf, int t, int c) {
+    const int row0 = ((ci32_ptr)a.col)[t] * BLK + 32 * c;
+    uint32_t base = (uint32_t)(uintptr_t)buf;
+    asm volatile("" : "+s"(base));
+    if (lane < 32) {
+#pragma unroll
+      for (int m = 0; m < 8; ++m) {
+        const int plane = m >> 2, row = wid + 8 * (m & 3);
+        const uint32_t src = (uint32_t)(row0 + row) * (plane ? osnb : snb) + (uint32_t)(16 * lane);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            plane ? rO : rQ, (__attribute__((address_space(3))) void*)(uintptr_t)(base + (uint32_t)(plane * PB + row * RB)),
+            16, (int)src, 0, 0, 0);
+      }
+    }
+    if (wid == 0) {
+      const int so = lane < 32 ? (row0 + lane) * 4 : (int)kPastEndF;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rL, (__attribute__((address_space(3))) void*)(buf + SB), 4, so, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rD, (__attribute__((address_space(3))) void*)(buf + SB + 256), 4, so, 0,
+                                               0, 0);
+    }
+  };
+  lds_char* b0 = (lds_char*)gb0;
+  lds_char* b1 = (lds_char*)gb1;
+  int tc = 0, cc = 0, tn = 0, cn = 0;
+  bool vc = take(tc, cc), vn = false;
+  uint64_t mwc = 0, mwn = 0;
+  if (vc) {
+    copy(b0, tc, cc);
+    mwc = mword[(int64_t)tc * 256];
+    vn = take(tn, cn);
+  }
+  auto step = [&](lds_char* cur, lds_char* nxt) {
+    wait_vmem();  // this wave's part of the current step (wave 0: the statistics) and its mask word
+    if (wid == 0 && lane < 16) {
+      // lse -> -lse / scale and delta -> -delta: the initial values of the S and dP accumulators.
+      __attribute__((address_space(3))) f32x4* x =
+          (__attribute__((address_space(3))) f32x4*)(cur + SB + (lane < 8 ? 16 * lane : 256 + 16 * (lane - 8)));
+      float mul = lane < 8 ? a.nlse_mul : -1.f;
+      asm volatile("" : "+v"(mul));
+      *x = *x * mul;
+    }
+    __syncthreads();  // the step landed; every wave is done with the previous step's buffer
+    if (vn) {
+      copy(nxt, tn, cn);
+      mwn = tn != tc ? mword[(int64_t)tn * 256] : mwc;
+    }
+    // The wave's 16 keys have a valid element in query group cc.
+    const uint64_t mw = mwc >> mshift;
+    const bool live = __builtin_amdgcn_ballot_w64((((uint32_t)(mw >> (16 * cc))) & 0x0F0Fu) != 0u) != 0u;
+    bool have_unit = false;
+    uint32_t u_idx = 0u;
+    if constexpr (DS) {
+      const uint32_t ub = ((cmap_ptr)a.tmap)[2 * tc];
+      const uint32_t gw = ((cmap_ptr)a.tmap)[2 * tc + 1];
+      const uint32_t bit = 4u * (uint32_t)cc + (uint32_t)(wid >> 1);
+      have_unit = (gw >> bit & 1u) != 0u;
+      u_idx = ub + (uint32_t)__builtin_popcount(gw & 0xffffu & ((1u << bit) - 1u));
+    }
+    if (live) {
+      unit(cc, cur, mw, have_unit, u_idx);
+    } else if (DS && have_unit) {
+      const float z[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      store_chunks(false, z, u_idx);
+    }
+    tc = tn;
+    cc = cn;
+    mwc = mwn;
+    vc = vn;
+    vn = vc && take(tn, cn);
+  };
+  while (vc) {
+    step(b0, b1);
+    if (!vc) break;
+    step(b1, b0);
+  }
+  if (j.part >= 0) {
+    const rsrc_t r = part_slot<D>(a, j);
+    const int prow = 16 * wid + t16;
+#pragma unroll
+    for (int n = 0; n < NB; ++n) {
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, dk[n]), r,
+                                             (int)((uint32_t)(prow * D + 16 * n + 4 * g) * 4), 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, dv[n]), r,
+                                             (int)((uint32_t)((128 + prow) * D + 16 * n + 4 * g) * 4), 0, 0);
+    }
+    return;
+  }
+  const rsrc_t rdk = make_rsrc((float*)a.out0 + j.base, a.slice_bytes);
+  const rsrc_t rdv = make_rsrc((float*)a.out1 + j.base, a.slice_bytes);
+#pragma unroll
+  for (int n = 0; n < NB; ++n) {
+    const uint32_t off = (uint32_t)krow * snb + (uint32_t)(4 * (16 * n + 4 * g));
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, dk[n] * a.scale), rdk, (int)off, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, dv[n]), rdv, (int)off, 0, 0);
+  }
+}
+
+// ------------------------------------------------------------------------------------------
 // delta = rowsum(o * dout) (pallas_attn.py:278): L lanes per (batch, head, row), 16 B per lane.
 
 template <typename T, int D>
@@ -715,8 +1008,14 @@ hipError_t launch_d(Kind kind, const KArgs& a, hipStream_t stream) {
   switch (kind) {
     case Kind::kFwd: hipLaunchKernelGGL(fwd_f32g_kernel<D>, grid, block, 0, stream, a); break;
     case Kind::kDq: hipLaunchKernelGGL(dq_f32_kernel<D>, grid, block, 0, stream, a); break;
-    case Kind::kDkv: hipLaunchKernelGGL((dkv_f32_kernel<D, false>), grid, block, 0, stream, a); break;
-    case Kind::kDkvDs: hipLaunchKernelGGL((dkv_f32_kernel<D, true>), grid, block, 0, stream, a); break;
+    case Kind::kDkv:
+      if constexpr (D == 128) hipLaunchKernelGGL((dkv16_f32_kernel<false>), grid, dim3(512), 0, stream, a);
+      else hipLaunchKernelGGL((dkv_f32_kernel<D, false>), grid, block, 0, stream, a);
+      break;
+    case Kind::kDkvDs:
+      if constexpr (D == 128) hipLaunchKernelGGL((dkv16_f32_kernel<true>), grid, dim3(512), 0, stream, a);
+      else hipLaunchKernelGGL((dkv_f32_kernel<D, true>), grid, block, 0, stream, a);
+      break;
     case Kind::kDqDs: hipLaunchKernelGGL(dq_f32_ds_kernel<D>, grid, block, 0, stream, a); break;
     default: break;
   }

@@ -330,8 +330,8 @@ def test_ds_exchange_matches_recompute_and_oracle(case, d, dtype, monkeypatch):
   """Backward with the dS exchange: the dK/dV kernel writes every unit of dS (32 x 16 in bf16,
   32 x 32 in float32) and the dQ kernel reads it (5 contractions per tile instead of 7). dK and
   dV come from the same kernel arithmetic as without the exchange, bit for bit; dQ differs from
-  the recomputing kernel's only in rounding (S contracted in other MFMA shapes in bf16, delta
-  subtracted at another point in float32) and both meet the bars against the dense float64
+  the recomputing kernel's only in rounding (S contracted in other MFMA shapes and k orders, and
+  in float32 delta subtracted at another point) and both meet the bars against the dense float64
   oracle. Cases: a symmetric mask (one list) with rows and columns without a valid element, a
   non-symmetric mask with its transposed list, split schedules (items of 1 and 3 tiles, so
   partial dQ and dK/dV slots are combined) and the designed group/half patterns
@@ -364,7 +364,9 @@ def test_ds_exchange_matches_recompute_and_oracle(case, d, dtype, monkeypatch):
   got, ref = _run_modes(q, k, v, do, tiles, d ** -0.5, dtype, tiles_t, monkeypatch)
   for name in ("out", "dk", "dv"):
     np.testing.assert_array_equal(got[name], ref[name], err_msg=name)
-  close = 1e-3 if dtype == torch.bfloat16 else 1e-6
+  # float32: two summation orders of S and dP, then dS = P (dP - delta) with its cancellation,
+  # differ by a few units of rounding (about 1e-6 relative rms).
+  close = 1e-3 if dtype == torch.bfloat16 else 3e-6
   assert A.rel_rms(got["dq"], ref["dq"]) < close, A.rel_rms(got["dq"], ref["dq"])
   # Rows and columns cleared in the symmetric case get zero gradients; the oracle runs on the rest.
   keep = np.flatnonzero(m.getnnz(1) > 0)
