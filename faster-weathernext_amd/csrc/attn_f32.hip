@@ -775,8 +775,8 @@ __global__ void __launch_bounds__(512, 1) dkv16_f32_kernel(KArgs a) {
       __builtin_amdgcn_raw_buffer_store_b128(y[h], rS, 16 * (64 * (2 * (wid & 1) + h) + lane), (int)(u * 4096u), 2);
   };
 
-  // Unit: query group c of the group buffer buf (mask word mw of this lane).
-  auto unit = [&](int c, const lds_char* buf, uint64_t mw, bool have_unit, uint32_t u_idx) {
+  // Unit: query group c of the group buffer buf (mask word mw of this lane); dS into ds.
+  auto unit = [&](int c, const lds_char* buf, uint64_t mw, float (&ds)[8]) {
     const lds_char* lq = buf;
     const lds_char* lo = buf + PB;
     f32x4 sa[2], da[2];
@@ -806,7 +806,7 @@ __global__ void __launch_bounds__(512, 1) dkv16_f32_kernel(KArgs a) {
       }
       __builtin_amdgcn_sched_barrier(0);
     }
-    float p[8], ds[8];
+    float p[8];
     const uint32_t w32 = (uint32_t)(mw >> (32 * (c >> 1)));
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -843,9 +843,6 @@ __global__ void __launch_bounds__(512, 1) dkv16_f32_kernel(KArgs a) {
           dk[n] = mfma16f(ex[n & 1][8 * m + 2 * r + 1], ds[4 * m + r], dk[n]);
         }
       __builtin_amdgcn_sched_barrier(0);
-    }
-    if constexpr (DS) {
-      if (have_unit) store_chunks(true, ds, u_idx);
     }
   };
 
@@ -924,11 +921,13 @@ __global__ void __launch_bounds__(512, 1) dkv16_f32_kernel(KArgs a) {
       have_unit = (gw >> bit & 1u) != 0u;
       u_idx = ub + (uint32_t)__builtin_popcount(gw & 0xffffu & ((1u << bit) - 1u));
     }
-    if (live) {
-      unit(cc, cur, mw, have_unit, u_idx);
-    } else if (DS && have_unit) {
-      const float z[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      store_chunks(false, z, u_idx);
+    // One store path after the unit (dS of a unit the map has, zeros where these 16 keys have no
+    // valid element): a store inside the unit's branch, and another beside it, made the register
+    // allocator place dK^T / dV^T differently on each path and copy them (64 VGPRs) every step.
+    float ds[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (live) unit(cc, cur, mw, ds);
+    if constexpr (DS) {
+      if (have_unit) store_chunks(live, ds, u_idx);
     }
     tc = tn;
     cc = cn;

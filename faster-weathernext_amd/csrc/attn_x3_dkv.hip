@@ -160,8 +160,8 @@ __global__ void __launch_bounds__(NT8, 1) dkv16_x3_kernel(KArgs a) {
                                              kNonTemporal);
   };
 
-  // Unit: query group c of the group buffer buf (mask word mw of this lane).
-  auto unit = [&](int c, const lds_char* buf, uint64_t mw, bool have_unit, uint32_t u) {
+  // Unit: query group c of the group buffer buf (mask word mw of this lane); split dS into dh, dl.
+  auto unit = [&](int c, const lds_char* buf, uint64_t mw, u32x4& dh, u32x4& dl) {
     const lds_char* qh = buf;
     const lds_char* oh = buf + 2 * GB;
     f32x4 sa[2], da[2];
@@ -215,7 +215,7 @@ __global__ void __launch_bounds__(NT8, 1) dkv16_x3_kernel(KArgs a) {
       p[e] = pe;
       ds[e] = pe * de;
     }
-    u32x4 ph, pl, dh, dl;
+    u32x4 ph, pl;
     split8(p, ph, pl);
     split8(ds, dh, dl);
 #pragma unroll
@@ -227,7 +227,6 @@ __global__ void __launch_bounds__(NT8, 1) dkv16_x3_kernel(KArgs a) {
       dk[n] = mfma16_x3(x[2], x[3], dh, dl, dk[n]);
       __builtin_amdgcn_sched_barrier(0);
     }
-    if (have_unit) store_chunk(true, dh, dl, u);
   };
 
   int t0, t1;
@@ -289,11 +288,11 @@ __global__ void __launch_bounds__(NT8, 1) dkv16_x3_kernel(KArgs a) {
     const uint32_t bit = 4u * (uint32_t)cc + (uint32_t)(wid >> 1);
     const bool have_unit = (gw >> bit & 1u) != 0u;
     const uint32_t u = ub + (uint32_t)__builtin_popcount(gw & 0xffffu & ((1u << bit) - 1u));
-    if (live) {
-      unit(cc, cur, mw, have_unit, u);
-    } else if (have_unit) {
-      store_chunk(false, u32x4{0u, 0u, 0u, 0u}, u32x4{0u, 0u, 0u, 0u}, u);
-    }
+    // One store path after the unit (a store inside the unit's branch and another beside it made
+    // the register allocator place dK^T / dV^T differently on each path and copy them every step).
+    u32x4 dh = {0u, 0u, 0u, 0u}, dl = {0u, 0u, 0u, 0u};
+    if (live) unit(cc, cur, mw, dh, dl);
+    if (have_unit) store_chunk(live, dh, dl, u);
     tc = tn;
     cc = cn;
     mwc = mwn;
