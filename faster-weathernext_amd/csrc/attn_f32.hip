@@ -775,8 +775,12 @@ __global__ void __launch_bounds__(512, 1) dkv16_f32_kernel(KArgs a) {
       __builtin_amdgcn_raw_buffer_store_b128(y[h], rS, 16 * (64 * (2 * (wid & 1) + h) + lane), (int)(u * 4096u), 2);
   };
 
-  // Unit: query group c of the group buffer buf (mask word mw of this lane); dS into ds.
-  auto unit = [&](int c, const lds_char* buf, uint64_t mw, float (&ds)[8]) {
+  // Unit: query group c of the group buffer buf (mask word mw of this lane); dS into ds. hm is the
+  // set of 16-query halves (bit m: queries 16 m .. 16 m + 15) in which these 16 keys have a valid
+  // element (wave-uniform). A half without one would add exact zeros: its S, dP, dV and dK MFMAs
+  // are skipped by uniform branches and its dS stays zero. The reads are not: one code path keeps
+  // dK^T / dV^T in the same registers whichever halves run.
+  auto unit = [&](int c, const lds_char* buf, uint64_t mw, uint32_t hm, float (&ds)[8]) {
     const lds_char* lq = buf;
     const lds_char* lo = buf + PB;
     f32x4 sa[2], da[2];
@@ -799,10 +803,12 @@ __global__ void __launch_bounds__(512, 1) dkv16_f32_kernel(KArgs a) {
       if (it + 1 < 16) rows(rd[(it + 1) & 1], it + 1);
       __builtin_amdgcn_sched_barrier(0);
       const int u = it >> 1, m = it & 1;
+      if (hm >> m & 1u) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        sa[m] = mfma16f(rd[it & 1][0][e], kf[u][e], sa[m]);
-        da[m] = mfma16f(rd[it & 1][1][e], vf[u][e], da[m]);
+        for (int e = 0; e < 4; ++e) {
+          sa[m] = mfma16f(rd[it & 1][0][e], kf[u][e], sa[m]);
+          da[m] = mfma16f(rd[it & 1][1][e], vf[u][e], da[m]);
+        }
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -812,13 +818,14 @@ __global__ void __launch_bounds__(512, 1) dkv16_f32_kernel(KArgs a) {
     for (int e = 0; e < 8; ++e) {
       const float se = e < 4 ? sa[0][e & 3] : sa[1][e & 3];
       const float de = e < 4 ? da[0][e & 3] : da[1][e & 3];
+      // A skipped half's bits are all clear: p = 0 there, whatever its accumulators hold.
       const float pe = keep_or_zero(fast_exp2(se * a.c2),
                                     __builtin_amdgcn_sbfe(w32, (uint32_t)(16 * (c & 1) + 8 * (e >> 2) + (e & 3)), 1u));
       p[e] = pe;
       ds[e] = pe * de;
     }
     // dV^T and dK^T by 16-column block n; the block's 16 element reads go out before the previous
-    // block's 16 MFMAs.
+    // block's MFMAs.
     auto els = [&](float (&x)[16], int n) {
 #pragma unroll
       for (int m = 0; m < 2; ++m)
@@ -837,10 +844,12 @@ __global__ void __launch_bounds__(512, 1) dkv16_f32_kernel(KArgs a) {
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int m = 0; m < 2; ++m)
+        if (hm >> m & 1u) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          dv[n] = mfma16f(ex[n & 1][8 * m + 2 * r], p[4 * m + r], dv[n]);
-          dk[n] = mfma16f(ex[n & 1][8 * m + 2 * r + 1], ds[4 * m + r], dk[n]);
+          for (int r = 0; r < 4; ++r) {
+            dv[n] = mfma16f(ex[n & 1][8 * m + 2 * r], p[4 * m + r], dv[n]);
+            dk[n] = mfma16f(ex[n & 1][8 * m + 2 * r + 1], ds[4 * m + r], dk[n]);
+          }
         }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -909,9 +918,13 @@ __global__ void __launch_bounds__(512, 1) dkv16_f32_kernel(KArgs a) {
       copy(nxt, tn, cn);
       mwn = tn != tc ? mword[(int64_t)tn * 256] : mwc;
     }
-    // The wave's 16 keys have a valid element in query group cc.
+    // The 16-query halves of group cc in which the wave's 16 keys have a valid element: some
+    // lane's bits 16 cc + 8 m + r (shifted by 4 (g % 2)) are set.
     const uint64_t mw = mwc >> mshift;
-    const bool live = __builtin_amdgcn_ballot_w64((((uint32_t)(mw >> (16 * cc))) & 0x0F0Fu) != 0u) != 0u;
+    const uint32_t b8 = (uint32_t)(mw >> (16 * cc));
+    const bool live0 = __builtin_amdgcn_ballot_w64((b8 & 0x000Fu) != 0u) != 0u;
+    const bool live1 = __builtin_amdgcn_ballot_w64((b8 & 0x0F00u) != 0u) != 0u;
+    const bool live = live0 || live1;
     bool have_unit = false;
     uint32_t u_idx = 0u;
     if constexpr (DS) {
@@ -925,7 +938,7 @@ __global__ void __launch_bounds__(512, 1) dkv16_f32_kernel(KArgs a) {
     // valid element): a store inside the unit's branch, and another beside it, made the register
     // allocator place dK^T / dV^T differently on each path and copy them (64 VGPRs) every step.
     float ds[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    if (live) unit(cc, cur, mw, ds);
+    if (live) unit(cc, cur, mw, (live0 ? 1u : 0u) | (live1 ? 2u : 0u), ds);
     if constexpr (DS) {
       if (have_unit) store_chunks(live, ds, u_idx);
     }
