@@ -177,8 +177,10 @@ __global__ void __launch_bounds__(NT, 2) fwd_f32g_kernel(KArgs a) {
   for (int db = 0; db < D / 32; ++db) o[db] = zero16();
   SoftmaxState st{-__builtin_inff(), 0.f};
 
-  // Key group sb of a tile from group buffer gb.
-  auto group = [&](int sb, const char* gb, u32x2 mb) {
+  // Key group sb of a tile from group buffer gb. hv: the group's 16-key halves with a valid
+  // element for this wave (bit h: keys 16 h .. 16 h + 15, registers 8 h .. 8 h + 7 of S); a clear
+  // half has p = 0 throughout and skips its PV MFMAs.
+  auto group = [&](int sb, const char* gb, u32x2 mb, uint32_t hv) {
     const char* ldsK = gb;
     const char* ldsV = gb + GB;
     f32x16 s[1];
@@ -197,11 +199,15 @@ __global__ void __launch_bounds__(NT, 2) fwd_f32g_kernel(KArgs a) {
       for (int db = 0; db < D / 32; ++db) o[db] *= corr;
     }
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
+    for (int h = 0; h < 2; ++h)
+      if (hv >> h & 1u) {
 #pragma unroll
-      for (int db = 0; db < D / 32; ++db)
-        o[db] = mfma_f32(*(const float*)(ldsV + off.el_plain + off.el_imm(0, r, db)), s[0][r], o[db]);
-    }
+        for (int r = 8 * h; r < 8 * h + 8; ++r) {
+#pragma unroll
+          for (int db = 0; db < D / 32; ++db)
+            o[db] = mfma_f32(*(const float*)(ldsV + off.el_plain + off.el_imm(0, r, db)), s[0][r], o[db]);
+        }
+      }
   };
 
   int t0, t1;
@@ -241,7 +247,7 @@ __global__ void __launch_bounds__(NT, 2) fwd_f32g_kernel(KArgs a) {
       mbn = tn != tc ? tile_bits(a, tn, w, lane) : mbc;
     }
     const uint32_t live = tile_groups(a, tc) >> (4 * w) & 15u;
-    if (live >> cc & 1u) group(cc, cur, mbc);
+    if (live >> cc & 1u) group(cc, cur, mbc, tile_halves(a, tc) >> (8 * w + 2 * cc) & 3u);
     tc = tn;
     cc = cn;
     mbc = mbn;
@@ -428,19 +434,29 @@ __global__ void __launch_bounds__(NT, 2) dq_f32_ds_kernel(KArgs a) {
         ++u;
       }
   };
-  // Key group sl of the half buffer ldsK, with its unit d.
-  auto group = [&](int sl, const char* ldsK, const f32x4 (&d)[4]) {
-    float kt[16][D / 32];
+  // Key group sl of the half buffer ldsK, with its unit d. hv: the group's 16-key halves with a
+  // valid element for this wave (bit h: registers 8 h .. 8 h + 7 of the unit); a clear half has
+  // dS = 0 and skips its reads and MFMAs.
+  auto group = [&](int sl, const char* ldsK, const f32x4 (&d)[4], uint32_t hv) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r)
+    for (int h = 0; h < 2; ++h)
+      if (hv >> h & 1u) {
+        float kt[8][D / 32];
 #pragma unroll
-      for (int db = 0; db < D / 32; ++db) kt[r][db] = *(const float*)(ldsK + off.el[r & 3] + off.el_imm(sl, r, db));
+        for (int x = 0; x < 8; ++x)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
+          for (int db = 0; db < D / 32; ++db) {
+            const int r = 8 * h + x;
+            kt[x][db] = *(const float*)(ldsK + off.el[r & 3] + off.el_imm(sl, r, db));
+          }
 #pragma unroll
-      for (int db = 0; db < D / 32; ++db) acc[db] = mfma_f32(kt[r][db], d[r >> 2][r & 3], acc[db]);
-    }
-    sched_reads_ahead<16, D / 32, D / 32>();
+        for (int x = 0; x < 8; ++x) {
+          const int r = 8 * h + x;
+#pragma unroll
+          for (int db = 0; db < D / 32; ++db) acc[db] = mfma_f32(kt[x][db], d[r >> 2][r & 3], acc[db]);
+        }
+        sched_reads_ahead<8, D / 32, D / 32>();
+      }
   };
 
   int t0, t1;
@@ -458,6 +474,7 @@ __global__ void __launch_bounds__(NT, 2) dq_f32_ds_kernel(KArgs a) {
     const int kb = ((ci32_ptr)a.col)[t];
     const uint32_t gt = gcur, ut = ucur;
     const uint32_t live = gt >> (4 * w) & 15u;
+    const uint32_t hw = tile_halves(a, t) >> (8 * w) & 0xffu;  // bit 2 sb + h: live 16-key halves
     wait_vmem();      // this wave's part of half 0 of tile t and its units
     __syncthreads();  // half 0 landed; every wave is done with half 1 of tile t - 1
     dma.issue(rK, h1, kb * BLK, snb, w, 1, any_rows(gt));
@@ -467,9 +484,9 @@ __global__ void __launch_bounds__(NT, 2) dq_f32_ds_kernel(KArgs a) {
       ucur = (uint32_t)((cmap_ptr)a.ubase)[t + 1];
     }
     __builtin_amdgcn_sched_barrier(0);
-    if (live & 1u) group(0, h0, dsA[0]);
+    if (live & 1u) group(0, h0, dsA[0], hw & 3u);
     __builtin_amdgcn_sched_barrier(0);
-    if (live & 2u) group(1, h0, dsA[1]);
+    if (live & 2u) group(1, h0, dsA[1], hw >> 2 & 3u);
     __builtin_amdgcn_sched_barrier(0);
     wait_vmem();      // this wave's part of half 1 and its units
     __syncthreads();  // half 1 landed; every wave is done with half 0
@@ -478,9 +495,9 @@ __global__ void __launch_bounds__(NT, 2) dq_f32_ds_kernel(KArgs a) {
       load_units(dsA, gcur, ucur, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
-    if (live & 4u) group(0, h1, dsB[0]);
+    if (live & 4u) group(0, h1, dsB[0], hw >> 4 & 3u);
     __builtin_amdgcn_sched_barrier(0);
-    if (live & 8u) group(1, h1, dsB[1]);
+    if (live & 8u) group(1, h1, dsB[1], hw >> 6 & 3u);
     __builtin_amdgcn_sched_barrier(0);
   }
   if (j.part >= 0) {
