@@ -128,9 +128,10 @@ def test_matches_dense_reference(batch, dtype):
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("symmetric", [True, False])
 @pytest.mark.parametrize("batch", [1, 2])
-def test_grads_match_dense_reference(batch, symmetric, dtype):
+@pytest.mark.parametrize("d", [64, 128])
+def test_grads_match_dense_reference(d, batch, symmetric, dtype):
   rng = np.random.default_rng(2)
-  n, h, d = 300, 2, 64
+  n, h = 300, 2
   q, k, v, do = (_rounded(rng.standard_normal((batch, n, h, d)), dtype) for _ in range(4))
   m = _random_mask(n, 0.08, 3, symmetric=symmetric)
   tiles = fwn.TileList.from_mask(m)
@@ -508,12 +509,13 @@ def test_split_workspace_is_reused_across_calls():
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_packed_qkv_op_is_bitwise_the_unpacked_op(dtype):
+@pytest.mark.parametrize("d", [64, 128])
+def test_packed_qkv_op_is_bitwise_the_unpacked_op(d, dtype):
   """tiled_flash_attention_qkv reads q, k, v as views of one [B, n, 3, H, D] buffer and writes
   one packed gradient; the kernels see the same values, so outputs and gradients match the
   separate-tensor op bit for bit, and both match the dense oracle."""
   rng = np.random.default_rng(50)
-  b, n, h, d = 2, 500, 2, 64
+  b, n, h = 2, 500, 2
   qkv_h = _rounded(rng.standard_normal((b, n, 3, h, d)), dtype)
   do_h = _rounded(rng.standard_normal((b, n, h, d)), dtype)
   m = _random_mask(n, 0.04, 51, symmetric=True)
