@@ -121,10 +121,11 @@ struct Job {
 // (batch, head) major, then work items in block order, and XCD x gets a contiguous range of
 // them, so the workgroups resident on one XCD work on neighbouring blocks of one head and share
 // their K/V tiles in that XCD's L2. The map from workgroup id to job is a bijection for any count.
-__device__ __forceinline__ Job decode_job(const KArgs& a) {
+__device__ __forceinline__ Job decode_job(const KArgs& a, int pid = -1) {
   Job j;
   const int total = a.n_items * a.batch * a.heads;
-  const int pid = blockIdx.x, xcd = pid & 7, local = pid >> 3;
+  if (pid < 0) pid = blockIdx.x;
+  const int xcd = pid & 7, local = pid >> 3;
   const int small = total >> 3, rem = total & 7;
   const int job = xcd < rem ? xcd * (small + 1) + local : rem * (small + 1) + (xcd - rem) * small + local;
   j.bh = job / a.n_items;

@@ -687,9 +687,12 @@ __global__ void __launch_bounds__(NT, 1) dkv_f32_kernel(KArgs a) {
 }
 
 // ------------------------------------------------------------------------------------------
-// dK/dV, fp32, head_dim 128, 16 keys per wave (V_MFMA_F32_16X16X4F32), 8 waves, one workgroup per
-// CU: a wave's K and V rows (64 registers) and dK^T, dV^T (64) leave room for a second wave per
-// SIMD, twice dkv_f32_kernel's waves per CU.
+// dK/dV, fp32, head_dim 128, 16 keys per wave (V_MFMA_F32_16X16X4F32): a wave's K and V rows (64
+// registers) and dK^T, dV^T (64) leave room for a second wave per SIMD, twice dkv_f32_kernel's
+// waves per CU. Each work item's 128 keys are split between two 4-wave workgroups of 64 keys (78
+// KB of LDS each), two per CU: each streams only the query groups its own keys need, and the two
+// meet at barriers of their own, so one's waiting waves leave their SIMDs to the other's. The two
+// halves of an item sit on the same XCD and share its L2 for the Q and dO groups both read.
 //
 // The k order of the first contractions is permuted so that each lane's fragment is contiguous:
 // k-step s of lane group g (= lane / 16) contracts column 32 g + s, so lane (key l % 16, g) holds
@@ -706,8 +709,9 @@ __global__ void __launch_bounds__(NT, 1) dkv_f32_kernel(KArgs a) {
 // modulo the 256-byte bank line), and the 64 lanes of an element read cover rows 4 g + r at 16
 // columns (64 g bytes apart). A padded row is one LDS DMA instruction of 32 lanes.
 //
-// dS (DS): the float32 exchange's 4 KB units, written by the two waves of a 32-key group: wave w
-// writes dQ registers 8 (w % 2) .. + 7 of every dQ lane (chunks 2 (w % 2) and 2 (w % 2) + 1)
+// dS (DS): the float32 exchange's 4 KB units, written by the two waves of a 32-key group: the wave
+// of 16-key group kg writes dQ registers 8 (kg % 2) .. + 7 of every dQ lane (chunks 2 (kg % 2) and
+// 2 (kg % 2) + 1)
 // through its own LDS stage ([query][16 keys] fp32, 80-byte rows: conflict-free both ways). A wave
 // whose 16 keys have no valid element in a unit the map has writes zeros for its chunks.
 constexpr int kRowPad = 4 * 128 + 16;  // padded LDS row of a head_dim 128 fp32 tile
@@ -718,7 +722,7 @@ __device__ __forceinline__ f32x4 mfma16f(float a, float b, const f32x4& c) {
 }
 
 template <bool DS>
-__global__ void __launch_bounds__(512, 1) dkv16_f32_kernel(KArgs a) {
+__global__ void __launch_bounds__(256, 2) dkv16_f32_kernel(KArgs a) {
   constexpr int D = 128;
   constexpr int RB = kRowPad;
   constexpr int PB = 32 * RB;  // one plane: 32 padded rows
@@ -727,7 +731,7 @@ __global__ void __launch_bounds__(512, 1) dkv16_f32_kernel(KArgs a) {
   constexpr int SROW = 80;
   __shared__ __attribute__((aligned(1024))) char gb0[SB + 512];
   __shared__ __attribute__((aligned(1024))) char gb1[SB + 512];
-  __shared__ __attribute__((aligned(16))) char stage[DS ? 8 * 32 * SROW : 16];
+  __shared__ __attribute__((aligned(16))) char stage[DS ? 4 * 32 * SROW : 16];
   typedef const __attribute__((address_space(3))) f32x4* cf4;
   // Element reads are volatile so that the compiler does not pair them into ds_read2_b32 (rows r
   // and r + 1, or column blocks n and n + 1): with single reads the kernel measured 6% faster.
@@ -736,7 +740,13 @@ __global__ void __launch_bounds__(512, 1) dkv16_f32_kernel(KArgs a) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, t16 = lane & 15;
-  const Job j = decode_job(a);
+  // Two workgroups per work item, one per 64-key half of the block, on the same XCD (workgroup
+  // ids 16 i + x and 16 i + 8 + x): pid = 8 i + x is the item's id as decode_job numbers them.
+  const int half = (int)(blockIdx.x >> 3) & 1;
+  const int pid = (int)(((blockIdx.x >> 4) << 3) | (blockIdx.x & 7));
+  if (pid >= a.n_items * a.batch * a.heads) return;
+  const Job j = decode_job(a, pid);
+  const int kg = 4 * half + wid;  // this wave's 16-key group of the block
   const uint32_t snb = (uint32_t)a.sn * 4, osnb = (uint32_t)a.osn * 4;
   const rsrc_t rQ = make_rsrc((const float*)a.q + j.base, a.slice_bytes);
   const rsrc_t rO = make_rsrc((const float*)a.dout + j.obase, a.oslice_bytes);
@@ -744,7 +754,7 @@ __global__ void __launch_bounds__(512, 1) dkv16_f32_kernel(KArgs a) {
   const rsrc_t rD = make_rsrc(a.delta + stat_index(a, j, 0), (uint32_t)a.n * 4);
   const rsrc_t rS = make_rsrc(DS ? (const void*)(a.ds + (int64_t)j.bh * (a.ds_slice_bytes >> 1)) : (const void*)a.q,
                               DS ? a.ds_slice_bytes : 0u);
-  const int krow = j.blk * BLK + 16 * wid + t16;
+  const int krow = j.blk * BLK + 16 * kg + t16;
   // K and V of this lane's key: kf[u][e] = column 32 g + 4 u + e (k-step 4 u + e).
   f32x4 kf[8], vf[8];
   {
@@ -767,7 +777,7 @@ __global__ void __launch_bounds__(512, 1) dkv16_f32_kernel(KArgs a) {
     dk[n] = f32x4{0.f, 0.f, 0.f, 0.f};
     dv[n] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
-  const uint64_t* mword = key_mask_words(a, wid, g, t16);
+  const uint64_t* mword = key_mask_words(a, kg, g, t16);
   const int mshift = 4 * (g & 1);
   lds_char* stw = (lds_char*)stage + wid * 32 * SROW;
 
@@ -878,7 +888,9 @@ __global__ void __launch_bounds__(512, 1) dkv16_f32_kernel(KArgs a) {
   auto take = [&](int& t, int& c) -> bool {
     while (rem == 0u) {
       if (++ti >= t1) return false;
-      rem = any_rows(tile_groups(a, ti));
+      // query groups with a valid element for this half's keys (32-key groups 2 half, 2 half + 1)
+      const uint32_t tg = tile_groups(a, ti) >> (8 * half);
+      rem = (tg | tg >> 4) & 15u;
     }
     t = ti;
     c = __builtin_ctz(rem);
@@ -886,7 +898,7 @@ __global__ void __launch_bounds__(512, 1) dkv16_f32_kernel(KArgs a) {
     return true;
   };
   // Rows row0 .. row0 + 31 of Q (plane 0) and dO (plane 1), one padded row per instruction: wave w
-  // copies rows w + 8 m' of both planes with lanes 0-31 (16 bytes each); then, by wave 0, the
+  // copies rows w + 4 m' of both planes with lanes 0-31 (16 bytes each); then, by wave 0, the
   // group's lse and delta (rows past n read zeros).
   auto copy = [&](lds_char* buf, int t, int c) {
     const int row0 = ((ci32_ptr)a.col)[t] * BLK + 32 * c;
@@ -894,8 +906,8 @@ __global__ void __launch_bounds__(512, 1) dkv16_f32_kernel(KArgs a) {
     asm volatile("" : "+s"(base));
     if (lane < 32) {
 #pragma unroll
-      for (int m = 0; m < 8; ++m) {
-        const int plane = m >> 2, row = wid + 8 * (m & 3);
+      for (int m = 0; m < 16; ++m) {
+        const int plane = m >> 3, row = wid + 4 * (m & 7);
         const uint32_t src = (uint32_t)(row0 + row) * (plane ? osnb : snb) + (uint32_t)(16 * lane);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
             plane ? rO : rQ, (__attribute__((address_space(3))) void*)(uintptr_t)(base + (uint32_t)(plane * PB + row * RB)),
@@ -946,7 +958,7 @@ __global__ void __launch_bounds__(512, 1) dkv16_f32_kernel(KArgs a) {
     if constexpr (DS) {
       const uint32_t ub = ((cmap_ptr)a.tmap)[2 * tc];
       const uint32_t gw = ((cmap_ptr)a.tmap)[2 * tc + 1];
-      const uint32_t bit = 4u * (uint32_t)cc + (uint32_t)(wid >> 1);
+      const uint32_t bit = 4u * (uint32_t)cc + (uint32_t)(kg >> 1);
       have_unit = (gw >> bit & 1u) != 0u;
       u_idx = ub + (uint32_t)__builtin_popcount(gw & 0xffffu & ((1u << bit) - 1u));
     }
@@ -971,7 +983,7 @@ __global__ void __launch_bounds__(512, 1) dkv16_f32_kernel(KArgs a) {
   }
   if (j.part >= 0) {
     const rsrc_t r = part_slot<D>(a, j);
-    const int prow = 16 * wid + t16;
+    const int prow = 16 * kg + t16;
 #pragma unroll
     for (int n = 0; n < NB; ++n) {
       __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, dk[n]), r,
@@ -1036,15 +1048,17 @@ hipError_t launch_d(Kind kind, const KArgs& a, hipStream_t stream) {
     return hipGetLastError();
   }
   const dim3 grid((unsigned)a.n_items * (unsigned)(a.batch * a.heads));
+  // dkv16_f32_kernel: two workgroups per item, laid out in blocks of 16 ids (8 items x 2 halves).
+  const dim3 grid2(16u * (((unsigned)a.n_items * (unsigned)(a.batch * a.heads) + 7u) / 8u));
   switch (kind) {
     case Kind::kFwd: hipLaunchKernelGGL(fwd_f32g_kernel<D>, grid, block, 0, stream, a); break;
     case Kind::kDq: hipLaunchKernelGGL(dq_f32_kernel<D>, grid, block, 0, stream, a); break;
     case Kind::kDkv:
-      if constexpr (D == 128) hipLaunchKernelGGL((dkv16_f32_kernel<false>), grid, dim3(512), 0, stream, a);
+      if constexpr (D == 128) hipLaunchKernelGGL((dkv16_f32_kernel<false>), grid2, dim3(256), 0, stream, a);
       else hipLaunchKernelGGL((dkv_f32_kernel<D, false>), grid, block, 0, stream, a);
       break;
     case Kind::kDkvDs:
-      if constexpr (D == 128) hipLaunchKernelGGL((dkv16_f32_kernel<true>), grid, dim3(512), 0, stream, a);
+      if constexpr (D == 128) hipLaunchKernelGGL((dkv16_f32_kernel<true>), grid2, dim3(256), 0, stream, a);
       else hipLaunchKernelGGL((dkv_f32_kernel<D, true>), grid, block, 0, stream, a);
       break;
     case Kind::kDqDs: hipLaunchKernelGGL(dq_f32_ds_kernel<D>, grid, block, 0, stream, a); break;
