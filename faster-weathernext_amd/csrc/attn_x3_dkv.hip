@@ -10,7 +10,7 @@ namespace {
 
 using namespace dev;
 
-constexpr int NT8 = 512;  // 8 waves
+constexpr int NT4 = 256;  // 4 waves
 
 // 16x16x32 bf16 MFMA and its three-part product (cross terms first, then hi * hi).
 __device__ __forceinline__ f32x4 mfma16(const u32x4& a, const u32x4& b, const f32x4& c) {
@@ -25,11 +25,11 @@ __device__ __forceinline__ f32x4 mfma16_x3(const u32x4& ah, const u32x4& al, con
   return mfma16(ah, bh, c);
 }
 
-// X3Dma for 8 waves and the 16-key kernel's tile swizzle (swz16): instruction k = w + 8 m of the
+// X3Dma for NW waves and the 16-key kernel's tile swizzle (swz16): instruction k = w + NW m of the
 // 4 NI of a step fills rows RPO (k % NI) .. of plane k / NI. The swizzle depends on row % 8, the
-// same for every instruction of one wave.
-template <int D>
-struct X3Dma8 {
+// same for every instruction of one wave (RPO NW is a multiple of 8).
+template <int D, int NW>
+struct X3DmaW {
   static constexpr int C = D / 8;
   static constexpr int RPO = 1024 / (2 * D);
   static constexpr int NI = 32 / RPO;
@@ -46,8 +46,8 @@ struct X3Dma8 {
     uint32_t base = (uint32_t)(uintptr_t)buf;
     asm volatile("" : "+s"(base));
 #pragma unroll
-    for (int m = 0; m < NI / 2; ++m) {
-      const int k = w + 8 * m, plane = k / NI, sub = k % NI;
+    for (int m = 0; m < 4 * NI / NW; ++m) {
+      const int k = w + NW * m, plane = k / NI, sub = k % NI;
       const uint32_t src = (uint32_t)(row0 + RPO * sub) * XROW + voff + (uint32_t)(plane & 1) * (2 * D);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           plane < 2 ? rA : rB,
@@ -57,23 +57,28 @@ struct X3Dma8 {
   }
 };
 
-// dK/dV, float32 tensors, bf16x3 products, the dS exchange, 16 keys per wave: 8 waves, one
-// workgroup per CU, two waves per SIMD. Wave w owns keys 16 w .. + 15 of the key block and keeps
-// their K and V rows split in registers (64) and dK^T, dV^T (64); lane l holds key l % 16 and
-// queries 4 g + r, 16 + 4 g + r (g = l / 16, r < 4) of a 32-query group, as the bf16 16-key
-// kernel. Steps are the transposed list's (tile, query group) pairs, streamed through two group
-// buffers (Q hi, Q lo, dO hi, dO lo planes, swizzled by swz16, plus the group's statistics).
+// dK/dV, float32 tensors, bf16x3 products, the dS exchange, 16 keys per wave, two waves per SIMD.
+// Each work item's 128 keys are split between two 4-wave workgroups of 64 keys (75 KB of LDS
+// each), two per CU on the same XCD, each streaming only the query groups its own keys need and
+// meeting at barriers of its own. The wave of 16-key group kg owns keys 16 kg .. + 15 of the key
+// block and keeps their K and V rows split in registers (64) and dK^T, dV^T (64); lane l holds
+// key l % 16 and queries 4 g + r, 16 + 4 g + r (g = l / 16, r < 4) of a 32-query group, as the
+// bf16 16-key kernel. Steps are the transposed list's (tile, query group) pairs, streamed through
+// two group buffers (Q hi, Q lo, dO hi, dO lo planes, swizzled by swz16, plus the group's
+// statistics).
 // A unit (16 keys x 32 queries) streams its operand reads one MFMA step ahead: the four row reads
 // of (k-step, query half) before the previous pair's six MFMAs, the four transpose reads of a
 // 16-column block before the previous block's six.
 //
-// dS: a 32 x 32 unit of the float32 exchange belongs to the two waves of its 32-key group; wave w
-// writes 16-key chunk w % 2 of both planes (chunk 64 (2 p + w % 2) + L for dQ lane L), through a
-// per-wave LDS stage ([plane][query][16 keys] bf16, 32-byte rows: conflict-free 16-byte reads).
-// A wave whose 16 keys have no valid element in a unit the map has writes zeros for its chunk.
+// dS: a 32 x 32 unit of the float32 exchange belongs to the two waves of its 32-key group; the wave
+// of group kg writes 16-key chunk kg % 2 of both planes (chunk 64 (2 p + kg % 2) + L for dQ lane
+// L), through a per-wave LDS stage ([plane][query][16 keys] bf16, 32-byte rows: conflict-free
+// 16-byte reads). A wave whose 16 keys have no valid element in a unit the map has writes zeros
+// for its chunk.
 template <int D>
-__global__ void __launch_bounds__(NT8, 1) dkv16_x3_kernel(KArgs a) {
-  constexpr int GB = X3Dma8<D>::GB;
+__global__ void __launch_bounds__(NT4, 2) dkv16_x3_kernel(KArgs a) {
+  using Dma = X3DmaW<D, 4>;
+  constexpr int GB = Dma::GB;
   constexpr int SB = 4 * GB;  // Q hi | Q lo | dO hi | dO lo | -lse/scale [32], 0 [32] | -delta [32], 0 [32]
   constexpr int KS = D / 32;  // k-steps of S and dP
   constexpr int NB = D / 16;  // 16-column blocks of dK^T and dV^T
@@ -81,11 +86,17 @@ __global__ void __launch_bounds__(NT8, 1) dkv16_x3_kernel(KArgs a) {
   constexpr int C = D / 8;
   __shared__ __attribute__((aligned(1024))) char gb0[SB + 512];
   __shared__ __attribute__((aligned(1024))) char gb1[SB + 512];
-  __shared__ __attribute__((aligned(16))) char stage[8 * 2048];
+  __shared__ __attribute__((aligned(16))) char stage[4 * 2048];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, t16 = lane & 15;
-  const Job j = decode_job(a);
+  // Two workgroups per work item, one per 64-key half of the block, on the same XCD (workgroup
+  // ids 16 i + x and 16 i + 8 + x): pid = 8 i + x is the item's id as decode_job numbers them.
+  const int half = (int)(blockIdx.x >> 3) & 1;
+  const int pid = (int)(((blockIdx.x >> 4) << 3) | (blockIdx.x & 7));
+  if (pid >= a.n_items * a.batch * a.heads) return;
+  const Job j = decode_job(a, pid);
+  const int kg = 4 * half + wid;  // this wave's 16-key group of the block
   const int64_t xbase = (int64_t)j.bh * a.n * (2 * D);
   const rsrc_t rQ = make_rsrc(a.xa + xbase, a.xslice_bytes);
   const rsrc_t rO = make_rsrc(a.xb + xbase, a.xslice_bytes);
@@ -93,7 +104,7 @@ __global__ void __launch_bounds__(NT8, 1) dkv16_x3_kernel(KArgs a) {
   const rsrc_t rD = make_rsrc(a.delta + stat_index(a, j, 0), (uint32_t)a.n * 4);
   const rsrc_t rS = make_rsrc(a.ds + (int64_t)j.bh * (a.ds_slice_bytes >> 1), a.ds_slice_bytes);
   const uint32_t snb = (uint32_t)a.sn * 4;
-  const int krow = j.blk * BLK + 16 * wid + t16;
+  const int krow = j.blk * BLK + 16 * kg + t16;
   // K and V rows of this lane's key, columns 32 s + 8 g .. + 7, split.
   u32x4 kh[KS], kl[KS], vh[KS], vl[KS];
   {
@@ -119,7 +130,7 @@ __global__ void __launch_bounds__(NT8, 1) dkv16_x3_kernel(KArgs a) {
   const uint32_t tbase = (uint32_t)(trow * RS + (tq & 1) * 8);
   auto roff = [&](int s) { return rbase + (uint32_t)(((4 * s + g) ^ sr) << 4); };
   auto toff = [&](int n) { return tbase + (uint32_t)(((2 * n + (tq >> 1)) ^ tsw) << 4); };
-  X3Dma8<D> dma;
+  Dma dma;
   dma.init(wid, lane);
   f32x4 dk[NB], dv[NB];
 #pragma unroll
@@ -129,7 +140,7 @@ __global__ void __launch_bounds__(NT8, 1) dkv16_x3_kernel(KArgs a) {
   }
   typedef const __attribute__((address_space(4))) uint32_t* cmap_ptr;
   typedef const __attribute__((address_space(3))) f32x4* cf4;
-  const uint64_t* mword = key_mask_words(a, wid, g, t16);
+  const uint64_t* mword = key_mask_words(a, kg, g, t16);
   const int mshift = 4 * (g & 1);
   __attribute__((address_space(3))) char* stw = (__attribute__((address_space(3))) char*)stage + wid * 2048;
 
@@ -236,7 +247,9 @@ __global__ void __launch_bounds__(NT8, 1) dkv16_x3_kernel(KArgs a) {
   auto take = [&](int& t, int& c) -> bool {
     while (rem == 0u) {
       if (++ti >= t1) return false;
-      rem = any_rows(tile_groups(a, ti));
+      // query groups with a valid element for this half's keys (32-key groups 2 half, 2 half + 1)
+      const uint32_t tg = tile_groups(a, ti) >> (8 * half);
+      rem = (tg | tg >> 4) & 15u;
     }
     t = ti;
     c = __builtin_ctz(rem);
@@ -285,7 +298,7 @@ __global__ void __launch_bounds__(NT8, 1) dkv16_x3_kernel(KArgs a) {
     const bool live = __builtin_amdgcn_ballot_w64((((uint32_t)(mw >> (16 * cc))) & 0x0F0Fu) != 0u) != 0u;
     const uint32_t ub = ((cmap_ptr)a.tmap)[2 * tc];
     const uint32_t gw = ((cmap_ptr)a.tmap)[2 * tc + 1];
-    const uint32_t bit = 4u * (uint32_t)cc + (uint32_t)(wid >> 1);
+    const uint32_t bit = 4u * (uint32_t)cc + (uint32_t)(kg >> 1);
     const bool have_unit = (gw >> bit & 1u) != 0u;
     const uint32_t u = ub + (uint32_t)__builtin_popcount(gw & 0xffffu & ((1u << bit) - 1u));
     // One store path after the unit (a store inside the unit's branch and another beside it made
@@ -306,7 +319,7 @@ __global__ void __launch_bounds__(NT8, 1) dkv16_x3_kernel(KArgs a) {
   }
   if (j.part >= 0) {
     const rsrc_t r = part_slot<D>(a, j);
-    const int prow = 16 * wid + t16;
+    const int prow = 16 * kg + t16;
 #pragma unroll
     for (int n = 0; n < NB; ++n) {
       __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, dk[n]), r,
@@ -328,8 +341,9 @@ __global__ void __launch_bounds__(NT8, 1) dkv16_x3_kernel(KArgs a) {
 
 template <int D>
 hipError_t launch_d(const KArgs& a, hipStream_t stream) {
-  const dim3 grid((unsigned)a.n_items * (unsigned)(a.batch * a.heads));
-  hipLaunchKernelGGL((dkv16_x3_kernel<D>), grid, dim3(NT8), 0, stream, a);
+  // Two workgroups per item, laid out in blocks of 16 ids (8 items x 2 halves).
+  const dim3 grid(16u * (((unsigned)a.n_items * (unsigned)(a.batch * a.heads) + 7u) / 8u));
+  hipLaunchKernelGGL((dkv16_x3_kernel<D>), grid, dim3(NT4), 0, stream, a);
   return hipGetLastError();
 }
 
