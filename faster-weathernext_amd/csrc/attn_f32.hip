@@ -704,16 +704,15 @@ __global__ void __launch_bounds__(NT, 1) dkv_f32_kernel(KArgs a) {
 //
 // Tiles: the transposed list's (tile, query group) steps stream the group's Q and dO rows and its
 // statistics through two group buffers. Rows are padded to 528 bytes (16 bytes over a row), so
-// both read patterns are conflict-free without a swizzle and every LDS address is a per-lane base
-// plus an immediate: 16 lanes of a row read cover rows t .. t + 15 at one column (16 t bytes apart
-// modulo the 256-byte bank line), and the 64 lanes of an element read cover rows 4 g + r at 16
-// columns (64 g bytes apart). A padded row is one LDS DMA instruction of 32 lanes.
+// every LDS address is a per-lane base plus an immediate and both read patterns spread over the
+// banks without a swizzle: 16 lanes of a row read cover rows t .. t + 15 at one column (16 t bytes
+// apart modulo the 256-byte bank line), and the 64 lanes of an element read cover rows 4 g + r at
+// 16 columns (64 g bytes apart). A padded row is one LDS DMA instruction of 32 lanes.
 //
 // dS (DS): the float32 exchange's 4 KB units, written by the two waves of a 32-key group: the wave
 // of 16-key group kg writes dQ registers 8 (kg % 2) .. + 7 of every dQ lane (chunks 2 (kg % 2) and
-// 2 (kg % 2) + 1)
-// through its own LDS stage ([query][16 keys] fp32, 80-byte rows: conflict-free both ways). A wave
-// whose 16 keys have no valid element in a unit the map has writes zeros for its chunks.
+// 2 (kg % 2) + 1) through its own LDS stage ([query][16 keys] fp32, 80-byte rows). A wave whose
+// 16 keys have no valid element in a unit the map has writes zeros for its chunks.
 constexpr int kRowPad = 4 * 128 + 16;  // padded LDS row of a head_dim 128 fp32 tile
 constexpr uint32_t kPastEndF = 0x7FFFFFF0u;  // a buffer offset past every slice: reads zeros
 
