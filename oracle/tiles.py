@@ -50,14 +50,22 @@ def hilbert3(ints, bits):
   return code
 
 
-def hilbert_order(lat_deg, lon_deg, bits=10):
-  """Permutation sorting points on the sphere along a 3-D Hilbert curve, non-finite points last."""
+def quantise_sphere(lat_deg, lon_deg, bits=10):
+  """(ints int64[n, 3], finite bool[n]): unit xyz of each point (x towards lat 0 / lon 0, y towards
+  lon 90, z towards the north pole) mapped from [-1, 1] to [0, 2**bits - 1], rounded half to even
+  (``pallas_attn.py:75-78``)."""
   lat = np.deg2rad(np.asarray(lat_deg, np.float64).ravel())
   lon = np.deg2rad(np.asarray(lon_deg, np.float64).ravel())
   xyz = np.stack([np.cos(lat) * np.cos(lon), np.cos(lat) * np.sin(lon), np.sin(lat)], -1)
   finite = np.isfinite(xyz).all(-1)
   top = 2 ** bits - 1
   ints = np.clip(np.round((np.nan_to_num(xyz) + 1.0) / 2.0 * top), 0, top).astype(np.int64)
+  return ints, finite
+
+
+def hilbert_order(lat_deg, lon_deg, bits=10):
+  """Permutation sorting points on the sphere along a 3-D Hilbert curve, non-finite points last."""
+  ints, finite = quantise_sphere(lat_deg, lon_deg, bits)
   code = np.where(finite, hilbert3(ints, bits), np.iinfo(np.int64).max)
   return np.argsort(code, kind="stable")
 

@@ -9,6 +9,7 @@ import numpy as np
 import pytest
 from scipy import sparse
 
+import hilbert_cases as HC
 from oracle import attention as A
 from oracle import mesh, rows, tiles
 
@@ -210,6 +211,50 @@ def test_hilbert3_is_a_hilbert_curve(bits):
   path = cells[np.argsort(code)]
   assert (np.abs(np.diff(path, axis=0)).sum(1) == 1).all()     # unit steps along the curve
   assert (path[0] == 0).all()                                  # starts at the origin
+
+
+@pytest.mark.parametrize("bits", [1, 2, 3, 4])
+def test_hilbert3_inverts_skillings_transpose_to_axes(bits):
+  # The paper's other routine (index -> axes), written independently in hilbert_cases: every index
+  # must come back, so hilbert3 is exactly Skilling's AxestoTranspose with axis 0 leading.
+  h = np.arange(8 ** bits)
+  cells = HC.skilling_transpose_to_axes(h, bits)
+  np.testing.assert_array_equal(tiles.hilbert3(cells, bits), h)
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_hilbert_order_octant_centres_follow_gray_code(seed):
+  lat, lon, want = HC.octant_case(seed)
+  np.testing.assert_array_equal(tiles.hilbert_order(lat, lon), want)
+
+
+def _planted_order(lat, lon, axes=(0, 1, 2), signs=(1, 1, 1)):
+  """The oracle's order with a planted slip: xyz axes permuted and / or negated."""
+  lat, lon = np.asarray(lat, np.float64), np.asarray(lon, np.float64)
+  ints, _ = tiles.quantise_sphere(lat, lon)
+  ints = ints[:, list(axes)]
+  for a, s in enumerate(signs):
+    if s < 0:
+      ints[:, a] = 1023 - ints[:, a]
+  return np.argsort(tiles.hilbert3(ints, 10), kind="stable")
+
+
+@pytest.mark.parametrize("axes,signs", [(p, (1, 1, 1)) for p in itertools.permutations(range(3)) if p != (0, 1, 2)] +
+                         [((0, 1, 2), s) for s in ((-1, 1, 1), (1, -1, 1), (1, 1, -1))])
+def test_octant_check_catches_planted_axis_slips(axes, signs):
+  # Each of the five wrong axis orders, and each negated axis, fails the octant known answer.
+  lat, lon, want = HC.octant_case(0)
+  assert (_planted_order(lat, lon) == want).all()
+  assert not (_planted_order(lat, lon, axes, signs) == want).all()
+
+
+def test_hilbert_quantises_axis_points():
+  names = list(HC.AXIS_POINTS)
+  lat, lon = np.array([HC.AXIS_POINTS[k] for k in names]).T
+  ints, finite = tiles.quantise_sphere(lat, lon, 10)
+  assert finite.all()
+  assert [tuple(c) for c in ints.tolist()] == [HC.AXIS_CELLS[k] for k in names]
+  assert HC.axis_order_ok(tiles.hilbert_order(lat, lon), names)
 
 
 def test_hilbert_order_is_permutation_and_local():
