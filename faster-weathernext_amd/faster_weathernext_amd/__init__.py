@@ -24,8 +24,10 @@ __version__ = "0.1.0"
 def enable(force: bool = False, **options):
   """Selects the HIP attention path; keyword options update ``patch.Options``.
 
-  Mirrors ``faster_weathernext.enable`` (``__init__.py:14-30``): unknown options raise TypeError,
-  an unknown ``attention`` value ValueError. Unless ``force`` (the reference's switch past its
+  Mirrors ``faster_weathernext.enable`` (``__init__.py:14-30``): every field of the reference's
+  Options is accepted (those for parts of the reference this library does not contain have no
+  effect, see ``patch.Options``), unknown options raise TypeError, an unknown ``attention`` value
+  ValueError. Unless ``force`` (the reference's switch past its
   compatibility check), the native library must load and the default device must be a gfx950
   (RuntimeError otherwise). Returns the Options.
   """
@@ -34,8 +36,8 @@ def enable(force: bool = False, **options):
       raise TypeError(f"unknown option {key!r}; see faster_weathernext_amd.patch.Options")
   if options.get("attention", patch.OPTIONS.attention) not in ("auto", "hip"):
     raise ValueError(f"unknown attention implementation {options['attention']!r} (auto, hip)")
-  if options.get("precision", patch.OPTIONS.precision) not in ("native", "bf16x3"):
-    raise ValueError(f"unknown precision {options['precision']!r} (native, bf16x3)")
+  if options.get("precision", patch.OPTIONS.precision) not in (None,) + patch.PRECISIONS:
+    raise ValueError(f"unknown precision {options['precision']!r} (None, native, bf16x3)")
   if not force:
     from . import _native
     _native.lib()

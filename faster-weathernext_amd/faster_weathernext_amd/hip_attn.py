@@ -18,6 +18,7 @@ device memory and the stream. Tensors must be on a ROCm device: there is no CPU 
 import collections
 import ctypes
 import threading
+import weakref
 
 import numpy as np
 import torch
@@ -152,12 +153,12 @@ class TileList:
     for a symmetric mask) for units of `unit_keys` keys (16 for bf16, 32 for float32), or None
     when `tiles_t` is not this list's exact transpose; built on first use and kept with this
     list."""
-    key = (id(tiles_t), int(unit_keys))
-    hit = self._ds_maps.get(key)
-    if hit is None or hit[0] is not tiles_t:
-      hit = (tiles_t, DsMap.build(self, tiles_t, unit_keys))
-      self._ds_maps[key] = hit
-    return hit[1]
+    # Weakly keyed by the transposed list: a map lives only as long as its tiles_t (which may be
+    # this list), so lists evicted from _as_tiles' cache take their maps with them.
+    maps = self._ds_maps.setdefault(int(unit_keys), weakref.WeakKeyDictionary())
+    if tiles_t not in maps:
+      maps[tiles_t] = DsMap.build(self, tiles_t, unit_keys)
+    return maps[tiles_t]
 
   @classmethod
   def from_mask(cls, mask, perm=None, device="cuda", max_item_tiles=None):
@@ -487,16 +488,13 @@ def tiled_flash_attention_qkv(qkv, tiles, *, scale, tiles_t=None, precision="nat
   return _TiledAttentionQKV.apply(qkv, tiles, tiles_t, float(scale), precision)
 
 
-def _reference_options(strict_fp32, precision, block_q, block_k, interpret):
+def _reference_options(block_q, block_k, interpret):
   """The reference's keyword arguments (pallas_attn.py:317-347) in this build's terms.
 
-  strict_fp32 asks for IEEE float32 products, which is "native"; block_q / block_k must be the
-  tile size the lists are built with (128); num_warps, num_stages, bwd_num_warps and bwd_split
-  tune the reference's Triton programs and have no counterpart (the kernels fix their own
-  launch shapes), so any value is accepted; interpret=True asks for the CPU interpreter, which
-  does not exist here."""
-  if strict_fp32 and precision != "native":
-    raise ValueError("strict_fp32 asks for IEEE float32 products: precision must be 'native'")
+  block_q / block_k must be the tile size the lists are built with (128); num_warps, num_stages,
+  bwd_num_warps and bwd_split tune the reference's Triton programs and have no counterpart (the
+  kernels fix their own launch shapes), so any value is accepted; interpret=True asks for the
+  CPU interpreter, which does not exist here. strict_fp32 goes to patch.resolve_precision."""
   for name, val in (("block_q", block_q), ("block_k", block_k)):
     if val is not None and val != nat.BLOCK:
       raise ValueError(f"{name}={val}: the kernels use {nat.BLOCK} x {nat.BLOCK} tiles (build the lists with "
@@ -507,19 +505,23 @@ def _reference_options(strict_fp32, precision, block_q, block_k, interpret):
 
 def tiled_flash_attention(q, k, v, tile_ptr, tile_kb=None, tile_bits=None, *, scale, strict_fp32=False,
                           tiles_t=None, block_q=None, block_k=None, num_warps=None, num_stages=None,
-                          bwd_num_warps=None, bwd_split=None, interpret=False, precision="native"):
+                          bwd_num_warps=None, bwd_split=None, interpret=False, precision=None):
   """q, k, v: [batch, n, heads, head_dim] float32/bfloat16 on the GPU -> [batch, n, heads, head_dim].
 
   The reference's signature (pallas_attn.py:317-320). ``tile_ptr`` may be a prepared TileList (then
   tile_kb and tile_bits are omitted) or the first of the three arrays of ``build_tile_mask``.
   ``tiles_t`` (TileList or array triple) is the transposed mask's list for the dK/dV kernel; it
-  defaults to the forward's (symmetric masks). ``precision`` ("native" or "bf16x3", float32
-  only): the products, see PRECISIONS; ``strict_fp32`` requires "native". The Triton tuning
-  arguments are accepted and have no effect (see _reference_options).
+  defaults to the forward's (symmetric masks). The products on float32 tensors follow the
+  reference's rule (pallas_attn.py:336-341) with torch's float32 matmul precision in place of
+  JAX's: IEEE float32 under "highest" (torch's default) or with ``strict_fp32``, bf16x3 under
+  "high" / "medium" (patch.resolve_precision); ``precision`` ("native" or "bf16x3") overrides it.
+  The Triton tuning arguments are accepted and have no effect (see _reference_options).
   """
+  from . import patch
   del num_warps, num_stages, bwd_num_warps, bwd_split
-  _reference_options(strict_fp32, precision, block_q, block_k, interpret)
+  _reference_options(block_q, block_k, interpret)
   _check(q)
+  precision = patch.resolve_precision(precision, q.dtype, strict_fp32)
   _precision(precision, q.dtype)
   tiles = tile_ptr if isinstance(tile_ptr, TileList) else (tile_ptr, tile_kb, tile_bits)
   if tiles_t is not None and not isinstance(tiles_t, TileList):

@@ -57,7 +57,8 @@ class TiledMHA(torch.nn.Module):
   ``tiles`` is the mesh's TileList (or the array triple of ``build_tile_mask``), built once and
   shared by every layer; ``tiles_t`` is the transposed mask's list for non-symmetric masks.
   ``dtype`` None takes the enable() option (bfloat16 when ``bf16``, else float32), ``precision``
-  None the enable() option ``precision`` (float32 only: "native" or "bf16x3").
+  None the precision ``patch.resolve_precision`` picks from the enable() options ``precision``
+  and ``strict_fp32`` and torch's float32 matmul precision (float32 only: "native" or "bf16x3").
   """
 
   def __init__(self, d_model, num_heads, key_size, tiles, tiles_t=None, *, device=None, dtype=None, precision=None):

@@ -10,6 +10,7 @@ from scipy import sparse
 
 import faster_weathernext_amd as fwn
 from faster_weathernext_amd import _native as nat
+import hilbert_cases as HC
 from oracle import mesh as om
 from oracle import tiles as ot
 
@@ -69,6 +70,21 @@ def test_khop_r6_32hop_reference_keys_per_query():
   n_qb, n_kb = -(-n // 64), -(-n // 32)
   tiles = np.count_nonzero(np.bincount(qb * n_kb + kb, minlength=n_qb * n_kb))
   assert abs(tiles * 32 / n_qb - 5480) / 5480 < 1e-3
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_hilbert_octant_centres_follow_gray_code(seed):
+  # Known answer from the mathematics of Skilling's transform and the reference's xyz convention
+  # (tests/hilbert_cases.py): the eight octant centres in reflected Gray-code order, x leading.
+  lat, lon, want = HC.octant_case(seed)
+  np.testing.assert_array_equal(fwn.hilbert_order(lat, lon), want)
+
+
+def test_hilbert_axis_points_quantise_to_the_formula_cells():
+  # +-1 -> 0 / 1023 and 0 -> 511.5 rounded half to even (512), so -x, -z, {+x, +y, +z}, -y.
+  names = list(HC.AXIS_POINTS)
+  lat, lon = np.array([HC.AXIS_POINTS[k] for k in names]).T
+  assert HC.axis_order_ok(fwn.hilbert_order(lat, lon), names)
 
 
 def test_hilbert_matches_oracle():
@@ -774,7 +790,7 @@ def test_split_precision_python_options():
     assert fwn.TiledMHA(16, 2, 8, None, device="cpu", precision="native").precision == "native"
   finally:
     fwn.disable()
-  assert patch.OPTIONS.precision == "native"
+  assert patch.OPTIONS.precision is None
   assert hip_attn._precision("bf16x3", torch.float32) == nat.PREC_BF16X3
   assert hip_attn._precision("native", torch.bfloat16) == nat.PREC_NATIVE
   with pytest.raises(TypeError):
@@ -785,13 +801,12 @@ def test_split_precision_python_options():
 
 def test_reference_keyword_arguments():
   """tiled_flash_attention takes the reference's keywords (pallas_attn.py:317-320): Triton tuning
-  values are accepted, strict_fp32 requires IEEE products, other tile sizes and the CPU
-  interpreter are refused with ValueError before any GPU work."""
+  values are accepted, other tile sizes and the CPU interpreter are refused with ValueError
+  before any GPU work."""
   from faster_weathernext_amd import hip_attn
-  hip_attn._reference_options(True, "native", 128, 128, False)
-  hip_attn._reference_options(False, "bf16x3", None, None, False)
-  for args in ((True, "bf16x3", None, None, False), (False, "native", 64, None, False),
-               (False, "native", None, 32, False), (False, "native", None, None, True)):
+  hip_attn._reference_options(128, 128, False)
+  hip_attn._reference_options(None, None, False)
+  for args in ((64, None, False), (None, 32, False), (None, None, True)):
     with pytest.raises(ValueError):
       hip_attn._reference_options(*args)
   import inspect
@@ -799,6 +814,59 @@ def test_reference_keyword_arguments():
   for name in ("scale", "strict_fp32", "tiles_t", "block_q", "block_k", "num_warps", "num_stages", "bwd_num_warps",
                "bwd_split", "interpret"):
     assert name in params, name
+
+
+# The reference's Options fields and defaults (patch.py:50-79).
+REFERENCE_OPTIONS = dict(attention="auto", replace_attention=True, reorder=True, strict_fp32=False, attn_chunk=512,
+                         grid_chunk=32768, edge_chunk=65536, layer_loop=True, remat=False, sequential_samples=False)
+
+
+def test_enable_accepts_every_reference_option():
+  from faster_weathernext_amd import patch
+  try:
+    opts = fwn.enable(force=True, **REFERENCE_OPTIONS)
+    for key, value in REFERENCE_OPTIONS.items():
+      assert getattr(opts, key) == value, key
+    opts = fwn.enable(force=True, strict_fp32=True, attn_chunk=256, remat=True)
+    assert opts.strict_fp32 is True and opts.attn_chunk == 256
+  finally:
+    fwn.disable()
+  assert patch.OPTIONS.strict_fp32 is False
+
+
+def test_strict_fp32_selects_the_ieee_kernels():
+  """The reference's dot choice (pallas_attn.py:336-341) with torch's float32 matmul precision in
+  place of JAX's: "highest" -> IEEE products; "high" / "medium" -> bf16x3 unless strict_fp32."""
+  import torch
+  from faster_weathernext_amd import patch
+  resolve = patch.resolve_precision
+  saved = torch.get_float32_matmul_precision()
+  try:
+    torch.set_float32_matmul_precision("highest")
+    assert resolve(None, torch.float32, False) == "native"
+    assert resolve(None, torch.float32, True) == "native"
+    for knob in ("high", "medium"):
+      torch.set_float32_matmul_precision(knob)
+      assert resolve(None, torch.float32, False) == "bf16x3"
+      assert resolve(None, torch.float32, True) == "native"
+      assert resolve("native", torch.float32, False) == "native"
+      assert resolve(None, torch.bfloat16, False) == "native"
+      with pytest.raises(ValueError):
+        resolve("bf16x3", torch.float32, True)
+      # The enable() option reaches the modules built afterwards.
+      try:
+        fwn.enable(force=True, strict_fp32=True)
+        assert fwn.TiledMHA(16, 2, 8, None, device="cpu").precision == "native"
+        assert resolve(None, torch.float32) == "native"
+      finally:
+        fwn.disable()
+      assert fwn.TiledMHA(16, 2, 8, None, device="cpu").precision == "bf16x3"
+  finally:
+    torch.set_float32_matmul_precision(saved)
+  with pytest.raises(TypeError):
+    resolve("bf16x3", torch.bfloat16)
+  with pytest.raises(ValueError):
+    resolve("tf32", torch.float32)
 
 
 def test_build_tile_mask_takes_the_reference_signature():
@@ -837,3 +905,30 @@ def test_output_strides_must_not_overlap():
   # the packed qkv views are disjoint
   packed = _desc(stride_b=300 * 3 * 2 * 64, stride_n=3 * 2 * 64, stride_h=64)
   assert L.fwn_attn_fwd_launch(packed, F, F, F, _tiles(n_blocks=5), F, None, None, 0, None) == nat.ERR_TILES
+
+
+def test_mesh_transformer_refuses_caller_tiles_without_transpose():
+  """A non-symmetric adjacency with caller-built tiles and no tiles_t would make the backward walk
+  the forward list as its own transpose; the constructor refuses it before building any layer."""
+  n = 200
+  adj = sparse.random(n, n, density=0.02, random_state=3, format="csr").astype(bool)
+  assert (adj != adj.T).nnz
+  mask = fwn.khop_mask(adj, 2)
+  tiles = fwn.TileList.from_mask(mask, device="cpu")
+  with pytest.raises(ValueError, match="tiles_t"):
+    fwn.MeshTransformer(num_layers=1, d_model=16, num_heads=2, key_size=8, ffw_hidden=32, cond_size=4,
+                        reorder=False, device="cpu", tiles=tiles, adjacency=adj, k_hop=2)
+
+
+def test_ds_maps_live_as_long_as_their_transposed_list():
+  import gc
+  m = _random_mask(300, 0.05, 5, symmetric=True)
+  tl = fwn.TileList.from_mask(m, device="cpu")
+  assert tl.ds_map(tl) is not None and tl.ds_map(tl) is tl.ds_map(tl)
+  other = fwn.TileList.from_mask(m, device="cpu")
+  assert other.ds_map(tl) is not None
+  maps = other._ds_maps[16]
+  assert len(maps) == 1
+  del tl
+  gc.collect()
+  assert len(maps) == 0
