@@ -146,6 +146,10 @@ class MeshTransformer(torch.nn.Module):
       if not symmetric and tiles_t is None:
         permuted = mask if perm is None else mask[perm][:, perm]
         tiles_t = TileList.from_mask(permuted.T.tocsr(), device=device)
+    elif not symmetric and tiles_t is None:
+      # The backward would walk the forward list as its own transpose: wrong dK/dV.
+      raise ValueError("a non-symmetric adjacency with caller-built tiles needs tiles_t, the transposed mask's "
+                       "tile list")
     self.tiles, self.tiles_t = tiles, tiles_t
     self.register_buffer("perm", None if perm is None else torch.from_numpy(np.asarray(perm, np.int64)).to(device),
                          persistent=False)
