@@ -22,7 +22,11 @@ this process may use (os.sched_getaffinity), with the CPU model.
 
 c5bwd and c5f32 are the reference's own attention benchmark (scripts/attn_bench.py --grad: 32-hop,
 Hilbert order, 6 x 128 heads, one layer's forward + backward) in bf16 and in float32; the line
-carries the reference's published RTX 5090 times for the same shape beside it.
+carries the reference's published RTX 5090 times for the same shape beside it. The default run
+(configuration 3) also times that shape in bf16 and in float32 with bf16x3 products, 10 steps each
+after the headline, under "reference_shape" (--no-extra skips them).
+
+The CPU baseline is the median of three timed runs over one fixed subset of query chunks.
 """
 import argparse
 import json
@@ -78,7 +82,10 @@ def parse():
   p.add_argument("--steps", type=int, default=20)
   p.add_argument("--warmup", type=int, default=3)
   p.add_argument("--workload", default="c3", choices=sorted(WORKLOADS))
-  p.add_argument("--cpu-seconds", type=float, default=12.0, help="bounded CPU-baseline sample length")
+  p.add_argument("--cpu-seconds", type=float, default=18.0,
+                 help="bounded CPU-baseline length (the median of three samples of one chunk subset)")
+  p.add_argument("--no-extra", action="store_true",
+                 help="default workload: skip the reference-shape lines (c5bwd bf16, c5f32 bf16x3)")
   p.add_argument("--no-cpu", action="store_true")
   p.add_argument("--item-tiles", type=int, default=0,
                  help="longest run of tiles per work item (0: chosen per launch by the library)")
@@ -345,9 +352,11 @@ def cpu_model():
   return platform.processor() or "unknown"
 
 
-def cpu_baseline(cfg, q, k, v, do, mask, tiles, scale, budget_s):
-  """Times the restated reference XLA chunked path on whole query chunks until `budget_s` elapses,
-  with the BLAS thread pool set to the cores this process may run on."""
+def cpu_baseline(cfg, q, k, v, do, mask, tiles, scale, budget_s, samples=3):
+  """Times the restated reference XLA chunked path on a fixed subset of whole query chunks,
+  `samples` times, with the BLAS thread pool set to the cores this process may run on; reports the
+  median rate and the spread. The subset is the first query chunks, as many as the first sample
+  covers in budget_s / samples seconds."""
   import numpy as np
   from threadpoolctl import threadpool_info, threadpool_limits
 
@@ -356,26 +365,39 @@ def cpu_baseline(cfg, q, k, v, do, mask, tiles, scale, budget_s):
   chunk = 512
   starts, bits, window, n_kv = A.build_chunked_mask(mask, chunk)
   D, B, H = cfg["head_dim"], cfg["batch"], cfg["heads"]
+
+  def one(c):
+    A.chunked_attention(q, k, v, starts, bits, window, n_kv, chunk, scale, chunks=[c])
+    if cfg["backward"]:
+      A.chunked_attention_grads(q, k, v, do, starts, bits, window, n_kv, chunk, scale, chunks=[c])
+
   with threadpool_limits(limits=cores):
     threads = max([t.get("num_threads", 1) for t in threadpool_info()] or [1])
     done, t0 = 0, time.perf_counter()
     while True:
-      A.chunked_attention(q, k, v, starts, bits, window, n_kv, chunk, scale, chunks=[done])
-      if cfg["backward"]:
-        A.chunked_attention_grads(q, k, v, do, starts, bits, window, n_kv, chunk, scale, chunks=[done])
+      one(done)
       done += 1
-      if time.perf_counter() - t0 >= budget_s or done == len(starts):
+      if time.perf_counter() - t0 >= budget_s / samples or done == len(starts):
         break
-    elapsed = time.perf_counter() - t0
+    times = [time.perf_counter() - t0]
+    for _ in range(samples - 1):
+      t0 = time.perf_counter()
+      for c in range(done):
+        one(c)
+      times.append(time.perf_counter() - t0)
   qb_per_chunk = chunk // 128
   ptr = tiles.ptr.cpu().numpy()
   live = int(ptr[min(done * qb_per_chunk, len(ptr) - 1)] - ptr[0])
   flops = (14 if cfg["backward"] else 4) * D * 128 * 128 * live * B * H
-  return {"value": flops / elapsed / 1e12, "unit": "TFLOP/s", "cores": cores, "blas_threads": int(threads),
-          "cpu_model": cpu_model(), "kind": "port",
-          "sample": f"{done} of {len(starts)} query chunks of {chunk} (window {window} keys), "
-                    f"{'fwd+bwd' if cfg['backward'] else 'fwd'} float32 numpy/BLAS, {elapsed:.1f} s",
-          "seconds": round(elapsed, 2)}
+  rates = sorted(flops / t / 1e12 for t in times)
+  return {"value": float(np.median(rates)), "unit": "TFLOP/s", "cores": cores, "blas_threads": int(threads),
+          "cpu_model": cpu_model(), "kind": "port", "samples": len(times),
+          "spread": [round(rates[0], 5), round(rates[-1], 5)],
+          "sample": f"median of {len(times)} runs over the same {done} of {len(starts)} query chunks of {chunk} "
+                    f"(window {window} keys, {done / len(starts):.0%} of the workload), "
+                    f"{'fwd+bwd' if cfg['backward'] else 'fwd'} float32 numpy/BLAS, "
+                    f"{min(times):.1f}-{max(times):.1f} s each",
+          "seconds": round(sum(times), 2)}
 
 
 def main():
@@ -393,6 +415,46 @@ def main():
     return row_passes(args)
   if args.workload == "c5stack":
     return mesh_stack(args)
+  result = attention(args)
+  if result is None:
+    return 2
+  if args.workload == "c3" and not args.no_extra:
+    result["reference_shape"] = reference_shape(args)
+  print(json.dumps(result), flush=True)
+  return 0
+
+
+# The reference's own attention benchmark (scripts/attn_bench.py --grad: refinement 6, 32-hop,
+# Hilbert order, 6 x 128, one layer's forward + backward), timed in the default run beside the
+# configuration-3 headline: bf16, and float32 with bf16x3 products (the counterpart of the
+# reference's TF32 / 3xTF32 dots), against its published RTX 5090 times.
+EXTRA_STEPS, EXTRA_WARMUP = 10, 3
+
+
+def reference_shape(args):
+  import argparse as ap
+  import torch
+  out = {}
+  for name, wl, prec in (("c5bwd_bf16", "c5bwd", "native"), ("c5f32_bf16x3", "c5f32", "bf16x3")):
+    sub = ap.Namespace(**{**vars(args), "workload": wl, "precision": prec, "steps": EXTRA_STEPS,
+                          "warmup": EXTRA_WARMUP, "no_cpu": True, "layout": "node", "item_tiles": 0})
+    r = attention(sub)
+    torch.cuda.empty_cache()
+    out[name] = {"ms_per_layer": r["ms_per_step"], "effective_tflops": r["value"],
+                 "valid_entry_tflops": r["valid_entry_tflops"], "dtype": r["dtype"], "steps": EXTRA_STEPS,
+                 "warmup": EXTRA_WARMUP, "kernels_ms": r["kernels_ms"], "live_tiles": r["config"]["live_tiles"],
+                 "valid_entries": r["config"]["valid_entries"],
+                 "reference_rtx5090_ms": WORKLOADS[wl]["reference_ms"]}
+  out["note"] = ("the reference's attention benchmark shape (scripts/attn_bench.py:23, 98-119): r6 mesh, 32-hop, "
+                 "Hilbert order, 6 x 128, forward + backward of one layer; ms_per_layer against the reference's "
+                 "RTX 5090 ms; valid_entry_tflops counts only the mask's valid entries (14 D per entry), which does "
+                 "not depend on the tile size")
+  return out
+
+
+def attention(args):
+  """One attention workload (the forward, plus the backward as the package runs it): the result
+  line as a dict, or None when the arguments do not fit the workload."""
   import numpy as np
   import torch
 
@@ -405,7 +467,7 @@ def main():
   x3 = args.precision == "bf16x3"
   if x3 and dtype != torch.float32:
     print("--precision bf16x3 applies to float32 workloads (c2, c5f32)", file=sys.stderr)
-    return 2
+    return None
   dev = torch.device("cuda:0")
   torch.cuda.set_device(dev)
 
@@ -619,8 +681,7 @@ def main():
   if not args.no_cpu:
     host_np = [x.astype(np.float32) for x in host]
     result["cpu_baseline"] = cpu_baseline(cfg, *host_np, mask, tiles, scale, args.cpu_seconds)
-  print(json.dumps(result), flush=True)
-  return 0
+  return result
 
 
 if __name__ == "__main__":
