@@ -43,7 +43,7 @@ class AttnDesc(ctypes.Structure):
 
 
 PREC_NATIVE = 0  # FWN_PREC_NATIVE: products in the tensors' dtype
-PREC_BF16X3 = 1  # FWN_PREC_BF16X3: float32 tensors, products from three bf16 parts (forward only)
+PREC_BF16X3 = 1  # FWN_PREC_BF16X3: float32 tensors, products from three bf16 parts (forward and dS-exchange backward)
 
 
 class Tiles(ctypes.Structure):

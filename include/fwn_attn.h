@@ -240,8 +240,9 @@ int fwn_attn_bwd_dkv_launch(const fwn_attn_desc* desc, const void* q, const void
  * on `stream` and share it). The dq and dk/dv launches only read what delta and the forward
  * wrote, so a caller with two streams may instead enqueue delta, then dq and dk/dv on different
  * streams, each with its own workspace, and join them: the two kernels then fill each other's
- * idle CUs (the Python package does this; 1.89 -> 1.80 ms per fwd+bwd step at refinement 6,
- * 16-hop, 4 x 128, bf16). */
+ * idle CUs. The Python package does this only for tile lists that are not exact transposes of
+ * each other; otherwise it takes the dS exchange (fwn_attn_bwd_ds_launch), which computes S and
+ * dP once. */
 int fwn_attn_bwd_launch(const fwn_attn_desc* desc, const void* q, const void* k, const void* v,
                         const void* o, const void* dout, const float* lse, float* delta,
                         const fwn_tiles* tiles, const fwn_tiles* tiles_t, void* dq, void* dk,
