@@ -11,10 +11,12 @@
 //     addresses 4 consecutive columns d0+4q.. of row k0+e, and lane j receives column d0+j of rows
 //     k0..k0+3, i.e. four consecutive keys of its own column, which is the key-contiguous operand
 //     the MFMA needs. Two such reads form the 8-element operand.
-// gfx950's LDS has 64 banks of 4 bytes, so a b128 read is served 16 lanes (256 bytes) and a b64
-// read 32 lanes (256 bytes) at a time. The swizzle keeps both access patterns conflict-free: the 16
-// lanes of a row read hit 16 distinct rows at one logical chunk, and the 32 lanes of a transpose
-// read hit 4 consecutive rows x 4 consecutive chunks.
+// gfx950's LDS has 64 banks of 4 bytes. A b128 read is served 16 lanes (256 bytes) at a time
+// (measured: the lanes of one half-wave whose quad index l / 4 has the same parity), a b64
+// transpose read 32 lanes (256 bytes). The swizzle keeps both access patterns conflict-free
+// (measured: no conflict cycles in the forward): the lanes of a row read hit distinct rows at one
+// logical chunk, and the 32 lanes of a transpose read hit 4 consecutive rows x 4 consecutive
+// chunks.
 //
 // Reference: pallas_attn.py:112-141 (forward), 161-215 (dQ, dK/dV), 274-311 (VJP driver).
 #include "attn_bf16_tiles.h"
@@ -302,13 +304,17 @@ __global__ void __launch_bounds__(NT, 2) dq_kernel(KArgs a) {
 // queries 4g..4g+3, then 16+4g..16+4g+3. The dQ contraction runs over keys, so its B operand
 // (V_MFMA_F32_32X32X16_BF16, lane L: query L % 32, keys 8 (L / 32) .. +7) is the transpose; the
 // dQ kernel does that transpose through LDS, where it has bandwidth to spare (dK/dV has none).
-// Lane L writes chunk L to 16-byte slot p(k, g) = 16 (k / 4) + 4 (k % 4) + (g ^ (k / 4)), then
-// two transpose reads (ds_read_b64_tr_b16: lane j of a 16-lane group gets column d0 + j of 4 rows)
-// give keys 8 (L / 32) .. +3 and +4 .. +7 of query L % 32. Over 32 lanes the reads hit 4 keys x 4
-// chunks x 2 halves, distinct banks. The writes hit 16 distinct slots of a 256-byte bank line
-// both over 16 consecutive lanes and over the lane groups {l, l + 32 : l in [8m, 8m + 8)} in which
-// gfx950 serves b128 reads (a first layout that was conflict-free only for the latter measured
-// 22% bank-conflict cycles).
+// Lane L writes chunk L to 16-byte slot p(k, g) = 16 (k / 4) + 4 (g ^ (k / 4)) + k % 4, then two
+// transpose reads (ds_read_b64_tr_b16: lane j of a 16-lane group gets column d0 + j of 4 rows)
+// give keys 8 (L / 32) .. +3 and +4 .. +7 of query L % 32.
+// LDS service on gfx950, measured with single-pattern probes (SQ_LDS_BANK_CONFLICT): a
+// ds_write_b128 is served 8 consecutive lanes per cycle, without conflict when their 16-byte
+// chunks are distinct modulo 128 bytes; here lanes 8m .. 8m + 7 (keys 8 (m % 2) .. +7, one g) write
+// p mod 8 = 4 ((g ^ (k / 4)) % 2) + k % 4, eight distinct values. The transpose reads hit 32
+// distinct bank pairs over lanes 0-31 and over lanes 32-63 (keys k0 .. k0 + 3 of one quarter:
+// 4 (q ^ (k / 4)) + k % 4 takes 16 values, times the two halves). An earlier slot order,
+// 16 (k / 4) + 4 (k % 4) + (g ^ (k / 4)), put keys k and k + 2 on one 128-byte position: every
+// write group 2-way, 8 conflict cycles per unit, 22% of the kernel's LDS cycles.
 constexpr int kNonTemporal = 2;  // buffer store cache policy: non-temporal (gfx950 "nt")
 
 struct DsUnit {
@@ -316,7 +322,7 @@ struct DsUnit {
   uint32_t r0, r1;  // this lane's transpose reads: keys 8 (L / 32) .. +3 and +4 .. +7
 
   static __device__ __forceinline__ uint32_t slot(int k, int g) {
-    return (uint32_t)(16 * (16 * (k >> 2) + 4 * (k & 3) + (g ^ (k >> 2))));
+    return (uint32_t)(16 * (16 * (k >> 2) + 4 * (g ^ (k >> 2)) + (k & 3)));
   }
   __device__ __forceinline__ void init(int lane) {
     w = slot(lane & 15, lane >> 4);
@@ -723,8 +729,9 @@ __global__ void __launch_bounds__(NT8, 1) dkv16_kernel(KArgs a) {
   const uint64_t* mword = key_mask_words(a, wid, g, t16);
   const int mshift = 4 * (g & 1);
 
-  // dS exchange state: the unit computed last (its dS in dsv, its byte offset in pend; an offset
-  // of ds_slice_bytes is past the slice, so that store is dropped) and the forward tile's
+  // dS exchange state: the unit computed last (its dS in dsv, its byte offset in pend; pend =
+  // ds_slice_bytes means no unit yet, and that store falls outside the buffer range) and the
+  // forward tile's
   // (ubase, halves) for the current tile, read at the end of the previous tile's step (a scalar
   // load pending when the units start would make their first LDS wait wait for it too).
   rsrc_t rS;
@@ -735,8 +742,12 @@ __global__ void __launch_bounds__(NT8, 1) dkv16_kernel(KArgs a) {
     rS = make_rsrc(a.ds + (int64_t)j.bh * (a.ds_slice_bytes >> 1), a.ds_slice_bytes);
     pend = a.ds_slice_bytes;
   }
+  // The unit's offset goes into the per-lane offset (voffset), which the buffer unit checks
+  // against the slice size (soffset is not checked): with pend = ds_slice_bytes every lane's
+  // 16 bytes lie past the range and the store writes nothing. A branch on pend instead measured
+  // 2% slower.
   auto store_ds = [&]() {
-    if constexpr (DS) __builtin_amdgcn_raw_buffer_store_b128(dsv, rS, 16 * lane, (int)pend, kNonTemporal);
+    if constexpr (DS) __builtin_amdgcn_raw_buffer_store_b128(dsv, rS, (int)(16u * lane + pend), 0, kNonTemporal);
   };
 
   // The next tile's group bits and column block are read a tile ahead (scalar loads), so issuing
@@ -809,7 +820,7 @@ __global__ void __launch_bounds__(NT8, 1) dkv16_kernel(KArgs a) {
     tile_step(tt, t1, b0, b1, mnext, gnext, cnext);
     if (tt + 1 < t1) tile_step(tt + 1, t1, b1, b0, mnext, gnext, cnext);
   }
-  store_ds();  // the last unit's dS (dropped when the wave computed none)
+  store_ds();  // the last unit's dS (none when the wave computed no unit)
   kw.store(a, j, krow, 16 * wid + t16, g);
 }
 
