@@ -593,3 +593,47 @@ def test_reference_keywords_give_the_same_result():
   torch.cuda.synchronize()
   for a, b in zip(*res):
     np.testing.assert_array_equal(a, b)
+
+
+def _tiled_mha_reference(x, wqkv, wf, bf, mask, heads, key_size):
+  """The reference's tiled_mha (patch.py:165-177) in float64 on the CPU: q, k, v projections
+  [batch, n, heads, key_size] (the fused weight's rows are q, k, v in turn, each head-major), masked
+  softmax attention with scale key_size**-0.5 (masked logits -inf), reshape to
+  [batch, n, heads * key_size], then the mha_final projection with bias."""
+  b, n, _ = x.shape
+  q, k, v = (x @ w.T for w in wqkv.split(heads * key_size))
+  q, k, v = (t.view(b, n, heads, key_size).transpose(1, 2) for t in (q, k, v))
+  s = (q @ k.transpose(-1, -2)) * key_size ** -0.5
+  p = torch.softmax(s.masked_fill(~mask, float("-inf")), dim=-1)
+  o = (p @ v).transpose(1, 2).reshape(b, n, heads * key_size)
+  return o @ wf.T + bf
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_tiled_mha_block_matches_reference_composition(dtype):
+  """TiledMHA (the reference's tiled_mha caller, patch.py:165-177) against that composition
+  restated in float64 autograd on the CPU with the block's own weights (rounded to dtype): the
+  output and the gradients of the input and of every weight, max rel RMS 1e-5 (float32) /
+  5e-3 (bf16)."""
+  print(f"tiled_mha composition {dtype}", flush=True)
+  torch.manual_seed(1)
+  b, n, h, d, dm = 2, 600, 2, 64, 96
+  m = _random_mask(n, 0.05, 53, symmetric=True)
+  tiles = fwn.TileList.from_mask(m, device=DEV)
+  block = fwn.TiledMHA(dm, h, d, tiles, device=DEV, dtype=dtype, precision="native")
+  with torch.no_grad():
+    block.final.bias.normal_(0, 0.5)
+  x = torch.randn(b, n, dm, device=DEV, dtype=dtype, requires_grad=True)
+  g = torch.randn(b, n, dm, device=DEV, dtype=dtype)
+  y = block(x)
+  y.backward(g)
+  torch.cuda.synchronize()
+  ws = [p.detach().double().cpu().requires_grad_(True) for p in (block.qkv.weight, block.final.weight, block.final.bias)]
+  xr = x.detach().double().cpu().requires_grad_(True)
+  ref = _tiled_mha_reference(xr, *ws, torch.from_numpy(m.toarray()), h, d)
+  ref.backward(g.double().cpu())
+  pairs = [("out", y, ref), ("dx", x.grad, xr.grad), ("dWqkv", block.qkv.weight.grad, ws[0].grad),
+           ("dWfinal", block.final.weight.grad, ws[1].grad), ("dbias", block.final.bias.grad, ws[2].grad)]
+  for what, got, want in pairs:
+    got, want = got.detach().double().cpu().numpy(), want.detach().numpy()
+    assert A.rel_rms(got, want) <= TOL[dtype], (what, A.rel_rms(got, want))
