@@ -823,6 +823,7 @@ __global__ void __launch_bounds__(256, 2) dkv16_f32_kernel(KArgs a) {
     };
     f32x4 rd[2][2];
     rows(rd[0], 0);
+    __builtin_amdgcn_s_setprio(1);  // MFMA phases at issue priority 1, the exponentials at 0
 #pragma unroll
     for (int it = 0; it < 16; ++it) {
       if (it + 1 < 16) rows(rd[(it + 1) & 1], it + 1);
@@ -837,6 +838,7 @@ __global__ void __launch_bounds__(256, 2) dkv16_f32_kernel(KArgs a) {
       }
       __builtin_amdgcn_sched_barrier(0);
     }
+    __builtin_amdgcn_s_setprio(0);
     float p[8];
     const uint32_t w32 = (uint32_t)(mw >> (32 * (c >> 1)));
 #pragma unroll
@@ -863,6 +865,7 @@ __global__ void __launch_bounds__(256, 2) dkv16_f32_kernel(KArgs a) {
     };
     float ex[2][16];
     els(ex[0], 0);
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int n = 0; n < NB; ++n) {
       if (n + 1 < NB) els(ex[(n + 1) & 1], n + 1);
@@ -878,6 +881,7 @@ __global__ void __launch_bounds__(256, 2) dkv16_f32_kernel(KArgs a) {
         }
       __builtin_amdgcn_sched_barrier(0);
     }
+    __builtin_amdgcn_s_setprio(0);
   };
 
   int t0, t1;

@@ -191,6 +191,7 @@ __global__ void __launch_bounds__(NT4, 2) dkv16_x3_kernel(KArgs a) {
     };
     u32x4 rd[2][4];
     rows(rd[0], 0);
+    __builtin_amdgcn_s_setprio(1);  // MFMA phases at issue priority 1, the exponentials at 0
 #pragma unroll
     for (int it = 0; it < 2 * KS; ++it) {
       if (it + 1 < 2 * KS) rows(rd[(it + 1) & 1], it + 1);
@@ -215,6 +216,7 @@ __global__ void __launch_bounds__(NT4, 2) dkv16_x3_kernel(KArgs a) {
     u32x4 tb[2][4];
     trs(tb[0], 0);
     __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_setprio(0);
     float p[8], ds[8];
     const uint32_t w32 = (uint32_t)(mw >> (32 * (c >> 1)));
 #pragma unroll
@@ -229,6 +231,7 @@ __global__ void __launch_bounds__(NT4, 2) dkv16_x3_kernel(KArgs a) {
     u32x4 ph, pl;
     split8(p, ph, pl);
     split8(ds, dh, dl);
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int n = 0; n < NB; ++n) {
       if (n + 1 < NB) trs(tb[(n + 1) & 1], n + 1);
@@ -238,6 +241,7 @@ __global__ void __launch_bounds__(NT4, 2) dkv16_x3_kernel(KArgs a) {
       dk[n] = mfma16_x3(x[2], x[3], dh, dl, dk[n]);
       __builtin_amdgcn_sched_barrier(0);
     }
+    __builtin_amdgcn_s_setprio(0);
   };
 
   int t0, t1;
