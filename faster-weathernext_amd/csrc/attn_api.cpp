@@ -332,6 +332,10 @@ int fwn_attn_bwd_delta_launch(const fwn_attn_desc* desc, const void* o, const vo
   if (int rc = check_tensor(o, "o")) return rc;
   if (int rc = check_tensor(dout, "dout")) return rc;
   if (!delta) return fail(FWN_ERR_INVALID_ARG, "delta is null");
+  // The delta kernel's grid: one workgroup per 8 rows (float32, head_dim 128; more rows otherwise)
+  // of each batch member, in one 32-bit grid dimension.
+  if (((int64_t)desc->n + 7) / 8 * desc->batch > INT32_MAX)
+    return fail(FWN_ERR_INVALID_ARG, "delta: batch * n too large for one launch (%d x %d)", desc->batch, desc->n);
   KArgs a = base_args(desc);
   a.o = o;
   a.dout = dout;

@@ -1008,7 +1008,8 @@ __global__ void __launch_bounds__(256, 2) dkv16_f32_kernel(KArgs a) {
 
 // ------------------------------------------------------------------------------------------
 // delta = rowsum(o * dout) (pallas_attn.py:278): L lanes per (batch, row, head), 16 B per lane.
-// The grid is (row blocks, batch): each lane group owns one row and walks its heads, four at a
+// The grid is (row blocks x batch), flattened into x (a y extent would cap batch at 65,535): each
+// workgroup takes one row block of one batch member, each lane group one row, and walks its heads, four at a
 // time with every load issued before the first sum, so consecutive lane groups read consecutive
 // rows and no lane divides by a runtime size (the earlier per-lane 64-bit index divisions took
 // about 1,000 VALU instructions per four rows). Measured at 4.9-5.4 TB/s of O and dO reads
@@ -1021,8 +1022,9 @@ __global__ void __launch_bounds__(NT) delta_kernel(KArgs a) {
   constexpr int GROUPS = NT / L;  // rows per workgroup
   constexpr int HB = 4;           // heads in flight per lane
   const int part = (int)(threadIdx.x % L);
-  const int row = (int)blockIdx.x * GROUPS + (int)(threadIdx.x / L);
-  const int b = (int)blockIdx.y;
+  const int nrb = (a.n + GROUPS - 1) / GROUPS;  // row blocks per batch member (uniform)
+  const int b = (int)blockIdx.x / nrb;
+  const int row = ((int)blockIdx.x - b * nrb) * GROUPS + (int)(threadIdx.x / L);
   const bool ok = row < a.n;
   const int64_t rbase = (int64_t)b * a.osb + (int64_t)row * a.osn + part * EPC;
   for (int h0 = 0; h0 < a.heads; h0 += HB) {
@@ -1057,11 +1059,11 @@ __global__ void __launch_bounds__(NT) delta_kernel(KArgs a) {
   }
 }
 
-// Grid of the delta kernel for a call: (row blocks, batch).
+// Grid of the delta kernel for a call: row blocks x batch members.
 template <typename T, int D>
 dim3 delta_grid(const KArgs& a) {
   constexpr int rows = NT / (D / (16 / (int)sizeof(T)));
-  return dim3((unsigned)((a.n + rows - 1) / rows), (unsigned)a.batch);
+  return dim3((unsigned)(((int64_t)a.n + rows - 1) / rows * a.batch));
 }
 
 template <int D>

@@ -932,3 +932,13 @@ def test_ds_maps_live_as_long_as_their_transposed_list():
   del tl
   gc.collect()
   assert len(maps) == 0
+
+
+def test_delta_launch_refuses_a_grid_past_32_bits():
+  """The delta kernel's one-dimensional grid holds (n / 8) x batch workgroups at most: a call past
+  2^31 of them is refused before any HIP call."""
+  L = nat.lib()
+  n, batch = 1 << 15, 1 << 20
+  big = _desc(batch=batch, n=n, heads=1, head_dim=128, stride_b=n * 128, stride_n=128, stride_h=128)
+  assert L.fwn_attn_bwd_delta_launch(big, FAKE, FAKE, FAKE, None) == nat.ERR_INVALID_ARG
+  assert "too large" in L.fwn_last_error().decode()
