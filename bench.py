@@ -92,6 +92,9 @@ def parse():
   p.add_argument("--no-cpu", action="store_true")
   p.add_argument("--item-tiles", type=int, default=0,
                  help="longest run of tiles per work item (0: chosen per launch by the library)")
+  p.add_argument("--order", default="auto", choices=["auto", "items"],
+                 help="auto: the library's choice (an order table for bf16 launches with few jobs); items: "
+                      "every launch in the plain (batch, head)-major item order")
   p.add_argument("--serial-bwd", action="store_true",
                  help="run dQ and then dK/dV on one stream instead of side by side on two streams")
   p.add_argument("--no-ds", action="store_true",
@@ -548,7 +551,8 @@ def attention(args):
   L = nat.lib()
   stream = torch.cuda.current_stream(dev)
   sp = stream.cuda_stream
-  ts = tiles.struct_for(B, H)
+  ts = tiles.struct_for_desc(fdesc) if args.order == "auto" else tiles.struct_for(B, H)
+  tst = tiles.struct_for_desc(fdesc, kv=True) if args.order == "auto" else ts  # dK/dV's (the list is its transpose)
   ws = fwn.hip_attn.workspace(fdesc, dev, tiles)
   wsp, wsn = (ws.data_ptr(), ws.numel()) if ws is not None else (None, 0)
   # dK/dV runs on a second stream beside dQ (as the package's backward does), with its own
@@ -571,7 +575,7 @@ def attention(args):
   def bwd_dkv(st):
     own = st is side  # beside dQ: its own workspace
     nat.check(L.fwn_attn_bwd_dkv_launch(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(),
-                                        lse.data_ptr(), delta.data_ptr(), ts, dk.data_ptr(), dv.data_ptr(),
+                                        lse.data_ptr(), delta.data_ptr(), tst, dk.data_ptr(), dv.data_ptr(),
                                         ws2p if own else wsp, ws2n if own else wsn, st.cuda_stream))
 
   # The bf16 backward's dS exchange, as the package runs it (symmetric k-hop mask: the forward
@@ -584,7 +588,7 @@ def attention(args):
 
   def bwd_dkv_ds(st):
     nat.check(L.fwn_attn_bwd_dkv_ds_launch(fdesc, q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(),
-                                           lse.data_ptr(), delta.data_ptr(), ts, dmap.struct, dk.data_ptr(),
+                                           lse.data_ptr(), delta.data_ptr(), tst, dmap.struct, dk.data_ptr(),
                                            dv.data_ptr(), dsbuf.data_ptr(), dsbuf.numel(), wsp, wsn, st.cuda_stream))
 
   def bwd_dq_ds(st):
@@ -679,7 +683,7 @@ def attention(args):
                  "sigma": cfg["sigma"], "live_tiles": T, "tile_density": round(tiles.density, 4),
                  "live_group_fraction": round(tiles.group_fraction, 4),
                  "valid_entries": int(mask.nnz), "item_tiles": tiles.item_cap_for(B, H),
-                 "precision": args.precision},
+                 "order": "windows" if ts.n_work else "items", "precision": args.precision},
       "roofline": {"bound": "mfma", "kernel": dominant, "achieved": round(achieved, 3), "peak": peak,
                    "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": traffic,
                    "traffic_source": traffic_src, "ms": round(per_solo[dominant], 4),

@@ -134,6 +134,17 @@ int check_tiles(const fwn_attn_desc* d, const fwn_tiles* t, const char* name) {
   if (t->n_parts < 0 || t->n_split < 0 || (t->n_split > 0 && !t->split) || (t->n_split > 0) != (t->n_parts > 0))
     return fail(FWN_ERR_TILES, "%s: inconsistent split schedule (%d parts, %d split blocks)", name, t->n_parts,
                 t->n_split);
+  if (t->work) {
+    // An order table serves the (batch, head) count it was built for and holds every job.
+    if (t->work_pairs != d->batch * d->heads)
+      return fail(FWN_ERR_TILES, "%s: order table built for %d (batch, head) pairs, the call has %d", name,
+                  t->work_pairs, d->batch * d->heads);
+    if ((int64_t)t->n_work < (int64_t)t->n_items * d->batch * d->heads)
+      return fail(FWN_ERR_TILES, "%s: order table of %d entries for %lld jobs", name, t->n_work,
+                  (long long)t->n_items * d->batch * d->heads);
+  } else if (t->n_work != 0) {
+    return fail(FWN_ERR_TILES, "%s: %d order table entries but no table", name, t->n_work);
+  }
   if ((int64_t)t->n_items * d->batch * d->heads > INT32_MAX ||
       (int64_t)t->n_split * d->batch * d->heads * (d->head_dim / 16) > INT32_MAX)
     return fail(FWN_ERR_INVALID_ARG, "%s: grid too large", name);
@@ -223,6 +234,8 @@ void set_tiles(KArgs& a, const fwn_tiles* t, void* ws) {
   a.n_items = t->n_items;
   a.n_parts = t->n_parts;
   a.n_split = t->n_split;
+  a.order = t->work;
+  a.n_order = t->work ? t->n_work : 0;
   a.work = (float*)ws;
 }
 

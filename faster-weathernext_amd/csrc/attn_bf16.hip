@@ -44,6 +44,7 @@ __global__ void __launch_bounds__(NT, 2) fwd_kernel(KArgs a) {
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int i = lane & 31, g = lane >> 5;
   const Job j = decode_job(a);
+  if (j.skip) return;  // an empty entry of the order table
   const uint32_t snb = (uint32_t)a.sn * 2;
   const rsrc_t rK = make_rsrc((const uint16_t*)a.k + j.base, a.slice_bytes);
   const rsrc_t rV = make_rsrc((const uint16_t*)a.v + j.base, a.slice_bytes);
@@ -177,6 +178,7 @@ __global__ void __launch_bounds__(NT, 2) dq_kernel(KArgs a) {
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int i = lane & 31, g = lane >> 5;
   const Job j = decode_job(a);
+  if (j.skip) return;  // an empty entry of the order table
   const uint32_t snb = (uint32_t)a.sn * 2;
   const rsrc_t rK = make_rsrc((const uint16_t*)a.k + j.base, a.slice_bytes);
   const rsrc_t rV = make_rsrc((const uint16_t*)a.v + j.base, a.slice_bytes);
@@ -352,6 +354,7 @@ __global__ void __launch_bounds__(NT, 2) dq_ds_kernel(KArgs a) {
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int i = lane & 31, g = lane >> 5;
   const Job j = decode_job(a);
+  if (j.skip) return;  // an empty entry of the order table
   const uint32_t snb = (uint32_t)a.sn * 2;
   const rsrc_t rK = make_rsrc((const uint16_t*)a.k + j.base, a.slice_bytes);
   const rsrc_t rS = make_rsrc(a.ds + (int64_t)j.bh * (a.ds_slice_bytes >> 1), a.ds_slice_bytes);
@@ -705,6 +708,7 @@ __global__ void __launch_bounds__(NT8, 1) dkv16_kernel(KArgs a) {
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // keys 16 wid .. 16 wid + 15 of the block
   const int g = lane >> 4, t16 = lane & 15;
   const Job j = decode_job(a);
+  if (j.skip) return;  // an empty entry of the order table
   const uint32_t snb = (uint32_t)a.sn * 2, osnb = (uint32_t)a.osn * 2;
   const rsrc_t rQ = make_rsrc((const uint16_t*)a.q + j.base, a.slice_bytes);
   const rsrc_t rO = make_rsrc((const uint16_t*)a.dout + j.obase, a.oslice_bytes);
@@ -834,7 +838,7 @@ __global__ void __launch_bounds__(NT8, 1) dkv16_kernel(KArgs a) {
 
 template <int D>
 hipError_t launch_d(Kind kind, const KArgs& a, hipStream_t stream) {
-  const dim3 grid((unsigned)a.n_items * (unsigned)(a.batch * a.heads)), block(NT);
+  const dim3 grid((unsigned)job_count(a)), block(NT);
   switch (kind) {
     case Kind::kFwd: hipLaunchKernelGGL(fwd_kernel<D>, grid, block, 0, stream, a); break;
     case Kind::kDq: hipLaunchKernelGGL(dq_kernel<D>, grid, block, 0, stream, a); break;

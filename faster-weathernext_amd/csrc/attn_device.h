@@ -115,21 +115,40 @@ struct Job {
   int part;      // partial slot, or -1 when the item covers its whole block
   int64_t base;   // element offset of (b, h) in q, k, v, dq, dk, dv
   int64_t obase;  // element offset of (b, h) in o, dout
+  bool skip;     // an empty entry of the order table: the workgroup does nothing
 };
 
-// Workgroups are dealt round-robin over the 8 XCDs, each with its own L2. Jobs are ordered
-// (batch, head) major, then work items in block order, and XCD x gets a contiguous range of
-// them, so the workgroups resident on one XCD work on neighbouring blocks of one head and share
-// their K/V tiles in that XCD's L2. The map from workgroup id to job is a bijection for any count.
+// Without an order table, workgroups are dealt round-robin over the 8 XCDs, each with its own
+// L2. Jobs are ordered (batch, head) major, then work items in block order, and XCD x gets a
+// contiguous range of them, so the workgroups resident on one XCD work on neighbouring blocks of
+// one head and share their K/V tiles in that XCD's L2. The map from workgroup id to job is a
+// bijection for any count.
+//
+// With an order table (fwn_tiles_order_fill), workgroup `pid` runs the (batch * heads + head,
+// item) pair of entry pid; the host has placed each XCD's jobs at the ids pid = x mod 8 it
+// serves. Entries outside the call's pairs or items are skipped, so a malformed table cannot
+// send a workgroup outside the tensors.
 __device__ __forceinline__ Job decode_job(const KArgs& a, int pid = -1) {
   Job j;
-  const int total = a.n_items * a.batch * a.heads;
   if (pid < 0) pid = blockIdx.x;
-  const int xcd = pid & 7, local = pid >> 3;
-  const int small = total >> 3, rem = total & 7;
-  const int job = xcd < rem ? xcd * (small + 1) + local : rem * (small + 1) + (xcd - rem) * small + local;
-  j.bh = job / a.n_items;
-  const int slot = job - j.bh * a.n_items;
+  int slot;
+  if (a.order) {
+    j.bh = ((ci32_ptr)a.order)[2 * pid];
+    slot = ((ci32_ptr)a.order)[2 * pid + 1];
+    j.skip = (unsigned)j.bh >= (unsigned)(a.batch * a.heads) || (unsigned)slot >= (unsigned)a.n_items;
+    if (j.skip) {
+      j.bh = 0;
+      slot = 0;
+    }
+  } else {
+    const int total = a.n_items * a.batch * a.heads;
+    const int xcd = pid & 7, local = pid >> 3;
+    const int small = total >> 3, rem = total & 7;
+    const int job = xcd < rem ? xcd * (small + 1) + local : rem * (small + 1) + (xcd - rem) * small + local;
+    j.bh = job / a.n_items;
+    slot = job - j.bh * a.n_items;
+    j.skip = false;
+  }
   const ci32_ptr item = (ci32_ptr)a.items + 4 * slot;
   j.blk = item[0];
   j.t0 = item[1] < 0 ? 0 : item[1];

@@ -161,6 +161,7 @@ __global__ void __launch_bounds__(NT, 2) fwd_f32g_kernel(KArgs a) {
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int i = lane & 31, g = lane >> 5;
   const Job j = decode_job(a);
+  if (j.skip) return;  // an empty entry of the order table
   const uint32_t snb = (uint32_t)a.sn * 4;
   const rsrc_t rK = make_rsrc((const float*)a.k + j.base, a.slice_bytes);
   const rsrc_t rV = make_rsrc((const float*)a.v + j.base, a.slice_bytes);
@@ -281,6 +282,7 @@ __global__ void __launch_bounds__(NT, 1) dq_f32_kernel(KArgs a) {
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int i = lane & 31, g = lane >> 5;
   const Job j = decode_job(a);
+  if (j.skip) return;  // an empty entry of the order table
   const uint32_t snb = (uint32_t)a.sn * 4;
   const rsrc_t rK = make_rsrc((const float*)a.k + j.base, a.slice_bytes);
   const rsrc_t rV = make_rsrc((const float*)a.v + j.base, a.slice_bytes);
@@ -405,6 +407,7 @@ __global__ void __launch_bounds__(NT, 2) dq_f32_ds_kernel(KArgs a) {
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int i = lane & 31, g = lane >> 5;
   const Job j = decode_job(a);
+  if (j.skip) return;  // an empty entry of the order table
   const uint32_t snb = (uint32_t)a.sn * 4;
   const rsrc_t rK = make_rsrc((const float*)a.k + j.base, a.slice_bytes);
   const rsrc_t rS = make_rsrc((const float*)a.ds + (int64_t)j.bh * (a.ds_slice_bytes >> 2), a.ds_slice_bytes);
@@ -527,6 +530,7 @@ __global__ void __launch_bounds__(NT, 1) dkv_f32_kernel(KArgs a) {
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int i = lane & 31, g = lane >> 5;
   const Job j = decode_job(a);
+  if (j.skip) return;  // an empty entry of the order table
   const uint32_t snb = (uint32_t)a.sn * 4;
   const rsrc_t rQ = make_rsrc((const float*)a.q + j.base, a.slice_bytes);
   const rsrc_t rO = make_rsrc((const float*)a.dout + j.obase, a.oslice_bytes);
@@ -743,8 +747,9 @@ __global__ void __launch_bounds__(256, 2) dkv16_f32_kernel(KArgs a) {
   // ids 16 i + x and 16 i + 8 + x): pid = 8 i + x is the item's id as decode_job numbers them.
   const int half = (int)(blockIdx.x >> 3) & 1;
   const int pid = (int)(((blockIdx.x >> 4) << 3) | (blockIdx.x & 7));
-  if (pid >= a.n_items * a.batch * a.heads) return;
+  if (pid >= job_count(a)) return;
   const Job j = decode_job(a, pid);
+  if (j.skip) return;  // an empty entry of the order table
   const int kg = 4 * half + wid;  // this wave's 16-key group of the block
   const uint32_t snb = (uint32_t)a.sn * 4, osnb = (uint32_t)a.osn * 4;
   const rsrc_t rQ = make_rsrc((const float*)a.q + j.base, a.slice_bytes);
@@ -1073,9 +1078,9 @@ hipError_t launch_d(Kind kind, const KArgs& a, hipStream_t stream) {
     hipLaunchKernelGGL((delta_kernel<float, D>), (delta_grid<float, D>(a)), block, 0, stream, a);
     return hipGetLastError();
   }
-  const dim3 grid((unsigned)a.n_items * (unsigned)(a.batch * a.heads));
+  const dim3 grid((unsigned)job_count(a));
   // dkv16_f32_kernel: two workgroups per item, laid out in blocks of 16 ids (8 items x 2 halves).
-  const dim3 grid2(16u * (((unsigned)a.n_items * (unsigned)(a.batch * a.heads) + 7u) / 8u));
+  const dim3 grid2(16u * (((unsigned)job_count(a) + 7u) / 8u));
   switch (kind) {
     case Kind::kFwd: hipLaunchKernelGGL(fwd_f32g_kernel<D>, grid, block, 0, stream, a); break;
     case Kind::kDq: hipLaunchKernelGGL(dq_f32_kernel<D>, grid, block, 0, stream, a); break;

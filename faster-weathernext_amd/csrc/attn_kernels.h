@@ -24,6 +24,7 @@ struct KArgs {
   const uint32_t* halves;  // per tile: bit 8r + 2c + h = ... in columns 32c + 16h..; NULL = all live
   const int32_t* items;   // fwn_item[n_items] as int32 quadruples (block, t0, t1, part)
   const int32_t* split;   // [n_split * 3] block, first partial slot, slot count (combine pass)
+  const int32_t* order;   // order table: [n_order][2] (pair b * heads + h, item) per workgroup, or NULL
   float* work;            // partial slots: [n_parts][batch * heads][128][2 * head_dim + 2] float32
   uint16_t* ds;           // dS units (bf16 backward with the dS exchange): [batch * heads][n_units][512]
   const int32_t* ubase;   // dq from dS: first unit of each tile of the forward list
@@ -32,7 +33,7 @@ struct KArgs {
   const uint16_t* xa;     // bf16x3 kernels: split operands, [batch * heads][n][2][head_dim] bf16 (hi row,
   const uint16_t* xb;     //   lo row; written by the split pass): forward k, v; dK/dV q, dout; dQ k
   uint32_t xslice_bytes;  // bytes of one (batch, head) slice of xa / xb: n * 4 * head_dim
-  int32_t n, heads, batch, n_blocks, n_tiles, n_items, n_parts, n_split;
+  int32_t n, heads, batch, n_blocks, n_tiles, n_items, n_parts, n_split, n_order;
   int64_t sb, sn, sh;     // strides of q, k, v, dq, dk, dv
   int64_t osb, osn, osh;  // strides of o, dout
   uint32_t slice_bytes;   // bytes of one (batch, head) slice: ((n - 1) * sn + head_dim) * elem
@@ -65,6 +66,12 @@ inline hipError_t launch(Kind kind, int dtype, int head_dim, const KArgs& a, hip
   if (dtype == 0) return launch_f32(kind, head_dim, a, stream);
   if (kind == Kind::kDelta) return launch_delta_bf16(head_dim, a, stream);
   return launch_bf16(kind, head_dim, a, stream);
+}
+
+// Workgroups of a per-item launch: one per entry of the order table, else one per (item, batch,
+// head).
+__host__ __device__ inline int64_t job_count(const KArgs& a) {
+  return a.order ? (int64_t)a.n_order : (int64_t)a.n_items * a.batch * a.heads;
 }
 
 // Float32 words of one partial slot of one (batch, head): O or dQ or dK rows [128][D], then dV

@@ -67,6 +67,7 @@ __global__ void __launch_bounds__(NT, 2) fwd_x3_kernel(KArgs a) {
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int i = lane & 31, g = lane >> 5;
   const Job j = decode_job(a);
+  if (j.skip) return;  // an empty entry of the order table
   const int64_t xbase = (int64_t)j.bh * a.n * (2 * D);
   const rsrc_t rK = make_rsrc(a.xa + xbase, a.xslice_bytes);
   const rsrc_t rV = make_rsrc(a.xb + xbase, a.xslice_bytes);
@@ -194,6 +195,7 @@ __global__ void __launch_bounds__(NT, 2) dq_x3_ds_kernel(KArgs a) {
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int i = lane & 31, g = lane >> 5;
   const Job j = decode_job(a);
+  if (j.skip) return;  // an empty entry of the order table
   const int64_t xbase = (int64_t)j.bh * a.n * (2 * D);
   const rsrc_t rK = make_rsrc(a.xa + xbase, a.xslice_bytes);
   // The same slice from row 32 on: planes 2, 3 of a half hold its second key group.
@@ -295,7 +297,7 @@ __global__ void __launch_bounds__(NT, 2) dq_x3_ds_kernel(KArgs a) {
 
 template <int D>
 hipError_t launch_d(Kind kind, const KArgs& a, hipStream_t stream) {
-  const dim3 grid((unsigned)a.n_items * (unsigned)(a.batch * a.heads)), block(NT);
+  const dim3 grid((unsigned)job_count(a)), block(NT);
   switch (kind) {
     case Kind::kFwd: hipLaunchKernelGGL(fwd_x3_kernel<D>, grid, block, 0, stream, a); break;
     case Kind::kDqDs: hipLaunchKernelGGL(dq_x3_ds_kernel<D>, grid, block, 0, stream, a); break;

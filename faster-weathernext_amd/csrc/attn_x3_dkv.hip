@@ -94,8 +94,9 @@ __global__ void __launch_bounds__(NT4, 2) dkv16_x3_kernel(KArgs a) {
   // ids 16 i + x and 16 i + 8 + x): pid = 8 i + x is the item's id as decode_job numbers them.
   const int half = (int)(blockIdx.x >> 3) & 1;
   const int pid = (int)(((blockIdx.x >> 4) << 3) | (blockIdx.x & 7));
-  if (pid >= a.n_items * a.batch * a.heads) return;
+  if (pid >= job_count(a)) return;
   const Job j = decode_job(a, pid);
+  if (j.skip) return;  // an empty entry of the order table
   const int kg = 4 * half + wid;  // this wave's 16-key group of the block
   const int64_t xbase = (int64_t)j.bh * a.n * (2 * D);
   const rsrc_t rQ = make_rsrc(a.xa + xbase, a.xslice_bytes);
@@ -346,7 +347,7 @@ __global__ void __launch_bounds__(NT4, 2) dkv16_x3_kernel(KArgs a) {
 template <int D>
 hipError_t launch_d(const KArgs& a, hipStream_t stream) {
   // Two workgroups per item, laid out in blocks of 16 ids (8 items x 2 halves).
-  const dim3 grid(16u * (((unsigned)a.n_items * (unsigned)(a.batch * a.heads) + 7u) / 8u));
+  const dim3 grid(16u * (((unsigned)job_count(a) + 7u) / 8u));
   hipLaunchKernelGGL((dkv16_x3_kernel<D>), grid, dim3(NT4), 0, stream, a);
   return hipGetLastError();
 }

@@ -504,3 +504,101 @@ int fwn_tiles_schedule_fill(int32_t n_blocks, const int32_t* tile_ptr, int32_t m
 }
 
 }  // extern "C"
+
+namespace {
+
+// The jobs of each XCD for an order table (fwn_tiles_order_count / _fill): job j is item
+// j % n_items of pair j / n_items.
+int order_ranges(int32_t n_items, const fwn_item* items, int32_t pairs, int32_t order, int32_t window,
+                 const char* what, std::vector<std::vector<int64_t>>& xcd) {
+  if (n_items <= 0 || !items || pairs <= 0)
+    return fwn::fail(FWN_ERR_INVALID_ARG, "%s: null or empty argument", what);
+  if (order != FWN_ORDER_ITEMS && order != FWN_ORDER_BALANCED)
+    return fwn::fail(FWN_ERR_INVALID_ARG, "%s: unknown order %d", what, order);
+  const int64_t jobs = (int64_t)n_items * pairs;
+  if (jobs > INT32_MAX) return fwn::fail(FWN_ERR_INVALID_ARG, "%s: too many jobs", what);
+  std::vector<int64_t> cost((size_t)n_items);
+  int64_t per_pair = 0;
+  for (int32_t i = 0; i < n_items; ++i) {
+    const int64_t len = (int64_t)items[i].t1 - items[i].t0;
+    if (len < 0) return fwn::fail(FWN_ERR_TILES, "%s: item %d ends before it starts", what, i);
+    cost[i] = FWN_ITEM_COST + len;
+    per_pair += cost[i];
+  }
+  // XCD x takes jobs [bound[x], bound[x + 1]): equal counts as the kernels' own mapping, or the
+  // first job whose running cost reaches x / 8 of the total.
+  int64_t bound[9];
+  if (order == FWN_ORDER_ITEMS) {
+    const int64_t small = jobs / 8, rem = jobs % 8;
+    bound[0] = 0;
+    for (int x = 0; x < 8; ++x) bound[x + 1] = bound[x] + small + (x < rem ? 1 : 0);
+  } else {
+    const int64_t total = per_pair * pairs;
+    int64_t run = 0, j = 0;
+    bound[0] = 0;
+    for (int x = 1; x < 8; ++x) {
+      // first j with run(j) = cost of jobs 0..j >= total * x / 8, as a boundary before job j
+      while (j < jobs && (run + cost[j % n_items]) * 8 < total * x) run += cost[j++ % n_items];
+      bound[x] = j;
+    }
+    bound[8] = jobs;
+  }
+  xcd.assign(8, {});
+  for (int x = 0; x < 8; ++x) {
+    std::vector<int64_t>& r = xcd[x];
+    for (int64_t j = bound[x]; j < bound[x + 1]; ++j) r.push_back(j);
+    if (window > 1)
+      for (size_t w = 0; w < r.size(); w += (size_t)window) {
+        const auto e = r.begin() + (ptrdiff_t)std::min(r.size(), w + (size_t)window);
+        std::stable_sort(r.begin() + (ptrdiff_t)w, e,
+                         [&](int64_t p, int64_t q) { return cost[p % n_items] > cost[q % n_items]; });
+      }
+  }
+  return FWN_OK;
+}
+
+int64_t order_entries(const std::vector<std::vector<int64_t>>& xcd) {
+  size_t most = 0;
+  for (const auto& r : xcd) most = std::max(most, r.size());
+  return 8 * (int64_t)most;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fwn_tiles_order_count(int32_t n_items, const fwn_item* items, int32_t pairs, int32_t order, int32_t window,
+                          int32_t* n_work) {
+  fwn::clear_error();
+  if (!n_work) return fwn::fail(FWN_ERR_INVALID_ARG, "fwn_tiles_order_count: null output");
+  std::vector<std::vector<int64_t>> xcd;
+  if (int rc = order_ranges(n_items, items, pairs, order, window, "fwn_tiles_order_count", xcd)) return rc;
+  const int64_t entries = order_entries(xcd);
+  if (entries > INT32_MAX) return fwn::fail(FWN_ERR_INVALID_ARG, "fwn_tiles_order_count: too many entries");
+  *n_work = (int32_t)entries;
+  return FWN_OK;
+}
+
+int fwn_tiles_order_fill(int32_t n_items, const fwn_item* items, int32_t pairs, int32_t order, int32_t window,
+                         int32_t* work) {
+  fwn::clear_error();
+  if (!work) return fwn::fail(FWN_ERR_INVALID_ARG, "fwn_tiles_order_fill: null output");
+  std::vector<std::vector<int64_t>> xcd;
+  if (int rc = order_ranges(n_items, items, pairs, order, window, "fwn_tiles_order_fill", xcd)) return rc;
+  const int64_t entries = order_entries(xcd);
+  if (entries > INT32_MAX) return fwn::fail(FWN_ERR_INVALID_ARG, "fwn_tiles_order_fill: too many entries");
+  // The k-th job of XCD x goes to workgroup 8 k + x; the rest are padding.
+  for (int64_t w = 0; w < entries; ++w) {
+    work[2 * w] = -1;
+    work[2 * w + 1] = 0;
+  }
+  for (int x = 0; x < 8; ++x)
+    for (size_t k = 0; k < xcd[x].size(); ++k) {
+      const int64_t j = xcd[x][k], w = 8 * (int64_t)k + x;
+      work[2 * w] = (int32_t)(j / n_items);
+      work[2 * w + 1] = (int32_t)(j % n_items);
+    }
+  return FWN_OK;
+}
+
+}  // extern "C"

@@ -42,9 +42,28 @@ _DTYPES = {torch.float32: nat.F32, torch.bfloat16: nat.BF16}
 WIDE_ITEM_TILES = 128
 WIDE_JOBS = 1536
 
+# Order tables (fwn_tiles_order_fill) for bf16 calls whose per-item launch has fewer than
+# ORDER_JOBS jobs: each XCD takes a contiguous range of equal estimated cost, run longest first
+# within windows of two rounds of its slots: ORDER_WINDOW jobs for the forward and dQ (64
+# workgroups per XCD), ORDER_WINDOW_KV for dK/dV (32). Measured on MI355X (bf16 fwd+bwd step,
+# three runs each on one box): C3 1.562 -> 1.496 ms, the C5 attention shape 2.897 -> 2.852 ms.
+# Windows of 128 for dK/dV as well gave C3 1.490 and C5 2.899; no window (equal-cost ranges in
+# block order) C3 1.50-1.52; sorting whole ranges, or all jobs, longest first lost the
+# neighbouring blocks' shared K/V and dS reads (C5 dQ +6% and +30%). With many jobs per slot
+# (C4's 10,464) the plain ranges are already even, so such calls keep the plain order.
+ORDER_JOBS = 4096
+ORDER_WINDOW = 128
+ORDER_WINDOW_KV = 64
+
+
+def ordered(desc):
+  """True when a call with descriptor `desc` takes an order table (bf16 products)."""
+  return desc.dtype == nat.BF16 and desc.precision == nat.PREC_NATIVE
+
 
 class _Schedule:
-  """One split-K schedule of a TileList: its work items, split records and C struct."""
+  """One split-K schedule of a TileList: its work items, split records and C struct, plus the
+  order tables built for it (``ordered_struct``)."""
 
   def __init__(self, tl, tile_ptr, cap):
     L = nat.lib()
@@ -59,10 +78,35 @@ class _Schedule:
     self.split_host = split[:self.n_split]
     self.items = torch.from_numpy(items).to(tl.device)
     self.split = torch.from_numpy(split).to(tl.device)
-    addr = lambda t: t.data_ptr() if t.numel() else None
-    self.struct = nat.Tiles(tl.n_blocks, tl.n_tiles, addr(tl.ptr), addr(tl.col), addr(tl.lanes), addr(tl.groups),
-                            self.n_items, self.n_parts, self.n_split, 0, addr(self.items),
-                            addr(self.split) if self.n_split else None, addr(tl.halves))
+    self._tl = tl
+    self._orders = {}
+    self.struct = self._struct()
+
+  def _struct(self, work=None, pairs=0):
+    addr = lambda t: t.data_ptr() if t is not None and t.numel() else None
+    tl = self._tl
+    return nat.Tiles(tl.n_blocks, tl.n_tiles, addr(tl.ptr), addr(tl.col), addr(tl.lanes), addr(tl.groups),
+                     self.n_items, self.n_parts, self.n_split, 0 if work is None else work.shape[0],
+                     addr(self.items), addr(self.split) if self.n_split else None, addr(tl.halves), addr(work),
+                     pairs, 0)
+
+  def order_table(self, pairs, order=nat.ORDER_BALANCED, window=ORDER_WINDOW):
+    """Host order table [n_work, 2] of this schedule for calls of `pairs` (batch, head) pairs."""
+    L = nat.lib()
+    n = np.zeros(1, np.int32)
+    args = (self.n_items, nat.ptr(self.items_host), int(pairs), int(order), int(window))
+    nat.check(L.fwn_tiles_order_count(*args, nat.ptr(n)))
+    work = np.zeros((int(n[0]), 2), np.int32)
+    nat.check(L.fwn_tiles_order_fill(*args, nat.ptr(work)))
+    return work
+
+  def ordered_struct(self, pairs, order=nat.ORDER_BALANCED, window=ORDER_WINDOW):
+    """The C struct with an order table for calls of `pairs` (batch, head) pairs (built once)."""
+    key = (int(pairs), int(order), int(window))
+    if key not in self._orders:
+      work = torch.from_numpy(self.order_table(pairs, order, window)).to(self._tl.device)
+      self._orders[key] = (work, self._struct(work, int(pairs)))
+    return self._orders[key][1]
 
 
 class TileList:
@@ -137,15 +181,30 @@ class TileList:
     """The split-K schedule a call of `batch` x `heads` launches (items, split blocks, C struct)."""
     return self._schedule(self.item_cap_for(batch, heads))
 
-  def struct_for(self, batch, heads):
-    """The C struct to launch a call of `batch` x `heads` with (the schedule chosen for it)."""
-    return self.schedule_for(batch, heads).struct
+  def order_for(self, batch, heads):
+    """Whether a bf16 call of `batch` x `heads` takes an order table: fewer than ORDER_JOBS jobs
+    in its per-item launch."""
+    sch = self.schedule_for(batch, heads)
+    return sch.n_items * int(batch) * int(heads) < ORDER_JOBS
+
+  def struct_for(self, batch, heads, order=False, window=ORDER_WINDOW):
+    """The C struct to launch a call of `batch` x `heads` with (the schedule chosen for it); with
+    `order` (bf16 calls, ``ordered``) and few jobs (``order_for``), with its order table."""
+    sch = self.schedule_for(batch, heads)
+    if order and self.order_for(batch, heads):
+      return sch.ordered_struct(int(batch) * int(heads), nat.ORDER_BALANCED, window)
+    return sch.struct
+
+  def struct_for_desc(self, desc, kv=False):
+    """The C struct for a call with descriptor `desc`: for the forward and dQ kernels, or with
+    `kv` for dK/dV (this list as a transposed list)."""
+    return self.struct_for(desc.batch, desc.heads, ordered(desc), ORDER_WINDOW_KV if kv else ORDER_WINDOW)
 
   def workspace_bytes(self, desc):
     """Workspace the launchers need for this list and the call shape `desc`: the size for the
-    schedule ``struct_for`` picks for it (0 if that schedule splits no block)."""
+    schedule ``struct_for_desc`` picks for it (0 if that schedule splits no block)."""
     n = ctypes.c_uint64(0)
-    nat.check(nat.lib().fwn_attn_workspace_size(desc, self.struct_for(desc.batch, desc.heads), ctypes.byref(n)))
+    nat.check(nat.lib().fwn_attn_workspace_size(desc, self.struct_for_desc(desc), ctypes.byref(n)))
     return int(n.value)
 
   def ds_map(self, tiles_t, unit_keys=16):
@@ -349,7 +408,7 @@ def attention_forward(q, k, v, tiles, scale, with_lse=True, precision="native"):
   tl = _as_tiles(tiles, q.shape[1], q.device)
   lse = torch.empty((q.shape[0], q.shape[2], q.shape[1]), dtype=torch.float32, device=q.device) if with_lse else None
   ws = workspace(desc, q.device, tl)
-  ts = tl.struct_for(desc.batch, desc.heads)
+  ts = tl.struct_for_desc(desc)
   nat.check(nat.lib().fwn_attn_fwd_launch(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), ts, out.data_ptr(),
                                           lse.data_ptr() if with_lse else None, *_ws_args(ws), _stream(q.device)))
   return out, lse
@@ -396,7 +455,7 @@ def _backward_into(q, k, v, out, lse, dout, tiles, tiles_t, scale, dq, dk, dv, p
     desc = _desc(q, scale, out, _precision(precision, q.dtype))
     ws = workspace(desc, q.device, tl, tlt)
     ds = torch.empty(max(dmap.ds_bytes(desc), 256), dtype=torch.uint8, device=q.device)
-    ts, tst = tl.struct_for(desc.batch, desc.heads), tlt.struct_for(desc.batch, desc.heads)
+    ts, tst = tl.struct_for_desc(desc), tlt.struct_for_desc(desc, kv=True)
     nat.check(L.fwn_attn_bwd_ds_launch(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
                                        dout.data_ptr(), lse.data_ptr(), delta.data_ptr(), ts, tst, dmap.struct,
                                        dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ds.data_ptr(), ds.numel(),
@@ -406,7 +465,7 @@ def _backward_into(q, k, v, out, lse, dout, tiles, tiles_t, scale, dq, dk, dv, p
   nat.check(L.fwn_attn_bwd_delta_launch(desc, out.data_ptr(), dout.data_ptr(), delta.data_ptr(), main.cuda_stream))
   side = _side_stream(q.device)
   side.wait_stream(main)
-  ts, tst = tl.struct_for(desc.batch, desc.heads), tlt.struct_for(desc.batch, desc.heads)
+  ts, tst = tl.struct_for_desc(desc), tlt.struct_for_desc(desc, kv=True)
   nat.check(L.fwn_attn_bwd_dkv_launch(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), dout.data_ptr(),
                                       lse.data_ptr(), delta.data_ptr(), tst, dk.data_ptr(), dv.data_ptr(),
                                       *_ws_args(ws_kv), side.cuda_stream))

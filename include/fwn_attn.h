@@ -114,13 +114,22 @@ typedef struct fwn_tiles {
   int32_t n_items;          /* work items: every block appears, empty blocks included */
   int32_t n_parts;          /* partial slots (items with part >= 0) */
   int32_t n_split;          /* blocks cut into more than one item */
-  int32_t reserved;         /* 0 */
+  int32_t n_work;           /* entries of the order table `work`, or 0 */
   const fwn_item* items;    /* [n_items], in block order */
   const int32_t* split;     /* [n_split * 3]: block, first partial slot, slot count */
   const uint32_t* halves;   /* [n_tiles] or NULL: bit 8r + 2c + h set when rows 32r..32r+31 of the
                                tile have a valid element in columns 32c + 16h .. +15; the bf16 dq
                                kernel skips the other 16-column halves of live groups (NULL:
                                every half of a live group is processed) */
+  const int32_t* work;      /* [n_work][2] or NULL: the order table (fwn_tiles_order_fill).
+                               Workgroup w runs item work[2w + 1] of (batch, head) pair work[2w]
+                               (pair b * heads + h), or nothing when the entry is outside the
+                               call's pairs or items (padding). NULL: workgroup w runs job w of
+                               the jobs in (batch, head)-major, item order, each XCD taking a
+                               contiguous range of them. */
+  int32_t work_pairs;       /* batch * heads the order table was built for (launches of another
+                               shape are refused) */
+  int32_t reserved;         /* 0 */
 } fwn_tiles;
 
 /* Thread-local message of the last failure on this thread ("" if none). */
@@ -179,6 +188,25 @@ int fwn_tiles_schedule_count(int32_t n_blocks, const int32_t* tile_ptr, int32_t 
                              int32_t* n_items, int32_t* n_parts, int32_t* n_split);
 int fwn_tiles_schedule_fill(int32_t n_blocks, const int32_t* tile_ptr, int32_t max_item_tiles,
                             fwn_item* items, int32_t* split);
+
+/* Order table of a per-item schedule for calls of `pairs` (batch, head) pairs (no counterpart in
+ * the reference, whose grid runs one program per block in block order). The GPU deals workgroups
+ * round-robin over its 8 XCDs (workgroup w to XCD w mod 8), each with its own L2; each XCD then
+ * starts its workgroups in id order as slots free up. The table gives each XCD a contiguous range
+ * of the jobs ((batch, head)-major, then items in block order, as without a table): of equal
+ * count with FWN_ORDER_ITEMS (the same jobs on the same workgroups as no table), of equal
+ * estimated cost (FWN_ITEM_COST plus the item's tiles) with FWN_ORDER_BALANCED. With window > 1
+ * each consecutive `window` jobs of a range run longest first, so short jobs end the launch
+ * while the jobs running together stay neighbours. Ranges of unequal count leave padding entries
+ * (pair -1) that exit at once. fwn_tiles_order_count gives n_work; fwn_tiles_order_fill writes
+ * work[n_work * 2] (host buffer). */
+#define FWN_ITEM_COST 3
+#define FWN_ORDER_ITEMS 0
+#define FWN_ORDER_BALANCED 1
+int fwn_tiles_order_count(int32_t n_items, const fwn_item* items, int32_t pairs, int32_t order, int32_t window,
+                          int32_t* n_work);
+int fwn_tiles_order_fill(int32_t n_items, const fwn_item* items, int32_t pairs, int32_t order, int32_t window,
+                         int32_t* work);
 
 /* ---------------------------------------------------------------------------------------------
  * Device launchers (enqueue on `stream`).

@@ -241,6 +241,161 @@ def test_schedule_covers_every_tile_once(max_item_tiles):
   assert n_parts == int(per_block[per_block > 1].sum())
 
 
+def _order(items, pairs, order, window=0):
+  L = nat.lib()
+  n = np.zeros(1, np.int32)
+  nat.check(L.fwn_tiles_order_count(len(items), nat.ptr(items), pairs, order, window, nat.ptr(n)))
+  work = np.full((int(n[0]), 2), -7, np.int32)
+  nat.check(L.fwn_tiles_order_fill(len(items), nat.ptr(items), pairs, order, window, nat.ptr(work)))
+  return work
+
+
+def _xcd_jobs(work, n_items):
+  """Per XCD (entry w runs on XCD w % 8), the jobs (pair * n_items + item) of its non-padding
+  entries in launch order."""
+  jobs = [[] for _ in range(8)]
+  for w, (pair, item) in enumerate(work):
+    if pair >= 0:
+      jobs[w % 8].append(int(pair) * n_items + int(item))
+  return jobs
+
+
+@pytest.mark.parametrize("order,window", [(nat.ORDER_ITEMS, 0), (nat.ORDER_BALANCED, 0), (nat.ORDER_BALANCED, 1),
+                                          (nat.ORDER_BALANCED, 7), (nat.ORDER_BALANCED, 128),
+                                          (nat.ORDER_ITEMS, 32)])
+@pytest.mark.parametrize("pairs", [1, 3, 8, 13])
+def test_order_table_runs_every_job_once_in_contiguous_xcd_ranges(pairs, order, window):
+  """An order table runs every (pair, item) job exactly once; XCD x (entries w = x mod 8) takes a
+  contiguous range of the jobs in (pair, item) order, the ranges in XCD order; padding entries
+  have pair -1. ITEMS: equal counts (without a window, the kernels' own mapping without a table,
+  workgroup for workgroup). BALANCED: each range's cost (FWN_ITEM_COST + tiles per job) is the
+  even share total / 8 to within one job's cost. A window w > 1 sorts each consecutive w jobs of
+  a range longest first (stable: ties in job order); w <= 1 keeps job order."""
+  rng = np.random.default_rng(pairs)
+  counts = rng.integers(0, 200, 70)
+  counts[:4] = 320  # long blocks first, as the subdivision order's coarse nodes
+  tp = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+  items, _, _ = _schedule(tp, 64)
+  ni = len(items)
+  cost = nat.ITEM_COST + items[:, 2] - items[:, 1]
+  jcost = np.tile(cost, pairs)
+  work = _order(items, pairs, order, window)
+  total = ni * pairs
+  assert len(work) % 8 == 0 and (work[:, 0] >= -1).all() and (work[:, 0] < pairs).all()
+  assert ((work[:, 1] >= 0) & (work[:, 1] < ni)).all()
+  assert (work[work[:, 0] < 0, 1] == 0).all()
+  per = _xcd_jobs(work, ni)
+  assert sorted(j for r in per for j in r) == list(range(total))
+  starts = [min(r) if r else None for r in per]
+  lo = 0
+  for r in per:
+    assert sorted(r) == list(range(lo, lo + len(r)))
+    lo += len(r)
+  # Every XCD's entries are its first len(r) slots (no padding between jobs).
+  assert len(work) == 8 * max(len(r) for r in per)
+  if order == nat.ORDER_ITEMS:
+    small, rem = divmod(total, 8)
+    assert [len(r) for r in per] == [small + (x < rem) for x in range(8)]
+    assert len(work) == 8 * (small + (rem > 0))
+  else:
+    share = jcost.sum() / 8
+    for r in per:
+      assert abs(jcost[r].sum() - share) <= jcost.max()
+  if window <= 1:
+    assert all(r == sorted(r) for r in per)
+    if order == nat.ORDER_ITEMS:
+      # the kernels' mapping without a table: workgroup 8 k + x runs the k-th job of XCD x
+      for w in range(total):
+        x, k = w % 8, w // 8
+        job = x * (small + 1) + k if x < rem else rem * (small + 1) + (x - rem) * small + k
+        assert tuple(work[w]) == (job // ni, job % ni)
+  else:
+    for r in per:
+      for w0 in range(0, len(r), window):
+        win = r[w0:w0 + window]
+        assert win == sorted(sorted(win), key=lambda j: -jcost[j])  # stable: ties in job order
+    plain = _xcd_jobs(_order(items, pairs, order), ni)
+    assert [[sorted(r[w0:w0 + window]) for w0 in range(0, len(r), window)] for r in per] == \
+        [[r[w0:w0 + window] for w0 in range(0, len(r), window)] for r in plain]
+
+
+def test_order_table_known_answer():
+  """Two pairs of five items, tiles 10, 0, 50, 4, 20 (costs 13, 3, 53, 7, 23; 198 for the ten
+  jobs, 24.75 an XCD): the running costs 13, 16, 69, 76, 99, 112, 115, 168, 175, 198 reach
+  x / 8 of the total (24.75 x) first at jobs 2 (x = 1, 2), 3 (x = 3), 4 (x = 4), 7 (x = 5, 6)
+  and 8 (x = 7): XCD ranges [0, 2), [], [2, 3), [3, 4), [4, 7), [], [7, 8), [8, 10)."""
+  lens = [10, 0, 50, 4, 20]
+  t = np.concatenate([[0], np.cumsum(lens)])
+  items = np.array([[b, t[b], t[b + 1], -1] for b in range(5)], np.int32)
+  work = _order(items, 2, nat.ORDER_BALANCED)
+  per = _xcd_jobs(work, 5)
+  assert per == [[0, 1], [], [2], [3], [4, 5, 6], [], [7], [8, 9]]
+  assert len(work) == 24 and tuple(work[8 * 2 + 4]) == (1, 1)  # XCD 4's third job: pair 1, item 1
+  per = _xcd_jobs(_order(items, 2, nat.ORDER_BALANCED, 2), 5)
+  # windows of two: job 9 (23) before job 8 (7); job 4 (23) before 5 (13), then 6 alone
+  assert per == [[0, 1], [], [2], [3], [4, 5, 6], [], [7], [9, 8]]
+  per = _xcd_jobs(_order(items, 2, nat.ORDER_ITEMS, 4), 5)  # counts 2, 2, 1, 1, 1, 1, 1, 1
+  assert per == [[0, 1], [2, 3], [4], [5], [6], [7], [8], [9]]
+  per = _xcd_jobs(_order(items, 1, nat.ORDER_ITEMS, 0), 5)  # 5 jobs: XCDs 0-4 one each
+  assert per == [[0], [1], [2], [3], [4], [], [], []]
+
+
+def test_order_table_rejects_bad_arguments():
+  L = nat.lib()
+  items = np.array([[0, 0, 5, -1], [1, 5, 9, -1]], np.int32)
+  n = np.zeros(1, np.int32)
+  assert L.fwn_tiles_order_count(2, nat.ptr(items), 2, 7, 0, nat.ptr(n)) == nat.ERR_INVALID_ARG
+  assert b"unknown order" in L.fwn_last_error()
+  assert L.fwn_tiles_order_count(0, nat.ptr(items), 2, 1, 0, nat.ptr(n)) == nat.ERR_INVALID_ARG
+  assert L.fwn_tiles_order_count(2, nat.ptr(items), 0, 1, 0, nat.ptr(n)) == nat.ERR_INVALID_ARG
+  bad = items.copy()
+  bad[1, 2] = 4
+  assert L.fwn_tiles_order_count(2, nat.ptr(bad), 2, 1, 0, nat.ptr(n)) == nat.ERR_TILES
+  assert L.fwn_tiles_order_fill(2, nat.ptr(items), 2, 1, 0, None) == nat.ERR_INVALID_ARG
+
+
+def test_tile_list_orders_bf16_calls_with_few_jobs():
+  """bf16 calls whose per-item launch has fewer than ORDER_JOBS jobs get the schedule's
+  windowed order table for their (batch, head) count; float32 and bf16x3 calls and calls with
+  many jobs get none; the workspace does not depend on the table."""
+  from faster_weathernext_amd import hip_attn
+  mask, _, _, _ = fwn.mesh_mask(5, 4)
+  tl = hip_attn.TileList.from_mask(mask, device="cpu")
+  n = mask.shape[0]
+  bf16 = nat.AttnDesc(1, n, 4, 64, nat.BF16, 0.1, 4 * 64, 4 * 64, 64)
+  f32 = nat.AttnDesc(1, n, 4, 64, nat.F32, 0.1, 4 * 64, 4 * 64, 64)
+  x3 = nat.AttnDesc(1, n, 4, 64, nat.F32, 0.1, 4 * 64, 4 * 64, 64, 0, 0, 0, nat.PREC_BF16X3, 0)
+  sch = tl.schedule_for(1, 4)
+  st = tl.struct_for_desc(bf16)
+  assert tl.order_for(1, 4) and st.work and st.work_pairs == 4
+  table = sch.order_table(4, nat.ORDER_BALANCED, hip_attn.ORDER_WINDOW)
+  assert st.n_work == len(table) and tl.struct_for_desc(bf16) is st  # built once
+  kv = tl.struct_for_desc(bf16, kv=True)
+  assert kv.n_work == len(sch.order_table(4, nat.ORDER_BALANCED, hip_attn.ORDER_WINDOW_KV))
+  for d in (f32, x3):
+    assert tl.struct_for_desc(d).n_work == 0 and not tl.struct_for_desc(d).work
+  for desc in (bf16, f32):
+    size = ctypes.c_uint64(0)
+    nat.check(nat.lib().fwn_attn_workspace_size(desc, sch.struct, ctypes.byref(size)))
+    assert tl.workspace_bytes(desc) == int(size.value)
+  many = -(-hip_attn.ORDER_JOBS // (sch.n_items * 4))
+  assert not tl.order_for(many, 4) and tl.struct_for(many, 4, order=True).n_work == 0
+
+
+@pytest.mark.parametrize("case", ["pairs", "short", "no_table"])
+def test_launchers_reject_order_tables_that_do_not_fit_the_call(case):
+  tiles = _tiles()  # 3 items
+  if case == "pairs":
+    tiles.work, tiles.n_work, tiles.work_pairs = FAKE, 48, 1
+  elif case == "short":
+    tiles.work, tiles.n_work, tiles.work_pairs = FAKE, 5, 2
+  else:
+    tiles.n_work = 8
+  size = ctypes.c_uint64(0)
+  assert nat.lib().fwn_attn_workspace_size(_desc(n=300), tiles, ctypes.byref(size)) == nat.ERR_TILES  # heads 2
+  assert b"order table" in nat.lib().fwn_last_error()
+
+
 @pytest.mark.parametrize("case", ["ptr0", "decreasing", "col_range", "col_order", "total", "tail_bits"])
 def test_prepare_rejects_malformed_lists(case):
   n = 300
