@@ -509,10 +509,11 @@ namespace {
 
 // The jobs of each XCD for an order table (fwn_tiles_order_count / _fill): job j is item
 // j % n_items of pair j / n_items.
-int order_ranges(int32_t n_items, const fwn_item* items, int32_t pairs, int32_t order, int32_t window,
-                 const char* what, std::vector<std::vector<int64_t>>& xcd) {
-  if (n_items <= 0 || !items || pairs <= 0)
-    return fwn::fail(FWN_ERR_INVALID_ARG, "%s: null or empty argument", what);
+int order_ranges(int32_t n_items, const fwn_item* items, const int32_t* tile_cost, int32_t item_cost,
+                 int32_t pairs, int32_t order, int32_t window, const char* what,
+                 std::vector<std::vector<int64_t>>& xcd) {
+  if (n_items <= 0 || !items || pairs <= 0 || item_cost < 0)
+    return fwn::fail(FWN_ERR_INVALID_ARG, "%s: null, empty or negative argument", what);
   if (order != FWN_ORDER_ITEMS && order != FWN_ORDER_BALANCED)
     return fwn::fail(FWN_ERR_INVALID_ARG, "%s: unknown order %d", what, order);
   const int64_t jobs = (int64_t)n_items * pairs;
@@ -521,27 +522,39 @@ int order_ranges(int32_t n_items, const fwn_item* items, int32_t pairs, int32_t 
   int64_t per_pair = 0;
   for (int32_t i = 0; i < n_items; ++i) {
     const int64_t len = (int64_t)items[i].t1 - items[i].t0;
-    if (len < 0) return fwn::fail(FWN_ERR_TILES, "%s: item %d ends before it starts", what, i);
-    cost[i] = FWN_ITEM_COST + len;
+    if (len < 0 || items[i].t0 < 0) return fwn::fail(FWN_ERR_TILES, "%s: item %d has no valid tile range", what, i);
+    cost[i] = item_cost;
+    if (!tile_cost) {
+      cost[i] += len;
+    } else {
+      for (int32_t t = items[i].t0; t < items[i].t1; ++t) {
+        if (tile_cost[t] < 0) return fwn::fail(FWN_ERR_INVALID_ARG, "%s: tile %d has a negative cost", what, t);
+        cost[i] += tile_cost[t];
+      }
+    }
     per_pair += cost[i];
   }
-  // XCD x takes jobs [bound[x], bound[x + 1]): equal counts as the kernels' own mapping, or the
-  // first job whose running cost reaches x / 8 of the total.
+  // XCD x takes jobs [bound[x], bound[x + 1]): equal counts as the kernels' own mapping, or, by
+  // cost, the jobs whose cost midpoint lies in [x / 8, (x + 1) / 8) of the total (each range
+  // then costs its share to within one job).
   int64_t bound[9];
-  if (order == FWN_ORDER_ITEMS) {
+  const int64_t total = per_pair * pairs;
+  if (order == FWN_ORDER_ITEMS || total == 0) {
     const int64_t small = jobs / 8, rem = jobs % 8;
     bound[0] = 0;
     for (int x = 0; x < 8; ++x) bound[x + 1] = bound[x] + small + (x < rem ? 1 : 0);
   } else {
-    const int64_t total = per_pair * pairs;
-    int64_t run = 0, j = 0;
+    int64_t before = 0;
+    int x = 0;
     bound[0] = 0;
-    for (int x = 1; x < 8; ++x) {
-      // first j with run(j) = cost of jobs 0..j >= total * x / 8, as a boundary before job j
-      while (j < jobs && (run + cost[j % n_items]) * 8 < total * x) run += cost[j++ % n_items];
-      bound[x] = j;
+    for (int64_t j = 0; j < jobs; ++j) {
+      const int64_t c = cost[j % n_items];
+      // twice the midpoint, 2 before + c, in eighths of the total: XCD (2 before + c) * 4 / total
+      const int64_t xj = std::min<int64_t>(7, (2 * before + c) * 4 / total);
+      while (x < xj) bound[++x] = j;
+      before += c;
     }
-    bound[8] = jobs;
+    while (x < 8) bound[++x] = jobs;
   }
   xcd.assign(8, {});
   for (int x = 0; x < 8; ++x) {
@@ -567,24 +580,26 @@ int64_t order_entries(const std::vector<std::vector<int64_t>>& xcd) {
 
 extern "C" {
 
-int fwn_tiles_order_count(int32_t n_items, const fwn_item* items, int32_t pairs, int32_t order, int32_t window,
-                          int32_t* n_work) {
+int fwn_tiles_order_count(int32_t n_items, const fwn_item* items, const int32_t* tile_cost, int32_t item_cost,
+                          int32_t pairs, int32_t order, int32_t window, int32_t* n_work) {
   fwn::clear_error();
   if (!n_work) return fwn::fail(FWN_ERR_INVALID_ARG, "fwn_tiles_order_count: null output");
   std::vector<std::vector<int64_t>> xcd;
-  if (int rc = order_ranges(n_items, items, pairs, order, window, "fwn_tiles_order_count", xcd)) return rc;
+  if (int rc = order_ranges(n_items, items, tile_cost, item_cost, pairs, order, window, "fwn_tiles_order_count", xcd))
+    return rc;
   const int64_t entries = order_entries(xcd);
   if (entries > INT32_MAX) return fwn::fail(FWN_ERR_INVALID_ARG, "fwn_tiles_order_count: too many entries");
   *n_work = (int32_t)entries;
   return FWN_OK;
 }
 
-int fwn_tiles_order_fill(int32_t n_items, const fwn_item* items, int32_t pairs, int32_t order, int32_t window,
-                         int32_t* work) {
+int fwn_tiles_order_fill(int32_t n_items, const fwn_item* items, const int32_t* tile_cost, int32_t item_cost,
+                         int32_t pairs, int32_t order, int32_t window, int32_t* work) {
   fwn::clear_error();
   if (!work) return fwn::fail(FWN_ERR_INVALID_ARG, "fwn_tiles_order_fill: null output");
   std::vector<std::vector<int64_t>> xcd;
-  if (int rc = order_ranges(n_items, items, pairs, order, window, "fwn_tiles_order_fill", xcd)) return rc;
+  if (int rc = order_ranges(n_items, items, tile_cost, item_cost, pairs, order, window, "fwn_tiles_order_fill", xcd))
+    return rc;
   const int64_t entries = order_entries(xcd);
   if (entries > INT32_MAX) return fwn::fail(FWN_ERR_INVALID_ARG, "fwn_tiles_order_fill: too many entries");
   // The k-th job of XCD x goes to workgroup 8 k + x; the rest are padding.

@@ -54,6 +54,14 @@ WIDE_JOBS = 1536
 ORDER_JOBS = 4096
 ORDER_WINDOW = 128
 ORDER_WINDOW_KV = 64
+# A job's estimated cost: ORDER_ITEM_UNITS, plus per tile ORDER_TILE_UNITS and ORDER_HALF_UNITS
+# per live 32 x 16 half (the tile's set half bits). Fitted to per-workgroup durations at C3 and
+# the C5 shape (the tile count alone misjudged C3's sparse coarse-node blocks; with the halves
+# the predicted per-XCD work follows the measured XCD end times, correlation 0.9-1.0). Measured
+# against tiles + 3 per item: C3 1.493 -> 1.482 ms, C5 shape 2.871 -> 2.868 ms.
+ORDER_ITEM_UNITS = 20
+ORDER_TILE_UNITS = 20
+ORDER_HALF_UNITS = 1
 
 
 def ordered(desc):
@@ -94,7 +102,10 @@ class _Schedule:
     """Host order table [n_work, 2] of this schedule for calls of `pairs` (batch, head) pairs."""
     L = nat.lib()
     n = np.zeros(1, np.int32)
-    args = (self.n_items, nat.ptr(self.items_host), int(pairs), int(order), int(window))
+    halves = np.unpackbits(self._tl.halves_host.astype("<u4").view(np.uint8).reshape(-1, 4), axis=1).sum(1)
+    cost = (ORDER_TILE_UNITS + ORDER_HALF_UNITS * halves).astype(np.int32)
+    args = (self.n_items, nat.ptr(self.items_host), nat.ptr(cost) if len(cost) else None, ORDER_ITEM_UNITS,
+            int(pairs), int(order), int(window))
     nat.check(L.fwn_tiles_order_count(*args, nat.ptr(n)))
     work = np.zeros((int(n[0]), 2), np.int32)
     nat.check(L.fwn_tiles_order_fill(*args, nat.ptr(work)))

@@ -195,18 +195,18 @@ int fwn_tiles_schedule_fill(int32_t n_blocks, const int32_t* tile_ptr, int32_t m
  * starts its workgroups in id order as slots free up. The table gives each XCD a contiguous range
  * of the jobs ((batch, head)-major, then items in block order, as without a table): of equal
  * count with FWN_ORDER_ITEMS (the same jobs on the same workgroups as no table), of equal
- * estimated cost (FWN_ITEM_COST plus the item's tiles) with FWN_ORDER_BALANCED. With window > 1
- * each consecutive `window` jobs of a range run longest first, so short jobs end the launch
- * while the jobs running together stay neighbours. Ranges of unequal count leave padding entries
- * (pair -1) that exit at once. fwn_tiles_order_count gives n_work; fwn_tiles_order_fill writes
- * work[n_work * 2] (host buffer). */
-#define FWN_ITEM_COST 3
+ * estimated cost with FWN_ORDER_BALANCED. An item's cost is item_cost plus tile_cost[t] over its
+ * tiles (tile_cost NULL: 1 per tile; else at least as many entries as the largest t1, none
+ * negative). With window > 1 each consecutive `window` jobs of a range run longest first, so
+ * short jobs end the launch while the jobs running together stay neighbours. Ranges of unequal
+ * count leave padding entries (pair -1) that exit at once. fwn_tiles_order_count gives n_work;
+ * fwn_tiles_order_fill writes work[n_work * 2] (host buffers). */
 #define FWN_ORDER_ITEMS 0
 #define FWN_ORDER_BALANCED 1
-int fwn_tiles_order_count(int32_t n_items, const fwn_item* items, int32_t pairs, int32_t order, int32_t window,
-                          int32_t* n_work);
-int fwn_tiles_order_fill(int32_t n_items, const fwn_item* items, int32_t pairs, int32_t order, int32_t window,
-                         int32_t* work);
+int fwn_tiles_order_count(int32_t n_items, const fwn_item* items, const int32_t* tile_cost, int32_t item_cost,
+                          int32_t pairs, int32_t order, int32_t window, int32_t* n_work);
+int fwn_tiles_order_fill(int32_t n_items, const fwn_item* items, const int32_t* tile_cost, int32_t item_cost,
+                         int32_t pairs, int32_t order, int32_t window, int32_t* work);
 
 /* ---------------------------------------------------------------------------------------------
  * Device launchers (enqueue on `stream`).

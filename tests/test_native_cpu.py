@@ -241,12 +241,16 @@ def test_schedule_covers_every_tile_once(max_item_tiles):
   assert n_parts == int(per_block[per_block > 1].sum())
 
 
-def _order(items, pairs, order, window=0):
+ITEM_COST = 3  # the item cost these tests pass (tile costs of 1 when no per-tile costs are given)
+
+
+def _order(items, pairs, order, window=0, tile_cost=None, item_cost=ITEM_COST):
   L = nat.lib()
   n = np.zeros(1, np.int32)
-  nat.check(L.fwn_tiles_order_count(len(items), nat.ptr(items), pairs, order, window, nat.ptr(n)))
+  tc = nat.ptr(tile_cost) if tile_cost is not None else None
+  nat.check(L.fwn_tiles_order_count(len(items), nat.ptr(items), tc, item_cost, pairs, order, window, nat.ptr(n)))
   work = np.full((int(n[0]), 2), -7, np.int32)
-  nat.check(L.fwn_tiles_order_fill(len(items), nat.ptr(items), pairs, order, window, nat.ptr(work)))
+  nat.check(L.fwn_tiles_order_fill(len(items), nat.ptr(items), tc, item_cost, pairs, order, window, nat.ptr(work)))
   return work
 
 
@@ -268,7 +272,7 @@ def test_order_table_runs_every_job_once_in_contiguous_xcd_ranges(pairs, order, 
   """An order table runs every (pair, item) job exactly once; XCD x (entries w = x mod 8) takes a
   contiguous range of the jobs in (pair, item) order, the ranges in XCD order; padding entries
   have pair -1. ITEMS: equal counts (without a window, the kernels' own mapping without a table,
-  workgroup for workgroup). BALANCED: each range's cost (FWN_ITEM_COST + tiles per job) is the
+  workgroup for workgroup). BALANCED: each range's cost (item cost 3 + tiles per job) is the
   even share total / 8 to within one job's cost. A window w > 1 sorts each consecutive w jobs of
   a range longest first (stable: ties in job order); w <= 1 keeps job order."""
   rng = np.random.default_rng(pairs)
@@ -277,7 +281,7 @@ def test_order_table_runs_every_job_once_in_contiguous_xcd_ranges(pairs, order, 
   tp = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
   items, _, _ = _schedule(tp, 64)
   ni = len(items)
-  cost = nat.ITEM_COST + items[:, 2] - items[:, 1]
+  cost = ITEM_COST + items[:, 2] - items[:, 1]
   jcost = np.tile(cost, pairs)
   work = _order(items, pairs, order, window)
   total = ni * pairs
@@ -320,38 +324,59 @@ def test_order_table_runs_every_job_once_in_contiguous_xcd_ranges(pairs, order, 
 
 
 def test_order_table_known_answer():
-  """Two pairs of five items, tiles 10, 0, 50, 4, 20 (costs 13, 3, 53, 7, 23; 198 for the ten
-  jobs, 24.75 an XCD): the running costs 13, 16, 69, 76, 99, 112, 115, 168, 175, 198 reach
-  x / 8 of the total (24.75 x) first at jobs 2 (x = 1, 2), 3 (x = 3), 4 (x = 4), 7 (x = 5, 6)
-  and 8 (x = 7): XCD ranges [0, 2), [], [2, 3), [3, 4), [4, 7), [], [7, 8), [8, 10)."""
+  """Two pairs of five items, tiles 10, 0, 50, 4, 20 (costs 13, 3, 53, 7, 23 with item cost 3;
+  198 for the ten jobs). A job goes to XCD floor(8 m / 198) for its cost midpoint m: midpoints
+  6.5, 14.5, 42.5, 72.5, 87.5, 105.5, 113.5, 141.5, 171.5, 186.5 give XCDs 0, 0, 1, 2, 3, 4, 4,
+  5, 6, 7. A plain split by count (ITEMS) gives two jobs to XCDs 0 and 1 and one to the rest."""
   lens = [10, 0, 50, 4, 20]
   t = np.concatenate([[0], np.cumsum(lens)])
   items = np.array([[b, t[b], t[b + 1], -1] for b in range(5)], np.int32)
   work = _order(items, 2, nat.ORDER_BALANCED)
   per = _xcd_jobs(work, 5)
-  assert per == [[0, 1], [], [2], [3], [4, 5, 6], [], [7], [8, 9]]
-  assert len(work) == 24 and tuple(work[8 * 2 + 4]) == (1, 1)  # XCD 4's third job: pair 1, item 1
-  per = _xcd_jobs(_order(items, 2, nat.ORDER_BALANCED, 2), 5)
-  # windows of two: job 9 (23) before job 8 (7); job 4 (23) before 5 (13), then 6 alone
-  assert per == [[0, 1], [], [2], [3], [4, 5, 6], [], [7], [9, 8]]
+  assert per == [[0, 1], [2], [3], [4], [5, 6], [7], [8], [9]]
+  assert len(work) == 16 and tuple(work[8 + 4]) == (1, 1)  # XCD 4's second job: pair 1, item 1
+  # windows of two: XCD 0 runs job 0 (13) before job 1 (3), XCD 4 job 5 (13) before 6 (3)
+  assert _xcd_jobs(_order(items, 2, nat.ORDER_BALANCED, 2), 5) == per
+  lens2 = np.array([[0, 0, 1, -1], [1, 1, 9, -1]], np.int32)  # costs 4, 11: windows reorder
+  assert _xcd_jobs(_order(lens2, 8, nat.ORDER_ITEMS, 2), 2) == [[1, 0], [3, 2], [5, 4], [7, 6], [9, 8],
+                                                                  [11, 10], [13, 12], [15, 14]]
   per = _xcd_jobs(_order(items, 2, nat.ORDER_ITEMS, 4), 5)  # counts 2, 2, 1, 1, 1, 1, 1, 1
   assert per == [[0, 1], [2, 3], [4], [5], [6], [7], [8], [9]]
   per = _xcd_jobs(_order(items, 1, nat.ORDER_ITEMS, 0), 5)  # 5 jobs: XCDs 0-4 one each
   assert per == [[0], [1], [2], [3], [4], [], [], []]
 
 
+def test_order_table_weighs_tiles_by_their_costs():
+  """With per-tile costs an item costs item_cost plus its tiles' costs: two pairs of three items
+  of tiles [0, 2), [2, 3), [3, 6) with tile costs 5, 5, 40, 1, 1, 1 and item cost 2 cost 12, 42,
+  5 (118 in all). Midpoints 6, 33, 56.5, 65, 92, 115.5 give XCDs floor(8 m / 118) = 0, 2, 3, 4,
+  6, 7. With tile costs of 1 (costs 4, 3, 5; 24 in all) the midpoints 2, 5.5, 9.5, 14, 17.5, 21.5
+  give XCDs 0, 1, 3, 4, 5, 7."""
+  items = np.array([[0, 0, 2, -1], [1, 2, 3, -1], [2, 3, 6, -1]], np.int32)
+  tc = np.array([5, 5, 40, 1, 1, 1], np.int32)
+  per = _xcd_jobs(_order(items, 2, nat.ORDER_BALANCED, 0, tc, 2), 3)
+  assert per == [[0], [], [1], [2], [3], [], [4], [5]]
+  per = _xcd_jobs(_order(items, 2, nat.ORDER_BALANCED, 0, None, 2), 3)
+  assert per == [[0], [1], [], [2], [3], [4], [], [5]]
+
+
 def test_order_table_rejects_bad_arguments():
   L = nat.lib()
   items = np.array([[0, 0, 5, -1], [1, 5, 9, -1]], np.int32)
   n = np.zeros(1, np.int32)
-  assert L.fwn_tiles_order_count(2, nat.ptr(items), 2, 7, 0, nat.ptr(n)) == nat.ERR_INVALID_ARG
+  assert L.fwn_tiles_order_count(2, nat.ptr(items), None, 3, 2, 7, 0, nat.ptr(n)) == nat.ERR_INVALID_ARG
   assert b"unknown order" in L.fwn_last_error()
-  assert L.fwn_tiles_order_count(0, nat.ptr(items), 2, 1, 0, nat.ptr(n)) == nat.ERR_INVALID_ARG
-  assert L.fwn_tiles_order_count(2, nat.ptr(items), 0, 1, 0, nat.ptr(n)) == nat.ERR_INVALID_ARG
+  assert L.fwn_tiles_order_count(0, nat.ptr(items), None, 3, 2, 1, 0, nat.ptr(n)) == nat.ERR_INVALID_ARG
+  assert L.fwn_tiles_order_count(2, nat.ptr(items), None, 3, 0, 1, 0, nat.ptr(n)) == nat.ERR_INVALID_ARG
+  assert L.fwn_tiles_order_count(2, nat.ptr(items), None, -1, 2, 1, 0, nat.ptr(n)) == nat.ERR_INVALID_ARG
+  neg = np.ones(9, np.int32)
+  neg[6] = -2
+  assert L.fwn_tiles_order_count(2, nat.ptr(items), nat.ptr(neg), 3, 2, 1, 0, nat.ptr(n)) == nat.ERR_INVALID_ARG
+  assert b"negative cost" in L.fwn_last_error()
   bad = items.copy()
   bad[1, 2] = 4
-  assert L.fwn_tiles_order_count(2, nat.ptr(bad), 2, 1, 0, nat.ptr(n)) == nat.ERR_TILES
-  assert L.fwn_tiles_order_fill(2, nat.ptr(items), 2, 1, 0, None) == nat.ERR_INVALID_ARG
+  assert L.fwn_tiles_order_count(2, nat.ptr(bad), None, 3, 2, 1, 0, nat.ptr(n)) == nat.ERR_TILES
+  assert L.fwn_tiles_order_fill(2, nat.ptr(items), None, 3, 2, 1, 0, None) == nat.ERR_INVALID_ARG
 
 
 def test_tile_list_orders_bf16_calls_with_few_jobs():
