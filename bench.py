@@ -93,8 +93,8 @@ def parse():
   p.add_argument("--item-tiles", type=int, default=0,
                  help="longest run of tiles per work item (0: chosen per launch by the library)")
   p.add_argument("--order", default="auto", choices=["auto", "items"],
-                 help="auto: the library's choice (an order table for bf16 launches with few jobs); items: "
-                      "every launch in the plain (batch, head)-major item order")
+                 help="auto: the library's choice (order tables for launches with few jobs); items: every "
+                      "launch in the plain (batch, head)-major item order")
   p.add_argument("--serial-bwd", action="store_true",
                  help="run dQ and then dK/dV on one stream instead of side by side on two streams")
   p.add_argument("--no-ds", action="store_true",
@@ -551,8 +551,11 @@ def attention(args):
   L = nat.lib()
   stream = torch.cuda.current_stream(dev)
   sp = stream.cuda_stream
-  ts = tiles.struct_for_desc(fdesc) if args.order == "auto" else tiles.struct_for(B, H)
-  tst = tiles.struct_for_desc(fdesc, kv=True) if args.order == "auto" else ts  # dK/dV's (the list is its transpose)
+  # The schedule of each kernel (with --order auto, its order table): the forward's, dQ's and
+  # dK/dV's (the list is its own transpose); the recomputing kernels take the native descriptor.
+  sched = lambda d, kernel: tiles.struct_for_desc(d, kernel) if args.order == "auto" else tiles.struct_for(B, H)
+  ts, tsq, tst = sched(fdesc, "fwd"), sched(fdesc, "dq"), sched(fdesc, "kv")
+  tsq_n, tst_n = sched(desc, "dq"), sched(desc, "kv")
   ws = fwn.hip_attn.workspace(fdesc, dev, tiles)
   wsp, wsn = (ws.data_ptr(), ws.numel()) if ws is not None else (None, 0)
   # dK/dV runs on a second stream beside dQ (as the package's backward does), with its own
@@ -570,12 +573,12 @@ def attention(args):
 
   def bwd_dq(st):
     nat.check(L.fwn_attn_bwd_dq_launch(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(),
-                                       lse.data_ptr(), delta.data_ptr(), ts, dq.data_ptr(), wsp, wsn, st.cuda_stream))
+                                       lse.data_ptr(), delta.data_ptr(), tsq_n, dq.data_ptr(), wsp, wsn, st.cuda_stream))
 
   def bwd_dkv(st):
     own = st is side  # beside dQ: its own workspace
     nat.check(L.fwn_attn_bwd_dkv_launch(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(),
-                                        lse.data_ptr(), delta.data_ptr(), tst, dk.data_ptr(), dv.data_ptr(),
+                                        lse.data_ptr(), delta.data_ptr(), tst_n, dk.data_ptr(), dv.data_ptr(),
                                         ws2p if own else wsp, ws2n if own else wsn, st.cuda_stream))
 
   # The bf16 backward's dS exchange, as the package runs it (symmetric k-hop mask: the forward
@@ -592,7 +595,7 @@ def attention(args):
                                            dv.data_ptr(), dsbuf.data_ptr(), dsbuf.numel(), wsp, wsn, st.cuda_stream))
 
   def bwd_dq_ds(st):
-    nat.check(L.fwn_attn_bwd_dq_ds_launch(fdesc, k.data_ptr(), dsbuf.data_ptr(), dsbuf.numel(), ts, dmap.struct,
+    nat.check(L.fwn_attn_bwd_dq_ds_launch(fdesc, k.data_ptr(), dsbuf.data_ptr(), dsbuf.numel(), tsq, dmap.struct,
                                           dq.data_ptr(), wsp, wsn, st.cuda_stream))
 
   # (name, launch, stream it runs on). The step: with the dS exchange, every kernel in order on one
@@ -683,7 +686,8 @@ def attention(args):
                  "sigma": cfg["sigma"], "live_tiles": T, "tile_density": round(tiles.density, 4),
                  "live_group_fraction": round(tiles.group_fraction, 4),
                  "valid_entries": int(mask.nnz), "item_tiles": tiles.item_cap_for(B, H),
-                 "order": "windows" if ts.n_work else "items", "precision": args.precision},
+                 "order_tables": {"fwd": ts.n_work > 0, "dq": tsq.n_work > 0, "kv": tst.n_work > 0},
+                 "precision": args.precision},
       "roofline": {"bound": "mfma", "kernel": dominant, "achieved": round(achieved, 3), "peak": peak,
                    "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": traffic,
                    "traffic_source": traffic_src, "ms": round(per_solo[dominant], 4),

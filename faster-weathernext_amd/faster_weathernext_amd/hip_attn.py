@@ -42,18 +42,24 @@ _DTYPES = {torch.float32: nat.F32, torch.bfloat16: nat.BF16}
 WIDE_ITEM_TILES = 128
 WIDE_JOBS = 1536
 
-# Order tables (fwn_tiles_order_fill) for bf16 calls whose per-item launch has fewer than
-# ORDER_JOBS jobs: each XCD takes a contiguous range of equal estimated cost, run longest first
-# within windows of two rounds of its slots: ORDER_WINDOW jobs for the forward and dQ (64
-# workgroups per XCD), ORDER_WINDOW_KV for dK/dV (32). Measured on MI355X (bf16 fwd+bwd step,
-# three runs each on one box): C3 1.562 -> 1.496 ms, the C5 attention shape 2.897 -> 2.852 ms.
-# Windows of 128 for dK/dV as well gave C3 1.490 and C5 2.899; no window (equal-cost ranges in
-# block order) C3 1.50-1.52; sorting whole ranges, or all jobs, longest first lost the
-# neighbouring blocks' shared K/V and dS reads (C5 dQ +6% and +30%). With many jobs per slot
-# (C4's 10,464) the plain ranges are already even, so such calls keep the plain order.
+# Order tables (fwn_tiles_order_fill) for calls whose per-item launch has fewer than ORDER_JOBS
+# jobs: each XCD takes a contiguous range of equal estimated cost, run longest first within
+# windows of ORDER_WINDOWS[products][kernel] jobs (0: the range in block order). The windows are
+# two rounds of an XCD's slots where they pay: 128 for the bf16 and float32 forward and dQ (64
+# workgroups per XCD), 64 for dK/dV (32). Measured on MI355X (three or two runs each on one
+# box, plain order -> table):
+#   bf16 fwd+bwd: C3 1.562 -> 1.496 ms, the C5 attention shape 2.897 -> 2.852 ms. Windows of 128
+#     for dK/dV as well gave C3 1.490 and C5 2.899; no window C3 1.50-1.52.
+#   float32 (IEEE products): C2 forward 2.21 -> 1.94 ms; C5 shape fwd+bwd 19.40 -> 19.11 ms.
+#   bf16x3 products: C2 forward 0.764 -> 0.70-0.715 ms with windows of 128; at the C5 shape the
+#     windows made dK/dV +2.5% and dQ +4.5%, equal-cost ranges alone 7.04 -> 6.98 ms.
+# Sorting whole ranges, or all jobs, longest first lost the neighbouring blocks' shared K/V and
+# dS reads (C5 dQ +4-30%). With many jobs per slot (C4's 10,464) the plain ranges are already
+# even, so such calls keep the plain order.
 ORDER_JOBS = 4096
-ORDER_WINDOW = 128
-ORDER_WINDOW_KV = 64
+ORDER_WINDOWS = {"bf16": {"fwd": 128, "dq": 128, "kv": 64},
+                 "f32": {"fwd": 128, "dq": 128, "kv": 64},
+                 "bf16x3": {"fwd": 128, "dq": 0, "kv": 0}}
 # A job's estimated cost: ORDER_ITEM_UNITS, plus per tile ORDER_TILE_UNITS and ORDER_HALF_UNITS
 # per live 32 x 16 half (the tile's set half bits). Fitted to per-workgroup durations at C3 and
 # the C5 shape (the tile count alone misjudged C3's sparse coarse-node blocks; with the halves
@@ -64,9 +70,13 @@ ORDER_TILE_UNITS = 20
 ORDER_HALF_UNITS = 1
 
 
-def ordered(desc):
-  """True when a call with descriptor `desc` takes an order table (bf16 products)."""
-  return desc.dtype == nat.BF16 and desc.precision == nat.PREC_NATIVE
+def order_window(desc, kernel):
+  """The order-table window for `kernel` ("fwd", "dq" or "kv") of a call with descriptor `desc`."""
+  if desc.precision == nat.PREC_BF16X3:
+    products = "bf16x3"
+  else:
+    products = "bf16" if desc.dtype == nat.BF16 else "f32"
+  return ORDER_WINDOWS[products][kernel]
 
 
 class _Schedule:
@@ -98,7 +108,7 @@ class _Schedule:
                      addr(self.items), addr(self.split) if self.n_split else None, addr(tl.halves), addr(work),
                      pairs, 0)
 
-  def order_table(self, pairs, order=nat.ORDER_BALANCED, window=ORDER_WINDOW):
+  def order_table(self, pairs, order=nat.ORDER_BALANCED, window=0):
     """Host order table [n_work, 2] of this schedule for calls of `pairs` (batch, head) pairs."""
     L = nat.lib()
     n = np.zeros(1, np.int32)
@@ -111,7 +121,7 @@ class _Schedule:
     nat.check(L.fwn_tiles_order_fill(*args, nat.ptr(work)))
     return work
 
-  def ordered_struct(self, pairs, order=nat.ORDER_BALANCED, window=ORDER_WINDOW):
+  def ordered_struct(self, pairs, order=nat.ORDER_BALANCED, window=0):
     """The C struct with an order table for calls of `pairs` (batch, head) pairs (built once)."""
     key = (int(pairs), int(order), int(window))
     if key not in self._orders:
@@ -193,23 +203,23 @@ class TileList:
     return self._schedule(self.item_cap_for(batch, heads))
 
   def order_for(self, batch, heads):
-    """Whether a bf16 call of `batch` x `heads` takes an order table: fewer than ORDER_JOBS jobs
-    in its per-item launch."""
+    """Whether a call of `batch` x `heads` takes an order table: fewer than ORDER_JOBS jobs in
+    its per-item launch."""
     sch = self.schedule_for(batch, heads)
     return sch.n_items * int(batch) * int(heads) < ORDER_JOBS
 
-  def struct_for(self, batch, heads, order=False, window=ORDER_WINDOW):
+  def struct_for(self, batch, heads, window=None):
     """The C struct to launch a call of `batch` x `heads` with (the schedule chosen for it); with
-    `order` (bf16 calls, ``ordered``) and few jobs (``order_for``), with its order table."""
+    a `window` and few jobs (``order_for``), with its order table of that window."""
     sch = self.schedule_for(batch, heads)
-    if order and self.order_for(batch, heads):
+    if window is not None and self.order_for(batch, heads):
       return sch.ordered_struct(int(batch) * int(heads), nat.ORDER_BALANCED, window)
     return sch.struct
 
-  def struct_for_desc(self, desc, kv=False):
-    """The C struct for a call with descriptor `desc`: for the forward and dQ kernels, or with
-    `kv` for dK/dV (this list as a transposed list)."""
-    return self.struct_for(desc.batch, desc.heads, ordered(desc), ORDER_WINDOW_KV if kv else ORDER_WINDOW)
+  def struct_for_desc(self, desc, kernel="fwd"):
+    """The C struct for `kernel` ("fwd", "dq", or "kv" for dK/dV with this list as the transposed
+    list) of a call with descriptor `desc`."""
+    return self.struct_for(desc.batch, desc.heads, order_window(desc, kernel))
 
   def workspace_bytes(self, desc):
     """Workspace the launchers need for this list and the call shape `desc`: the size for the
@@ -419,7 +429,7 @@ def attention_forward(q, k, v, tiles, scale, with_lse=True, precision="native"):
   tl = _as_tiles(tiles, q.shape[1], q.device)
   lse = torch.empty((q.shape[0], q.shape[2], q.shape[1]), dtype=torch.float32, device=q.device) if with_lse else None
   ws = workspace(desc, q.device, tl)
-  ts = tl.struct_for_desc(desc)
+  ts = tl.struct_for_desc(desc, "fwd")
   nat.check(nat.lib().fwn_attn_fwd_launch(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), ts, out.data_ptr(),
                                           lse.data_ptr() if with_lse else None, *_ws_args(ws), _stream(q.device)))
   return out, lse
@@ -466,7 +476,7 @@ def _backward_into(q, k, v, out, lse, dout, tiles, tiles_t, scale, dq, dk, dv, p
     desc = _desc(q, scale, out, _precision(precision, q.dtype))
     ws = workspace(desc, q.device, tl, tlt)
     ds = torch.empty(max(dmap.ds_bytes(desc), 256), dtype=torch.uint8, device=q.device)
-    ts, tst = tl.struct_for_desc(desc), tlt.struct_for_desc(desc, kv=True)
+    ts, tst = tl.struct_for_desc(desc, "dq"), tlt.struct_for_desc(desc, "kv")
     nat.check(L.fwn_attn_bwd_ds_launch(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
                                        dout.data_ptr(), lse.data_ptr(), delta.data_ptr(), ts, tst, dmap.struct,
                                        dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ds.data_ptr(), ds.numel(),
@@ -476,7 +486,7 @@ def _backward_into(q, k, v, out, lse, dout, tiles, tiles_t, scale, dq, dk, dv, p
   nat.check(L.fwn_attn_bwd_delta_launch(desc, out.data_ptr(), dout.data_ptr(), delta.data_ptr(), main.cuda_stream))
   side = _side_stream(q.device)
   side.wait_stream(main)
-  ts, tst = tl.struct_for_desc(desc), tlt.struct_for_desc(desc, kv=True)
+  ts, tst = tl.struct_for_desc(desc, "dq"), tlt.struct_for_desc(desc, "kv")
   nat.check(L.fwn_attn_bwd_dkv_launch(desc, q.data_ptr(), k.data_ptr(), v.data_ptr(), dout.data_ptr(),
                                       lse.data_ptr(), delta.data_ptr(), tst, dk.data_ptr(), dv.data_ptr(),
                                       *_ws_args(ws_kv), side.cuda_stream))

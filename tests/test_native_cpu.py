@@ -379,10 +379,10 @@ def test_order_table_rejects_bad_arguments():
   assert L.fwn_tiles_order_fill(2, nat.ptr(items), None, 3, 2, 1, 0, None) == nat.ERR_INVALID_ARG
 
 
-def test_tile_list_orders_bf16_calls_with_few_jobs():
-  """bf16 calls whose per-item launch has fewer than ORDER_JOBS jobs get the schedule's
-  windowed order table for their (batch, head) count; float32 and bf16x3 calls and calls with
-  many jobs get none; the workspace does not depend on the table."""
+def test_tile_list_orders_calls_with_few_jobs():
+  """Calls whose per-item launch has fewer than ORDER_JOBS jobs get the schedule's order table
+  for their (batch, head) count and kernel, with the window ORDER_WINDOWS gives their products;
+  calls with many jobs get none; the workspace does not depend on the table."""
   from faster_weathernext_amd import hip_attn
   mask, _, _, _ = fwn.mesh_mask(5, 4)
   tl = hip_attn.TileList.from_mask(mask, device="cpu")
@@ -391,20 +391,21 @@ def test_tile_list_orders_bf16_calls_with_few_jobs():
   f32 = nat.AttnDesc(1, n, 4, 64, nat.F32, 0.1, 4 * 64, 4 * 64, 64)
   x3 = nat.AttnDesc(1, n, 4, 64, nat.F32, 0.1, 4 * 64, 4 * 64, 64, 0, 0, 0, nat.PREC_BF16X3, 0)
   sch = tl.schedule_for(1, 4)
-  st = tl.struct_for_desc(bf16)
-  assert tl.order_for(1, 4) and st.work and st.work_pairs == 4
-  table = sch.order_table(4, nat.ORDER_BALANCED, hip_attn.ORDER_WINDOW)
-  assert st.n_work == len(table) and tl.struct_for_desc(bf16) is st  # built once
-  kv = tl.struct_for_desc(bf16, kv=True)
-  assert kv.n_work == len(sch.order_table(4, nat.ORDER_BALANCED, hip_attn.ORDER_WINDOW_KV))
-  for d in (f32, x3):
-    assert tl.struct_for_desc(d).n_work == 0 and not tl.struct_for_desc(d).work
-  for desc in (bf16, f32):
-    size = ctypes.c_uint64(0)
-    nat.check(nat.lib().fwn_attn_workspace_size(desc, sch.struct, ctypes.byref(size)))
-    assert tl.workspace_bytes(desc) == int(size.value)
+  assert tl.order_for(1, 4)
+  for desc, products in ((bf16, "bf16"), (f32, "f32"), (x3, "bf16x3")):
+    for kernel in ("fwd", "dq", "kv"):
+      window = hip_attn.ORDER_WINDOWS[products][kernel]
+      assert hip_attn.order_window(desc, kernel) == window
+      st = tl.struct_for_desc(desc, kernel)
+      table = sch.order_table(4, nat.ORDER_BALANCED, window)
+      assert st.work and st.work_pairs == 4 and st.n_work == len(table)
+      assert tl.struct_for_desc(desc, kernel) is st  # built once
+      size = ctypes.c_uint64(0)
+      nat.check(nat.lib().fwn_attn_workspace_size(desc, sch.struct, ctypes.byref(size)))
+      assert tl.workspace_bytes(desc) == int(size.value)
+  assert hip_attn.ORDER_WINDOWS["bf16"] == {"fwd": 128, "dq": 128, "kv": 64}
   many = -(-hip_attn.ORDER_JOBS // (sch.n_items * 4))
-  assert not tl.order_for(many, 4) and tl.struct_for(many, 4, order=True).n_work == 0
+  assert not tl.order_for(many, 4) and tl.struct_for(many, 4, window=128).n_work == 0
 
 
 @pytest.mark.parametrize("case", ["pairs", "short", "no_table"])

@@ -92,14 +92,15 @@ def test_every_order_gives_the_plain_order_bits(cap, case):
 
 
 def test_library_orders_bf16_calls_and_matches_the_oracle():
-  """The op's bf16 calls with few jobs launch with the windowed order table; the result is the
-  plain order's bit for bit and within the bf16 bars of the dense oracle."""
+  """The op's bf16 calls with few jobs launch with the order tables (windows of
+  hip_attn.ORDER_WINDOWS); the result is the plain order's bit for bit and within the bf16 bars
+  of the dense oracle."""
   rng = np.random.default_rng(90)
   b, n, h, d = 1, 2000, 2, 64
   q, k, v, do = (rounded(rng.standard_normal((b, n, h, d)), torch.bfloat16) for _ in range(4))
   m = random_mask(n, 0.02, 91, symmetric=True)
   tiles = fwn.TileList(*fwn.build_tile_mask(m), n, DEV)
-  st = tiles.struct_for(b, h, order=True)
+  st = tiles.struct_for(b, h, window=fwn.hip_attn.ORDER_WINDOWS["bf16"]["fwd"])
   assert tiles.order_for(b, h) and st.n_work > 0 and st.work_pairs == b * h
   args = [dev(x, torch.bfloat16, grad=True) for x in (q, k, v)]
   out = fwn.tiled_flash_attention(*args, tiles, scale=d ** -0.5)
