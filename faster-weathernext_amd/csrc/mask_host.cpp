@@ -560,10 +560,12 @@ int order_ranges(int32_t n_items, const fwn_item* items, const int32_t* tile_cos
   for (int x = 0; x < 8; ++x) {
     std::vector<int64_t>& r = xcd[x];
     for (int64_t j = bound[x]; j < bound[x + 1]; ++j) r.push_back(j);
+    // Windows counted from the range's end, so the last `window` jobs (the launch's last rounds)
+    // are one full window; the first window takes the remainder.
     if (window > 1)
-      for (size_t w = 0; w < r.size(); w += (size_t)window) {
-        const auto e = r.begin() + (ptrdiff_t)std::min(r.size(), w + (size_t)window);
-        std::stable_sort(r.begin() + (ptrdiff_t)w, e,
+      for (size_t w0 = 0, w1 = r.size() % (size_t)window; w0 < r.size(); w0 = w1, w1 += (size_t)window) {
+        if (w1 == w0) continue;
+        std::stable_sort(r.begin() + (ptrdiff_t)w0, r.begin() + (ptrdiff_t)w1,
                          [&](int64_t p, int64_t q) { return cost[p % n_items] > cost[q % n_items]; });
       }
   }

@@ -44,11 +44,12 @@ WIDE_JOBS = 1536
 
 # Order tables (fwn_tiles_order_fill) for calls whose per-item launch has fewer than ORDER_JOBS
 # jobs: each XCD takes a contiguous range of equal estimated cost, run longest first within
-# windows of ORDER_WINDOWS[products][kernel] jobs (0: the range in block order). The windows are
-# two rounds of an XCD's slots where they pay: 128 for the bf16 and float32 forward and dQ (64
-# workgroups per XCD), 64 for dK/dV (32). Measured on MI355X (three or two runs each on one
-# box, plain order -> table):
-#   bf16 fwd+bwd: C3 1.562 -> 1.496 ms, the C5 attention shape 2.897 -> 2.852 ms. Windows of 128
+# windows of ORDER_WINDOWS[products][kernel] jobs counted from the range's end (0: the range in
+# block order). The windows are two rounds of an XCD's slots where they pay: 128 for the bf16
+# and float32 forward and dQ (64 workgroups per XCD), 64 for dK/dV (32). Measured on MI355X
+# (three or two runs each on one box, plain order -> table):
+#   bf16 fwd+bwd: C3 1.562 -> 1.496 ms, the C5 attention shape 2.897 -> 2.852 ms with windows
+#     counted from the start; from the end, C3 1.48 -> 1.44 ms and C5 unchanged. Windows of 128
 #     for dK/dV as well gave C3 1.490 and C5 2.899; no window C3 1.50-1.52.
 #   float32 (IEEE products): C2 forward 2.21 -> 1.94 ms; C5 shape fwd+bwd 19.40 -> 19.11 ms.
 #   bf16x3 products: C2 forward 0.764 -> 0.70-0.715 ms with windows of 128; at the C5 shape the

@@ -197,8 +197,9 @@ int fwn_tiles_schedule_fill(int32_t n_blocks, const int32_t* tile_ptr, int32_t m
  * count with FWN_ORDER_ITEMS (the same jobs on the same workgroups as no table), of equal
  * estimated cost with FWN_ORDER_BALANCED. An item's cost is item_cost plus tile_cost[t] over its
  * tiles (tile_cost NULL: 1 per tile; else at least as many entries as the largest t1, none
- * negative). With window > 1 each consecutive `window` jobs of a range run longest first, so
- * short jobs end the launch while the jobs running together stay neighbours. Ranges of unequal
+ * negative). With window > 1 each consecutive `window` jobs of a range run longest first
+ * (windows counted from the range's end, so its last `window` jobs are one window), so short
+ * jobs end the launch while the jobs running together stay neighbours. Ranges of unequal
  * count leave padding entries (pair -1) that exit at once. fwn_tiles_order_count gives n_work;
  * fwn_tiles_order_fill writes work[n_work * 2] (host buffers). */
 #define FWN_ORDER_ITEMS 0

@@ -274,7 +274,8 @@ def test_order_table_runs_every_job_once_in_contiguous_xcd_ranges(pairs, order, 
   have pair -1. ITEMS: equal counts (without a window, the kernels' own mapping without a table,
   workgroup for workgroup). BALANCED: each range's cost (item cost 3 + tiles per job) is the
   even share total / 8 to within one job's cost. A window w > 1 sorts each consecutive w jobs of
-  a range longest first (stable: ties in job order); w <= 1 keeps job order."""
+  a range longest first (stable: ties in job order), counting the windows from the range's end so
+  its last w jobs form one window; w <= 1 keeps job order."""
   rng = np.random.default_rng(pairs)
   counts = rng.integers(0, 200, 70)
   counts[:4] = 320  # long blocks first, as the subdivision order's coarse nodes
@@ -314,13 +315,14 @@ def test_order_table_runs_every_job_once_in_contiguous_xcd_ranges(pairs, order, 
         job = x * (small + 1) + k if x < rem else rem * (small + 1) + (x - rem) * small + k
         assert tuple(work[w]) == (job // ni, job % ni)
   else:
+    def windows(r):
+      first = len(r) % window
+      return ([r[:first]] if first else []) + [r[w0:w0 + window] for w0 in range(first, len(r), window)]
     for r in per:
-      for w0 in range(0, len(r), window):
-        win = r[w0:w0 + window]
+      for win in windows(r):
         assert win == sorted(sorted(win), key=lambda j: -jcost[j])  # stable: ties in job order
     plain = _xcd_jobs(_order(items, pairs, order), ni)
-    assert [[sorted(r[w0:w0 + window]) for w0 in range(0, len(r), window)] for r in per] == \
-        [[r[w0:w0 + window] for w0 in range(0, len(r), window)] for r in plain]
+    assert [[sorted(w) for w in windows(r)] for r in per] == [windows(r) for r in plain]
 
 
 def test_order_table_known_answer():
@@ -337,6 +339,10 @@ def test_order_table_known_answer():
   assert len(work) == 16 and tuple(work[8 + 4]) == (1, 1)  # XCD 4's second job: pair 1, item 1
   # windows of two: XCD 0 runs job 0 (13) before job 1 (3), XCD 4 job 5 (13) before 6 (3)
   assert _xcd_jobs(_order(items, 2, nat.ORDER_BALANCED, 2), 5) == per
+  # windows counted from the end: five jobs of costs 4, 11, 4, 11, 4 (one XCD's worth) in windows
+  # of two are [4], [11, 4], [11, 4] -> jobs 0, 1, 2, 3, 4; from the start they would be 1, 0, 3, 2, 4
+  five = np.array([[0, 0, 1, -1], [1, 1, 9, -1]], np.int32)  # costs 4, 11
+  assert _xcd_jobs(_order(five, 20, nat.ORDER_ITEMS, 2), 2)[0] == [0, 1, 2, 3, 4]
   lens2 = np.array([[0, 0, 1, -1], [1, 1, 9, -1]], np.int32)  # costs 4, 11: windows reorder
   assert _xcd_jobs(_order(lens2, 8, nat.ORDER_ITEMS, 2), 2) == [[1, 0], [3, 2], [5, 4], [7, 6], [9, 8],
                                                                   [11, 10], [13, 12], [15, 14]]
