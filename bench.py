@@ -13,10 +13,13 @@ beside dK/dV on a second stream. Inputs are resident in HBM before the timed reg
 TFLOP/s over live 128x128 tiles (14 * D * 128^2 per live tile, batch and head for fwd + bwd;
 4 * D * 128^2 for forward-only workloads). The mask build is timed separately.
 
-Prints one JSON line (rank 0). Also reports a roofline entry for the dominant kernel: its
-algorithmic FLOPs per launch over its mean HIP-event duration in a second timed pass of K steps
-in which every kernel runs alone on one stream (the first pass, which gives `value`, runs dQ and
-dK/dV side by side as the package does). And a CPU baseline: the restated reference XLA chunked
+Prints one JSON line (rank 0). `value` comes from K steps with nothing recorded between their
+launches. A second pass of K steps records an event pair around every launch (`kernels_ms`,
+`ms_per_step_with_kernel_events`). The roofline entry for the dominant kernel takes its
+algorithmic FLOPs per launch over its mean HIP-event duration in a pass in which every kernel
+runs alone on one stream: that event pass itself when the step is already one stream (the dS
+exchange), else a third pass (with --no-ds the step runs dQ and dK/dV side by side as the package
+does). And a CPU baseline: the restated reference XLA chunked
 path (oracle/attention.py) on a bounded sample of query chunks of the same workload, on the cores
 this process may use (os.sched_getaffinity), with the CPU model.
 
@@ -83,7 +86,9 @@ def parse():
   p = argparse.ArgumentParser()
   p.add_argument("--gpus", type=int, default=1)
   p.add_argument("--steps", type=int, default=20)
-  p.add_argument("--warmup", type=int, default=3)
+  # The GPU's clocks settle over the first tens of steps: at C3 the timed steps ran 1.40 ms after 3
+  # warm-up steps, 1.35 after 10 and 1.335 after 30 or 100 (one box).
+  p.add_argument("--warmup", type=int, default=30)
   p.add_argument("--workload", default="c3", choices=sorted(WORKLOADS))
   p.add_argument("--cpu-seconds", type=float, default=18.0,
                  help="bounded CPU-baseline length (the median of three samples of one chunk subset)")
@@ -449,7 +454,7 @@ def main():
 # Hilbert order, 6 x 128, one layer's forward + backward), timed in the default run beside the
 # configuration-3 headline: bf16, and float32 with bf16x3 products (the counterpart of the
 # reference's TF32 / 3xTF32 dots), against its published RTX 5090 times.
-EXTRA_STEPS, EXTRA_WARMUP = 10, 3
+EXTRA_STEPS, EXTRA_WARMUP = 10, 20
 
 
 def reference_shape(args):
@@ -622,25 +627,27 @@ def attention(args):
     if any(st is side for _, _, st in kernels):
       stream.wait_stream(side)
 
-  def timed_pass(kernels):
-    """K steps between two events on the main stream, an event pair on its own stream around every
-    launch: (ms per step, mean ms per kernel, events)."""
+  def timed_pass(kernels, kernel_events=True):
+    """K steps between two events on the main stream and, with `kernel_events`, an event pair on
+    its own stream around every launch: (ms per step, mean ms per kernel, events)."""
     events = [[[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in kernels] for _ in range(args.steps)]
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     start.record(stream)
     for s_ in range(args.steps):
-      step(kernels, events[s_])
+      step(kernels, events[s_] if kernel_events else None)
     stop.record(stream)
     torch.cuda.synchronize()
     per = {name: float(np.mean([events[s_][i][0].elapsed_time(events[s_][i][1]) for s_ in range(args.steps)]))
-           for i, (name, _, _) in enumerate(kernels)}
+           for i, (name, _, _) in enumerate(kernels)} if kernel_events else None
     return start.elapsed_time(stop) / args.steps, per, events
 
   for _ in range(args.warmup):
     step(paired)
-  # Timed region 1 (the metric): K steps as the package runs them.
-  ms_step, per_kernel, events = timed_pass(paired)
+  # Timed region 1 (the metric): K steps as the package runs them, with no event between launches.
+  ms_step, _, _ = timed_pass(paired, kernel_events=False)
+  # The same steps again with an event pair around every launch: the per-kernel times.
+  ms_step_events, per_kernel, events = timed_pass(paired)
   pair_ms = None
   if cfg["backward"] and paired is not solo:
     # dQ and dK/dV side by side: from the end of delta (both streams start there) to the later end.
@@ -648,9 +655,10 @@ def attention(args):
     i_d, i_q, i_kv = names.index("delta"), names.index("dq"), names.index("dkv")
     pair_ms = float(np.mean([max(events[s_][i_d][1].elapsed_time(events[s_][i_q][1]),
                                  events[s_][i_d][1].elapsed_time(events[s_][i_kv][1])) for s_ in range(args.steps)]))
-  # Timed region 2 (the roofline entry): K more steps with every kernel alone on the GPU.
+  # The roofline entry: K steps with every kernel alone on the GPU (the event pass when the step is
+  # one stream already).
   if paired is solo:
-    ms_solo, per_solo = ms_step, per_kernel
+    ms_solo, per_solo = ms_step_events, per_kernel
   else:
     for _ in range(args.warmup):
       step(solo)
@@ -695,8 +703,8 @@ def attention(args):
                            "without a valid element (config.live_group_fraction of them execute), so frac "
                            "can exceed 1" + ("; bf16x3: fp32-equivalent products against the bf16 MFMA "
                                              "peak / 3" if x3 and peak != PEAK["f32"] else ""),
-                   "timing": ("the timed pass (every kernel in order on one stream, each alone on the GPU)"
-                              if paired is solo else
+                   "timing": ("the event pass (the metric's steps again, every kernel in order on one stream, "
+                              "each alone on the GPU)" if paired is solo else
                               "solo pass: the same K steps again with every kernel on one stream (each alone on "
                               "the GPU)") + ", HIP events on that stream around each launch, split-K combine "
                                             "included"},
@@ -704,6 +712,7 @@ def attention(args):
           "dS exchange: delta, dK/dV writing dS, dQ from dS, one stream" if dmap is not None else
           "recomputing dQ kernel" + (" then dK/dV, one stream" if args.serial_bwd else
                                      " beside dK/dV on a second stream")),
+      "ms_per_step_with_kernel_events": round(ms_step_events, 4),
       "kernels_ms": {k_: round(v_, 4) for k_, v_ in per_kernel.items()},
       "kernels_ms_solo": {k_: round(v_, 4) for k_, v_ in per_solo.items()},
       "kernels_tflops_solo": {k_: rate(k_, v_) for k_, v_ in per_solo.items() if algo.get(k_)},
