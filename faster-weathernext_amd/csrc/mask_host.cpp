@@ -9,6 +9,8 @@
 #include <atomic>
 #include <cmath>
 #include <cstring>
+#include <functional>
+#include <queue>
 #include <thread>
 #include <vector>
 
@@ -509,13 +511,45 @@ namespace {
 
 // The jobs of each XCD for an order table (fwn_tiles_order_count / _fill): job j is item
 // j % n_items of pair j / n_items.
+// The jobs [b0, b1) of one XCD in launch order: job order, then each window of `window` jobs
+// (counted from the range's end, so the last `window` jobs, the launch's last rounds, are one
+// full window and the first window takes the remainder) sorted longest first.
+void range_order(int64_t b0, int64_t b1, int32_t window, const std::vector<int64_t>& cost, int32_t n_items,
+                 std::vector<int64_t>& r) {
+  r.clear();
+  for (int64_t j = b0; j < b1; ++j) r.push_back(j);
+  if (window > 1)
+    for (size_t w0 = 0, w1 = r.size() % (size_t)window; w0 < r.size(); w0 = w1, w1 += (size_t)window) {
+      if (w1 == w0) continue;
+      std::stable_sort(r.begin() + (ptrdiff_t)w0, r.begin() + (ptrdiff_t)w1,
+                       [&](int64_t p, int64_t q) { return cost[p % n_items] > cost[q % n_items]; });
+    }
+}
+
+// When the last of the jobs `r` ends if `slots` slots take them in order, each job going to the
+// first free slot and lasting its cost.
+int64_t makespan(const std::vector<int64_t>& r, const std::vector<int64_t>& cost, int32_t n_items, int32_t slots) {
+  std::priority_queue<int64_t, std::vector<int64_t>, std::greater<int64_t>> free_at;
+  for (int32_t s = 0; s < slots; ++s) free_at.push(0);
+  int64_t end = 0;
+  for (int64_t j : r) {
+    const int64_t t = free_at.top() + cost[j % n_items];
+    free_at.pop();
+    free_at.push(t);
+    end = std::max(end, t);
+  }
+  return end;
+}
+
 int order_ranges(int32_t n_items, const fwn_item* items, const int32_t* tile_cost, int32_t item_cost,
-                 int32_t pairs, int32_t order, int32_t window, const char* what,
+                 int32_t pairs, int32_t order, int32_t window, int32_t slots, const char* what,
                  std::vector<std::vector<int64_t>>& xcd) {
   if (n_items <= 0 || !items || pairs <= 0 || item_cost < 0)
     return fwn::fail(FWN_ERR_INVALID_ARG, "%s: null, empty or negative argument", what);
-  if (order != FWN_ORDER_ITEMS && order != FWN_ORDER_BALANCED)
+  if (order != FWN_ORDER_ITEMS && order != FWN_ORDER_BALANCED && order != FWN_ORDER_MAKESPAN)
     return fwn::fail(FWN_ERR_INVALID_ARG, "%s: unknown order %d", what, order);
+  if (order == FWN_ORDER_MAKESPAN && (slots <= 0 || slots > 65536))
+    return fwn::fail(FWN_ERR_INVALID_ARG, "%s: FWN_ORDER_MAKESPAN needs 1 to 65536 slots (got %d)", what, slots);
   const int64_t jobs = (int64_t)n_items * pairs;
   if (jobs > INT32_MAX) return fwn::fail(FWN_ERR_INVALID_ARG, "%s: too many jobs", what);
   std::vector<int64_t> cost((size_t)n_items);
@@ -557,17 +591,50 @@ int order_ranges(int32_t n_items, const fwn_item* items, const int32_t* tile_cos
     while (x < 8) bound[++x] = jobs;
   }
   xcd.assign(8, {});
-  for (int x = 0; x < 8; ++x) {
-    std::vector<int64_t>& r = xcd[x];
-    for (int64_t j = bound[x]; j < bound[x + 1]; ++j) r.push_back(j);
-    // Windows counted from the range's end, so the last `window` jobs (the launch's last rounds)
-    // are one full window; the first window takes the remainder.
-    if (window > 1)
-      for (size_t w0 = 0, w1 = r.size() % (size_t)window; w0 < r.size(); w0 = w1, w1 += (size_t)window) {
-        if (w1 == w0) continue;
-        std::stable_sort(r.begin() + (ptrdiff_t)w0, r.begin() + (ptrdiff_t)w1,
-                         [&](int64_t p, int64_t q) { return cost[p % n_items] > cost[q % n_items]; });
+  for (int x = 0; x < 8; ++x) range_order(bound[x], bound[x + 1], window, cost, n_items, xcd[x]);
+  if (order == FWN_ORDER_MAKESPAN && total > 0) {
+    // From the equal-cost ranges, move one job at a time across a boundary of the XCD that ends
+    // last (its first job to the XCD before, or its last to the XCD after), while that lowers
+    // the later end of the two.
+    int64_t ms[8];
+    for (int x = 0; x < 8; ++x) ms[x] = makespan(xcd[x], cost, n_items, slots);
+    std::vector<int64_t> ra, rb;
+    for (int64_t step = 0; step < 64 * (jobs + 8); ++step) {
+      const int x = (int)(std::max_element(ms, ms + 8) - ms);
+      int best_side = 0;
+      int64_t best = ms[x], best_a = 0, best_b = 0;
+      for (int side = -1; side <= 1; side += 2) {
+        const int y = x + side;
+        if (y < 0 || y > 7 || bound[x + 1] == bound[x]) continue;
+        // side -1: job bound[x] moves to XCD x - 1; side +1: job bound[x + 1] - 1 moves to x + 1
+        const int64_t nb = side < 0 ? bound[x] + 1 : bound[x + 1] - 1;
+        if (side < 0) {
+          range_order(nb, bound[x + 1], window, cost, n_items, ra);
+          range_order(bound[y], nb, window, cost, n_items, rb);
+        } else {
+          range_order(bound[x], nb, window, cost, n_items, ra);
+          range_order(nb, bound[y + 1], window, cost, n_items, rb);
+        }
+        const int64_t a = makespan(ra, cost, n_items, slots), b = makespan(rb, cost, n_items, slots);
+        if (std::max(a, b) < best) {
+          best = std::max(a, b);
+          best_side = side;
+          best_a = a;
+          best_b = b;
+        }
       }
+      if (best_side == 0) break;
+      const int y = x + best_side;
+      if (best_side < 0) {
+        ++bound[x];
+      } else {
+        --bound[x + 1];
+      }
+      range_order(bound[x], bound[x + 1], window, cost, n_items, xcd[x]);
+      range_order(bound[y], bound[y + 1], window, cost, n_items, xcd[y]);
+      ms[x] = best_a;
+      ms[y] = best_b;
+    }
   }
   return FWN_OK;
 }
@@ -583,11 +650,12 @@ int64_t order_entries(const std::vector<std::vector<int64_t>>& xcd) {
 extern "C" {
 
 int fwn_tiles_order_count(int32_t n_items, const fwn_item* items, const int32_t* tile_cost, int32_t item_cost,
-                          int32_t pairs, int32_t order, int32_t window, int32_t* n_work) {
+                          int32_t pairs, int32_t order, int32_t window, int32_t slots, int32_t* n_work) {
   fwn::clear_error();
   if (!n_work) return fwn::fail(FWN_ERR_INVALID_ARG, "fwn_tiles_order_count: null output");
   std::vector<std::vector<int64_t>> xcd;
-  if (int rc = order_ranges(n_items, items, tile_cost, item_cost, pairs, order, window, "fwn_tiles_order_count", xcd))
+  if (int rc = order_ranges(n_items, items, tile_cost, item_cost, pairs, order, window, slots, "fwn_tiles_order_count",
+                            xcd))
     return rc;
   const int64_t entries = order_entries(xcd);
   if (entries > INT32_MAX) return fwn::fail(FWN_ERR_INVALID_ARG, "fwn_tiles_order_count: too many entries");
@@ -596,11 +664,12 @@ int fwn_tiles_order_count(int32_t n_items, const fwn_item* items, const int32_t*
 }
 
 int fwn_tiles_order_fill(int32_t n_items, const fwn_item* items, const int32_t* tile_cost, int32_t item_cost,
-                         int32_t pairs, int32_t order, int32_t window, int32_t* work) {
+                         int32_t pairs, int32_t order, int32_t window, int32_t slots, int32_t* work) {
   fwn::clear_error();
   if (!work) return fwn::fail(FWN_ERR_INVALID_ARG, "fwn_tiles_order_fill: null output");
   std::vector<std::vector<int64_t>> xcd;
-  if (int rc = order_ranges(n_items, items, tile_cost, item_cost, pairs, order, window, "fwn_tiles_order_fill", xcd))
+  if (int rc = order_ranges(n_items, items, tile_cost, item_cost, pairs, order, window, slots, "fwn_tiles_order_fill",
+                            xcd))
     return rc;
   const int64_t entries = order_entries(xcd);
   if (entries > INT32_MAX) return fwn::fail(FWN_ERR_INVALID_ARG, "fwn_tiles_order_fill: too many entries");

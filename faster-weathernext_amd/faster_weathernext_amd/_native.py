@@ -61,7 +61,7 @@ class DsMap(ctypes.Structure):
 
 
 ITEM_TILES = 64  # FWN_ITEM_TILES: default longest run of tiles per work item
-ORDER_ITEMS, ORDER_BALANCED = 0, 1  # FWN_ORDER_*
+ORDER_ITEMS, ORDER_BALANCED, ORDER_MAKESPAN = 0, 1, 2  # FWN_ORDER_*
 SCRATCH_BYTES = 64 << 20  # FWN_SCRATCH_BYTES: static scratch of fwn_attn_fwd_launch_noalloc
 
 
@@ -91,8 +91,8 @@ SIGNATURES = {
     "fwn_tiles_prepare": [_I32, _I32, _I32, _P, _P, _P, _P, _P, _P],
     "fwn_tiles_schedule_count": [_I32, _P, _I32, _P, _P, _P],
     "fwn_tiles_schedule_fill": [_I32, _P, _I32, _P, _P],
-    "fwn_tiles_order_count": [_I32, _P, _P, _I32, _I32, _I32, _I32, _P],
-    "fwn_tiles_order_fill": [_I32, _P, _P, _I32, _I32, _I32, _I32, _P],
+    "fwn_tiles_order_count": [_I32, _P, _P, _I32, _I32, _I32, _I32, _I32, _P],
+    "fwn_tiles_order_fill": [_I32, _P, _P, _I32, _I32, _I32, _I32, _I32, _P],
     "fwn_attn_workspace_size": [_DESC, _TILES, _P],
     "fwn_attn_fwd_launch": [_DESC, _P, _P, _P, _TILES, _P, _P, _P, _U64, _P],
     "fwn_attn_fwd_launch_noalloc": [_DESC, _P, _P, _P, _TILES, _P, _P, _P],

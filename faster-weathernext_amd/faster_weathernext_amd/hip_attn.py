@@ -61,6 +61,15 @@ ORDER_JOBS = 4096
 ORDER_WINDOWS = {"bf16": {"fwd": 128, "dq": 128, "kv": 64},
                  "f32": {"fwd": 128, "dq": 128, "kv": 64},
                  "bf16x3": {"fwd": 128, "dq": 0, "kv": 0}}
+# How each kernel's ranges are cut (nat.ORDER_BALANCED: equal estimated cost; nat.ORDER_MAKESPAN:
+# equal simulated end on ORDER_SLOTS[kernel] slots per XCD) and its workgroups per XCD. For
+# dK/dV at C3 the equal-cost ranges left four XCDs with a last round of 7 jobs (199 on 32 slots)
+# and four with a full one (191), ending 29 us apart; the simulated ends matched the measured
+# ones (correlation 1.0), and cutting by them took dK/dV 0.668-0.670 -> 0.661-0.662 ms (C5 shape
+# unchanged). For the forward and dQ the cost model misjudges C3's coarse-node items, and the
+# simulated cut measured 1-2% slower.
+ORDER_CUTS = {"fwd": nat.ORDER_BALANCED, "dq": nat.ORDER_BALANCED, "kv": nat.ORDER_MAKESPAN}
+ORDER_SLOTS = {"fwd": 64, "dq": 64, "kv": 32}
 # A job's estimated cost: ORDER_ITEM_UNITS, plus per tile ORDER_TILE_UNITS and ORDER_HALF_UNITS
 # per live 32 x 16 half (the tile's set half bits). Fitted to per-workgroup durations at C3 and
 # the C5 shape (the tile count alone misjudged C3's sparse coarse-node blocks; with the halves
@@ -71,13 +80,14 @@ ORDER_TILE_UNITS = 20
 ORDER_HALF_UNITS = 1
 
 
-def order_window(desc, kernel):
-  """The order-table window for `kernel` ("fwd", "dq" or "kv") of a call with descriptor `desc`."""
+def order_plan(desc, kernel):
+  """(cut, window, slots) of the order table for `kernel` ("fwd", "dq" or "kv") of a call with
+  descriptor `desc`."""
   if desc.precision == nat.PREC_BF16X3:
     products = "bf16x3"
   else:
     products = "bf16" if desc.dtype == nat.BF16 else "f32"
-  return ORDER_WINDOWS[products][kernel]
+  return ORDER_CUTS[kernel], ORDER_WINDOWS[products][kernel], ORDER_SLOTS[kernel]
 
 
 class _Schedule:
@@ -109,24 +119,24 @@ class _Schedule:
                      addr(self.items), addr(self.split) if self.n_split else None, addr(tl.halves), addr(work),
                      pairs, 0)
 
-  def order_table(self, pairs, order=nat.ORDER_BALANCED, window=0):
+  def order_table(self, pairs, order=nat.ORDER_BALANCED, window=0, slots=64):
     """Host order table [n_work, 2] of this schedule for calls of `pairs` (batch, head) pairs."""
     L = nat.lib()
     n = np.zeros(1, np.int32)
     halves = np.unpackbits(self._tl.halves_host.astype("<u4").view(np.uint8).reshape(-1, 4), axis=1).sum(1)
     cost = (ORDER_TILE_UNITS + ORDER_HALF_UNITS * halves).astype(np.int32)
     args = (self.n_items, nat.ptr(self.items_host), nat.ptr(cost) if len(cost) else None, ORDER_ITEM_UNITS,
-            int(pairs), int(order), int(window))
+            int(pairs), int(order), int(window), int(slots))
     nat.check(L.fwn_tiles_order_count(*args, nat.ptr(n)))
     work = np.zeros((int(n[0]), 2), np.int32)
     nat.check(L.fwn_tiles_order_fill(*args, nat.ptr(work)))
     return work
 
-  def ordered_struct(self, pairs, order=nat.ORDER_BALANCED, window=0):
+  def ordered_struct(self, pairs, order=nat.ORDER_BALANCED, window=0, slots=64):
     """The C struct with an order table for calls of `pairs` (batch, head) pairs (built once)."""
-    key = (int(pairs), int(order), int(window))
+    key = (int(pairs), int(order), int(window), int(slots))
     if key not in self._orders:
-      work = torch.from_numpy(self.order_table(pairs, order, window)).to(self._tl.device)
+      work = torch.from_numpy(self.order_table(pairs, order, window, slots)).to(self._tl.device)
       self._orders[key] = (work, self._struct(work, int(pairs)))
     return self._orders[key][1]
 
@@ -209,18 +219,18 @@ class TileList:
     sch = self.schedule_for(batch, heads)
     return sch.n_items * int(batch) * int(heads) < ORDER_JOBS
 
-  def struct_for(self, batch, heads, window=None):
+  def struct_for(self, batch, heads, plan=None):
     """The C struct to launch a call of `batch` x `heads` with (the schedule chosen for it); with
-    a `window` and few jobs (``order_for``), with its order table of that window."""
+    a `plan` (cut, window, slots) and few jobs (``order_for``), with that order table."""
     sch = self.schedule_for(batch, heads)
-    if window is not None and self.order_for(batch, heads):
-      return sch.ordered_struct(int(batch) * int(heads), nat.ORDER_BALANCED, window)
+    if plan is not None and self.order_for(batch, heads):
+      return sch.ordered_struct(int(batch) * int(heads), *plan)
     return sch.struct
 
   def struct_for_desc(self, desc, kernel="fwd"):
     """The C struct for `kernel` ("fwd", "dq", or "kv" for dK/dV with this list as the transposed
     list) of a call with descriptor `desc`."""
-    return self.struct_for(desc.batch, desc.heads, order_window(desc, kernel))
+    return self.struct_for(desc.batch, desc.heads, order_plan(desc, kernel))
 
   def workspace_bytes(self, desc):
     """Workspace the launchers need for this list and the call shape `desc`: the size for the

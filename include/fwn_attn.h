@@ -199,15 +199,21 @@ int fwn_tiles_schedule_fill(int32_t n_blocks, const int32_t* tile_ptr, int32_t m
  * tiles (tile_cost NULL: 1 per tile; else at least as many entries as the largest t1, none
  * negative). With window > 1 each consecutive `window` jobs of a range run longest first
  * (windows counted from the range's end, so its last `window` jobs are one window), so short
- * jobs end the launch while the jobs running together stay neighbours. Ranges of unequal
- * count leave padding entries (pair -1) that exit at once. fwn_tiles_order_count gives n_work;
- * fwn_tiles_order_fill writes work[n_work * 2] (host buffers). */
+ * jobs end the launch while the jobs running together stay neighbours. FWN_ORDER_MAKESPAN starts
+ * from the equal-cost ranges and moves jobs across the boundaries of the XCD that would end last
+ * (its first job to the XCD before it, or its last to the one after) while that lowers the later
+ * of the two ends, each end simulated as `slots` slots taking the XCD's jobs in launch order
+ * (each job to the first free slot, lasting its cost): equal cost can leave one XCD with a last
+ * round of a few jobs while another's ends full. `slots` is ignored by the other orders. Ranges
+ * of unequal count leave padding entries (pair -1) that exit at once. fwn_tiles_order_count
+ * gives n_work; fwn_tiles_order_fill writes work[n_work * 2] (host buffers). */
 #define FWN_ORDER_ITEMS 0
 #define FWN_ORDER_BALANCED 1
+#define FWN_ORDER_MAKESPAN 2
 int fwn_tiles_order_count(int32_t n_items, const fwn_item* items, const int32_t* tile_cost, int32_t item_cost,
-                          int32_t pairs, int32_t order, int32_t window, int32_t* n_work);
+                          int32_t pairs, int32_t order, int32_t window, int32_t slots, int32_t* n_work);
 int fwn_tiles_order_fill(int32_t n_items, const fwn_item* items, const int32_t* tile_cost, int32_t item_cost,
-                         int32_t pairs, int32_t order, int32_t window, int32_t* work);
+                         int32_t pairs, int32_t order, int32_t window, int32_t slots, int32_t* work);
 
 /* ---------------------------------------------------------------------------------------------
  * Device launchers (enqueue on `stream`).

@@ -244,14 +244,28 @@ def test_schedule_covers_every_tile_once(max_item_tiles):
 ITEM_COST = 3  # the item cost these tests pass (tile costs of 1 when no per-tile costs are given)
 
 
-def _order(items, pairs, order, window=0, tile_cost=None, item_cost=ITEM_COST):
+def _order(items, pairs, order, window=0, tile_cost=None, item_cost=ITEM_COST, slots=32):
   L = nat.lib()
   n = np.zeros(1, np.int32)
   tc = nat.ptr(tile_cost) if tile_cost is not None else None
-  nat.check(L.fwn_tiles_order_count(len(items), nat.ptr(items), tc, item_cost, pairs, order, window, nat.ptr(n)))
+  nat.check(L.fwn_tiles_order_count(len(items), nat.ptr(items), tc, item_cost, pairs, order, window, slots,
+                                    nat.ptr(n)))
   work = np.full((int(n[0]), 2), -7, np.int32)
-  nat.check(L.fwn_tiles_order_fill(len(items), nat.ptr(items), tc, item_cost, pairs, order, window, nat.ptr(work)))
+  nat.check(L.fwn_tiles_order_fill(len(items), nat.ptr(items), tc, item_cost, pairs, order, window, slots,
+                                   nat.ptr(work)))
   return work
+
+
+def _makespan(costs, slots):
+  """When the last job ends if `slots` slots take jobs of these durations in order (each to the
+  first free slot): a brute-force event walk, independent of the library's heap."""
+  free = [0] * slots
+  end = 0
+  for c in costs:
+    s = min(range(slots), key=lambda i: (free[i], i))
+    free[s] += c
+    end = max(end, free[s])
+  return end
 
 
 def _xcd_jobs(work, n_items):
@@ -266,7 +280,8 @@ def _xcd_jobs(work, n_items):
 
 @pytest.mark.parametrize("order,window", [(nat.ORDER_ITEMS, 0), (nat.ORDER_BALANCED, 0), (nat.ORDER_BALANCED, 1),
                                           (nat.ORDER_BALANCED, 7), (nat.ORDER_BALANCED, 128),
-                                          (nat.ORDER_ITEMS, 32)])
+                                          (nat.ORDER_ITEMS, 32), (nat.ORDER_MAKESPAN, 0),
+                                          (nat.ORDER_MAKESPAN, 64)])
 @pytest.mark.parametrize("pairs", [1, 3, 8, 13])
 def test_order_table_runs_every_job_once_in_contiguous_xcd_ranges(pairs, order, window):
   """An order table runs every (pair, item) job exactly once; XCD x (entries w = x mod 8) takes a
@@ -302,10 +317,14 @@ def test_order_table_runs_every_job_once_in_contiguous_xcd_ranges(pairs, order, 
     small, rem = divmod(total, 8)
     assert [len(r) for r in per] == [small + (x < rem) for x in range(8)]
     assert len(work) == 8 * (small + (rem > 0))
-  else:
+  elif order == nat.ORDER_BALANCED:
     share = jcost.sum() / 8
     for r in per:
       assert abs(jcost[r].sum() - share) <= jcost.max()
+  else:
+    # no later end than the equal-cost cut's, simulated on the same 32 slots
+    even = _xcd_jobs(_order(items, pairs, nat.ORDER_BALANCED, window), ni)
+    assert max(_makespan(jcost[r], 32) for r in per) <= max(_makespan(jcost[r], 32) for r in even)
   if window <= 1:
     assert all(r == sorted(r) for r in per)
     if order == nat.ORDER_ITEMS:
@@ -321,8 +340,8 @@ def test_order_table_runs_every_job_once_in_contiguous_xcd_ranges(pairs, order, 
     for r in per:
       for win in windows(r):
         assert win == sorted(sorted(win), key=lambda j: -jcost[j])  # stable: ties in job order
-    plain = _xcd_jobs(_order(items, pairs, order), ni)
-    assert [[sorted(w) for w in windows(r)] for r in per] == [windows(r) for r in plain]
+    # each window holds the consecutive jobs at its positions of the (contiguous) range
+    assert all([sorted(w) for w in windows(r)] == windows(sorted(r)) for r in per)
 
 
 def test_order_table_known_answer():
@@ -366,23 +385,43 @@ def test_order_table_weighs_tiles_by_their_costs():
   assert per == [[0], [1], [], [2], [3], [4], [], [5]]
 
 
+def test_makespan_cut_evens_the_last_rounds():
+  """FWN_ORDER_MAKESPAN on 4 slots per XCD: four pairs of 24 items (tiles below, item cost 2).
+  The equal-cost cut gives the XCDs 11 and 13 jobs in turn, and the latest simulated end (each
+  job to the first free of 4 slots; `_makespan` walks it without the library) is 31. The makespan
+  cut gives every XCD 12 jobs and ends at 30; no order it returns ends later than the equal-cost
+  one (checked for every case in the test above)."""
+  lens = [8, 11, 10, 6, 11, 11, 11, 1, 5, 7, 4, 5, 7, 9, 7, 2, 8, 10, 3, 6, 4, 10, 1, 6]
+  t = np.concatenate([[0], np.cumsum(lens)])
+  items = np.array([[b, t[b], t[b + 1], -1] for b in range(24)], np.int32)
+  cost = np.tile(2 + np.array(lens), 4)
+  even = _xcd_jobs(_order(items, 4, nat.ORDER_BALANCED, 0, None, 2), 24)
+  cut = _xcd_jobs(_order(items, 4, nat.ORDER_MAKESPAN, 0, None, 2, slots=4), 24)
+  assert [len(r) for r in even] == [11, 13] * 4 and [len(r) for r in cut] == [12] * 8
+  assert sorted(j for r in cut for j in r) == list(range(96))
+  assert max(_makespan(cost[r], 4) for r in even) == 31 and max(_makespan(cost[r], 4) for r in cut) == 30
+
+
 def test_order_table_rejects_bad_arguments():
   L = nat.lib()
   items = np.array([[0, 0, 5, -1], [1, 5, 9, -1]], np.int32)
   n = np.zeros(1, np.int32)
-  assert L.fwn_tiles_order_count(2, nat.ptr(items), None, 3, 2, 7, 0, nat.ptr(n)) == nat.ERR_INVALID_ARG
+  assert L.fwn_tiles_order_count(2, nat.ptr(items), None, 3, 2, 7, 0, 32, nat.ptr(n)) == nat.ERR_INVALID_ARG
   assert b"unknown order" in L.fwn_last_error()
-  assert L.fwn_tiles_order_count(0, nat.ptr(items), None, 3, 2, 1, 0, nat.ptr(n)) == nat.ERR_INVALID_ARG
-  assert L.fwn_tiles_order_count(2, nat.ptr(items), None, 3, 0, 1, 0, nat.ptr(n)) == nat.ERR_INVALID_ARG
-  assert L.fwn_tiles_order_count(2, nat.ptr(items), None, -1, 2, 1, 0, nat.ptr(n)) == nat.ERR_INVALID_ARG
+  assert L.fwn_tiles_order_count(0, nat.ptr(items), None, 3, 2, 1, 0, 32, nat.ptr(n)) == nat.ERR_INVALID_ARG
+  assert L.fwn_tiles_order_count(2, nat.ptr(items), None, 3, 0, 1, 0, 32, nat.ptr(n)) == nat.ERR_INVALID_ARG
+  assert L.fwn_tiles_order_count(2, nat.ptr(items), None, -1, 2, 1, 0, 32, nat.ptr(n)) == nat.ERR_INVALID_ARG
+  assert L.fwn_tiles_order_count(2, nat.ptr(items), None, 3, 2, nat.ORDER_MAKESPAN, 0, 0, nat.ptr(n)) \
+      == nat.ERR_INVALID_ARG
+  assert b"slots" in L.fwn_last_error()
   neg = np.ones(9, np.int32)
   neg[6] = -2
-  assert L.fwn_tiles_order_count(2, nat.ptr(items), nat.ptr(neg), 3, 2, 1, 0, nat.ptr(n)) == nat.ERR_INVALID_ARG
+  assert L.fwn_tiles_order_count(2, nat.ptr(items), nat.ptr(neg), 3, 2, 1, 0, 32, nat.ptr(n)) == nat.ERR_INVALID_ARG
   assert b"negative cost" in L.fwn_last_error()
   bad = items.copy()
   bad[1, 2] = 4
-  assert L.fwn_tiles_order_count(2, nat.ptr(bad), None, 3, 2, 1, 0, nat.ptr(n)) == nat.ERR_TILES
-  assert L.fwn_tiles_order_fill(2, nat.ptr(items), None, 3, 2, 1, 0, None) == nat.ERR_INVALID_ARG
+  assert L.fwn_tiles_order_count(2, nat.ptr(bad), None, 3, 2, 1, 0, 32, nat.ptr(n)) == nat.ERR_TILES
+  assert L.fwn_tiles_order_fill(2, nat.ptr(items), None, 3, 2, 1, 0, 32, None) == nat.ERR_INVALID_ARG
 
 
 def test_tile_list_orders_calls_with_few_jobs():
@@ -400,10 +439,10 @@ def test_tile_list_orders_calls_with_few_jobs():
   assert tl.order_for(1, 4)
   for desc, products in ((bf16, "bf16"), (f32, "f32"), (x3, "bf16x3")):
     for kernel in ("fwd", "dq", "kv"):
-      window = hip_attn.ORDER_WINDOWS[products][kernel]
-      assert hip_attn.order_window(desc, kernel) == window
+      plan = (hip_attn.ORDER_CUTS[kernel], hip_attn.ORDER_WINDOWS[products][kernel], hip_attn.ORDER_SLOTS[kernel])
+      assert hip_attn.order_plan(desc, kernel) == plan
       st = tl.struct_for_desc(desc, kernel)
-      table = sch.order_table(4, nat.ORDER_BALANCED, window)
+      table = sch.order_table(4, *plan)
       assert st.work and st.work_pairs == 4 and st.n_work == len(table)
       assert tl.struct_for_desc(desc, kernel) is st  # built once
       size = ctypes.c_uint64(0)
@@ -411,7 +450,7 @@ def test_tile_list_orders_calls_with_few_jobs():
       assert tl.workspace_bytes(desc) == int(size.value)
   assert hip_attn.ORDER_WINDOWS["bf16"] == {"fwd": 128, "dq": 128, "kv": 64}
   many = -(-hip_attn.ORDER_JOBS // (sch.n_items * 4))
-  assert not tl.order_for(many, 4) and tl.struct_for(many, 4, window=128).n_work == 0
+  assert not tl.order_for(many, 4) and tl.struct_for(many, 4, (nat.ORDER_BALANCED, 128, 64)).n_work == 0
 
 
 @pytest.mark.parametrize("case", ["pairs", "short", "no_table"])

@@ -18,7 +18,8 @@ from gpu_helpers import DEV, TOL, MAXTOL, random_mask, rounded, dev, host
 
 pytestmark = pytest.mark.gpu
 
-ORDERS = [(nat.ORDER_ITEMS, 0), (nat.ORDER_BALANCED, 0), (nat.ORDER_BALANCED, 128), (nat.ORDER_ITEMS, 5)]
+ORDERS = [(nat.ORDER_ITEMS, 0), (nat.ORDER_BALANCED, 0), (nat.ORDER_BALANCED, 128), (nat.ORDER_ITEMS, 5),
+          (nat.ORDER_MAKESPAN, 64)]
 
 
 def _workspace(desc, struct):
@@ -82,8 +83,8 @@ def test_every_order_gives_the_plain_order_bits(cap, case):
   args = [dev(x, dtype) for x in (q, k, v, do)]
   want = _run(sch.struct, tiles, *args, d ** -0.5, precision, precision == nat.PREC_NATIVE)
   for order, window in ORDERS:
-    st = sch.ordered_struct(b * h, order, window)
-    table = sch.order_table(b * h, order, window)
+    st = sch.ordered_struct(b * h, order, window, 32)
+    table = sch.order_table(b * h, order, window, 32)
     assert st.n_work == len(table) >= sch.n_items * b * h
     print(f"{case} cap {cap} order {order} window {window}: {st.n_work} entries", flush=True)
     got = _run(st, tiles, *args, d ** -0.5, precision, precision == nat.PREC_NATIVE)
@@ -100,7 +101,7 @@ def test_library_orders_bf16_calls_and_matches_the_oracle():
   q, k, v, do = (rounded(rng.standard_normal((b, n, h, d)), torch.bfloat16) for _ in range(4))
   m = random_mask(n, 0.02, 91, symmetric=True)
   tiles = fwn.TileList(*fwn.build_tile_mask(m), n, DEV)
-  st = tiles.struct_for(b, h, window=fwn.hip_attn.ORDER_WINDOWS["bf16"]["fwd"])
+  st = tiles.struct_for(b, h, (nat.ORDER_BALANCED, fwn.hip_attn.ORDER_WINDOWS["bf16"]["fwd"], 64))
   assert tiles.order_for(b, h) and st.n_work > 0 and st.work_pairs == b * h
   args = [dev(x, torch.bfloat16, grad=True) for x in (q, k, v)]
   out = fwn.tiled_flash_attention(*args, tiles, scale=d ** -0.5)
