@@ -128,7 +128,8 @@ typedef struct fwn_tiles {
                                the jobs in (batch, head)-major, item order, each XCD taking a
                                contiguous range of them. */
   int32_t work_pairs;       /* batch * heads the order table was built for (launches of another
-                               shape are refused) */
+                               shape are refused); the table must come from this `items` array
+                               (the launchers check its size, not its entries) */
   int32_t reserved;         /* 0 */
 } fwn_tiles;
 
