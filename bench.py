@@ -558,7 +558,8 @@ def attention(args):
   sp = stream.cuda_stream
   # The schedule of each kernel (with --order auto, its order table): the forward's, dQ's and
   # dK/dV's (the list is its own transpose); the recomputing kernels take the native descriptor.
-  sched = lambda d, kernel: tiles.struct_for_desc(d, kernel) if args.order == "auto" else tiles.struct_for(B, H)
+  sched = lambda d, kernel: (tiles.struct_for_desc(d, kernel) if args.order == "auto" else
+                             tiles.struct_for(B, H, kernel=kernel))
   ts, tsq, tst = sched(fdesc, "fwd"), sched(fdesc, "dq"), sched(fdesc, "kv")
   tsq_n, tst_n = sched(desc, "dq"), sched(desc, "kv")
   ws = fwn.hip_attn.workspace(fdesc, dev, tiles)
@@ -693,7 +694,8 @@ def attention(args):
                  "heads": H, "head_dim": D, "order": "hilbert" if cfg["reorder"] else "subdivision",
                  "sigma": cfg["sigma"], "live_tiles": T, "tile_density": round(tiles.density, 4),
                  "live_group_fraction": round(tiles.group_fraction, 4),
-                 "valid_entries": int(mask.nnz), "item_tiles": tiles.item_cap_for(B, H),
+                 "valid_entries": int(mask.nnz),
+                 "item_tiles": {kn: tiles.item_cap_for(B, H, kn) for kn in ("fwd", "dq", "kv")},
                  "order_tables": {"fwd": ts.n_work > 0, "dq": tsq.n_work > 0, "kv": tst.n_work > 0},
                  "precision": args.precision},
       "roofline": {"bound": "mfma", "kernel": dominant, "achieved": round(achieved, 3), "peak": peak,

@@ -202,42 +202,51 @@ class TileList:
       self._schedules[cap] = _Schedule(self, self._tile_ptr, cap)
     return self._schedules[cap]
 
-  def item_cap_for(self, batch, heads):
-    """Longest run of tiles per work item for a call of `batch` x `heads`."""
+  def item_cap_for(self, batch, heads, kernel="fwd"):
+    """Longest run of tiles per work item for `kernel` ("fwd", "dq" or "kv") of a call of
+    `batch` x `heads`: the cap fixed at construction, else WIDE_ITEM_TILES for dK/dV and for the
+    others from WIDE_JOBS jobs up, nat.ITEM_TILES below. With the order tables, C3 (1,284 jobs)
+    measured dK/dV 0.663 ms at 64, 0.660 at 96 or 128 and 0.693 at 160 (step 1.331 -> 1.326
+    ms), and the forward 0.398 ms at 64 against 0.415 at 128."""
     if self._fixed_cap is not None:
       return self._fixed_cap if self._fixed_cap > 0 else nat.ITEM_TILES
-    wide = self.n_blocks * int(batch) * int(heads) >= WIDE_JOBS
+    wide = kernel == "kv" or self.n_blocks * int(batch) * int(heads) >= WIDE_JOBS
     return WIDE_ITEM_TILES if wide else nat.ITEM_TILES
 
-  def schedule_for(self, batch, heads):
-    """The split-K schedule a call of `batch` x `heads` launches (items, split blocks, C struct)."""
-    return self._schedule(self.item_cap_for(batch, heads))
+  def schedule_for(self, batch, heads, kernel="fwd"):
+    """The split-K schedule `kernel` of a call of `batch` x `heads` launches (items, split blocks,
+    C struct)."""
+    return self._schedule(self.item_cap_for(batch, heads, kernel))
 
-  def order_for(self, batch, heads):
-    """Whether a call of `batch` x `heads` takes an order table: fewer than ORDER_JOBS jobs in
-    its per-item launch."""
-    sch = self.schedule_for(batch, heads)
+  def order_for(self, batch, heads, kernel="fwd"):
+    """Whether `kernel` of a call of `batch` x `heads` takes an order table: fewer than
+    ORDER_JOBS jobs in its per-item launch."""
+    sch = self.schedule_for(batch, heads, kernel)
     return sch.n_items * int(batch) * int(heads) < ORDER_JOBS
 
-  def struct_for(self, batch, heads, plan=None):
-    """The C struct to launch a call of `batch` x `heads` with (the schedule chosen for it); with
-    a `plan` (cut, window, slots) and few jobs (``order_for``), with that order table."""
-    sch = self.schedule_for(batch, heads)
-    if plan is not None and self.order_for(batch, heads):
+  def struct_for(self, batch, heads, plan=None, kernel="fwd"):
+    """The C struct to launch `kernel` of a call of `batch` x `heads` with (the schedule chosen
+    for it); with a `plan` (cut, window, slots) and few jobs (``order_for``), with that order
+    table."""
+    sch = self.schedule_for(batch, heads, kernel)
+    if plan is not None and self.order_for(batch, heads, kernel):
       return sch.ordered_struct(int(batch) * int(heads), *plan)
     return sch.struct
 
   def struct_for_desc(self, desc, kernel="fwd"):
     """The C struct for `kernel` ("fwd", "dq", or "kv" for dK/dV with this list as the transposed
     list) of a call with descriptor `desc`."""
-    return self.struct_for(desc.batch, desc.heads, order_plan(desc, kernel))
+    return self.struct_for(desc.batch, desc.heads, order_plan(desc, kernel), kernel)
 
   def workspace_bytes(self, desc):
-    """Workspace the launchers need for this list and the call shape `desc`: the size for the
-    schedule ``struct_for_desc`` picks for it (0 if that schedule splits no block)."""
+    """Workspace the launchers need for this list and the call shape `desc`: the most any of
+    the schedules ``struct_for_desc`` picks for its kernels needs (0 if none splits a block)."""
     n = ctypes.c_uint64(0)
-    nat.check(nat.lib().fwn_attn_workspace_size(desc, self.struct_for_desc(desc), ctypes.byref(n)))
-    return int(n.value)
+    most = 0
+    for kernel in ("fwd", "dq", "kv"):
+      nat.check(nat.lib().fwn_attn_workspace_size(desc, self.struct_for_desc(desc, kernel), ctypes.byref(n)))
+      most = max(most, int(n.value))
+    return most
 
   def ds_map(self, tiles_t, unit_keys=16):
     """The dS exchange's unit numbering of this (forward) list and `tiles_t` (this list itself

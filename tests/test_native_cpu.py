@@ -442,13 +442,23 @@ def test_tile_list_orders_calls_with_few_jobs():
       plan = (hip_attn.ORDER_CUTS[kernel], hip_attn.ORDER_WINDOWS[products][kernel], hip_attn.ORDER_SLOTS[kernel])
       assert hip_attn.order_plan(desc, kernel) == plan
       st = tl.struct_for_desc(desc, kernel)
-      table = sch.order_table(4, *plan)
+      table = tl.schedule_for(1, 4, kernel).order_table(4, *plan)
       assert st.work and st.work_pairs == 4 and st.n_work == len(table)
       assert tl.struct_for_desc(desc, kernel) is st  # built once
       size = ctypes.c_uint64(0)
-      nat.check(nat.lib().fwn_attn_workspace_size(desc, sch.struct, ctypes.byref(size)))
-      assert tl.workspace_bytes(desc) == int(size.value)
+      nat.check(nat.lib().fwn_attn_workspace_size(desc, st, ctypes.byref(size)))
+      assert tl.workspace_bytes(desc) >= int(size.value)
   assert hip_attn.ORDER_WINDOWS["bf16"] == {"fwd": 128, "dq": 128, "kv": 64}
+  # dK/dV's items are cut at WIDE_ITEM_TILES, the others at nat.ITEM_TILES below WIDE_JOBS; the
+  # workspace is the largest any of the three needs
+  assert tl.item_cap_for(1, 4, "kv") == hip_attn.WIDE_ITEM_TILES and tl.item_cap_for(1, 4) == nat.ITEM_TILES
+  assert tl.struct_for_desc(bf16, "kv").n_items == tl.schedule_for(1, 4, "kv").n_items
+  sizes = []
+  for kernel in ("fwd", "dq", "kv"):
+    size = ctypes.c_uint64(0)
+    nat.check(nat.lib().fwn_attn_workspace_size(bf16, tl.schedule_for(1, 4, kernel).struct, ctypes.byref(size)))
+    sizes.append(int(size.value))
+  assert tl.workspace_bytes(bf16) == max(sizes)
   many = -(-hip_attn.ORDER_JOBS // (sch.n_items * 4))
   assert not tl.order_for(many, 4) and tl.struct_for(many, 4, (nat.ORDER_BALANCED, 128, 64)).n_work == 0
 
