@@ -3,7 +3,8 @@ the library's static device scratch), against fwn_attn_fwd_launch with a caller 
 
 Two calls in a row share the scratch: the second, smaller call (fewer members, fewer nodes,
 another mask) must not see anything of the first. Both must equal the workspace launcher bit for
-bit (same kernels, same schedule) and the dense float64 oracle within the bars.
+bit (same kernels, same schedule), also when launched with the schedule's order table, and the
+dense float64 oracle within the bars.
 """
 import ctypes
 
@@ -42,7 +43,14 @@ def test_noalloc_forward_matches_workspace_forward(dtype):
                                     want_lse.data_ptr(), ws.data_ptr(), size.value, stream))
     nat.check(L.fwn_attn_fwd_launch_noalloc(desc, qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), tiles.struct,
                                             got.data_ptr(), got_lse.data_ptr(), stream))
+    # the same forward with the order table the library launches it with: the same bits
+    ordered = tiles.struct_for_desc(desc, "fwd")
+    assert ordered.n_work > 0
+    got2 = torch.full_like(qd, float("nan"))
+    nat.check(L.fwn_attn_fwd_launch_noalloc(desc, qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), ordered,
+                                            got2.data_ptr(), None, stream))
     torch.cuda.synchronize()
     np.testing.assert_array_equal(host(got), host(want), err_msg=f"call {call} out")
     np.testing.assert_array_equal(host(got_lse), host(want_lse), err_msg=f"call {call} lse")
+    np.testing.assert_array_equal(host(got2), host(want), err_msg=f"call {call} out, order table")
     check(host(got), A.dense_attention(q, k, v, m.toarray(), d ** -0.5), dtype, ("call", call))
