@@ -92,6 +92,28 @@ def test_every_order_gives_the_plain_order_bits(cap, case):
       np.testing.assert_array_equal(got[name], want[name], err_msg=f"{name} order {order} window {window}")
 
 
+@pytest.mark.parametrize("b,h,n", [(1, 1, 200), (1, 2, 642), (4, 4, 700), (3, 5, 1300)])
+def test_orders_at_edge_shapes(b, h, n):
+  """Order tables where most XCDs get one job or none (a 2-block list, one pair), odd pair
+  counts and more pairs than XCDs: the bf16 forward and dS-exchange backward give the plain
+  order's bits under every order."""
+  rng = np.random.default_rng(100 + n)
+  d = 64
+  q, k, v, do = (rounded(rng.standard_normal((b, n, h, d)), torch.bfloat16) for _ in range(4))
+  m = random_mask(n, 0.05, 101, symmetric=True)
+  tiles = fwn.TileList(*fwn.build_tile_mask(m), n, DEV)
+  sch = tiles.schedule_for(b, h)
+  args = [dev(x, torch.bfloat16) for x in (q, k, v, do)]
+  want = _run(sch.struct, tiles, *args, d ** -0.5, nat.PREC_NATIVE, True)
+  for order, window in ORDERS:
+    st = sch.ordered_struct(b * h, order, window, 32)
+    print(f"b {b} h {h} n {n} order {order} window {window}: {st.n_work} entries for {sch.n_items * b * h} jobs",
+          flush=True)
+    got = _run(st, tiles, *args, d ** -0.5, nat.PREC_NATIVE, True)
+    for name in want:
+      np.testing.assert_array_equal(got[name], want[name], err_msg=f"{name} order {order} window {window}")
+
+
 def test_library_orders_bf16_calls_and_matches_the_oracle():
   """The op's bf16 calls with few jobs launch with the order tables (windows of
   hip_attn.ORDER_WINDOWS); the result is the plain order's bit for bit and within the bf16 bars
