@@ -52,15 +52,17 @@ WIDE_JOBS = 1536
 #     counted from the start; from the end, C3 1.48 -> 1.44 ms and C5 unchanged. Windows of 128
 #     for dK/dV as well gave C3 1.490 and C5 2.899; no window C3 1.50-1.52.
 #   float32 (IEEE products): C2 forward 2.21 -> 1.94 ms; C5 shape fwd+bwd 19.40 -> 19.11 ms.
-#   bf16x3 products: C2 forward 0.764 -> 0.70-0.715 ms with windows of 128; at the C5 shape the
-#     windows made dK/dV +2.5% and dQ +4.5%, equal-cost ranges alone 7.04 -> 6.98 ms.
+#   bf16x3 products: C2 forward 0.764 -> 0.70-0.715 ms with windows of 128. At the C5 shape
+#     windows of 128 made dQ 5% slower (1.155 -> 1.22 ms), so dQ takes equal-cost ranges alone;
+#     dK/dV with windows of 64 counted from the end and the simulated cut 3.96 -> 3.89 ms (step
+#     7.00 -> 6.94 ms).
 # Sorting whole ranges, or all jobs, longest first lost the neighbouring blocks' shared K/V and
 # dS reads (C5 dQ +4-30%). With many jobs per slot (C4's 10,464) the plain ranges are already
 # even, so such calls keep the plain order.
 ORDER_JOBS = 4096
 ORDER_WINDOWS = {"bf16": {"fwd": 128, "dq": 128, "kv": 64},
                  "f32": {"fwd": 128, "dq": 128, "kv": 64},
-                 "bf16x3": {"fwd": 128, "dq": 0, "kv": 0}}
+                 "bf16x3": {"fwd": 128, "dq": 0, "kv": 64}}
 # How each kernel's ranges are cut (nat.ORDER_BALANCED: equal estimated cost; nat.ORDER_MAKESPAN:
 # equal simulated end on ORDER_SLOTS[kernel] slots per XCD) and its workgroups per XCD. For
 # dK/dV at C3 the equal-cost ranges left four XCDs with a last round of 7 jobs (199 on 32 slots)
