@@ -45,24 +45,24 @@ WIDE_JOBS = 1536
 # Order tables (fwn_tiles_order_fill) for calls whose per-item launch has fewer than ORDER_JOBS
 # jobs: each XCD takes a contiguous range of equal estimated cost, run longest first within
 # windows of ORDER_WINDOWS[products][kernel] jobs counted from the range's end (0: the range in
-# block order). The windows are two rounds of an XCD's slots where they pay: 128 for the bf16
-# and float32 forward and dQ (64 workgroups per XCD), 64 for dK/dV (32). Measured on MI355X
-# (three or two runs each on one box, plain order -> table):
-#   bf16 fwd+bwd: C3 1.562 -> 1.496 ms, the C5 attention shape 2.897 -> 2.852 ms with windows
-#     counted from the start; from the end, C3 1.48 -> 1.44 ms and C5 unchanged. Windows of 128
-#     for dK/dV as well gave C3 1.490 and C5 2.899; no window C3 1.50-1.52.
-#   float32 (IEEE products): C2 forward 2.21 -> 1.94 ms; C5 shape fwd+bwd 19.40 -> 19.11 ms.
-#   bf16x3 products: C2 forward 0.764 -> 0.70-0.715 ms with windows of 128. At the C5 shape
-#     windows of 128 made dQ 5% slower (1.155 -> 1.22 ms), so dQ takes equal-cost ranges alone;
-#     dK/dV with windows of 64 counted from the end and the simulated cut 3.96 -> 3.89 ms (step
-#     7.00 -> 6.94 ms).
+# block order). A window is one round of an XCD's slots: 64 jobs for the forward and dQ (two
+# workgroups per CU, 32 CUs per XCD), 32 for dK/dV (one per CU). Measured on MI355X (two or
+# three runs each on one box):
+#   bf16 fwd+bwd, plain order -> tables: C3 1.562 -> 1.496 ms and the C5 attention shape
+#     2.897 -> 2.852 ms with windows of two rounds counted from the start; counted from the end,
+#     C3 1.48 -> 1.44 ms, C5 unchanged; then one round (64 / 64 / 32 against 128 / 128 / 64):
+#     C3 1.323 -> 1.292 ms, C5 2.775 -> 2.72 ms. Windows of 48 / 48 / 24 and 32 / 32 / 16 were
+#     slower (C3 1.367, 1.356 ms).
+#   float32 (IEEE products): C2 forward 2.21 -> 1.92 ms; C5 shape fwd+bwd 19.40 -> 18.32 ms.
+#   bf16x3 products: C2 forward 0.764 -> 0.62 ms; at the C5 shape windows made dQ 5% slower, so
+#     dQ takes equal-cost ranges alone (step 7.00 -> 6.86 ms).
 # Sorting whole ranges, or all jobs, longest first lost the neighbouring blocks' shared K/V and
 # dS reads (C5 dQ +4-30%). With many jobs per slot (C4's 10,464) the plain ranges are already
 # even, so such calls keep the plain order.
 ORDER_JOBS = 4096
-ORDER_WINDOWS = {"bf16": {"fwd": 128, "dq": 128, "kv": 64},
-                 "f32": {"fwd": 128, "dq": 128, "kv": 64},
-                 "bf16x3": {"fwd": 128, "dq": 0, "kv": 64}}
+ORDER_WINDOWS = {"bf16": {"fwd": 64, "dq": 64, "kv": 32},
+                 "f32": {"fwd": 64, "dq": 64, "kv": 32},
+                 "bf16x3": {"fwd": 64, "dq": 0, "kv": 32}}
 # How each kernel's ranges are cut (nat.ORDER_BALANCED: equal estimated cost; nat.ORDER_MAKESPAN:
 # equal simulated end on ORDER_SLOTS[kernel] slots per XCD) and its workgroups per XCD. For
 # dK/dV at C3 the equal-cost ranges left four XCDs with a last round of 7 jobs (199 on 32 slots)

@@ -448,7 +448,7 @@ def test_tile_list_orders_calls_with_few_jobs():
       size = ctypes.c_uint64(0)
       nat.check(nat.lib().fwn_attn_workspace_size(desc, st, ctypes.byref(size)))
       assert tl.workspace_bytes(desc) >= int(size.value)
-  assert hip_attn.ORDER_WINDOWS["bf16"] == {"fwd": 128, "dq": 128, "kv": 64}
+  assert hip_attn.ORDER_WINDOWS["bf16"] == {"fwd": 64, "dq": 64, "kv": 32}
   # dK/dV's items are cut at WIDE_ITEM_TILES, the others at nat.ITEM_TILES below WIDE_JOBS; the
   # workspace is the largest any of the three needs
   assert tl.item_cap_for(1, 4, "kv") == hip_attn.WIDE_ITEM_TILES and tl.item_cap_for(1, 4) == nat.ITEM_TILES
