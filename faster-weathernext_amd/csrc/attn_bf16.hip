@@ -337,19 +337,22 @@ struct DsUnit {
 // dQ from the dS units (pallas_attn.py:177-184, with dS taken from the dK/dV pass instead of
 // recomputed): per work item of the forward list, dQ^T += K^T dS^T over the live 16-key halves of
 // each wave's 32 query rows. Each live half is one unit, loaded with one 16-byte load per lane
-// and transposed through this wave's 2 KB of LDS (DsUnit): no S, no dP, no exponentials, one of
+// and transposed through this wave's LDS stage (DsUnit): no S, no dP, no exponentials, one of
 // dq_kernel's three contractions.
 //
 // K tiles are double-buffered in LDS (64 KB at D = 128, one barrier per tile), two workgroups per
 // CU. After the barrier of tile t the K rows and the dS units of tile t + 1 are requested, so
 // both arrive while tile t is computed; the column block, group and half bits and first unit of
-// tile t + 2 are read with scalar loads at the same point.
+// tile t + 3 are read with scalar loads at the end of the step. Within a tile the wave's live
+// halves run as a two-stage pipeline: half k + 1's unit goes through the other 1 KB stage slot
+// and its LDS reads are in flight while half k's MFMAs issue (C3 dQ -2% against one key group at
+// a time, whose MFMAs waited for all of the group's reads).
 template <int D>
 __global__ void __launch_bounds__(NT, 2) dq_ds_kernel(KArgs a) {
   constexpr int TB = Tile<D>::BYTES;
   __shared__ __attribute__((aligned(1024))) char lk0[TB];
   __shared__ __attribute__((aligned(1024))) char lk1[TB];
-  __shared__ __attribute__((aligned(1024))) char lstage[4 * 2048];  // per wave: two units (a key group)
+  __shared__ __attribute__((aligned(1024))) char lstage[4 * 2048];  // per wave: two unit slots
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int i = lane & 31, g = lane >> 5;
@@ -371,45 +374,39 @@ __global__ void __launch_bounds__(NT, 2) dq_ds_kernel(KArgs a) {
   for (int db = 0; db < D / 32; ++db) acc[db] = zero16();
   typedef const __attribute__((address_space(4))) int32_t* cmap_ptr;
 
-  // This wave's units of a tile: half bits 8w .. 8w + 7 of the tile's word, numbered from the
-  // tile's first unit by their rank among all of the word's set bits. Each unit is read once:
+  // This wave's units of a tile, in the order of its set half bits 8w .. 8w + 7: a tile's units
+  // are numbered by rank among all of the word's set bits, so the wave's are consecutive, from
+  // the tile's first unit plus the set bits of the waves before it. Each unit is read once:
   // non-temporal loads.
   auto load_units = [&](u32x4 (&dst)[8], uint32_t hf, uint32_t ub) {
-    const uint32_t hw = hf >> (8 * w) & 0xffu;
-    uint32_t u = ub + (uint32_t)__builtin_popcount(hf & ((1u << (8 * w)) - 1u));
+    const uint32_t n = (uint32_t)__builtin_popcount(hf >> (8 * w) & 0xffu);
+    const uint32_t u0 = ub + (uint32_t)__builtin_popcount(hf & ((1u << (8 * w)) - 1u));
 #pragma unroll
-    for (int x = 0; x < 8; ++x)
-      if (hw >> x & 1u) {
-        dst[x] = __builtin_amdgcn_raw_buffer_load_b128(rS, 16 * lane, (int)(u * 1024u), kNonTemporal);
-        ++u;
-      }
+    for (int k = 0; k < 8; ++k)
+      if ((uint32_t)k < n)
+        dst[k] = __builtin_amdgcn_raw_buffer_load_b128(rS, 16 * lane, (int)((u0 + (uint32_t)k) * 1024u), kNonTemporal);
   };
-  // Tile t's halves of key group sb for this wave (bit h of hv), from K buffer `K`: the units
-  // through this wave's stage (the previous group's reads of it come first in program order, and
-  // LDS runs one wave's accesses in order), then the K^T operands, then the MFMAs.
-  auto group = [&](const lds_char* K, int sb, uint32_t hv, const u32x4 (&ds)[8]) {
+  // One live half: its unit through stage slot k % 2 (the slot's previous reads come first in
+  // program order, and LDS runs one wave's accesses in order), then the dS^T operand and the
+  // half's K^T operands (keys 16x .. 16x + 15, x = 2 sb + h the half's bit) into set `o`.
+  struct HalfOps {
+    u32x4 kt[D / 32], bs;
+  };
+  auto issue = [&](HalfOps& o, int k, const lds_char* K, uint32_t x, const u32x4& unit) {
     typedef __attribute__((address_space(3))) u32x4* l4p;
+    *(l4p)(st + 1024 * (k & 1) + du.w) = unit;
+    const u32x2 x0 = tr_read(st + 1024 * (k & 1), du.r0), x1 = tr_read(st + 1024 * (k & 1), du.r1);
+    o.bs = u32x4{x0[0], x0[1], x1[0], x1[1]};
+    const lds_char* Kx = K + x * (16u * 2u * D);
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
-      if (hv >> h & 1u) *(l4p)(st + 1024 * h + du.w) = ds[2 * sb + h];
-    asm volatile("" ::: "memory");
-    u32x4 kt[2][D / 32], bs[2];
+    for (int db = 0; db < D / 32; ++db) {
+      const u32x2 lo = tr_read(Kx, off.tr[db][0]), hi = tr_read(Kx, off.tr[db][1]);
+      o.kt[db] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+    }
+  };
+  auto mfmas = [&](const HalfOps& o) {
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
-      if (hv >> h & 1u) {
-        const u32x2 x0 = tr_read(st + 1024 * h, du.r0), x1 = tr_read(st + 1024 * h, du.r1);
-        bs[h] = u32x4{x0[0], x0[1], x1[0], x1[1]};
-#pragma unroll
-        for (int db = 0; db < D / 32; ++db) kt[h][db] = tr_operand<D>(K, off, db, sb, h);
-      }
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-      if (hv >> h & 1u) {
-#pragma unroll
-        for (int db = 0; db < D / 32; ++db) acc[db] = mfma_bf16(kt[h][db], bs[h], acc[db]);
-      }
-    asm volatile("" ::: "memory");
+    for (int db = 0; db < D / 32; ++db) acc[db] = mfma_bf16(o.kt[db], o.bs, acc[db]);
   };
 
   int t0, t1;
@@ -418,33 +415,57 @@ __global__ void __launch_bounds__(NT, 2) dq_ds_kernel(KArgs a) {
   int c1 = 0, c2 = 0;
   uint32_t g1 = 0u, g2 = 0u, h1 = 0u, h2 = 0u, u1 = 0u, u2 = 0u;
   u32x4 dsA[8], dsB[8];
-  uint32_t gcur = 0u, hcur = 0u;
+  uint32_t hcur = 0u;
+  // Step t: the live halves of tile t run as a two-stage pipeline, the LDS reads of half k + 1
+  // in flight while the MFMAs of half k issue.
   auto step = [&](int tt, const lds_char* cur, lds_char* nxt, const u32x4 (&dsc)[8], u32x4 (&dsn)[8]) {
     const int t = __builtin_amdgcn_readfirstlane(tt);
     wait_vmem();      // this wave's part of tile t's K rows and its dS units
     __syncthreads();  // all of tile t's K rows landed; every wave is done with tile t - 1 (buffer nxt)
-    const uint32_t gt = gcur, ht = hcur;
+    const uint32_t ht = hcur;
     if (t + 1 < t1) {
       dma.issue(rK, nxt, w, c1 * BLK, snb, any_rows(g1));
       load_units(dsn, h1, u1);
     }
-    gcur = g1;
     hcur = h1;
     c1 = c2;
     g1 = g2;
     h1 = h2;
     u1 = u2;
+    uint32_t rem = ht >> (8 * w) & 0xffu;
+    const uint32_t n = (uint32_t)__builtin_popcount(rem);
+    HalfOps P, Q;
+    if (n != 0u) {
+      issue(P, 0, cur, (uint32_t)__builtin_ctz(rem), dsc[0]);
+      rem &= rem - 1u;
+#pragma unroll
+      for (int k = 1; k < 8; ++k) {
+        if ((uint32_t)k < n) {
+          if (k & 1) {
+            issue(Q, k, cur, (uint32_t)__builtin_ctz(rem), dsc[k]);
+            mfmas(P);
+          } else {
+            issue(P, k, cur, (uint32_t)__builtin_ctz(rem), dsc[k]);
+            mfmas(Q);
+          }
+          rem &= rem - 1u;
+        }
+      }
+      // The last live half's MFMAs: one call site, its operands selected by the half's parity (a
+      // branch per set would give the accumulators two register assignments and copies between).
+      const bool odd = ((n - 1u) & 1u) != 0u;
+      HalfOps F;
+      F.bs = odd ? Q.bs : P.bs;
+#pragma unroll
+      for (int db = 0; db < D / 32; ++db) F.kt[db] = odd ? Q.kt[db] : P.kt[db];
+      mfmas(F);
+    }
     if (t + 3 < t1) {
       c2 = ((ci32_ptr)a.col)[t + 3];
       g2 = tile_groups(a, t + 3);
       h2 = tile_halves(a, t + 3);
       u2 = (uint32_t)((cmap_ptr)a.ubase)[t + 3];
     }
-    const uint32_t live = gt >> (4 * w) & 15u;
-    const uint32_t hw = ht >> (8 * w) & 0xffu;
-#pragma unroll
-    for (int sb = 0; sb < 4; ++sb)
-      if (live >> sb & 1u) group(cur, sb, hw >> (2 * sb) & 3u, dsc);
   };
   lds_char* K0 = (lds_char*)lk0;
   lds_char* K1 = (lds_char*)lk1;
@@ -452,7 +473,6 @@ __global__ void __launch_bounds__(NT, 2) dq_ds_kernel(KArgs a) {
     const uint32_t g0 = tile_groups(a, t0), hf0 = tile_halves(a, t0);
     dma.issue(rK, K0, w, ((ci32_ptr)a.col)[t0] * BLK, snb, any_rows(g0));
     load_units(dsA, hf0, (uint32_t)((cmap_ptr)a.ubase)[t0]);
-    gcur = g0;
     hcur = hf0;
     if (t0 + 1 < t1) {
       c1 = ((ci32_ptr)a.col)[t0 + 1];
