@@ -343,10 +343,10 @@ struct DsUnit {
 // K tiles are double-buffered in LDS (64 KB at D = 128, one barrier per tile), two workgroups per
 // CU. After the barrier of tile t the K rows of tile t + 1 are requested, and its dS units after
 // the first half's LDS work, so both arrive while tile t is computed; the column block, group and
-// half bits and first unit of tile t + 3 are read with scalar loads at the end of the step. Within a tile the wave's live
-// halves run as a two-stage pipeline: half k + 1's unit goes through the other 1 KB stage slot
-// and its LDS reads are in flight while half k's MFMAs issue (C3 dQ -2% against one key group at
-// a time, whose MFMAs waited for all of the group's reads).
+// half bits and first unit of tile t + 3 are read with scalar loads at the end of the step. Within
+// a tile the wave's live halves run as a two-stage pipeline: half k + 1's unit goes through the
+// other 1 KB stage slot and its LDS reads are in flight while half k's MFMAs issue (C3 dQ -2%
+// against one key group at a time, whose MFMAs waited for all of the group's reads).
 template <int D>
 __global__ void __launch_bounds__(NT, 2) dq_ds_kernel(KArgs a) {
   constexpr int TB = Tile<D>::BYTES;
