@@ -429,7 +429,8 @@ __global__ void __launch_bounds__(NT, 2) dq_ds_kernel(KArgs a) {
 
   int t0, t1;
   tile_range(a, j, t0, t1);
-  // Scalars of tile t + 1 (n1: column block, half bits, first unit) and t + 2 (n2).
+  // Scalars of tile t + 1 (c1, h1, u1: column block, half bits, first unit) and of tile t + 2
+  // (c2, h2, u2), at the start of step t.
   int c1 = 0, c2 = 0;
   uint32_t h1 = 0u, h2 = 0u, u1 = 0u, u2 = 0u;
   u32x4 dsA[8], dsB[8];
