@@ -758,13 +758,18 @@ __global__ void __launch_bounds__(NT8, 1) dkv16_kernel(KArgs a) {
 
   // Tile copies, in one of three modes per wave: 0, waves 0-3 copy Q and waves 4-7 dO; 1, this
   // wave issues both shares of its SIMD pair (waves wid % 4 and wid % 4 + 4: the Q and dO ops of
-  // class wid % 4); 2, none (its partner is in mode 1). Wave 0 also copies the tile's 128 lse and
-  // delta (two branch-free full-wave copies; out-of-range halves read zeros into the gap).
+  // class wid % 4); 2, none (its partner is in mode 1). The tile's 128 lse and delta (two
+  // branch-free full-wave copies; out-of-range halves read zeros into the gap) go with wave 0 in
+  // mode 0 and with pair 0's copier otherwise; the same wave rescales them at the start of the
+  // tile's step, after waiting for its own copies (pair 0's copier has the fewer units, so its
+  // rescale delays the barrier least: C5-shape dK/dV -1%).
   TileDma<D, true> dma, dmaQ, dmaO;
   dma.init(wid & 3, lane, wid < 4 ? snb : osnb);
   dmaQ.init(wid & 3, lane, snb);
   dmaO.init(wid & 3, lane, osnb);
   constexpr uint32_t kPastEnd = 0x7FFFFFF0u;
+  auto stats_wave = [&](int mode) { return mode == 0 ? wid == 0 : (mode == 1 && (wid & 3) == 0); };
+  bool stats_cur = false;  // this wave copied the current tile's lse and delta (it rescales them)
   auto issue = [&](int qb, lds_char* buf, uint32_t copy, int mode) {
     if (mode == 0) {
       if (wid < 4) {
@@ -776,7 +781,7 @@ __global__ void __launch_bounds__(NT8, 1) dkv16_kernel(KArgs a) {
       dmaQ.issue(rQ, buf, wid & 3, qb * BLK, snb, copy);
       dmaO.issue(rO, buf + TB, wid & 3, qb * BLK, osnb, copy);
     }
-    if (wid == 0) {
+    if (stats_wave(mode)) {
       const uint32_t vo = (uint32_t)(qb * BLK + 4 * (lane & 31)) * 4;
       lds_char* stats = buf + 2 * TB;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rL, (__attribute__((address_space(3))) void*)stats, 16,
@@ -814,9 +819,10 @@ __global__ void __launch_bounds__(NT8, 1) dkv16_kernel(KArgs a) {
   auto tile_step = [&](int tt, int t1, lds_char* cur, lds_char* nxt, uint64_t& mnext, uint32_t& gnext,
                        int& cnext) {
     const int t = __builtin_amdgcn_readfirstlane(tt);
+    bool stats_nxt = false;
     wait_vmem();  // this wave's part of tile t and its mask word
     const uint64_t mw = mnext >> mshift;
-    if (wid == 0) {
+    if (stats_cur) {
       // lse -> -lse / scale and delta -> -delta, the initial values of the S and dP accumulators.
       __attribute__((address_space(3))) f32x4* x =
           (__attribute__((address_space(3))) f32x4*)(cur + 2 * TB + (lane < 32 ? 0 : 512) + 16 * lane);
@@ -841,6 +847,7 @@ __global__ void __launch_bounds__(NT8, 1) dkv16_kernel(KArgs a) {
         mode = ((wid < 4) == (ns <= ns4)) ? 1 : 2;
       }
       issue(cnext, nxt, any_rows(gnext), mode);
+      stats_nxt = stats_wave(mode);
     }
     if (t + 2 < t1) {
       gnext = tile_groups(a, t + 2);
@@ -867,6 +874,7 @@ __global__ void __launch_bounds__(NT8, 1) dkv16_kernel(KArgs a) {
         hfc = ((cmap_ptr)a.tmap)[2 * (t + 1) + 1];
       }
     }
+    stats_cur = stats_nxt;
   };
 
   int t0, t1;
@@ -887,6 +895,7 @@ __global__ void __launch_bounds__(NT8, 1) dkv16_kernel(KArgs a) {
       hfc = ((cmap_ptr)a.tmap)[2 * t0 + 1];
     }
     issue(((ci32_ptr)a.col)[t0], b0, any_rows(tile_groups(a, t0)), 0);
+    stats_cur = wid == 0;
   }
   for (int tt = t0; tt < t1; tt += 2) {
     tile_step(tt, t1, b0, b1, mnext, gnext, cnext);
