@@ -381,6 +381,66 @@ def test_ds_exchange_matches_recompute_and_oracle(case, d, dtype, monkeypatch):
       _check(res[name][:, keep], r, dtype, name)
 
 
+def _pair_skew_mask(n, heavy, seed):
+  """A non-symmetric banded mask whose valid keys crowd into one half of every 128-key block:
+  keys 64 * heavy .. 64 * heavy + 63 of a block are valid for every query within 150 rows, the
+  other half only on the diagonal and at a few scattered keys (heavy = 2: both halves dense). The bf16 dK/dV kernel gives keys
+  16 kg .. 16 kg + 15 of a block to wave kg and pairs waves s and s + 4 on one SIMD, so with
+  heavy = 0 the waves 0-3 hold most units of every tile (waves 4-7 then issue the pairs' copies),
+  with heavy = 1 the reverse, and with heavy = 2 the pairs mostly tie."""
+  rng = np.random.default_rng(seed)
+  rows, cols = [], []
+  for q in range(n):
+    ks = np.arange(max(0, q - 150), min(n, q + 150))
+    half = (ks % 128) // 64
+    dense = ks[(half == heavy) | (heavy == 2)]
+    sparse_ks = ks[(half != heavy) & (heavy != 2)]
+    sparse_ks = sparse_ks[rng.random(len(sparse_ks)) < 0.0005]
+    sel = np.unique(np.concatenate([dense, sparse_ks, [q]]))
+    rows.extend([q] * len(sel))
+    cols.extend(sel.tolist())
+  return sparse.csr_matrix((np.ones(len(rows), bool), (rows, cols)), shape=(n, n))
+
+
+@pytest.mark.parametrize("heavy", [0, 1, 2])
+def test_ds_exchange_paired_copies(heavy, monkeypatch):
+  """The bf16 dK/dV kernel with the dS exchange lets the wave of each SIMD pair with fewer units
+  in a tile issue the pair's whole Q/dO copy (and pair 0's copier the lse/delta copy and its
+  rescale). On masks that make one half of every pair heavy (both ways) or the pairs tie, dK and
+  dV equal the recomputing kernel's, which keeps the fixed split, bit for bit, and every output
+  meets the bf16 bars against the dense float64 oracle."""
+  print(f"paired copies heavy={heavy}", flush=True)
+  n, b, h, d = 700, 1, 2, 128
+  m = _pair_skew_mask(n, heavy, 70 + heavy)
+  tiles = fwn.TileList.from_mask(m)
+  tiles_t = fwn.TileList.from_mask(m.T.tocsr())
+  # The forward tile's half bits (bit 8c + kg: query group c, 16-key group kg) count each wave's
+  # units in a tile; check that the mask gives the pairs the intended balance: per tile and pair,
+  # which of waves s and s + 4 holds more units.
+  more = {"lo": 0, "hi": 0, "tie": 0}
+  for x in np.asarray(tiles.halves_host).astype(np.uint64).tolist():
+    for s in range(4):
+      a, c = (bin(x >> g & 0x01010101).count("1") for g in (s, s + 4))
+      more["lo" if a > c else "hi" if a < c else "tie"] += 1
+  print(more, flush=True)
+  if heavy < 2:
+    big, small = ("lo", "hi") if heavy == 0 else ("hi", "lo")
+    assert more[big] > 2 * (more[small] + more["tie"]), more
+  else:
+    assert min(more.values()) >= 8, more
+  dtype = torch.bfloat16
+  rng = np.random.default_rng(90 + heavy)
+  q, k, v, do = (_rounded(rng.standard_normal((b, n, h, d)), dtype) for _ in range(4))
+  got, ref = _run_modes(q, k, v, do, tiles, d ** -0.5, dtype, tiles_t, monkeypatch)
+  for name in ("out", "dk", "dv"):
+    np.testing.assert_array_equal(got[name], ref[name], err_msg=name)
+  assert A.rel_rms(got["dq"], ref["dq"]) < 1e-3, A.rel_rms(got["dq"], ref["dq"])
+  dense = m.toarray()
+  _check(got["out"], A.dense_attention(q, k, v, dense, d ** -0.5), dtype, "out")
+  for name, r in zip(("dq", "dk", "dv"), A.dense_grads(q, k, v, do, dense, d ** -0.5)):
+    _check(got[name], r, dtype, name)
+
+
 def test_ds_exchange_falls_back_for_a_list_that_is_not_the_transpose(monkeypatch):
   """A non-symmetric mask run without its transposed list (the reference's tiles_t=None) is not
   a transpose pair, so the dS exchange does not apply and the bf16 backward recomputes dQ: dQ
