@@ -636,6 +636,99 @@ def test_exp2_based_softmax_accuracy():
   np.testing.assert_allclose(_np(lse), ref, rtol=2e-6, atol=2e-6)
 
 
+def _extreme_logit_case(d, seed):
+  """Three row groups of 192 (n = 576, a ragged last block): rows 0-191 take keys 0-191, whose
+  logits are O(1); rows 192-383 take keys 192-383, whose logits are about +100 (natural units),
+  plus the keys of 0-191 within 100 rows; rows 384-575 take keys 384-575 only, whose logits are
+  about -100. Channel 0 carries the offsets (q = 1, k = +-100 / scale, exact in bf16), the other
+  channels are standard normal. Every masked key of the first and last groups has a logit far
+  above the valid ones: had it entered a row's reference max, exp2 of the valid logits would
+  underflow (2^-144 and below) and the row would come out zero or NaN. The middle rows' max
+  jumps by about 144 (log2 units) between tiles, so the running sums are rescaled by factors that
+  underflow."""
+  rng = np.random.default_rng(seed)
+  n, g = 576, 192
+  scale = d ** -0.5
+  rows, cols = [], []
+  for i in range(n):
+    grp = i // g
+    lo, hi = (i - 100, i + 40) if grp == 1 else (i - 60, i + 60)
+    ks = np.arange(max(lo, 0 if grp != 2 else 2 * g), min(hi, (grp + 1) * g - 1) + 1)
+    if grp == 0:
+      ks = ks[ks < g]
+    rows.extend([i] * len(ks))
+    cols.extend(ks.tolist())
+  m = sparse.csr_matrix((np.ones(len(rows), bool), (rows, cols)), shape=(n, n))
+  q = rng.standard_normal((1, n, 2, d))
+  k = rng.standard_normal((1, n, 2, d))
+  q[..., 0] = 1.0
+  k[:, :g, :, 0] = 0.0
+  k[:, g:2 * g, :, 0] = 100.0 / scale
+  k[:, 2 * g:, :, 0] = -100.0 / scale
+  v, do = (rng.standard_normal((1, n, 2, d)) for _ in range(2))
+  return m, scale, q, k, v, do
+
+
+def _dq_rounding_bound(q, k, v, do, out, dense, scale):
+  """Per element of dq, the float64 sum scale * (sum_j |dS_ij| |k_j| + |o_i| . |do_i| sum_j P_ij |k_j|).
+  dq = scale sum_j dS_ij k_j, with dS = P (dP - delta) and delta = o . do: a relative error u in
+  each dS_ij (dS rounded to bf16 for its product with K) and one of u times |o_i| . |do_i| in
+  delta_i (o is the rounded forward output) move dq by at most u times this sum. With keys whose
+  logits carry a large common offset, sum_j dS_ij k_j cancels to a small value while the terms
+  stay large, so dq's rounding error is set by this sum, not by dq itself."""
+  p = A._dense_probs(q, k, dense, scale)
+  q64, k64, v64, do64, o64 = (x.astype(np.float64) for x in (q, k, v, do, out))
+  dp = np.einsum("bnhd,bmhd->bhnm", do64, v64)
+  ds = p * (dp - (dp * p).sum(-1, keepdims=True))
+  ak = np.abs(k64)
+  t1 = np.einsum("bhnm,bmhd->bnhd", np.abs(ds), ak)
+  od = np.einsum("bnhd,bnhd->bnh", np.abs(do64), np.abs(o64))
+  t2 = np.einsum("bhnm,bmhd->bnhd", p, ak) * od[..., None]
+  return scale * (t1 + t2)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("d", [64, 128])
+def test_extreme_logits_and_masked_giants(d, dtype):
+  """Rows whose valid logits are all near -100, rows whose masked keys carry logits up to +100
+  above their valid ones, and rows whose max jumps by +100 halfway (_extreme_logit_case):
+  forward, log-sum-exp and gradients (bf16: the dS exchange) against the dense float64 oracle.
+  out, dk and dv meet the usual bars in bf16; in float32 the logits of magnitude 100 carry
+  rounding of about 1e-5 in absolute terms (one unit in the last place of 100 is 7.6e-6, and the
+  kernel scales and sums them), which enters each probability as a relative error of that size:
+  bars 4e-5 (rms) and 2e-4 (max). dq = scale sum_j dS_ij k_j cancels (channel 0 of k carries the
+  +-100 offsets, and sum_j dS_ij = 0), so it is held to the rounding bound of that sum
+  (_dq_rounding_bound) with u = 2^-7 in bf16 (twice bf16's unit roundoff) and 2^-14 in float32
+  (float32's unit roundoff times the about 1,000 terms an element sums)."""
+  print(f"extreme logits d={d} {dtype}", flush=True)
+  m, scale, q, k, v, do = _extreme_logit_case(d, 60 + d)
+  q, k, v, do = (_rounded(x, dtype) for x in (q, k, v, do))
+  tiles = fwn.TileList.from_mask(m)
+  tiles_t = fwn.TileList.from_mask(m.T.tocsr())
+  qt, kt, vt = (_dev(x, dtype) for x in (q, k, v))
+  out, lse = fwn.attention_forward(qt, kt, vt, tiles, scale)
+  got = _run(q, k, v, do, tiles, scale, dtype, tiles_t)
+  dense = m.toarray()
+  ref_lse = A.dense_lse(q, k, dense, scale)
+  assert np.isfinite(_np(lse)).all() and np.isfinite(got["out"]).all()
+  # lse sits near -100, 0 and +100 in the three groups; its error is the logits' rounding.
+  np.testing.assert_allclose(_np(lse), ref_lse, rtol=0, atol=2e-3 if dtype == torch.bfloat16 else 1e-4)
+  np.testing.assert_array_equal(_np(out), got["out"])
+  rms, mx = (5e-3, 3e-2) if dtype == torch.bfloat16 else (4e-5, 2e-4)
+  ref_dq, ref_dk, ref_dv = A.dense_grads(q, k, v, do, dense, scale)
+  for name, r in (("out", A.dense_attention(q, k, v, dense, scale)), ("dk", ref_dk), ("dv", ref_dv)):
+    assert np.isfinite(got[name]).all(), name
+    rr, mr = A.rel_rms(got[name], r), A.max_rel_err(got[name], r)
+    print(f"  {name}: rel rms {rr:.2e}, max {mr:.2e}", flush=True)
+    assert rr <= rms and mr <= mx, (name, rr, mr)
+  assert np.isfinite(got["dq"]).all()
+  bound = _dq_rounding_bound(q, k, v, do, got["out"], dense, scale)
+  u = 2.0 ** -7 if dtype == torch.bfloat16 else 2.0 ** -14
+  ratio = np.abs(got["dq"] - ref_dq) / (u * bound + 1e-30)
+  print(f"  dq: rel rms {A.rel_rms(got['dq'], ref_dq):.2e}, error / bound max {ratio.max():.3f}", flush=True)
+  assert ratio.max() <= 1.0, ratio.max()
+
+
 def test_reference_keywords_give_the_same_result():
   """A call written for the reference's signature (pallas_attn.py:317-320: strict_fp32, block
   sizes, Triton tuning values) runs the same kernels: bit-identical outputs and gradients."""
