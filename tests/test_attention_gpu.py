@@ -640,8 +640,8 @@ def _extreme_logit_case(d, seed):
   """Three row groups of 192 (n = 576, a ragged last block): rows 0-191 take keys 0-191, whose
   logits are O(1); rows 192-383 take keys 192-383, whose logits are about +100 (natural units),
   plus the keys of 0-191 within 100 rows; rows 384-575 take keys 384-575 only, whose logits are
-  about -100. Channel 0 carries the offsets (q = 1, k = +-100 / scale, exact in bf16), the other
-  channels are standard normal. Every masked key of the first and last groups has a logit far
+  about -100. Channel 0 carries the offsets (q = 1, k = +-100 / scale rounded to bf16, so that
+  every precision holds it exactly), the other channels are standard normal. Every masked key of the first and last groups has a logit far
   above the valid ones: had it entered a row's reference max, exp2 of the valid logits would
   underflow (2^-144 and below) and the row would come out zero or NaN. The middle rows' max
   jumps by about 144 (log2 units) between tiles, so the running sums are rescaled by factors that
@@ -663,8 +663,9 @@ def _extreme_logit_case(d, seed):
   k = rng.standard_normal((1, n, 2, d))
   q[..., 0] = 1.0
   k[:, :g, :, 0] = 0.0
-  k[:, g:2 * g, :, 0] = 100.0 / scale
-  k[:, 2 * g:, :, 0] = -100.0 / scale
+  off = float(torch.tensor(100.0 / scale).to(torch.bfloat16))
+  k[:, g:2 * g, :, 0] = off
+  k[:, 2 * g:, :, 0] = -off
   v, do = (rng.standard_normal((1, n, 2, d)) for _ in range(2))
   return m, scale, q, k, v, do
 
@@ -687,9 +688,9 @@ def _dq_rounding_bound(q, k, v, do, out, dense, scale):
   return scale * (t1 + t2)
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("case", ["bf16", "f32", "bf16x3"])
 @pytest.mark.parametrize("d", [64, 128])
-def test_extreme_logits_and_masked_giants(d, dtype):
+def test_extreme_logits_and_masked_giants(d, case):
   """Rows whose valid logits are all near -100, rows whose masked keys carry logits up to +100
   above their valid ones, and rows whose max jumps by +100 halfway (_extreme_logit_case):
   forward, log-sum-exp and gradients (bf16: the dS exchange) against the dense float64 oracle.
@@ -699,15 +700,22 @@ def test_extreme_logits_and_masked_giants(d, dtype):
   bars 4e-5 (rms) and 2e-4 (max). dq = scale sum_j dS_ij k_j cancels (channel 0 of k carries the
   +-100 offsets, and sum_j dS_ij = 0), so it is held to the rounding bound of that sum
   (_dq_rounding_bound) with u = 2^-7 in bf16 (twice bf16's unit roundoff) and 2^-14 in float32
-  (float32's unit roundoff times the about 1,000 terms an element sums)."""
-  print(f"extreme logits d={d} {dtype}", flush=True)
+  (float32's unit roundoff times the about 1,000 terms an element sums). bf16x3 (float32 tensors,
+  products from bf16 parts) is held to the float32 bars: the offsets are exact in bf16, so the
+  split leaves them whole, and the other channels are of order one."""
+  print(f"extreme logits d={d} {case}", flush=True)
+  dtype = torch.bfloat16 if case == "bf16" else torch.float32
+  precision = "bf16x3" if case == "bf16x3" else "native"
   m, scale, q, k, v, do = _extreme_logit_case(d, 60 + d)
   q, k, v, do = (_rounded(x, dtype) for x in (q, k, v, do))
   tiles = fwn.TileList.from_mask(m)
   tiles_t = fwn.TileList.from_mask(m.T.tocsr())
-  qt, kt, vt = (_dev(x, dtype) for x in (q, k, v))
-  out, lse = fwn.attention_forward(qt, kt, vt, tiles, scale)
-  got = _run(q, k, v, do, tiles, scale, dtype, tiles_t)
+  out, lse = fwn.attention_forward(*(_dev(x, dtype) for x in (q, k, v)), tiles, scale, precision=precision)
+  qt, kt, vt = (_dev(x, dtype, True) for x in (q, k, v))
+  res = fwn.tiled_flash_attention(qt, kt, vt, tiles, scale=scale, tiles_t=tiles_t, precision=precision)
+  res.backward(_dev(do, dtype))
+  got = {"out": _np(res), "dq": _np(qt.grad), "dk": _np(kt.grad), "dv": _np(vt.grad)}
+  torch.cuda.synchronize()
   dense = m.toarray()
   ref_lse = A.dense_lse(q, k, dense, scale)
   assert np.isfinite(_np(lse)).all() and np.isfinite(got["out"]).all()
