@@ -269,7 +269,10 @@ int check_ds(const fwn_attn_desc* d, const fwn_ds_map* m, const void* ds, uint64
   if (m->n_units < 0 || m->n_units * ds_unit_bytes(m) >= ((int64_t)1 << 31))
     return fail(FWN_ERR_INVALID_ARG, "ds map: %lld units of %lld bytes (a (batch, head) slice must stay below 2 GiB)",
                 (long long)m->n_units, (long long)ds_unit_bytes(m));
-  if ((need_ubase && !m->ubase) || (need_tmap && !m->tmap)) return fail(FWN_ERR_INVALID_ARG, "ds map: null arrays");
+  // Every listed tile holds a valid element, hence a unit: a map without units belongs to lists
+  // without tiles, whose per-tile arrays are empty and may be null.
+  if (m->n_units > 0 && ((need_ubase && !m->ubase) || (need_tmap && !m->tmap)))
+    return fail(FWN_ERR_INVALID_ARG, "ds map: null arrays");
   if (!ds) return fail(FWN_ERR_INVALID_ARG, "ds is null");
   if (((uintptr_t)ds & 255u) != 0) return fail(FWN_ERR_INVALID_ARG, "ds is not 256-byte aligned");
   const uint64_t need = (uint64_t)d->batch * (uint64_t)d->heads * (uint64_t)(m->n_units * ds_unit_bytes(m));

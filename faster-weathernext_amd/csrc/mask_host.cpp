@@ -271,9 +271,11 @@ int fwn_tiles_fill(int32_t n_rows, int32_t n_cols, const int64_t* row_ptr, const
   fwn::clear_error();
   Csr m;
   if (int rc = make_csr(m, n_rows, n_cols, row_ptr, idx, perm)) return rc;
-  if (!tile_ptr || !tile_col || !tile_bits)
-    return fwn::fail(FWN_ERR_INVALID_ARG, "fwn_tiles_fill: null output");
   const int32_t n_qb = (n_rows + FWN_BLOCK - 1) / FWN_BLOCK;
+  // A mask without a valid element has no tiles: the column and bit arrays are then empty and may
+  // be null.
+  if (!tile_ptr || ((!tile_col || !tile_bits) && tile_ptr[n_qb] > 0))
+    return fwn::fail(FWN_ERR_INVALID_ARG, "fwn_tiles_fill: null output");
   const int32_t n_kb = (n_cols + FWN_BLOCK - 1) / FWN_BLOCK;
   const int64_t words = FWN_BLOCK * (FWN_BLOCK / 32);
   std::atomic<bool> bad(false);

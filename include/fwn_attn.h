@@ -163,7 +163,8 @@ int fwn_hilbert_order(int64_t n, const double* lat_deg, const double* lon_deg, i
  * permuted as mask[perm][:, perm] (perm of length n_rows == n_cols, or NULL). Two passes:
  * fwn_tiles_count writes tile_ptr[ceil(n_rows / 128) + 1]; fwn_tiles_fill writes
  * tile_col[tile_ptr[last]] and tile_bits[tile_ptr[last] * 128 * 4] (bit j of word w of row r:
- * key col*128 + 32w + j). Replaces pallas_attn.build_tile_mask (pallas_attn.py:85-109). */
+ * key col*128 + 32w + j); both may be NULL when the mask has no valid element (no tiles).
+ * Replaces pallas_attn.build_tile_mask (pallas_attn.py:85-109). */
 int fwn_tiles_count(int32_t n_rows, int32_t n_cols, const int64_t* row_ptr, const int32_t* idx,
                     const int64_t* perm, int32_t* tile_ptr);
 int fwn_tiles_fill(int32_t n_rows, int32_t n_cols, const int64_t* row_ptr, const int32_t* idx,
@@ -299,7 +300,8 @@ int fwn_attn_bwd_launch(const fwn_attn_desc* desc, const void* q, const void* k,
 /* Unit numbering of a forward tile list and its transposed list (device arrays). */
 typedef struct fwn_ds_map {
   int64_t n_units;       /* units of the forward list */
-  const int32_t* ubase;  /* [tiles->n_tiles] first unit of each forward tile */
+  const int32_t* ubase;  /* [tiles->n_tiles] first unit of each forward tile (ubase and tmap
+                            may be NULL when n_units is 0: lists without tiles) */
   const int32_t* tmap;   /* [tiles_t->n_tiles][2]: for each transposed tile, ubase and the unit
                             bits word (as int32: halves for 16, groups for 32) of the same tile of
                             the forward list */

@@ -219,6 +219,66 @@ def test_rows_without_keys_are_zero_and_finite():
     np.testing.assert_array_equal(res[name][:, empty], 0.0)
 
 
+@pytest.mark.parametrize("case", ["bf16", "f32", "bf16x3"])
+@pytest.mark.parametrize("n", [1, 2, 33, 129])
+def test_tiny_sequences(n, case):
+  """Sequences shorter than one 32-row group, one block plus one row: a single partial tile (or
+  two blocks), most of its rows and columns past n. Forward and backward against the dense
+  float64 oracle. With so few keys per row dq = scale sum_j dS_ij k_j is a difference of a few
+  rounded terms (sum_j dS_ij = 0) and dS = P (dP - delta) a difference of a few products (with
+  n = 1, P = 1 and dS = 0 exactly), so dq and dk are held to the rounding bounds of their sums
+  (_grad_rounding_bounds, u = 2^-7 in bf16, 2^-14 in float32 and bf16x3); out and dv to the
+  usual bars."""
+  print(f"tiny n={n} {case}", flush=True)
+  dtype = torch.bfloat16 if case == "bf16" else torch.float32
+  precision = "bf16x3" if case == "bf16x3" else "native"
+  rng = np.random.default_rng(n)
+  b, h, d = 2, 2, 64
+  q, k, v, do = (_rounded(rng.standard_normal((b, n, h, d)), dtype) for _ in range(4))
+  m = _random_mask(n, 0.3, n, symmetric=True)
+  tiles = fwn.TileList.from_mask(m)
+  qt, kt, vt = (_dev(x, dtype, True) for x in (q, k, v))
+  out = fwn.tiled_flash_attention(qt, kt, vt, tiles, scale=d ** -0.5, precision=precision)
+  out.backward(_dev(do, dtype))
+  torch.cuda.synchronize()
+  dense = m.toarray()
+  # bf16x3 keeps its own float32 bars (max 2e-5 of max|ref|, tests/test_x3_gpu.py).
+  rms, mx = (TOL[dtype], MAXTOL[dtype]) if precision == "native" else (1e-5, 2e-5)
+
+  def check(got, ref, what):
+    rr, mr = A.rel_rms(got, ref), A.max_rel_err(got, ref)
+    assert rr <= rms and mr <= mx, (what, rr, mr)
+
+  check(_np(out), A.dense_attention(q, k, v, dense, d ** -0.5), "out")
+  ref_dq, ref_dk, ref_dv = A.dense_grads(q, k, v, do, dense, d ** -0.5)
+  bq, bk = _grad_rounding_bounds(q, k, v, do, _np(out), dense, d ** -0.5)
+  u = 2.0 ** -7 if dtype == torch.bfloat16 else 2.0 ** -14
+  for t, r, b, name in ((qt, ref_dq, bq, "dq"), (kt, ref_dk, bk, "dk")):
+    ratio = np.abs(_np(t.grad) - r) / (u * b + 1e-30)
+    assert ratio.max() <= 1.0, (name, ratio.max())
+  check(_np(vt.grad), ref_dv, "dv")
+
+
+@pytest.mark.parametrize("case", ["bf16", "f32", "bf16x3"])
+def test_mask_without_valid_elements(case):
+  """A mask with no valid element at all has no tiles (every array of the list empty): every
+  row is a row without keys, so the output and every gradient are zero."""
+  print(f"empty mask {case}", flush=True)
+  dtype = torch.bfloat16 if case == "bf16" else torch.float32
+  precision = "bf16x3" if case == "bf16x3" else "native"
+  rng = np.random.default_rng(3)
+  n, h, d = 300, 2, 64
+  q, k, v, do = (rng.standard_normal((1, n, h, d)) for _ in range(4))
+  tiles = fwn.TileList.from_mask(sparse.csr_matrix((n, n), dtype=bool))
+  assert tiles.n_tiles == 0
+  qt, kt, vt = (_dev(x, dtype, True) for x in (q, k, v))
+  out = fwn.tiled_flash_attention(qt, kt, vt, tiles, scale=d ** -0.5, precision=precision)
+  out.backward(_dev(do, dtype))
+  torch.cuda.synchronize()
+  for t in (out, qt.grad, kt.grad, vt.grad):
+    np.testing.assert_array_equal(_np(t), 0.0)
+
+
 def _group_pattern_mask(seed):
   """n = 512 mask built from 32 x 32 groups so that the group skipping meets every case: per
   tile, waves (row groups) with different live column groups, waves with none, column groups
@@ -670,22 +730,24 @@ def _extreme_logit_case(d, seed):
   return m, scale, q, k, v, do
 
 
-def _dq_rounding_bound(q, k, v, do, out, dense, scale):
-  """Per element of dq, the float64 sum scale * (sum_j |dS_ij| |k_j| + |o_i| . |do_i| sum_j P_ij |k_j|).
-  dq = scale sum_j dS_ij k_j, with dS = P (dP - delta) and delta = o . do: a relative error u in
-  each dS_ij (dS rounded to bf16 for its product with K) and one of u times |o_i| . |do_i| in
-  delta_i (o is the rounded forward output) move dq by at most u times this sum. With keys whose
-  logits carry a large common offset, sum_j dS_ij k_j cancels to a small value while the terms
-  stay large, so dq's rounding error is set by this sum, not by dq itself."""
+def _grad_rounding_bounds(q, k, v, do, out, dense, scale):
+  """Per element of dq and of dk, float64 sums that bound their rounding error:
+  dq_i: scale sum_j (|dS_ij| + P_ij |o_i| . |do_i|) |k_j|;  dk_j: scale sum_i (same) |q_i|.
+  dq = scale sum_j dS_ij k_j and dk = scale sum_i dS_ij q_i, with dS = P (dP - delta) and
+  delta = o . do: a relative error u in each dS_ij (dS rounded to bf16 for its products with K
+  and Q) and one of u times |o_i| . |do_i| in delta_i (o is the rounded forward output) move dq
+  and dk by at most u times these sums. Where sum_j dS_ij k_j cancels (sum_j dS_ij = 0: keys
+  whose logits share a large offset, or rows with very few keys) or dP - delta does (few keys),
+  the error is set by these sums, not by the gradients themselves."""
   p = A._dense_probs(q, k, dense, scale)
   q64, k64, v64, do64, o64 = (x.astype(np.float64) for x in (q, k, v, do, out))
   dp = np.einsum("bnhd,bmhd->bhnm", do64, v64)
   ds = p * (dp - (dp * p).sum(-1, keepdims=True))
-  ak = np.abs(k64)
-  t1 = np.einsum("bhnm,bmhd->bnhd", np.abs(ds), ak)
-  od = np.einsum("bnhd,bnhd->bnh", np.abs(do64), np.abs(o64))
-  t2 = np.einsum("bhnm,bmhd->bnhd", p, ak) * od[..., None]
-  return scale * (t1 + t2)
+  od = np.einsum("bnhd,bnhd->bhn", np.abs(do64), np.abs(o64))
+  w = np.abs(ds) + p * od[..., None]
+  bq = scale * np.einsum("bhnm,bmhd->bnhd", w, np.abs(k64))
+  bk = scale * np.einsum("bhnm,bnhd->bmhd", w, np.abs(q64))
+  return bq, bk
 
 
 @pytest.mark.parametrize("case", ["bf16", "f32", "bf16x3"])
@@ -699,7 +761,7 @@ def test_extreme_logits_and_masked_giants(d, case):
   kernel scales and sums them), which enters each probability as a relative error of that size:
   bars 4e-5 (rms) and 2e-4 (max). dq = scale sum_j dS_ij k_j cancels (channel 0 of k carries the
   +-100 offsets, and sum_j dS_ij = 0), so it is held to the rounding bound of that sum
-  (_dq_rounding_bound) with u = 2^-7 in bf16 (twice bf16's unit roundoff) and 2^-14 in float32
+  (_grad_rounding_bounds) with u = 2^-7 in bf16 (twice bf16's unit roundoff) and 2^-14 in float32
   (float32's unit roundoff times the about 1,000 terms an element sums). bf16x3 (float32 tensors,
   products from bf16 parts) is held to the float32 bars: the offsets are exact in bf16, so the
   split leaves them whole, and the other channels are of order one."""
@@ -730,7 +792,7 @@ def test_extreme_logits_and_masked_giants(d, case):
     print(f"  {name}: rel rms {rr:.2e}, max {mr:.2e}", flush=True)
     assert rr <= rms and mr <= mx, (name, rr, mr)
   assert np.isfinite(got["dq"]).all()
-  bound = _dq_rounding_bound(q, k, v, do, got["out"], dense, scale)
+  bound = _grad_rounding_bounds(q, k, v, do, got["out"], dense, scale)[0]
   u = 2.0 ** -7 if dtype == torch.bfloat16 else 2.0 ** -14
   ratio = np.abs(got["dq"] - ref_dq) / (u * bound + 1e-30)
   print(f"  dq: rel rms {A.rel_rms(got['dq'], ref_dq):.2e}, error / bound max {ratio.max():.3f}", flush=True)

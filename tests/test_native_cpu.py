@@ -110,6 +110,23 @@ def test_tile_list_matches_oracle(n, density, permute):
     np.testing.assert_array_equal(g, r)
 
 
+def test_mask_without_valid_elements_has_no_tiles():
+  """A mask with no valid element (and one of a single row) builds as the oracle does: every
+  row block present in tile_ptr, no tiles (empty column and bit arrays); the schedule still has
+  an item per block and the dS map no units."""
+  for n in (1, 300):
+    m = sparse.csr_matrix((n, n), dtype=bool)
+    got = fwn.build_tile_mask(m)
+    ref = ot.build_tile_mask(m, 128, 128)
+    for g, r in zip(got, ref):
+      np.testing.assert_array_equal(g, r)
+    assert len(got[1]) == 0 and got[2].shape == (0, 128, 4)
+    tl = fwn.TileList.from_mask(m, device="cpu")
+    assert tl.n_tiles == 0 and tl.schedule_for(1, 2).n_items == -(-n // 128)
+    status, ubase, tmap, n_units = _ds_map(got, got, 16)
+    assert status == nat.OK and n_units == 0 and len(ubase) == 0 and len(tmap) == 0
+
+
 def _decode_lanes(lanes, n_tiles):
   """Inverse of fwn_tiles_prepare's lane layout, written from the layout's definition."""
   bits = np.zeros((n_tiles, 128, 128), bool)
