@@ -259,11 +259,14 @@ def test_tiny_sequences(n, case):
   check(_np(vt.grad), ref_dv, "dv")
 
 
+@pytest.mark.parametrize("exchange", [True, False])
 @pytest.mark.parametrize("case", ["bf16", "f32", "bf16x3"])
-def test_mask_without_valid_elements(case):
+def test_mask_without_valid_elements(case, exchange, monkeypatch):
   """A mask with no valid element at all has no tiles (every array of the list empty): every
-  row is a row without keys, so the output and every gradient are zero."""
-  print(f"empty mask {case}", flush=True)
+  row is a row without keys, so the output and every gradient are zero, with the dS exchange
+  and with the recomputing backward."""
+  print(f"empty mask {case} exchange={exchange}", flush=True)
+  monkeypatch.setattr(fwn.hip_attn, "DS_EXCHANGE", exchange)
   dtype = torch.bfloat16 if case == "bf16" else torch.float32
   precision = "bf16x3" if case == "bf16x3" else "native"
   rng = np.random.default_rng(3)
