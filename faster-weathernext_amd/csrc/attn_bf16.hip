@@ -795,9 +795,9 @@ __global__ void __launch_bounds__(NT8, 1) dkv16_kernel(KArgs a) {
 
   // dS exchange state: the unit computed last (its dS in dsv, its byte offset in pend; pend =
   // ds_slice_bytes means no unit yet, and that store falls outside the buffer range) and the
-  // forward tile's
-  // (ubase, halves) for the current tile, read at the end of the previous tile's step (a scalar
-  // load pending when the units start would make their first LDS wait wait for it too).
+  // forward tile's (ubase, halves) for the current tile, read at the end of the previous tile's
+  // step (a scalar load pending when the units start would make their first LDS wait wait for it
+  // too).
   rsrc_t rS;
   u32x4 dsv = {0u, 0u, 0u, 0u};
   uint32_t pend = 0u, ubc = 0u, hfc = 0u;
