@@ -377,14 +377,16 @@ __global__ void __launch_bounds__(NT, 2) dq_ds_kernel(KArgs a) {
   // This wave's units of a tile, in the order of its set half bits 8w .. 8w + 7: a tile's units
   // are numbered by rank among all of the word's set bits, so the wave's are consecutive, from
   // the tile's first unit plus the set bits of the waves before it. Each unit is read once:
-  // non-temporal loads.
+  // non-temporal loads. The unit's offset is part of the per-lane offset, which the buffer unit
+  // checks against the slice size (the scalar offset is not checked), so a dS map that does not
+  // match the list cannot reach past its slice.
   auto load_units = [&](u32x4 (&dst)[8], uint32_t hf, uint32_t ub) {
     const uint32_t n = (uint32_t)__builtin_popcount(hf >> (8 * w) & 0xffu);
     const uint32_t u0 = ub + (uint32_t)__builtin_popcount(hf & ((1u << (8 * w)) - 1u));
 #pragma unroll
     for (int k = 0; k < 8; ++k)
       if ((uint32_t)k < n)
-        dst[k] = __builtin_amdgcn_raw_buffer_load_b128(rS, 16 * lane, (int)((u0 + (uint32_t)k) * 1024u), kNonTemporal);
+        dst[k] = __builtin_amdgcn_raw_buffer_load_b128(rS, (int)(16u * lane + (u0 + (uint32_t)k) * 1024u), 0, kNonTemporal);
   };
   // One live half: its unit through stage slot k % 2 (the slot's previous reads come first in
   // program order, and LDS runs one wave's accesses in order), then the dS^T operand and the

@@ -432,8 +432,9 @@ __global__ void __launch_bounds__(NT, 2) dq_f32_ds_kernel(KArgs a) {
       if (gw >> (b0 + x) & 1u) {
 #pragma unroll
         for (int k = 0; k < 4; ++k)
+          // The unit's offset in the per-lane offset: checked against the slice size.
           dst[x][k] = __builtin_bit_cast(
-              f32x4, __builtin_amdgcn_raw_buffer_load_b128(rS, 16 * (64 * k + lane), (int)(u * 4096u), 2));
+              f32x4, __builtin_amdgcn_raw_buffer_load_b128(rS, (int)(16u * (64 * k + lane) + u * 4096u), 0, 2));
         ++u;
       }
   };
@@ -801,8 +802,8 @@ __global__ void __launch_bounds__(256, 2) dkv16_f32_kernel(KArgs a) {
       asm volatile("" ::: "memory");
     }
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
-      __builtin_amdgcn_raw_buffer_store_b128(y[h], rS, 16 * (64 * (2 * (wid & 1) + h) + lane), (int)(u * 4096u), 2);
+    for (int h = 0; h < 2; ++h)  // the unit's offset in the per-lane offset: checked against the slice size
+      __builtin_amdgcn_raw_buffer_store_b128(y[h], rS, (int)(16u * (64 * (2 * (wid & 1) + h) + lane) + u * 4096u), 0, 2);
   };
 
   // Unit: query group c of the group buffer buf (mask word mw of this lane); dS into ds. hm is the

@@ -221,7 +221,8 @@ __global__ void __launch_bounds__(NT, 2) dq_x3_ds_kernel(KArgs a) {
       if (gw >> (b0 + x) & 1u) {
 #pragma unroll
         for (int k = 0; k < 4; ++k)
-          dst[x][k] = __builtin_amdgcn_raw_buffer_load_b128(rS, 16 * (64 * k + lane), (int)(u * 4096u), kNonTemporal);
+          // The unit's offset in the per-lane offset: checked against the slice size.
+          dst[x][k] = __builtin_amdgcn_raw_buffer_load_b128(rS, (int)(16u * (64 * k + lane) + u * 4096u), 0, kNonTemporal);
         ++u;
       }
   };

@@ -167,8 +167,8 @@ __global__ void __launch_bounds__(NT4, 2) dkv16_x3_kernel(KArgs a) {
       asm volatile("" ::: "memory");
     }
 #pragma unroll
-    for (int pl = 0; pl < 2; ++pl)
-      __builtin_amdgcn_raw_buffer_store_b128(y[pl], rS, 16 * (64 * (2 * pl + (wid & 1)) + lane), (int)(u * 4096u),
+    for (int pl = 0; pl < 2; ++pl)  // the unit's offset in the per-lane offset: checked against the slice size
+      __builtin_amdgcn_raw_buffer_store_b128(y[pl], rS, (int)(16u * (64 * (2 * pl + (wid & 1)) + lane) + u * 4096u), 0,
                                              kNonTemporal);
   };
 
